@@ -1,0 +1,152 @@
+/*
+ * rusticide_hip.h -- C ABI of the MI355X (gfx950) quantized matrix-product
+ * path: Q4_K / Q6_K / I2_S weights resident in HBM in their GGUF block
+ * layouts, multiplied by f32 activations that are quantized on the device
+ * exactly as rusticide's CPU kernels quantize them.
+ *
+ * The ABI is what a thin Rust crate (`rusticide-hip`) binds over FFI; each
+ * entry point names the rusticide interface it stands in for (paths relative
+ * to the rusticide repository root). Plain pointers and sizes only; no C++
+ * exceptions cross it. A context owns one HIP stream and is externally
+ * synchronized: calls on one context must not overlap.
+ */
+#ifndef RUSTICIDE_HIP_H
+#define RUSTICIDE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes. They mirror the error kinds of ModelError
+ * (crates/rusticide-model/src/error.rs:11-44) and DispatchError
+ * (crates/rusticide-dispatch/src/error.rs:7-21). */
+typedef enum rh_status {
+    RH_OK = 0,
+    RH_ERR_INVALID_ARGUMENT = 1, /* null pointer, unknown kind, bad length  */
+    RH_ERR_MISSING_KERNEL = 2,   /* ModelError::MissingKernel              */
+    RH_ERR_INVALID_TENSOR = 3,   /* ModelError::InvalidTensor (I2_S scale)  */
+    RH_ERR_SHAPE_MISMATCH = 4,   /* data too short for rows x cols          */
+    RH_ERR_INVALID_CONFIG = 5,   /* ModelError::InvalidConfig (cols == 0)  */
+    RH_ERR_DEVICE = 6,           /* a HIP runtime error; see rh_last_error  */
+    RH_ERR_OUT_OF_MEMORY = 7,
+    RH_ERR_NO_DEVICE = 8         /* no gfx950 device: the caller falls back */
+} rh_status;
+
+/* GGML type ids (crates/rusticide-quantize/src/format.rs:31-92), plus the
+ * dense widths Matrix::load accepts (crates/rusticide-model/src/weights.rs:241-247). */
+enum {
+    RH_TYPE_F32 = 0,
+    RH_TYPE_F16 = 1,
+    RH_TYPE_Q4_K = 12,
+    RH_TYPE_Q6_K = 14,
+    RH_TYPE_I2_S = 36
+};
+
+/* Q8Kind (crates/rusticide-kernels/src/q8_input.rs:86-100). */
+enum { RH_Q8_SUPER_BLOCK = 1, RH_Q8_ROW = 2 };
+
+typedef struct rh_ctx rh_ctx;
+typedef struct rh_matrix rh_matrix;
+
+/* One entry of a batch: a matrix and the output it fills,
+ * out[row * tokens + token]; out_len bounds what is written. The
+ * (Weights, &mut [f32]) pair of matmul_batch
+ * (crates/rusticide-kernels/src/matmul.rs:229). */
+typedef struct rh_job {
+    const rh_matrix *weights;
+    float *out;
+    size_t out_len;
+} rh_job;
+
+/* Opens device `device` and a stream on it. Stands in for the process-wide
+ * adapter selection `active()` (crates/rusticide-kernels/src/adapter.rs:86-169):
+ * RH_ERR_NO_DEVICE tells the caller to keep the CPU adapter. */
+rh_status rh_init(int device, rh_ctx **out);
+void rh_destroy(rh_ctx *ctx);
+/* The message of the last failed call on this context ("" if none). */
+const char *rh_last_error(const rh_ctx *ctx);
+/* Adapter name, as `Adapter::name` (adapter.rs:40-45): "hip-gfx950". */
+const char *rh_adapter_name(void);
+/* The context's HIP stream (a hipStream_t), for rh_matmul_batch_device. */
+void *rh_stream(rh_ctx *ctx);
+
+/* Matrix::load_on (crates/rusticide-model/src/weights.rs:53-98) + the upload:
+ * validates `len` against rows x cols for `type_id`, copies the native
+ * blocks to HBM once (rows padded to a 16-byte stride), and for I2_S parses
+ * and validates the trailer scale (weights.rs:190-202). F16 is widened to
+ * f32 as `widen` does (weights.rs:241-247). */
+rh_status rh_matrix_load(rh_ctx *ctx, uint32_t type_id, const void *data, size_t len,
+                         size_t rows, size_t cols, rh_matrix **out);
+void rh_matrix_free(rh_matrix *m);
+size_t rh_matrix_rows(const rh_matrix *m);
+size_t rh_matrix_cols(const rh_matrix *m);
+uint32_t rh_matrix_type(const rh_matrix *m);
+/* Weights::Ternary::scale (matmul.rs:41-45); 0 for other formats. */
+float rh_matrix_ternary_scale(const rh_matrix *m);
+/* Bytes of HBM the matrix occupies. */
+size_t rh_matrix_device_bytes(const rh_matrix *m);
+
+/* Matrix::copy_row (weights.rs:120-150): dequantizes row `index` into the
+ * host buffer `out` (at most out_len values; I2_S rows are scaled by the
+ * tensor scale). *found = 0 when the row does not exist. */
+rh_status rh_matrix_copy_row(rh_ctx *ctx, const rh_matrix *m, size_t index, float *out,
+                             size_t out_len, int *found);
+
+/* matmul_batch (crates/rusticide-kernels/src/matmul.rs:229-248) on host
+ * buffers: `inputs` holds `tokens` rows of inputs_len / tokens values; each
+ * job's output gets out[row * tokens + token], bit-identical to a
+ * rh_matvec_batch of that token alone. No-op when tokens == 0 or
+ * tokens > inputs_len. Synchronous. */
+rh_status rh_matmul_batch(rh_ctx *ctx, const float *inputs, size_t inputs_len, size_t tokens,
+                          const rh_job *jobs, size_t n_jobs);
+/* matvec_batch (matmul.rs:218-220). */
+rh_status rh_matvec_batch(rh_ctx *ctx, const float *input, size_t len, const rh_job *jobs,
+                          size_t n_jobs);
+/* The device-resident form: `inputs` and every job's `out` are device
+ * pointers; the work is queued on `stream` (a hipStream_t; NULL = the
+ * context's stream) and the call returns without waiting. */
+rh_status rh_matmul_batch_device(rh_ctx *ctx, const float *inputs, size_t inputs_len,
+                                 size_t tokens, const rh_job *jobs, size_t n_jobs, void *stream);
+
+/* A quantized activation batch on the device: Q8Input
+ * (crates/rusticide-kernels/src/q8_input.rs:66-73), one per token. */
+typedef struct rh_q8 rh_q8;
+rh_status rh_q8_new(rh_ctx *ctx, rh_q8 **out);
+void rh_q8_free(rh_q8 *q);
+/* Q8Input::quantize (q8_input.rs:105-108) of every token of `inputs`, a
+ * device pointer holding `tokens` rows of inputs_len / tokens values. Queued
+ * on `stream` (NULL = the context's stream). */
+rh_status rh_q8_quantize_device(rh_ctx *ctx, rh_q8 *q, int kind, const float *inputs,
+                                size_t inputs_len, size_t tokens, void *stream);
+/* QuantKernel::dot_matrix (crates/rusticide-kernels/src/quant_kernel.rs:372-379)
+ * and dot_ternary_matrix (portable/ternary.rs:66-82): every row of `m`
+ * against every token of `q` into the device buffer out[row * tokens + token].
+ * `q` must hold the kind the matrix pairs with (SUPER_BLOCK for Q4_K/Q6_K,
+ * ROW for I2_S). Queued on `stream`. */
+rh_status rh_dot_matrix_device(rh_ctx *ctx, const rh_matrix *m, const rh_q8 *q, float *out,
+                               size_t out_len, void *stream);
+
+/* Test hook: Q8Input::quantize (q8_input.rs:105-108, portable/q8.rs:64-106)
+ * on the device, for one row of `len` host values. Writes n_blocks =
+ * whole 32-blocks (whole 256-blocks for SUPER_BLOCK) quants, scales, sums. */
+rh_status rh_quantize(rh_ctx *ctx, int kind, const float *x, size_t len, int8_t *quants,
+                      float *scales, int32_t *sums, size_t *n_blocks);
+
+/* Test hook: the raw i32 accumulators of an I2_S matrix
+ * (portable/ternary.rs:21-42) against Row-quantized tokens,
+ * out[row * tokens + token], for the bit-exact check. */
+rh_status rh_ternary_dot_i32(rh_ctx *ctx, const rh_matrix *m, const float *inputs,
+                             size_t inputs_len, size_t tokens, int32_t *out, size_t out_len);
+
+/* Token count from which rh_matmul_batch* run k-quant matrices on the MFMA
+ * GEMM instead of the GEMV kernels (both give the same bits). */
+size_t rh_gemm_min_tokens(void);
+void rh_set_gemm_min_tokens(size_t tokens);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,558 @@
+// api.hip -- the C ABI of include/rusticide_hip.h.
+//
+// Host-side mirror of rusticide's kernel facade for the quantized path:
+// Matrix::load_on (crates/rusticide-model/src/weights.rs:53-98) becomes a
+// one-time upload to HBM, and matmul_batch
+// (crates/rusticide-kernels/src/matmul.rs:229-248) becomes: quantize each
+// activation kind once per batch on the device, then one grouped GEMV launch
+// per weight format covering every matrix of that format.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/rusticide_hip.h"
+#include "rh_internal.h"
+
+using namespace rh;
+
+struct rh_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  std::string last_error;
+  // scratch, grown on demand
+  void* buf[8] = {};
+  size_t cap[8] = {};
+  Q8Dev super_q, row_q;
+  size_t gemm_min_tokens = SIZE_MAX;
+};
+
+struct rh_matrix {
+  rh_ctx* ctx = nullptr;
+  uint32_t type_id = 0;
+  size_t rows = 0, cols = 0;
+  size_t row_bytes = 0;  // bytes of one row's data (f32 for dense)
+  size_t stride = 0;     // bytes between rows in HBM
+  size_t nblocks = 0;    // blocks per row (elements for dense)
+  float scale = 0.0f;
+  uint8_t* data = nullptr;
+  size_t bytes = 0;
+};
+
+struct rh_q8 {
+  rh_ctx* ctx = nullptr;
+  int kind = 0;
+  size_t width = 0, tokens = 0;
+  Q8Dev q;
+  void* mem = nullptr;
+  size_t cap = 0;
+};
+
+namespace {
+
+enum Scratch { kIn = 0, kOut, kQuants, kScales, kSums, kSums16, kRaw, kRowQ };
+
+size_t g_gemm_min_tokens = SIZE_MAX;
+
+rh_status fail(rh_ctx* ctx, rh_status st, const std::string& msg) {
+  if (ctx) ctx->last_error = msg;
+  return st;
+}
+
+rh_status hip_fail(rh_ctx* ctx, hipError_t e, const char* what) {
+  return fail(ctx, e == hipErrorOutOfMemory ? RH_ERR_OUT_OF_MEMORY : RH_ERR_DEVICE,
+              std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define RH_HIP(ctx, expr)                            \
+  do {                                               \
+    hipError_t e_ = (expr);                          \
+    if (e_ != hipSuccess) return hip_fail(ctx, e_, #expr); \
+  } while (0)
+
+size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+// Grows scratch slot `i` to at least `bytes`.
+rh_status ensure(rh_ctx* ctx, int i, size_t bytes) {
+  if (ctx->cap[i] >= bytes) return RH_OK;
+  if (ctx->buf[i]) {
+    // work queued on any stream may still read the old buffer
+    RH_HIP(ctx, hipDeviceSynchronize());
+    RH_HIP(ctx, hipFree(ctx->buf[i]));
+    ctx->buf[i] = nullptr;
+    ctx->cap[i] = 0;
+  }
+  size_t want = round_up(bytes < 4096 ? 4096 : bytes, 4096);
+  RH_HIP(ctx, hipMalloc(&ctx->buf[i], want));
+  ctx->cap[i] = want;
+  return RH_OK;
+}
+
+bool is_kquant(uint32_t t) { return t == RH_TYPE_Q4_K || t == RH_TYPE_Q6_K; }
+
+// Block geometry (quantize/src/format.rs:31-92).
+bool geometry(uint32_t type_id, size_t* bs, size_t* bb) {
+  switch (type_id) {
+    case RH_TYPE_Q4_K: *bs = 256; *bb = 144; return true;
+    case RH_TYPE_Q6_K: *bs = 256; *bb = 210; return true;
+    case RH_TYPE_I2_S: *bs = 128; *bb = 32; return true;
+    default: return false;
+  }
+}
+
+// Activation buffers for `tokens` rows of `width` values, both kinds.
+rh_status ensure_q8(rh_ctx* ctx, size_t width, size_t tokens) {
+  const size_t qstride = round_up(width < 256 ? 256 : width, 256);
+  const size_t bstride = round_up(qstride / 32, 8);
+  rh_status st;
+  if ((st = ensure(ctx, kQuants, 2 * tokens * qstride)) != RH_OK) return st;
+  if ((st = ensure(ctx, kScales, 2 * tokens * bstride * sizeof(float))) != RH_OK) return st;
+  if ((st = ensure(ctx, kSums, 2 * tokens * bstride * sizeof(int32_t))) != RH_OK) return st;
+  if ((st = ensure(ctx, kSums16, 3 * tokens * bstride * sizeof(int32_t))) != RH_OK) return st;
+  Q8Dev s;
+  s.qstride = qstride;
+  s.bstride = bstride;
+  s.quants = static_cast<int8_t*>(ctx->buf[kQuants]);
+  s.scales = static_cast<float*>(ctx->buf[kScales]);
+  s.sums = static_cast<int32_t*>(ctx->buf[kSums]);
+  s.sums16 = static_cast<int32_t*>(ctx->buf[kSums16]);
+  s.n_blocks = width / 256 * 8;
+  Q8Dev r = s;
+  r.quants = s.quants + tokens * qstride;
+  r.scales = s.scales + tokens * bstride;
+  r.sums = s.sums + tokens * bstride;
+  r.sums16 = s.sums16 + 2 * tokens * bstride;  // per-16 sums: super kind only
+  r.n_blocks = width / 32;
+  ctx->super_q = s;
+  ctx->row_q = r;
+  return RH_OK;
+}
+
+// Rows worth computing: out_len bounds them (quant_kernel.rs:416-419).
+size_t rows_for(const rh_matrix* m, size_t out_len, size_t tokens) {
+  size_t by_out = (out_len + tokens - 1) / tokens;
+  return m->rows < by_out ? m->rows : by_out;
+}
+
+// One grouped launch per format over `jobs`, against quantized activations
+// `super_q` / `row_q` (or the raw f32 inputs for dense rows).
+rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t tokens, const rh_job* jobs,
+                      size_t n_jobs, const Q8Dev& super_q, const Q8Dev& row_q, hipStream_t s,
+                      int32_t* raw) {
+  rh_status st = RH_OK;
+  const uint32_t kinds[4] = {RH_TYPE_Q4_K, RH_TYPE_Q6_K, RH_TYPE_I2_S, RH_TYPE_F32};
+  for (uint32_t kind : kinds) {
+    GemvJobs g{};
+    uint32_t nbmax = 0;
+    auto flush = [&]() -> rh_status {
+      if (g.n == 0) return RH_OK;
+      size_t tmax = kMaxTokens;
+      if (kind != RH_TYPE_F32) tmax = gemv_max_tokens(kind, nbmax);
+      if (tmax == 0) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "rows too wide for the GEMV kernels");
+      const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
+      for (size_t t0 = 0; t0 < tokens; t0 += tmax) {
+        size_t tn = tokens - t0 < tmax ? tokens - t0 : tmax;
+        RH_HIP(ctx, launch_gemv(kind, g, q, d_in, width, tokens, t0, tn, s, raw));
+      }
+      g = GemvJobs{};
+      nbmax = 0;
+      return RH_OK;
+    };
+    for (size_t i = 0; i < n_jobs; i++) {
+      const rh_matrix* m = jobs[i].weights;
+      const uint32_t t = (m->type_id == RH_TYPE_F16) ? RH_TYPE_F32 : m->type_id;
+      if (t != kind) continue;
+      const size_t rows = rows_for(m, jobs[i].out_len, tokens);
+      if (rows == 0) continue;
+      size_t nb;
+      if (kind == RH_TYPE_F32) nb = m->cols < width ? m->cols : width;
+      else if (kind == RH_TYPE_I2_S) nb = row_q.n_blocks / 4;
+      else nb = super_q.n_blocks / 8;
+      if (kind != RH_TYPE_F32 && m->nblocks < nb) nb = m->nblocks;
+      GemvJob& j = g.j[g.n++];
+      j.w = m->data;
+      j.stride = m->stride;
+      j.rows = static_cast<uint32_t>(rows);
+      j.nb = static_cast<uint32_t>(nb);
+      j.out = jobs[i].out;
+      j.out_len = jobs[i].out_len;
+      j.scale = m->scale;
+      if (kind != RH_TYPE_F32 && nb > nbmax) nbmax = static_cast<uint32_t>(nb);
+      if (g.n == static_cast<uint32_t>(kMaxJobs) && (st = flush()) != RH_OK) return st;
+    }
+    if ((st = flush()) != RH_OK) return st;
+  }
+  return RH_OK;
+}
+
+rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t tokens,
+                    const rh_job* jobs, size_t n_jobs, hipStream_t s, int32_t* raw) {
+  const size_t width = inputs_len / tokens;
+  bool need_super = false, need_row = false;
+  for (size_t i = 0; i < n_jobs; i++) {
+    if (!jobs[i].weights) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a job has no matrix");
+    if (!jobs[i].out && jobs[i].out_len) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a job has no output");
+    need_super |= is_kquant(jobs[i].weights->type_id);
+    need_row |= jobs[i].weights->type_id == RH_TYPE_I2_S;
+  }
+  rh_status st = ensure_q8(ctx, width, tokens);
+  if (st != RH_OK) return st;
+  if (need_super) RH_HIP(ctx, launch_quantize_super(d_in, width, tokens, ctx->super_q, s));
+  if (need_row) RH_HIP(ctx, launch_quantize_row(d_in, width, tokens, ctx->row_q, s));
+  return launch_jobs(ctx, d_in, width, tokens, jobs, n_jobs, ctx->super_q, ctx->row_q, s, raw);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rh_adapter_name(void) { return "hip-gfx950"; }
+
+rh_status rh_init(int device, rh_ctx** out) {
+  if (!out) return RH_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return RH_ERR_NO_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return RH_ERR_NO_DEVICE;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RH_ERR_NO_DEVICE;
+  rh_ctx* ctx = new (std::nothrow) rh_ctx();
+  if (!ctx) return RH_ERR_OUT_OF_MEMORY;
+  ctx->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
+    delete ctx;
+    return RH_ERR_DEVICE;
+  }
+  *out = ctx;
+  return RH_OK;
+}
+
+void rh_destroy(rh_ctx* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  for (void* b : ctx->buf)
+    if (b) hipFree(b);
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+
+void* rh_stream(rh_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+size_t rh_gemm_min_tokens(void) { return g_gemm_min_tokens; }
+void rh_set_gemm_min_tokens(size_t tokens) { g_gemm_min_tokens = tokens; }
+
+rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t len, size_t rows,
+                         size_t cols, rh_matrix** out) {
+  if (!ctx || !out || (!data && len)) return RH_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  if (cols == 0) return fail(ctx, RH_ERR_INVALID_CONFIG, "a weight matrix has no columns");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  rh_matrix* m = new (std::nothrow) rh_matrix();
+  if (!m) return fail(ctx, RH_ERR_OUT_OF_MEMORY, "host allocation failed");
+  m->ctx = ctx;
+  m->type_id = type_id;
+  m->rows = rows;
+  m->cols = cols;
+  std::vector<float> widened;
+  const uint8_t* src = static_cast<const uint8_t*>(data);
+  size_t bs = 0, bb = 0;
+  if (type_id == RH_TYPE_F32 || type_id == RH_TYPE_F16) {
+    const size_t esz = type_id == RH_TYPE_F32 ? 4 : 2;
+    if (rows && len / esz / rows < cols) {
+      delete m;
+      return fail(ctx, RH_ERR_SHAPE_MISMATCH, "data too short for rows x cols");
+    }
+    if (type_id == RH_TYPE_F16) {  // widen (model/src/weights.rs:241-247)
+      widened.resize(rows * cols);
+      for (size_t i = 0; i < rows * cols; i++) {
+        uint16_t h;
+        std::memcpy(&h, src + 2 * i, 2);
+        _Float16 f;
+        std::memcpy(&f, &h, 2);
+        widened[i] = static_cast<float>(f);
+      }
+      src = reinterpret_cast<const uint8_t*>(widened.data());
+      m->type_id = RH_TYPE_F32;
+    }
+    m->row_bytes = cols * 4;
+    m->stride = m->row_bytes;
+    m->nblocks = cols;
+  } else if (geometry(type_id, &bs, &bb)) {
+    if (cols % bs != 0) {
+      delete m;
+      return fail(ctx, RH_ERR_SHAPE_MISMATCH, "cols is not a whole number of blocks");
+    }
+    m->nblocks = cols / bs;
+    m->row_bytes = m->nblocks * bb;
+    m->stride = round_up(m->row_bytes, 16);
+    const size_t body = rows * m->row_bytes;
+    if (type_id == RH_TYPE_I2_S) {
+      // model/src/weights.rs:70-80,190-202: the trailer's leading f32
+      if (len < body || len - body < 4) {
+        delete m;
+        return fail(ctx, RH_ERR_INVALID_TENSOR, "its data is too short to hold its scale");
+      }
+      float scale;
+      std::memcpy(&scale, src + body, 4);
+      if (!std::isfinite(scale)) {
+        delete m;
+        return fail(ctx, RH_ERR_INVALID_TENSOR, "its scale is not finite");
+      }
+      m->scale = scale;
+    } else if (len < body) {
+      delete m;
+      return fail(ctx, RH_ERR_SHAPE_MISMATCH, "data too short for rows x cols");
+    }
+  } else {
+    delete m;
+    return fail(ctx, RH_ERR_MISSING_KERNEL, "no kernel reads this block format");
+  }
+  m->bytes = round_up(rows * m->stride + kPad, 256);
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(&m->data), m->bytes);
+  if (e != hipSuccess) {
+    delete m;
+    return hip_fail(ctx, e, "hipMalloc(matrix)");
+  }
+  e = hipMemsetAsync(m->data, 0, m->bytes, ctx->stream);
+  if (e == hipSuccess && rows) {
+    if (m->stride == m->row_bytes)
+      e = hipMemcpyAsync(m->data, src, rows * m->row_bytes, hipMemcpyHostToDevice, ctx->stream);
+    else
+      e = hipMemcpy2DAsync(m->data, m->stride, src, m->row_bytes, m->row_bytes, rows,
+                           hipMemcpyHostToDevice, ctx->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+  if (e != hipSuccess) {
+    hipFree(m->data);
+    delete m;
+    return hip_fail(ctx, e, "upload");
+  }
+  *out = m;
+  return RH_OK;
+}
+
+void rh_matrix_free(rh_matrix* m) {
+  if (!m) return;
+  hipSetDevice(m->ctx->device);
+  hipStreamSynchronize(m->ctx->stream);
+  hipFree(m->data);
+  delete m;
+}
+
+size_t rh_matrix_rows(const rh_matrix* m) { return m ? m->rows : 0; }
+size_t rh_matrix_cols(const rh_matrix* m) { return m ? m->cols : 0; }
+uint32_t rh_matrix_type(const rh_matrix* m) { return m ? m->type_id : 0; }
+float rh_matrix_ternary_scale(const rh_matrix* m) { return m ? m->scale : 0.0f; }
+size_t rh_matrix_device_bytes(const rh_matrix* m) { return m ? m->bytes : 0; }
+
+rh_status rh_matrix_copy_row(rh_ctx* ctx, const rh_matrix* m, size_t index, float* out,
+                             size_t out_len, int* found) {
+  if (!ctx || !m || !found || (!out && out_len)) return RH_ERR_INVALID_ARGUMENT;
+  *found = 0;
+  if (index >= m->rows) return RH_OK;
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  const uint8_t* row = m->data + index * m->stride;
+  if (m->type_id == RH_TYPE_F32) {
+    // a dense row is copied whole into an output of its length (weights.rs:122-125)
+    if (out_len < m->cols) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "output shorter than the row");
+    RH_HIP(ctx, hipMemcpyAsync(out, row, m->cols * 4, hipMemcpyDeviceToHost, ctx->stream));
+    RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    *found = 1;
+    return RH_OK;
+  }
+  // Blocks: whole blocks the output holds (format.rs:219-226). Ternary: the
+  // first min(cols, out_len) values, decoded as whole blocks and then all
+  // multiplied by the tensor scale (weights.rs:134-147).
+  const size_t bs = m->type_id == RH_TYPE_I2_S ? 128 : 256;
+  const size_t span = m->type_id == RH_TYPE_I2_S ? (m->cols < out_len ? m->cols : out_len) : out_len;
+  size_t nb = span / bs;
+  if (nb > m->nblocks) nb = m->nblocks;
+  rh_status st = ensure(ctx, kOut, (nb * bs + 1) * 4);
+  if (st != RH_OK) return st;
+  float* d = static_cast<float*>(ctx->buf[kOut]);
+  if (nb) {
+    RH_HIP(ctx, launch_dequantize_row(m->type_id, row, static_cast<uint32_t>(nb), m->scale, d, nb * bs,
+                                      ctx->stream));
+    RH_HIP(ctx, hipMemcpyAsync(out, d, nb * bs * 4, hipMemcpyDeviceToHost, ctx->stream));
+  }
+  RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  if (m->type_id == RH_TYPE_I2_S)
+    for (size_t i = nb * bs; i < span; i++) out[i] *= m->scale;
+  *found = 1;
+  return RH_OK;
+}
+
+rh_status rh_matmul_batch_device(rh_ctx* ctx, const float* inputs, size_t inputs_len, size_t tokens,
+                                 const rh_job* jobs, size_t n_jobs, void* stream) {
+  if (!ctx || (!jobs && n_jobs)) return RH_ERR_INVALID_ARGUMENT;
+  if (tokens == 0 || tokens > inputs_len) return RH_OK;  // matmul.rs:230-232
+  if (!inputs) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "no inputs");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+  return run_batch(ctx, inputs, inputs_len, tokens, jobs, n_jobs, s, nullptr);
+}
+
+rh_status rh_matmul_batch(rh_ctx* ctx, const float* inputs, size_t inputs_len, size_t tokens,
+                          const rh_job* jobs, size_t n_jobs) {
+  if (!ctx || (!jobs && n_jobs)) return RH_ERR_INVALID_ARGUMENT;
+  if (tokens == 0 || tokens > inputs_len) return RH_OK;
+  if (!inputs) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "no inputs");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  size_t total_out = 0;
+  std::vector<size_t> written(n_jobs);
+  for (size_t i = 0; i < n_jobs; i++) {
+    if (!jobs[i].weights) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a job has no matrix");
+    const size_t rows = rows_for(jobs[i].weights, jobs[i].out_len, tokens);
+    const size_t w = rows * tokens < jobs[i].out_len ? rows * tokens : jobs[i].out_len;
+    written[i] = w;
+    total_out += round_up(w + 1, 64);
+  }
+  rh_status st;
+  if ((st = ensure(ctx, kIn, inputs_len * sizeof(float))) != RH_OK) return st;
+  if ((st = ensure(ctx, kOut, total_out * sizeof(float))) != RH_OK) return st;
+  float* d_in = static_cast<float*>(ctx->buf[kIn]);
+  float* d_out = static_cast<float*>(ctx->buf[kOut]);
+  RH_HIP(ctx, hipMemcpyAsync(d_in, inputs, inputs_len * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  std::vector<rh_job> dj(jobs, jobs + n_jobs);
+  size_t off = 0;
+  for (size_t i = 0; i < n_jobs; i++) {
+    dj[i].out = d_out + off;
+    off += round_up(written[i] + 1, 64);
+  }
+  if ((st = run_batch(ctx, d_in, inputs_len, tokens, dj.data(), n_jobs, ctx->stream, nullptr)) != RH_OK)
+    return st;
+  for (size_t i = 0; i < n_jobs; i++)
+    if (written[i])
+      RH_HIP(ctx, hipMemcpyAsync(jobs[i].out, dj[i].out, written[i] * sizeof(float), hipMemcpyDeviceToHost,
+                                 ctx->stream));
+  RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return RH_OK;
+}
+
+rh_status rh_matvec_batch(rh_ctx* ctx, const float* input, size_t len, const rh_job* jobs, size_t n_jobs) {
+  return rh_matmul_batch(ctx, input, len, 1, jobs, n_jobs);
+}
+
+rh_status rh_q8_new(rh_ctx* ctx, rh_q8** out) {
+  if (!ctx || !out) return RH_ERR_INVALID_ARGUMENT;
+  *out = new (std::nothrow) rh_q8();
+  if (!*out) return fail(ctx, RH_ERR_OUT_OF_MEMORY, "host allocation failed");
+  (*out)->ctx = ctx;
+  return RH_OK;
+}
+
+void rh_q8_free(rh_q8* q) {
+  if (!q) return;
+  if (q->mem) {
+    hipSetDevice(q->ctx->device);
+    hipDeviceSynchronize();
+    hipFree(q->mem);
+  }
+  delete q;
+}
+
+rh_status rh_q8_quantize_device(rh_ctx* ctx, rh_q8* q, int kind, const float* inputs, size_t inputs_len,
+                                size_t tokens, void* stream) {
+  if (!ctx || !q) return RH_ERR_INVALID_ARGUMENT;
+  if (kind != RH_Q8_SUPER_BLOCK && kind != RH_Q8_ROW)
+    return fail(ctx, RH_ERR_INVALID_ARGUMENT, "unknown activation kind");
+  if (tokens == 0 || tokens > inputs_len) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "no whole token");
+  if (!inputs) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "no inputs");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+  const size_t width = inputs_len / tokens;
+  const size_t qstride = round_up(width < 256 ? 256 : width, 256);
+  const size_t bstride = round_up(qstride / 32, 8);
+  const size_t need = tokens * qstride + 4 * tokens * bstride * (1 + 1 + 2) + 1024;
+  if (q->cap < need) {
+    if (q->mem) {
+      RH_HIP(ctx, hipDeviceSynchronize());
+      RH_HIP(ctx, hipFree(q->mem));
+      q->mem = nullptr;
+      q->cap = 0;
+    }
+    RH_HIP(ctx, hipMalloc(&q->mem, need));
+    q->cap = need;
+  }
+  uint8_t* base = static_cast<uint8_t*>(q->mem);
+  q->q.qstride = qstride;
+  q->q.bstride = bstride;
+  q->q.quants = reinterpret_cast<int8_t*>(base);
+  q->q.scales = reinterpret_cast<float*>(base + tokens * qstride);
+  q->q.sums = reinterpret_cast<int32_t*>(base + tokens * qstride + 4 * tokens * bstride);
+  q->q.sums16 = reinterpret_cast<int32_t*>(base + tokens * qstride + 8 * tokens * bstride);
+  q->q.n_blocks = kind == RH_Q8_SUPER_BLOCK ? width / 256 * 8 : width / 32;
+  q->kind = kind;
+  q->width = width;
+  q->tokens = tokens;
+  if (kind == RH_Q8_SUPER_BLOCK) RH_HIP(ctx, launch_quantize_super(inputs, width, tokens, q->q, s));
+  else RH_HIP(ctx, launch_quantize_row(inputs, width, tokens, q->q, s));
+  return RH_OK;
+}
+
+rh_status rh_dot_matrix_device(rh_ctx* ctx, const rh_matrix* m, const rh_q8* q, float* out, size_t out_len,
+                               void* stream) {
+  if (!ctx || !m || !q || (!out && out_len)) return RH_ERR_INVALID_ARGUMENT;
+  if (q->tokens == 0) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "the activation holds no token");
+  const int want = m->type_id == RH_TYPE_I2_S ? RH_Q8_ROW : RH_Q8_SUPER_BLOCK;
+  if (!is_kquant(m->type_id) && m->type_id != RH_TYPE_I2_S)
+    return fail(ctx, RH_ERR_INVALID_ARGUMENT, "dense rows take f32 inputs: use rh_matmul_batch_device");
+  if (q->kind != want) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "activation kind does not match the format");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+  rh_job job{m, out, out_len};
+  return launch_jobs(ctx, nullptr, q->width, q->tokens, &job, 1, q->q, q->q, s, nullptr);
+}
+
+rh_status rh_quantize(rh_ctx* ctx, int kind, const float* x, size_t len, int8_t* quants, float* scales,
+                      int32_t* sums, size_t* n_blocks) {
+  if (!ctx || !n_blocks || (!x && len)) return RH_ERR_INVALID_ARGUMENT;
+  if (kind != RH_Q8_SUPER_BLOCK && kind != RH_Q8_ROW)
+    return fail(ctx, RH_ERR_INVALID_ARGUMENT, "unknown activation kind");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  const size_t nb = kind == RH_Q8_SUPER_BLOCK ? len / 256 * 8 : len / 32;
+  *n_blocks = nb;
+  if (nb == 0) return RH_OK;
+  if (!quants || !scales || !sums) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "null output");
+  rh_status st;
+  if ((st = ensure(ctx, kIn, len * sizeof(float))) != RH_OK) return st;
+  if ((st = ensure_q8(ctx, len, 1)) != RH_OK) return st;
+  float* d_in = static_cast<float*>(ctx->buf[kIn]);
+  RH_HIP(ctx, hipMemcpyAsync(d_in, x, len * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  const Q8Dev& q = kind == RH_Q8_SUPER_BLOCK ? ctx->super_q : ctx->row_q;
+  if (kind == RH_Q8_SUPER_BLOCK) RH_HIP(ctx, launch_quantize_super(d_in, len, 1, q, ctx->stream));
+  else RH_HIP(ctx, launch_quantize_row(d_in, len, 1, q, ctx->stream));
+  RH_HIP(ctx, hipMemcpyAsync(quants, q.quants, nb * 32, hipMemcpyDeviceToHost, ctx->stream));
+  RH_HIP(ctx, hipMemcpyAsync(scales, q.scales, nb * 4, hipMemcpyDeviceToHost, ctx->stream));
+  RH_HIP(ctx, hipMemcpyAsync(sums, q.sums, nb * 4, hipMemcpyDeviceToHost, ctx->stream));
+  RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return RH_OK;
+}
+
+rh_status rh_ternary_dot_i32(rh_ctx* ctx, const rh_matrix* m, const float* inputs, size_t inputs_len,
+                             size_t tokens, int32_t* out, size_t out_len) {
+  if (!ctx || !m || (!out && out_len)) return RH_ERR_INVALID_ARGUMENT;
+  if (m->type_id != RH_TYPE_I2_S) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "not an I2_S matrix");
+  if (tokens == 0 || tokens > inputs_len) return RH_OK;
+  if (!inputs) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "no inputs");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  const size_t rows = rows_for(m, out_len, tokens);
+  const size_t w = rows * tokens < out_len ? rows * tokens : out_len;
+  rh_status st;
+  if ((st = ensure(ctx, kIn, inputs_len * sizeof(float))) != RH_OK) return st;
+  if ((st = ensure(ctx, kRaw, (w + 1) * sizeof(int32_t))) != RH_OK) return st;
+  float* d_in = static_cast<float*>(ctx->buf[kIn]);
+  int32_t* d_raw = static_cast<int32_t*>(ctx->buf[kRaw]);
+  RH_HIP(ctx, hipMemcpyAsync(d_in, inputs, inputs_len * sizeof(float), hipMemcpyHostToDevice, ctx->stream));
+  rh_job job{m, reinterpret_cast<float*>(d_raw), out_len};
+  if ((st = run_batch(ctx, d_in, inputs_len, tokens, &job, 1, ctx->stream, d_raw)) != RH_OK) return st;
+  if (w) RH_HIP(ctx, hipMemcpyAsync(out, d_raw, w * sizeof(int32_t), hipMemcpyDeviceToHost, ctx->stream));
+  RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return RH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,512 @@
+// gemv.hip -- decode GEMV on gfx950: Q4_K / Q6_K / I2_S weights in their
+// native GGUF block layouts against device-quantized activations.
+//
+// Work split: a workgroup of 256 lanes owns R consecutive rows of one matrix
+// (several matrices share a launch, as matmul_batch shares one parallel
+// region: crates/rusticide-kernels/src/matmul.rs:229-248). The activation of
+// every token in the launch is staged in LDS once per workgroup.
+//
+// k-quants: a team of 4 lanes decodes one 256-weight super-block in
+// registers from three 16-byte loads per lane, forms the block's integer sums
+// with v_dot4_i32_i8 and DPP quad reductions (exact, so their order is free),
+// and writes the block's float term. The terms of a row are then added in
+// block order from -0.0 by one lane, which is the order of the CPU path
+// (portable/int_dot/rows.rs:9-12,59): the result is bit-identical.
+//
+// I2_S: a team of 8 lanes walks a row 16 bytes at a time; the i32 dot is
+// order-free (wrapping) and is scaled once per row, as portable/ternary.rs:48-58.
+#include "rh_device.h"
+#include "rh_internal.h"
+
+namespace rh {
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+
+__device__ __forceinline__ uint32_t find_job(const GemvJobs& jobs) {
+  uint32_t j = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < static_cast<uint32_t>(kMaxJobs); i++)
+    if (i < jobs.n && blockIdx.x >= jobs.j[i].wg_begin) j = i;
+  return j;
+}
+
+// Copies `bytes` (a multiple of 16) of each token's quants into LDS.
+template <int T>
+__device__ __forceinline__ void stage_quants(int8_t* act, uint32_t bytes, const Q8Dev& q, size_t t0) {
+  for (uint32_t t = 0; t < static_cast<uint32_t>(T); t++) {
+    const int8_t* src = q.quants + (t0 + t) * q.qstride;
+    for (uint32_t i = threadIdx.x * 16u; i < bytes; i += kThreads * 16u)
+      *reinterpret_cast<u32x4*>(act + t * bytes + i) = *reinterpret_cast<const u32x4*>(src + i);
+  }
+}
+
+// Q4_K x Q8_K --------------------------------------------------------------
+// LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
+//      terms [R][nbmax][T] f32
+template <int T>
+__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
+                                                       uint32_t nbmax, size_t tokens, size_t t0) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t abytes = nbmax * 256u;
+  int8_t* act = reinterpret_cast<int8_t*>(lds);
+  float* d8 = reinterpret_cast<float*>(lds + T * abytes);
+  int32_t* sums = reinterpret_cast<int32_t*>(d8 + T * nbmax);
+  float* terms = reinterpret_cast<float*>(sums + T * nbmax * 8u);
+
+  const GemvJob& J = jobs.j[find_job(jobs)];
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
+  const uint32_t nrows = min(R, J.rows - row0);
+  const uint32_t nb = J.nb;
+
+  stage_quants<T>(act, abytes, q, t0);
+  for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += kThreads) {
+    const uint32_t t = i / (nbmax * 8u), k = i - t * nbmax * 8u;
+    const size_t src = (t0 + t) * q.bstride + k;
+    sums[i] = q.sums[src];
+    if ((k & 7u) == 0) d8[t * nbmax + k / 8u] = q.scales[src];
+  }
+  __syncthreads();
+
+  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
+  const uint32_t j0 = 2u * (p >> 1), e0 = 16u * (p & 1u);
+  const bool min_lane = (p & 1u) == 0;
+  for (uint32_t g = team; g < nrows * nb; g += kThreads / 4u) {
+    const uint32_t r = g / nb, b = g - r * nb;
+    const uint8_t* blk = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 144u;
+    const u32x4 hd = load16(blk);
+    const u32x4 c0 = load16(blk + 16u + 16u * p);
+    const u32x4 c1 = load16(blk + 80u + 16u * p);
+    // 6-bit scales/mins of sub-blocks j0, j0+1, j0+4, j0+5 (ggml get_scale_min_k4,
+    // quantize/src/q4_k.rs:17-25)
+    const int32_t sc0 = static_cast<int32_t>(bfe(hd.y, 8u * j0, 6));
+    const int32_t sc1 = static_cast<int32_t>(bfe(hd.y, 8u * j0 + 8u, 6));
+    const int32_t sc2 = static_cast<int32_t>(bfe(hd.w, 8u * j0, 4) | (bfe(hd.y, 8u * j0 + 6u, 2) << 4));
+    const int32_t sc3 = static_cast<int32_t>(bfe(hd.w, 8u * j0 + 8u, 4) | (bfe(hd.y, 8u * j0 + 14u, 2) << 4));
+    const int32_t m0 = static_cast<int32_t>(bfe(hd.z, 8u * j0, 6));
+    const int32_t m1 = static_cast<int32_t>(bfe(hd.z, 8u * j0 + 8u, 6));
+    const int32_t m2 = static_cast<int32_t>(bfe(hd.w, 8u * j0 + 4u, 4) | (bfe(hd.z, 8u * j0 + 6u, 2) << 4));
+    const int32_t m3 = static_cast<int32_t>(bfe(hd.w, 8u * j0 + 12u, 4) | (bfe(hd.z, 8u * j0 + 14u, 2) << 4));
+    const float d = f16_lo(hd.x), dmin = f16_hi(hd.x);
+    uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      lo0[k] = c0[k] & 0x0F0F0F0Fu;
+      hi0[k] = (c0[k] >> 4) & 0x0F0F0F0Fu;
+      lo1[k] = c1[k] & 0x0F0F0F0Fu;
+      hi1[k] = (c1[k] >> 4) & 0x0F0F0F0Fu;
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const int8_t* a = act + t * abytes + b * 256u + e0;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a + 32u * j0);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u * j0 + 32u);
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 32u * j0 + 128u);
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 32u * j0 + 160u);
+      int32_t D0 = 0, D1 = 0, D2 = 0, D3 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        D0 = dot4(lo0[k], a0[k], D0);
+        D1 = dot4(hi0[k], a1[k], D1);
+        D2 = dot4(lo1[k], a2[k], D2);
+        D3 = dot4(hi1[k], a3[k], D3);
+      }
+      int32_t isum = sc0 * D0 + sc1 * D1 + sc2 * D2 + sc3 * D3;
+      const int32_t* S = sums + t * nbmax * 8u + b * 8u + j0;
+      int32_t msum = min_lane ? (m0 * S[0] + m1 * S[1] + m2 * S[4] + m3 * S[5]) : 0;
+      isum = quad_sum(isum);
+      msum = quad_sum(msum);
+      if (p == 0) {
+        // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
+        const float neg = -(dmin * static_cast<float>(msum));
+        terms[(r * nbmax + b) * T + t] = d8[t * nbmax + b] * __builtin_fmaf(d, static_cast<float>(isum), neg);
+      }
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < nrows * T; i += kThreads) {
+    const uint32_t r = i / T, t = i - r * T;
+    float s = -0.0f;
+    for (uint32_t b = 0; b < nb; b++) s += terms[(r * nbmax + b) * T + t];
+    const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
+    if (idx < J.out_len) J.out[idx] = s;
+  }
+}
+
+// Q6_K x Q8_K --------------------------------------------------------------
+// LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | bias [T][nbmax*16] i32
+//      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
+template <int T>
+__global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
+                                                       uint32_t nbmax, size_t tokens, size_t t0) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t abytes = nbmax * 256u;
+  int8_t* act = reinterpret_cast<int8_t*>(lds);
+  float* d8 = reinterpret_cast<float*>(lds + T * abytes);
+  int32_t* bias = reinterpret_cast<int32_t*>(d8 + T * nbmax);
+  float* terms = reinterpret_cast<float*>(bias + T * nbmax * 16u);
+
+  const GemvJob& J = jobs.j[find_job(jobs)];
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
+  const uint32_t nrows = min(R, J.rows - row0);
+  const uint32_t nb = J.nb;
+
+  stage_quants<T>(act, abytes, q, t0);
+  for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += kThreads) {
+    const uint32_t t = i / (nbmax * 16u), k = i - t * nbmax * 16u;
+    bias[i] = -32 * q.sums16[2u * (t0 + t) * q.bstride + k];
+    if ((k & 15u) == 0) d8[t * nbmax + k / 16u] = q.scales[(t0 + t) * q.bstride + k / 2u];
+  }
+  __syncthreads();
+
+  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
+  const uint32_t h = p >> 1, gq = p & 1u;
+  for (uint32_t g = team; g < nrows * nb; g += kThreads / 4u) {
+    const uint32_t r = g / nb, b = g - r * nb;
+    const uint8_t* blk = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 210u;
+    // ql[64h+16gq..], ql[64h+32+16gq..], qh[32h+16gq..] (quantize/src/q6_k.rs:13-43)
+    const u32x4 A = load16_unaligned(blk + 64u * h + 16u * gq);
+    const u32x4 B = load16_unaligned(blk + 64u * h + 32u + 16u * gq);
+    const u32x4 C = load16_unaligned(blk + 128u + 32u * h + 16u * gq);
+    // scales[16] at 192 and d at 208, realigned from six aligned dwords
+    const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 3u);
+    const uint8_t* hb = blk + 192u - sh;
+    const u32x4 w03 = load16_a4(hb);
+    const uint32_t w4 = load4(hb + 16u), w5 = load4(hb + 20u);
+    const uint32_t X0 = __builtin_amdgcn_alignbyte(w03.y, w03.x, sh);
+    const uint32_t X1 = __builtin_amdgcn_alignbyte(w03.z, w03.y, sh);
+    const uint32_t X2 = __builtin_amdgcn_alignbyte(w03.w, w03.z, sh);
+    const uint32_t X3 = __builtin_amdgcn_alignbyte(w4, w03.w, sh);
+    const uint32_t X4 = __builtin_amdgcn_alignbyte(w5, w4, sh);
+    const uint32_t slo = h ? X2 : X0, shi = h ? X3 : X1;
+    // scale of run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
+    const int32_t sc0 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq, 8);
+    const int32_t sc1 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq + 16u, 8);
+    const int32_t sc2 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq, 8);
+    const int32_t sc3 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq + 16u, 8);
+    const float d = f16_lo(X4);
+    uint32_t q0[4], q1[4], q2[4], q3[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      q0[k] = (A[k] & 0x0F0F0F0Fu) | ((C[k] << 4) & 0x30303030u);
+      q1[k] = (B[k] & 0x0F0F0F0Fu) | ((C[k] << 2) & 0x30303030u);
+      q2[k] = ((A[k] >> 4) & 0x0F0F0F0Fu) | (C[k] & 0x30303030u);
+      q3[k] = ((B[k] >> 4) & 0x0F0F0F0Fu) | ((C[k] >> 2) & 0x30303030u);
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const int8_t* a = act + t * abytes + b * 256u + 128u * h + 16u * gq;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+      const int32_t* bb = bias + t * nbmax * 16u + b * 16u + 8u * h + gq;
+      int32_t D0 = bb[0], D1 = bb[2], D2 = bb[4], D3 = bb[6];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        D0 = dot4(q0[k], a0[k], D0);
+        D1 = dot4(q1[k], a1[k], D1);
+        D2 = dot4(q2[k], a2[k], D2);
+        D3 = dot4(q3[k], a3[k], D3);
+      }
+      int32_t isum = quad_sum(sc0 * D0 + sc1 * D1 + sc2 * D2 + sc3 * D3);
+      if (p == 0) {
+        // int_dot.rs:203: read_f16_le(block, 208) * span.scales[0] * lossy(sum)
+        const float dd = d * d8[t * nbmax + b];
+        terms[(r * nbmax + b) * T + t] = dd * static_cast<float>(isum);
+      }
+    }
+  }
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < nrows * T; i += kThreads) {
+    const uint32_t r = i / T, t = i - r * T;
+    float s = -0.0f;
+    for (uint32_t b = 0; b < nb; b++) s += terms[(r * nbmax + b) * T + t];
+    const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
+    if (idx < J.out_len) J.out[idx] = s;
+  }
+}
+
+// I2_S x I8_S --------------------------------------------------------------
+// LDS: act [T][nbmax*128] i8 | prefix [T][nbmax+1] i32 (sums of the first 4b
+// activation blocks) | divisor [T] f32
+template <int T>
+__global__ __launch_bounds__(256) void gemv_i2s_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
+                                                       uint32_t nbmax, size_t tokens, size_t t0,
+                                                       int32_t* raw) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t abytes = nbmax * 128u;
+  int8_t* act = reinterpret_cast<int8_t*>(lds);
+  int32_t* prefix = reinterpret_cast<int32_t*>(lds + T * abytes);
+  float* divisor = reinterpret_cast<float*>(prefix + T * (nbmax + 1u));
+
+  const GemvJob& J = jobs.j[find_job(jobs)];
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
+  const uint32_t nrows = min(R, J.rows - row0);
+  const uint32_t nb = J.nb;
+
+  stage_quants<T>(act, abytes, q, t0);
+  if (threadIdx.x < static_cast<uint32_t>(T)) {
+    const uint32_t t = threadIdx.x;
+    const int32_t* s = q.sums + (t0 + t) * q.bstride;
+    uint32_t acc = 0;
+    prefix[t * (nbmax + 1u)] = 0;
+    for (uint32_t b = 0; b < nbmax; b++) {
+      acc += static_cast<uint32_t>(s[4u * b]) + static_cast<uint32_t>(s[4u * b + 1u]) +
+             static_cast<uint32_t>(s[4u * b + 2u]) + static_cast<uint32_t>(s[4u * b + 3u]);
+      prefix[t * (nbmax + 1u) + b + 1u] = static_cast<int32_t>(acc);
+    }
+    divisor[t] = q.n_blocks ? q.scales[(t0 + t) * q.bstride] : 0.0f;
+  }
+  __syncthreads();
+
+  const uint32_t team = threadIdx.x >> 3, u = threadIdx.x & 7u;
+  const uint32_t nchunk = 2u * nb;
+  for (uint32_t r = team; r < nrows; r += kThreads / 8u) {
+    const uint8_t* row = J.w + static_cast<size_t>(row0 + r) * J.stride;
+    uint32_t acc[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] = 0;
+    for (uint32_t c = u; c < nchunk; c += 8u) {
+      const u32x4 w = load16(row + 16u * c);
+      const uint32_t block = c >> 1, half = c & 1u;
+      uint32_t c6[4], c4[4], c2[4], c0[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        c6[k] = (w[k] >> 2) & 0x30303030u;  // code of shift 6, times 16
+        c4[k] = w[k] & 0x30303030u;         // shift 4, times 16
+        c2[k] = w[k] & 0x0C0C0C0Cu;         // shift 2, times 4
+        c0[k] = w[k] & 0x03030303u;         // shift 0
+      }
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const int8_t* a = act + t * abytes + 128u * block + 16u * half;
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
+        const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
+        const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+        int32_t P16 = 0, P4 = 0, P1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          P16 = dot4(c6[k], a0[k], P16);
+          P16 = dot4(c4[k], a1[k], P16);
+          P4 = dot4(c2[k], a2[k], P4);
+          P1 = dot4(c0[k], a3[k], P1);
+        }
+        acc[t] += static_cast<uint32_t>(P1 + (P4 >> 2) + (P16 >> 4));
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const uint32_t total = octet_sum(acc[t]);
+      if (u == 0) {
+        // ternary.rs:39,41: sum(code*q) - sum(q), wrapping
+        const int32_t dot = static_cast<int32_t>(total - static_cast<uint32_t>(prefix[t * (nbmax + 1u) + nb]));
+        const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
+        if (idx < J.out_len) {
+          if (raw) {
+            raw[idx] = dot;
+          } else {
+            // ternary.rs:53-57: (dot as f32) / s * scale; 0 without a scale
+            const float s = divisor[t];
+            J.out[idx] = q.n_blocks ? __fdiv_rn(static_cast<float>(dot), s) * J.scale : 0.0f;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Dense f32 ---------------------------------------------------------------
+// rusticide-simd/src/float.rs:23-36: eight fused lanes over the whole chunks,
+// the lanes added in order from -0.0, then the unfused tail (from -0.0).
+// A team of 8 lanes per row keeps exactly those eight accumulators.
+template <int T>
+__global__ __launch_bounds__(256) void gemv_dense_kernel(GemvJobs jobs, const float* __restrict__ x,
+                                                         size_t width, uint32_t R, size_t tokens,
+                                                         size_t t0) {
+  const GemvJob& J = jobs.j[find_job(jobs)];
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
+  const uint32_t nrows = min(R, J.rows - row0);
+  const uint32_t n = J.nb;  // elements both operands hold
+  const uint32_t team = threadIdx.x >> 3, i = threadIdx.x & 7u;
+  const uint32_t chunks = n / 8u;
+  for (uint32_t r = team; r < nrows; r += kThreads / 8u) {
+    const float* w = reinterpret_cast<const float*>(J.w + static_cast<size_t>(row0 + r) * J.stride);
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const float* xt = x + (t0 + t) * width;
+      float acc = 0.0f;
+      for (uint32_t c = 0; c < chunks; c++) acc = __builtin_fmaf(w[8u * c + i], xt[8u * c + i], acc);
+      float lanes[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) lanes[k] = __shfl(acc, (threadIdx.x & ~7u) + k, 64);
+      if (i == 0) {
+        float tail = -0.0f;
+        for (uint32_t k = 8u * chunks; k < n; k++) {
+          const float prod = w[k] * xt[k];
+          tail += prod;
+        }
+        float s = -0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; k++) s += lanes[k];
+        const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
+        if (idx < J.out_len) J.out[idx] = s + tail;
+      }
+    }
+  }
+}
+
+// Dequantize one row (Matrix::copy_row, model/src/weights.rs:120-150) -------
+__global__ __launch_bounds__(256) void dequantize_row_kernel(uint32_t type_id, const uint8_t* row,
+                                                             uint32_t nb, float scale, float* out,
+                                                             size_t out_len) {
+  const uint32_t bs = type_id == 36u ? 128u : 256u;
+  const size_t n = min(static_cast<size_t>(nb) * bs, out_len);
+  for (size_t e = static_cast<size_t>(blockIdx.x) * kThreads + threadIdx.x; e < n;
+       e += static_cast<size_t>(gridDim.x) * kThreads) {
+    const uint32_t b = static_cast<uint32_t>(e / bs), l = static_cast<uint32_t>(e % bs);
+    float v;
+    if (type_id == 12u) {  // quantize/src/q4_k.rs:32-66
+      const uint8_t* blk = row + static_cast<size_t>(b) * 144u;
+      const float d = f16_lo(load4(blk)), dmin = f16_hi(load4(blk));
+      const uint32_t j = l / 32u, li = l % 32u;
+      const uint8_t* s = blk + 4;
+      uint32_t sc, m;
+      if (j < 4u) {
+        sc = s[j] & 63u;
+        m = s[j + 4u] & 63u;
+      } else {
+        sc = (s[j + 4u] & 0x0Fu) | ((s[j - 4u] >> 6) << 4);
+        m = (s[j + 4u] >> 4) | ((s[j] >> 6) << 4);
+      }
+      const uint8_t qb = blk[16u + 32u * (j / 2u) + li];
+      const uint32_t qv = (j & 1u) ? (qb >> 4) : (qb & 0x0Fu);
+      const float ds = d * static_cast<float>(sc), dm = dmin * static_cast<float>(m);
+      const float prod = ds * static_cast<float>(qv);
+      v = prod - dm;
+    } else if (type_id == 14u) {  // quantize/src/q6_k.rs:13-43
+      const uint8_t* blk = row + static_cast<size_t>(b) * 210u;
+      const float d = f16_lo(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
+      const uint32_t hh = l / 128u, rr = (l % 128u) / 32u, li = l % 32u;
+      const uint8_t low = blk[64u * hh + 32u * (rr & 1u) + li];
+      const uint8_t high = blk[128u + 32u * hh + li];
+      const uint32_t nib = rr < 2u ? (low & 0x0Fu) : (low >> 4);
+      const int32_t qv = static_cast<int32_t>(nib | (((high >> (2u * rr)) & 3u) << 4)) - 32;
+      const float sc = static_cast<float>(static_cast<int8_t>(blk[192u + 8u * hh + 2u * rr + li / 16u]));
+      const float ds = d * sc;
+      v = ds * static_cast<float>(qv);
+    } else {  // quantize/src/i2_s.rs:15-21 then i2_s_apply_scale (:33-37)
+      const uint8_t byte = row[static_cast<size_t>(b) * 32u + l % 32u];
+      const uint32_t code = (byte >> (6u - 2u * (l / 32u))) & 3u;
+      const float c = static_cast<float>(code) - 1.0f;
+      v = c * scale;
+    }
+    out[e] = v;
+  }
+}
+
+template <int T>
+size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
+  if (type_id == 12u) return T * nbmax * 256u + T * nbmax * 4u + T * nbmax * 32u + R * nbmax * T * 4u;
+  if (type_id == 14u) return T * nbmax * 256u + T * nbmax * 4u + T * nbmax * 64u + R * nbmax * T * 4u;
+  if (type_id == 36u) return T * nbmax * 128u + T * (nbmax + 1u) * 4u + T * 4u;
+  return 0;
+}
+
+uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t total_rows) {
+  if (type_id == 36u || type_id == 0u) return 32u;  // one row per 8-lane team
+  // enough rows that each 4-lane team decodes about two blocks
+  uint32_t R = (2u * 64u + nb - 1u) / nb;
+  if (R < 1u) R = 1u;
+  (void)total_rows;
+  return R;
+}
+
+template <int T>
+hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float* x, size_t width,
+                    size_t tokens, size_t t0, hipStream_t s, int32_t* raw) {
+  uint32_t nbmax = 0, total_rows = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    nbmax = jobs.j[i].nb > nbmax ? jobs.j[i].nb : nbmax;
+    total_rows += jobs.j[i].rows;
+  }
+  // Rows whose blocks the input does not reach still get an output (-0.0 for
+  // the k-quants, as an empty f32 sum); size everything for at least one block.
+  const uint32_t nbl = nbmax ? nbmax : 1u;
+  const uint32_t R = rows_per_wg(type_id, nbl, total_rows);
+  uint32_t wgs = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    jobs.j[i].wg_begin = wgs;
+    wgs += (jobs.j[i].rows + R - 1u) / R;
+  }
+  if (wgs == 0) return hipSuccess;
+  if (type_id == 0u) {
+    hipLaunchKernelGGL(gemv_dense_kernel<T>, dim3(wgs), dim3(kThreads), 0, s, jobs, x, width, R,
+                       tokens, t0);
+    return hipGetLastError();
+  }
+  const size_t lds = lds_bytes<T>(type_id, nbl, R);
+  if (type_id == 12u)
+    hipLaunchKernelGGL(gemv_q4k_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+  else if (type_id == 14u)
+    hipLaunchKernelGGL(gemv_q6k_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+  else
+    hipLaunchKernelGGL(gemv_i2s_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0,
+                       raw);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+size_t gemv_max_tokens(uint32_t type_id, uint32_t nb) {
+  // LDS per workgroup stays within 64 KiB.
+  const uint32_t nbl = nb ? nb : 1u;
+  const uint32_t R = rows_per_wg(type_id, nbl, 0);
+  size_t t = kMaxTokens;
+  while (t > 1) {
+    size_t need = 0;
+    switch (t) {
+      case 8: need = lds_bytes<8>(type_id, nbl, R); break;
+      case 7: need = lds_bytes<7>(type_id, nbl, R); break;
+      case 6: need = lds_bytes<6>(type_id, nbl, R); break;
+      case 5: need = lds_bytes<5>(type_id, nbl, R); break;
+      case 4: need = lds_bytes<4>(type_id, nbl, R); break;
+      case 3: need = lds_bytes<3>(type_id, nbl, R); break;
+      default: need = lds_bytes<2>(type_id, nbl, R); break;
+    }
+    if (need <= 64u * 1024u) break;
+    t--;
+  }
+  return lds_bytes<1>(type_id, nbl, R) <= 64u * 1024u ? t : 0;
+}
+
+hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, const float* x,
+                       size_t width, size_t tokens, size_t t0, size_t tn, hipStream_t s,
+                       int32_t* raw) {
+  switch (tn) {
+    case 1: return launch_t<1>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 2: return launch_t<2>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 3: return launch_t<3>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 4: return launch_t<4>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 5: return launch_t<5>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 6: return launch_t<6>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 7: return launch_t<7>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 8: return launch_t<8>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
+                                 float* out, size_t out_len, hipStream_t s) {
+  const size_t n = static_cast<size_t>(nb) * (type_id == 36u ? 128u : 256u);
+  const size_t m = n < out_len ? n : out_len;
+  if (m == 0) return hipSuccess;
+  const uint32_t grid = static_cast<uint32_t>((m + kThreads - 1) / kThreads);
+  hipLaunchKernelGGL(dequantize_row_kernel, dim3(grid < 1024u ? grid : 1024u), dim3(kThreads), 0, s,
+                     type_id, row, nb, scale, out, out_len);
+  return hipGetLastError();
+}
+
+}  // namespace rh

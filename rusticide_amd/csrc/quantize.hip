@@ -1,0 +1,169 @@
+// quantize.hip -- the activation quantizers on the device.
+//
+// SuperBlock (ggml Q8_K) follows crates/rusticide-kernels/src/portable/q8.rs:64-98;
+// Row (bitnet.cpp's legacy I8_S) follows portable/q8.rs:38-49 and :99-105.
+// Both produce exactly the quants, scales and sums the CPU path produces.
+#include "rh_device.h"
+#include "rh_internal.h"
+
+namespace rh {
+
+// One wave per 256-element super-block, four values per lane.
+__global__ __launch_bounds__(256) void quantize_super_kernel(const float* __restrict__ x,
+                                                             size_t width, uint32_t n_super,
+                                                             Q8Dev q) {
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t sb = blockIdx.x * 4u + (threadIdx.x >> 6);
+  const size_t t = blockIdx.y;
+  if (sb >= n_super) return;  // wave-uniform
+  const float* v = x + t * width + static_cast<size_t>(sb) * 256u;
+  float f[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) f[i] = v[lane * 4u + i];
+
+  // amax: f32::max folded from 0.0 (q8.rs:12-14,19-25). Comparisons keep a
+  // NaN from ever entering the running maximum, as maxNum does.
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float m = __builtin_fabsf(f[i]);
+    amax = m > amax ? m : amax;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    float o = __shfl_xor(amax, off, 64);
+    amax = o > amax ? o : amax;
+  }
+  // The first element, in order, whose magnitude is amax (q8.rs:26-32).
+  uint32_t idx = 256u;
+#pragma unroll
+  for (int i = 3; i >= 0; i--)
+    if (__builtin_fabsf(f[i]) == amax) idx = lane * 4u + i;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(idx), off, 64));
+    idx = o < idx ? o : idx;
+  }
+  const float max = idx < 256u ? v[idx] : 0.0f;
+  const float inverse = (max == 0.0f) ? 0.0f : __fdiv_rn(-127.0f, max);
+  const float step = (max == 0.0f) ? 0.0f : __fdiv_rn(1.0f, inverse);
+
+  int32_t qv[4];
+  int32_t s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    float prod = f[i] * inverse;
+    qv[i] = round_to_i8(prod);
+    s += qv[i];
+  }
+  uint32_t packed = (static_cast<uint32_t>(qv[0]) & 0xffu) | ((static_cast<uint32_t>(qv[1]) & 0xffu) << 8) |
+                    ((static_cast<uint32_t>(qv[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qv[3]) << 24);
+  *reinterpret_cast<uint32_t*>(q.quants + t * q.qstride + static_cast<size_t>(sb) * 256u + lane * 4u) = packed;
+  // sums per 16 (4 lanes) and per 32 (8 lanes)
+  int32_t s16 = s + __shfl_xor(s, 1, 64);
+  s16 += __shfl_xor(s16, 2, 64);
+  int32_t s32 = s16 + __shfl_xor(s16, 4, 64);
+  const size_t b0 = t * q.bstride + static_cast<size_t>(sb) * 8u;
+  if ((lane & 3u) == 0) q.sums16[2 * t * q.bstride + static_cast<size_t>(sb) * 16u + lane / 4u] = s16;
+  if ((lane & 7u) == 0) q.sums[b0 + lane / 8u] = s32;
+  if (lane < 8u) q.scales[b0 + lane] = step;
+}
+
+// One workgroup per token: the row divisor in f64 with C's MAX semantics,
+// then the quants. A NaN element restarts the running maximum at the next
+// element (q8.rs:42-45), so the divisor depends on the elements after the
+// last NaN only; a trailing NaN makes it NaN.
+__global__ __launch_bounds__(256) void quantize_row_kernel(const float* __restrict__ x, size_t width,
+                                                           uint32_t n_blocks, Q8Dev q) {
+  __shared__ int s_last_nan;
+  __shared__ float s_max[4];
+  __shared__ int s_nan_wave[4];
+  const size_t t = blockIdx.x;
+  const float* v = x + t * width;
+  const uint32_t n = n_blocks * 32u;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+
+  int last_nan = -1;
+  for (uint32_t i = tid; i < n; i += 256u)
+    if (v[i] != v[i]) last_nan = static_cast<int>(i);
+  for (int off = 32; off > 0; off >>= 1) {
+    int o = __shfl_xor(last_nan, off, 64);
+    last_nan = o > last_nan ? o : last_nan;
+  }
+  if (lane == 0) s_nan_wave[wave] = last_nan;
+  __syncthreads();
+  if (tid == 0) {
+    int m = s_nan_wave[0];
+    for (int w = 1; w < 4; w++) m = s_nan_wave[w] > m ? s_nan_wave[w] : m;
+    s_last_nan = m;
+  }
+  __syncthreads();
+  const int p = s_last_nan;
+  float mag_max = 0.0f;
+  for (uint32_t i = tid; i < n; i += 256u) {
+    if (static_cast<int>(i) > p) {
+      float m = __builtin_fabsf(v[i]);
+      mag_max = m > mag_max ? m : mag_max;
+    }
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    float o = __shfl_xor(mag_max, off, 64);
+    mag_max = o > mag_max ? o : mag_max;
+  }
+  if (lane == 0) s_max[wave] = mag_max;
+  __syncthreads();
+  float mm = s_max[0];
+  for (int w = 1; w < 4; w++) mm = s_max[w] > mm ? s_max[w] : mm;
+  double mx;
+  if (p < 0) {
+    mx = static_cast<double>(mm);
+    mx = 1e-5 > mx ? 1e-5 : mx;
+  } else if (p == static_cast<int>(n) - 1) {
+    mx = __builtin_nan("");
+  } else {
+    mx = static_cast<double>(mm);
+  }
+  const float divisor = static_cast<float>(127.0 / mx);
+
+  // quants and per-32 sums: one 32-block per 8 lanes, 4 values per lane
+  for (uint32_t base = tid * 4u; base < n; base += 1024u) {
+    int32_t qv[4];
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float prod = v[base + i] * divisor;
+      qv[i] = round_row_to_i8(prod);
+      s += qv[i];
+    }
+    uint32_t packed = (static_cast<uint32_t>(qv[0]) & 0xffu) | ((static_cast<uint32_t>(qv[1]) & 0xffu) << 8) |
+                      ((static_cast<uint32_t>(qv[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qv[3]) << 24);
+    *reinterpret_cast<uint32_t*>(q.quants + t * q.qstride + base) = packed;
+    int32_t s32 = s + __shfl_xor(s, 1, 64);
+    s32 += __shfl_xor(s32, 2, 64);
+    s32 += __shfl_xor(s32, 4, 64);
+    if ((lane & 7u) == 0) {
+      q.sums[t * q.bstride + base / 32u] = s32;
+      q.scales[t * q.bstride + base / 32u] = divisor;
+    }
+  }
+}
+
+hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, const Q8Dev& q,
+                                 hipStream_t s) {
+  const uint32_t n_super = static_cast<uint32_t>(width / 256u);
+  if (n_super == 0 || tokens == 0) return hipSuccess;
+  dim3 grid((n_super + 3u) / 4u, static_cast<uint32_t>(tokens));
+  hipLaunchKernelGGL(quantize_super_kernel, grid, dim3(256), 0, s, x, width, n_super, q);
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, const Q8Dev& q,
+                               hipStream_t s) {
+  const uint32_t n_blocks = static_cast<uint32_t>(width / 32u);
+  if (n_blocks == 0 || tokens == 0) return hipSuccess;
+  hipLaunchKernelGGL(quantize_row_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, s, x,
+                     width, n_blocks, q);
+  return hipGetLastError();
+}
+
+}  // namespace rh

@@ -1,0 +1,98 @@
+// rh_device.h -- device helpers shared by the gfx950 kernels.
+//
+// Every kernel here is built with -ffp-contract=off: a float expression is
+// evaluated one IEEE operation at a time, and fused multiply-adds appear only
+// where the source calls fmaf(), matching the places rusticide's CPU path calls
+// mul_add. Division uses __fdiv_rn (correctly rounded), never a reciprocal.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rh {
+
+// 16 bytes loaded with a 4-byte alignment guarantee only: LLVM lowers this to
+// one global_load_dwordx4, which needs dword alignment.
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ u32x4 load16(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ u32x4 load16_a4(const uint8_t* p) {
+  u32x4_a4 v = *reinterpret_cast<const u32x4_a4*>(p);
+  return u32x4{v.x, v.y, v.z, v.w};
+}
+
+__device__ __forceinline__ uint32_t load4(const uint8_t* p) {
+  return *reinterpret_cast<const uint32_t*>(p);
+}
+
+// The 16 bytes at p, where p is only 2-byte aligned: five aligned dwords
+// funnel-shifted by (p & 3) bytes. Reads up to 4 bytes past p + 16.
+__device__ __forceinline__ u32x4 load16_unaligned(const uint8_t* p) {
+  const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint8_t* base = p - sh;
+  u32x4 v = load16_a4(base);
+  uint32_t e = load4(base + 16);
+  return u32x4{__builtin_amdgcn_alignbyte(v.y, v.x, sh), __builtin_amdgcn_alignbyte(v.z, v.y, sh),
+               __builtin_amdgcn_alignbyte(v.w, v.z, sh), __builtin_amdgcn_alignbyte(e, v.w, sh)};
+}
+
+// Exact IEEE half -> float widening (v_cvt_f32_f16).
+__device__ __forceinline__ float f16_lo(uint32_t w) {
+  _Float16 h;
+  uint16_t b = static_cast<uint16_t>(w & 0xffffu);
+  __builtin_memcpy(&h, &b, 2);
+  return static_cast<float>(h);
+}
+__device__ __forceinline__ float f16_hi(uint32_t w) { return f16_lo(w >> 16); }
+
+// Four signed byte products accumulated into c (v_dot4_i32_i8, no clamp).
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t c) {
+  return __builtin_amdgcn_sdot4(static_cast<int32_t>(a), static_cast<int32_t>(b), c, false);
+}
+
+__device__ __forceinline__ uint32_t bfe(uint32_t v, uint32_t off, uint32_t width) {
+  return __builtin_amdgcn_ubfe(v, off, width);
+}
+
+// Sum over the 4 lanes of a quad (DPP quad_perm); exact for integers.
+__device__ __forceinline__ int32_t quad_sum(int32_t v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+  return v;
+}
+
+// Sum over aligned groups of 8 lanes; exact (wrapping) for integers.
+__device__ __forceinline__ uint32_t octet_sum(uint32_t v) {
+  v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 1, 64));
+  v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 2, 64));
+  v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 4, 64));
+  return v;
+}
+
+// Q8Kind::SuperBlock round_to_i8 (portable/q8.rs:114-116): ties to even,
+// clamp to +-127, NaN to 0.
+__device__ __forceinline__ int32_t round_to_i8(float v) {
+  float r = __builtin_rintf(v);
+  if (r != r) return 0;
+  r = r < -127.0f ? -127.0f : r;
+  r = r > 127.0f ? 127.0f : r;
+  return static_cast<int32_t>(r);
+}
+
+// Q8Kind::Row round_row_to_i8 (portable/q8.rs:128-130): ties to even, then a
+// saturating cast to [-128, 127] with NaN to 0.
+__device__ __forceinline__ int32_t round_row_to_i8(float v) {
+  float r = __builtin_rintf(v);
+  if (r != r) return 0;
+  if (r <= -128.0f) return -128;
+  if (r >= 127.0f) return 127;
+  return static_cast<int32_t>(r);
+}
+
+}  // namespace rh

@@ -1,0 +1,61 @@
+// rh_internal.h -- types shared by the C ABI (api.hip) and the kernel
+// launchers (quantize.hip, gemv.hip, gemm.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rh {
+
+constexpr int kMaxJobs = 8;       // matrices one GEMV launch can serve
+constexpr int kMaxTokens = 8;     // tokens one GEMV launch can serve
+constexpr size_t kPad = 256;      // bytes of slack after every device matrix
+
+// The quantized activations of one batch on the device, laid out per token:
+// quants [tokens][qstride] i8, scales/sums [tokens][bstride] per 32-block,
+// sums16 [tokens][2*bstride] per 16-block (Q6_K's -32 offset), and for the
+// Row kind the one divisor per token.
+struct Q8Dev {
+  int8_t* quants = nullptr;
+  float* scales = nullptr;
+  int32_t* sums = nullptr;
+  int32_t* sums16 = nullptr;
+  size_t qstride = 0;   // bytes of quants per token
+  size_t bstride = 0;   // 32-blocks reserved per token
+  size_t n_blocks = 0;  // 32-blocks actually quantized per token
+};
+
+// One matrix of a grouped launch.
+struct GemvJob {
+  const uint8_t* w;     // row-major native blocks (or f32 rows)
+  size_t stride;        // bytes between rows
+  uint32_t rows;        // rows to compute (already bounded by out_len)
+  uint32_t nb;          // blocks per row both operands cover
+  float* out;           // out[row * tokens + token]
+  size_t out_len;
+  float scale;          // I2_S tensor scale
+  uint32_t wg_begin;    // first workgroup of this job in the grid
+};
+
+struct GemvJobs {
+  GemvJob j[kMaxJobs];
+  uint32_t n;
+};
+
+// Launchers (stream-ordered; they return the launch status).
+hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, const Q8Dev& q,
+                                 hipStream_t s);
+hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, const Q8Dev& q,
+                               hipStream_t s);
+
+// Grouped GEMV for one format: tokens [t0, t0+tn) of `tokens` total.
+hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, const float* x,
+                       size_t width, size_t tokens, size_t t0, size_t tn, hipStream_t s,
+                       int32_t* raw_i32);
+size_t gemv_max_tokens(uint32_t type_id, uint32_t nb);
+
+hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
+                                 float* out, size_t out_len, hipStream_t s);
+
+}  // namespace rh

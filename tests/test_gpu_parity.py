@@ -1,0 +1,302 @@
+"""GPU parity: the HIP path against the CPU oracle, through the C ABI.
+
+The bar: I2_S int32 accumulators bit-exact; k-quant f32
+outputs bit-identical to the CPU integer path (which is stricter than the
+stated 1e-4 relative tolerance); every token of a batch identical to a
+single-token call. Shapes include the benchmark workloads at full size.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rusticide_amd as R
+from rusticide_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = R.Context(0)
+    yield c
+    c.close()
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def assert_same_bits(got, want, what=""):
+    got, want = np.asarray(got, np.float32), np.asarray(want, np.float32)
+    assert got.shape == want.shape, what
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan), what
+    bad = np.flatnonzero(bits(got)[~nan] != bits(want)[~nan])
+    assert bad.size == 0, f"{what}: {bad.size} mismatches, first {bad[:5]}: {got[~nan][bad[:5]]} vs {want[~nan][bad[:5]]}"
+
+
+def oracle_matmul(type_id, data, rows, cols, x, tokens, scale=0.0, threads=8):
+    rb = synth.row_bytes(type_id, cols) if type_id != 0 else cols
+    if type_id == 36:
+        w = O.Weights.ternary(data[: rows * rb], rb, scale)
+    elif type_id == 0:
+        w = O.Weights.dense(data, cols)
+    else:
+        w = O.Weights.blocks(type_id, data, rb)
+    out = np.full(rows * tokens, np.nan, np.float32)
+    O.matmul_batch(x, tokens, [(w, out)], threads=threads)
+    return out
+
+
+# ------------------------------------------------------------- quantizers
+
+
+def quant_cases():
+    rng = np.random.default_rng(7)
+    cases = [rng.standard_normal(2048).astype(np.float32),
+             (rng.standard_normal(5632) * 30).astype(np.float32),
+             np.zeros(512, np.float32),
+             O.pseudo_random_values(768, 3)]
+    ties = np.zeros(256, np.float32)
+    ties[:6] = [127.0, 2.5, 3.5, -2.5, -3.5, 0.5]
+    cases.append(ties)
+    nan = rng.standard_normal(512).astype(np.float32)
+    nan[[3, 300]] = np.nan
+    cases.append(nan)
+    inf = rng.standard_normal(256).astype(np.float32)
+    inf[17] = -np.inf
+    cases.append(inf)
+    tail_nan = rng.standard_normal(64).astype(np.float32)
+    tail_nan[-1] = np.nan
+    cases.append(tail_nan)
+    sub = (rng.standard_normal(256) * 1e-40).astype(np.float32)
+    cases.append(sub)
+    cases.append(rng.standard_normal(300).astype(np.float32))  # partial blocks
+    return cases
+
+
+@pytest.mark.parametrize("kind", [R.SUPER_BLOCK, R.ROW])
+def test_device_quantizers_match_the_oracle(ctx, kind):
+    for i, x in enumerate(quant_cases()):
+        q, s, m = ctx.quantize(x, kind)
+        want = O.quantize(x, kind)
+        assert np.array_equal(q, want.quants), (kind, i)
+        assert_same_bits(s, want.scales, f"scales kind={kind} case={i}")
+        assert np.array_equal(m, want.sums), (kind, i)
+
+
+# ---------------------------------------------------------- k-quant GEMV
+
+
+KQ_SHAPES = [
+    (12, 5632, 2048, [1]),      # Q4_K ffn_gate shape (benchmark workload)
+    (12, 2048, 5632, [1, 2]),   # Q4_K ffn_down shape (22 blocks per row)
+    (12, 37, 512, [1, 3, 8, 11]),
+    (14, 32000, 2048, [1]),     # Q6_K lm_head (benchmark workload)
+    (14, 2048, 5632, [1, 3]),   # Q6_K ffn_down: 4620-byte rows, padded stride
+    (14, 45, 768, [1, 2, 9]),
+]
+
+
+@pytest.mark.parametrize("type_id,rows,cols,token_counts", KQ_SHAPES)
+def test_kquant_gemv_is_bit_identical_to_the_cpu_path(ctx, type_id, rows, cols, token_counts):
+    data = synth.matrix(type_id, rows, cols, seed=rows + cols)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    for tokens in token_counts:
+        x = synth.normal_f32(tokens * cols, seed=tokens)
+        want = oracle_matmul(type_id, data, rows, cols, x, tokens)
+        out = np.full(rows * tokens, np.nan, np.float32)
+        R.matmul_batch(ctx, x, tokens, [(m, out)])
+        assert_same_bits(out, want, f"type={type_id} {rows}x{cols} tokens={tokens}")
+
+
+@pytest.mark.parametrize("type_id", [12, 14])
+def test_reference_synthetic_blocks(ctx, type_id):
+    # the reference's own generator (format.rs:204-214) and activations
+    rows, cols = 24, 1024
+    data = O.synthetic_blocks(type_id, rows * cols // 256, 1)
+    x = O.bench_activations(cols, 2)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    out = np.zeros(rows, np.float32)
+    m.matvec(x, out)
+    assert_same_bits(out, oracle_matmul(type_id, data, rows, cols, x, 1))
+
+
+@pytest.mark.parametrize("type_id", [12, 14])
+def test_kquant_dot_within_1e4_of_dequantize_and_dot(ctx, type_id):
+    # quant_kernel_tests.rs:60-79: against the dequantized operands
+    rows, cols = 16, 2048
+    data = synth.matrix(type_id, rows, cols, seed=3)
+    x = synth.normal_f32(cols, seed=4)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    out = np.zeros(rows, np.float32)
+    m.matvec(x, out)
+    xq = O.quantize(x, O.SUPER_BLOCK).dequantize()
+    rb = synth.row_bytes(type_id, cols)
+    for r in range(rows):
+        row = data[r * rb:(r + 1) * rb]
+        w = O.dequantize_row(type_id, row)
+        ref = float(np.dot(w.astype(np.float64), xq.astype(np.float64)))
+        assert abs(out[r] - ref) <= 1e-4 * max(1.0, float(np.abs(w).sum()))
+
+
+# --------------------------------------------------------------- I2_S GEMV
+
+
+I2S_SHAPES = [(6912, 2560, [1]), (2560, 6912, [1, 2]), (33, 384, [1, 4, 9])]
+
+
+@pytest.mark.parametrize("rows,cols,token_counts", I2S_SHAPES)
+def test_i2s_i32_accumulators_are_bit_exact(ctx, rows, cols, token_counts):
+    data = synth.i2s_matrix(rows, cols, seed=rows)
+    m = R.Matrix.load(ctx, 36, data, rows, cols)
+    assert m.ternary_scale == np.float32(0.02)
+    rb = cols // 4
+    for tokens in token_counts:
+        x = synth.normal_f32(tokens * cols, seed=10 + tokens)
+        raw = ctx.ternary_dot_i32(m, x, tokens)
+        want = O.ternary_dot_matrix_i32(data[: rows * rb], rb, x, tokens)
+        assert np.array_equal(raw, want), f"{rows}x{cols} tokens={tokens}"
+        out = np.full(rows * tokens, np.nan, np.float32)
+        R.matmul_batch(ctx, x, tokens, [(m, out)])
+        assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, tokens, scale=0.02))
+
+
+def test_i2s_code_three_and_hostile_bytes(ctx):
+    # i2_s.rs:96-104: code 3 decodes to +2; random bytes use every code
+    rows, cols = 16, 512
+    body = O.pseudo_random_bytes(rows * cols // 4, 9)
+    data = np.concatenate([body, np.array([0.75], np.float32).view(np.uint8), np.zeros(28, np.uint8)])
+    m = R.Matrix.load(ctx, 36, data, rows, cols)
+    x = O.pseudo_random_values(cols, 5)
+    raw = ctx.ternary_dot_i32(m, x, 1)
+    assert np.array_equal(raw, O.ternary_dot_matrix_i32(body, cols // 4, x, 1))
+
+
+# ------------------------------------------------------------ batch rules
+
+
+def test_one_batch_mixes_formats_and_matches_per_token_calls(ctx):
+    # attention.rs:215-223 (Q/K/V in one batch) + matmul_tests.rs:237-271
+    cols, tokens = 2048, 5
+    specs = [(12, 2048), (12, 256), (14, 256), (36, 300), (14, 40)]
+    mats, datas = [], []
+    for i, (t, rows) in enumerate(specs):
+        d = synth.matrix(t, rows, cols, seed=100 + i)
+        datas.append(d)
+        mats.append(R.Matrix.load(ctx, t, d, rows, cols))
+    x = synth.normal_f32(tokens * cols, seed=77)
+    outs = [np.full(rows * tokens, np.nan, np.float32) for _, rows in specs]
+    R.matmul_batch(ctx, x, tokens, list(zip(mats, outs)))
+    for (t, rows), d, m, out in zip(specs, datas, mats, outs):
+        assert_same_bits(out, oracle_matmul(t, d, rows, cols, x, tokens, scale=0.02), f"type {t}")
+        for tok in range(tokens):
+            single = np.zeros(rows, np.float32)
+            R.matvec_batch(ctx, x[tok * cols:(tok + 1) * cols], [(m, single)])
+            assert_same_bits(out[tok::tokens], single, f"type {t} token {tok}")
+
+
+def test_no_ops_and_output_bounds(ctx):
+    # matmul_tests.rs:188-235; quant_kernel.rs:416-419
+    rows, cols = 20, 512
+    data = synth.matrix(12, rows, cols, seed=5)
+    m = R.Matrix.load(ctx, 12, data, rows, cols)
+    out = np.full(rows, 7.0, np.float32)
+    R.matmul_batch(ctx, np.ones(cols, np.float32), 0, [(m, out)])
+    R.matmul_batch(ctx, np.ones(cols, np.float32), cols + 1, [(m, out)])
+    assert np.all(out == 7.0)
+    x = synth.normal_f32(2 * cols, seed=6)
+    full = np.zeros(rows * 2, np.float32)
+    R.matmul_batch(ctx, x, 2, [(m, full)])
+    short = np.full(13, 5.0, np.float32)  # 6.5 rows of 2 tokens
+    R.matmul_batch(ctx, x, 2, [(m, short)])
+    assert_same_bits(short, full[:13])
+    long = np.full(rows * 2 + 3, 5.0, np.float32)
+    R.matmul_batch(ctx, x, 2, [(m, long)])
+    assert_same_bits(long[:-3], full)
+    assert np.all(long[-3:] == 5.0)
+
+
+def test_an_input_narrower_than_the_rows_bounds_the_dot(ctx):
+    # int_dot.rs:36-47 and ternary.rs:21-26: the shorter operand bounds the work
+    rows, cols = 12, 1024
+    for t in (12, 14, 36):
+        data = synth.matrix(t, rows, cols, seed=8)
+        m = R.Matrix.load(ctx, t, data, rows, cols)
+        for width in (512, 300, 100, 0 if t != 36 else 40):
+            if width == 0:
+                continue
+            x = synth.normal_f32(width, seed=9)
+            out = np.full(rows, np.nan, np.float32)
+            R.matvec_batch(ctx, x, [(m, out)])
+            assert_same_bits(out, oracle_matmul(t, data, rows, cols, x, 1, scale=0.02), f"type {t} width {width}")
+
+
+def test_dense_f32_rows_follow_the_eight_lane_dot(ctx):
+    # rusticide-simd/src/float.rs:23-36
+    rng = np.random.default_rng(1)
+    for rows, cols in ((7, 37), (65, 2048), (3, 5)):
+        w = rng.standard_normal(rows * cols).astype(np.float32)
+        m = R.Matrix.load(ctx, R.F32, w, rows, cols)
+        x = rng.standard_normal(cols * 2).astype(np.float32)
+        out = np.zeros(rows * 2, np.float32)
+        R.matmul_batch(ctx, x, 2, [(m, out)])
+        assert_same_bits(out, oracle_matmul(0, w, rows, cols, x, 2))
+
+
+def test_hostile_block_bytes_match_the_oracle(ctx):
+    # the fuzz idea (rusticide-fuzz dequantize target): any bytes, incl. f16
+    # inf/NaN scales, must compute what the CPU path computes
+    rows, cols = 40, 512
+    for t in (12, 14):
+        data = O.pseudo_random_bytes(rows * synth.row_bytes(t, cols), 21 + t)
+        m = R.Matrix.load(ctx, t, data, rows, cols)
+        x = synth.normal_f32(cols * 2, seed=3)
+        out = np.zeros(rows * 2, np.float32)
+        R.matmul_batch(ctx, x, 2, [(m, out)])
+        assert_same_bits(out, oracle_matmul(t, data, rows, cols, x, 2), f"type {t}")
+
+
+# ------------------------------------------------------------ load errors
+
+
+def test_load_errors_mirror_model_error(ctx):
+    # model/src/weights.rs:41-47,190-211
+    with pytest.raises(R.RusticideError) as e:
+        R.Matrix.load(ctx, 12, np.zeros(144, np.uint8), 1, 0)
+    assert e.value.kind == "INVALID_CONFIG"
+    for scale in (np.nan, np.inf, -np.inf):
+        data = np.concatenate([np.zeros(32, np.uint8), np.array([scale], np.float32).view(np.uint8)])
+        with pytest.raises(R.RusticideError) as e:
+            R.Matrix.load(ctx, 36, data, 1, 128)
+        assert e.value.kind == "INVALID_TENSOR" and "not finite" in str(e.value)
+    with pytest.raises(R.RusticideError) as e:
+        R.Matrix.load(ctx, 36, np.zeros(34, np.uint8), 1, 128)
+    assert e.value.kind == "INVALID_TENSOR" and "too short" in str(e.value)
+    with pytest.raises(R.RusticideError) as e:
+        R.Matrix.load(ctx, 12, np.zeros(143, np.uint8), 1, 256)
+    assert e.value.kind == "SHAPE_MISMATCH"
+    with pytest.raises(R.RusticideError) as e:
+        R.Matrix.load(ctx, 2, np.zeros(18, np.uint8), 1, 32)
+    assert e.value.kind == "MISSING_KERNEL"
+
+
+# --------------------------------------------------------------- copy_row
+
+
+@pytest.mark.parametrize("type_id", [12, 14, 36])
+def test_copy_row_dequantizes_like_the_cpu_path(ctx, type_id):
+    # model/src/weights.rs:120-150
+    rows, cols = 9, 768 if type_id != 36 else 384
+    data = synth.matrix(type_id, rows, cols, seed=4)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    rb = synth.row_bytes(type_id, cols)
+    for r in (0, rows - 1):
+        out = np.full(cols, np.nan, np.float32)
+        assert m.copy_row(r, out)
+        want = O.dequantize_row(type_id, data[r * rb:(r + 1) * rb])
+        if type_id == 36:
+            want = (want * np.float32(0.02)).astype(np.float32)
+        assert_same_bits(out, want)
+    assert not m.copy_row(rows, np.zeros(cols, np.float32))
