@@ -57,8 +57,8 @@ def algorithmic_bytes(type_id: int, rows: int, cols: int) -> int:
 
 
 def measure_gpu(ctx, name: str, steps: int, warmup: int):
-    import torch
     import rusticide_amd as R
+    from rusticide_amd import hip as H
     from rusticide_amd import synth
 
     type_id, rows, cols, desc = WORKLOADS[name]
@@ -66,9 +66,9 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
     one = R.Matrix.load(ctx, type_id, data, rows, cols)
     ncopies = max(2, math.ceil(ROTATE_BYTES / one.device_bytes))
     mats = [one] + [R.Matrix.load(ctx, type_id, data, rows, cols) for _ in range(ncopies - 1)]
-    x = torch.from_numpy(synth.normal_f32(cols, seed=2)).cuda()
-    out = torch.empty(rows, dtype=torch.float32, device="cuda")
-    stream = torch.cuda.ExternalStream(ctx.stream)
+    x = H.DeviceArray.from_numpy(synth.normal_f32(cols, seed=2))
+    out = H.DeviceArray(rows)
+    stream = ctx.stream
     kind = R.ROW if type_id == 36 else R.SUPER_BLOCK
     B = algorithmic_bytes(type_id, rows, cols)
 
@@ -78,31 +78,31 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
     # whole step: quantize + GEMV, back to back on the context's stream
     for i in range(warmup):
         step(i)
-    torch.cuda.synchronize()
+    H.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
         step(i)
-    torch.cuda.synchronize()
+    H.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
 
     # the GEMV kernel alone, per launch, with events on its stream
     q8 = R.Q8(ctx).quantize(x, 1, kind)
 
     def kernel_avg_us(copies: int) -> float:
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        starts = [H.Event() for _ in range(steps)]
+        ends = [H.Event() for _ in range(steps)]
         for i in range(warmup):
             R.dot_matrix_device(mats[i % copies], q8, out)
         for i in range(steps):
             starts[i].record(stream)
             R.dot_matrix_device(mats[i % copies], q8, out)
             ends[i].record(stream)
-        torch.cuda.synchronize()
-        return 1e3 * float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
+        H.synchronize()
+        return 1e3 * float(np.mean([s.elapsed_ms(e) for s, e in zip(starts, ends)]))
 
     cold_us = kernel_avg_us(ncopies)
     warm_us = kernel_avg_us(1)
-    gpu_out = out.cpu().numpy()
+    gpu_out = out.numpy()
     for m in mats:
         m.free()
     q8.free()
@@ -112,7 +112,7 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
         "step_gbs": B / (ms_per_step * 1e-3) / 1e9,
         "kernel_us": cold_us, "kernel_gbs": B / (cold_us * 1e-6) / 1e9,
         "warm_kernel_us": warm_us, "warm_kernel_gbs": B / (warm_us * 1e-6) / 1e9,
-        "data": data, "x": x.cpu().numpy(), "gpu_out": gpu_out,
+        "data": data, "x": x.numpy(), "gpu_out": gpu_out,
     }
 
 
