@@ -7,6 +7,7 @@
 // activation kind once per batch on the device, then one grouped GEMV launch
 // per weight format covering every matrix of that format.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
@@ -72,6 +73,17 @@ rh_status hip_fail(rh_ctx* ctx, hipError_t e, const char* what) {
   } while (0)
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
+
+// Decode (one or two tokens) runs the k-quants on the LDS-staged kernels and
+// I2_S on the streaming one, the faster of each pair on MI355X.
+// RUSTICIDE_HIP_GEMV=lds|stream forces one family for every format (both give
+// the same bits; the switch exists to test and time one against the other).
+bool use_stream(uint32_t type_id) {
+  const char* v = std::getenv("RUSTICIDE_HIP_GEMV");
+  if (v && std::strcmp(v, "lds") == 0) return false;
+  if (v && std::strcmp(v, "stream") == 0) return true;
+  return type_id == RH_TYPE_I2_S;
+}
 
 // Grows scratch slot `i` to at least `bytes`.
 rh_status ensure(rh_ctx* ctx, int i, size_t bytes) {
@@ -151,6 +163,15 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (kind != RH_TYPE_F32) tmax = gemv_max_tokens(kind, nbmax);
       if (tmax == 0) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "rows too wide for the GEMV kernels");
       const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
+      if (kind != RH_TYPE_F32 && tokens <= 2 && use_stream(kind)) {
+        hipError_t e = hipSuccess;
+        if (launch_gemv_stream(kind, g, q, tokens, 0, tokens, s, raw, &e)) {
+          RH_HIP(ctx, e);
+          g = GemvJobs{};
+          nbmax = 0;
+          return RH_OK;
+        }
+      }
       for (size_t t0 = 0; t0 < tokens; t0 += tmax) {
         size_t tn = tokens - t0 < tmax ? tokens - t0 : tmax;
         RH_HIP(ctx, launch_gemv(kind, g, q, d_in, width, tokens, t0, tn, s, raw));

@@ -42,6 +42,12 @@ __device__ __forceinline__ void stage_quants(int8_t* act, uint32_t bytes, const 
   }
 }
 
+// Each 4-lane team decodes up to NI blocks. Their weight loads are issued
+// first, before the activation is staged and before the barrier, so every
+// resident workgroup has all of its rows in flight from its first cycles and
+// the decode of one workgroup overlaps the loads of the others.
+constexpr int NI = 2;
+
 // Q4_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
 //      terms [R][nbmax][T] f32
@@ -59,6 +65,20 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
   const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
   const uint32_t nrows = min(R, J.rows - row0);
   const uint32_t nb = J.nb;
+  const uint32_t total = nrows * nb;
+  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
+
+  u32x4 hd[NI], c0[NI], c1[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const uint32_t g = team + i * (kThreads / 4u);
+    const uint32_t gg = g < total ? g : 0u;  // a spare team re-reads block 0
+    const uint32_t r = nb ? gg / nb : 0u, b = gg - r * nb;
+    const uint8_t* blk = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 144u;
+    hd[i] = load16(blk);
+    c0[i] = load16(blk + 16u + 16u * p);
+    c1[i] = load16(blk + 80u + 16u * p);
+  }
 
   stage_quants<T>(act, abytes, q, t0);
   for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += kThreads) {
@@ -69,33 +89,32 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
   }
   __syncthreads();
 
-  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
   const uint32_t j0 = 2u * (p >> 1), e0 = 16u * (p & 1u);
   const bool min_lane = (p & 1u) == 0;
-  for (uint32_t g = team; g < nrows * nb; g += kThreads / 4u) {
+#pragma unroll
+  for (int it = 0; it < NI; it++) {
+    const uint32_t g = team + it * (kThreads / 4u);
+    if (g >= total) break;  // uniform over the team
     const uint32_t r = g / nb, b = g - r * nb;
-    const uint8_t* blk = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 144u;
-    const u32x4 hd = load16(blk);
-    const u32x4 c0 = load16(blk + 16u + 16u * p);
-    const u32x4 c1 = load16(blk + 80u + 16u * p);
+    const u32x4 h = hd[it];
     // 6-bit scales/mins of sub-blocks j0, j0+1, j0+4, j0+5 (ggml get_scale_min_k4,
     // quantize/src/q4_k.rs:17-25)
-    const int32_t sc0 = static_cast<int32_t>(bfe(hd.y, 8u * j0, 6));
-    const int32_t sc1 = static_cast<int32_t>(bfe(hd.y, 8u * j0 + 8u, 6));
-    const int32_t sc2 = static_cast<int32_t>(bfe(hd.w, 8u * j0, 4) | (bfe(hd.y, 8u * j0 + 6u, 2) << 4));
-    const int32_t sc3 = static_cast<int32_t>(bfe(hd.w, 8u * j0 + 8u, 4) | (bfe(hd.y, 8u * j0 + 14u, 2) << 4));
-    const int32_t m0 = static_cast<int32_t>(bfe(hd.z, 8u * j0, 6));
-    const int32_t m1 = static_cast<int32_t>(bfe(hd.z, 8u * j0 + 8u, 6));
-    const int32_t m2 = static_cast<int32_t>(bfe(hd.w, 8u * j0 + 4u, 4) | (bfe(hd.z, 8u * j0 + 6u, 2) << 4));
-    const int32_t m3 = static_cast<int32_t>(bfe(hd.w, 8u * j0 + 12u, 4) | (bfe(hd.z, 8u * j0 + 14u, 2) << 4));
-    const float d = f16_lo(hd.x), dmin = f16_hi(hd.x);
+    const int32_t sc0 = static_cast<int32_t>(bfe(h.y, 8u * j0, 6));
+    const int32_t sc1 = static_cast<int32_t>(bfe(h.y, 8u * j0 + 8u, 6));
+    const int32_t sc2 = static_cast<int32_t>(bfe(h.w, 8u * j0, 4) | (bfe(h.y, 8u * j0 + 6u, 2) << 4));
+    const int32_t sc3 = static_cast<int32_t>(bfe(h.w, 8u * j0 + 8u, 4) | (bfe(h.y, 8u * j0 + 14u, 2) << 4));
+    const int32_t m0 = static_cast<int32_t>(bfe(h.z, 8u * j0, 6));
+    const int32_t m1 = static_cast<int32_t>(bfe(h.z, 8u * j0 + 8u, 6));
+    const int32_t m2 = static_cast<int32_t>(bfe(h.w, 8u * j0 + 4u, 4) | (bfe(h.z, 8u * j0 + 6u, 2) << 4));
+    const int32_t m3 = static_cast<int32_t>(bfe(h.w, 8u * j0 + 12u, 4) | (bfe(h.z, 8u * j0 + 14u, 2) << 4));
+    const float d = f16_lo(h.x), dmin = f16_hi(h.x);
     uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      lo0[k] = c0[k] & 0x0F0F0F0Fu;
-      hi0[k] = (c0[k] >> 4) & 0x0F0F0F0Fu;
-      lo1[k] = c1[k] & 0x0F0F0F0Fu;
-      hi1[k] = (c1[k] >> 4) & 0x0F0F0F0Fu;
+      lo0[k] = c0[it][k] & 0x0F0F0F0Fu;
+      hi0[k] = (c0[it][k] >> 4) & 0x0F0F0F0Fu;
+      lo1[k] = c1[it][k] & 0x0F0F0F0Fu;
+      hi1[k] = (c1[it][k] >> 4) & 0x0F0F0F0Fu;
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
@@ -151,6 +170,28 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
   const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
   const uint32_t nrows = min(R, J.rows - row0);
   const uint32_t nb = J.nb;
+  const uint32_t total = nrows * nb;
+  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
+  const uint32_t h = p >> 1, gq = p & 1u;
+
+  // Rows start 16-byte aligned, so block b sits (210*b) mod 4 = 2*(b & 1)
+  // bytes past a dword boundary: load aligned dwords, realign in registers.
+  // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; W: scales at
+  // 192; E: the fifth dwords of A, B, C and the dword holding d (q6_k.rs:13-43).
+  u32x4 A[NI], B[NI], C[NI], W[NI], E[NI];
+#pragma unroll
+  for (int i = 0; i < NI; i++) {
+    const uint32_t g = team + i * (kThreads / 4u);
+    const uint32_t gg = g < total ? g : 0u;
+    const uint32_t r = nb ? gg / nb : 0u, b = gg - r * nb;
+    const uint8_t* base = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 210u - 2u * (b & 1u);
+    A[i] = load16_a4(base + 64u * h + 16u * gq);
+    B[i] = load16_a4(base + 64u * h + 32u + 16u * gq);
+    C[i] = load16_a4(base + 128u + 32u * h + 16u * gq);
+    W[i] = load16_a4(base + 192u);
+    E[i] = u32x4{load4(base + 64u * h + 16u * gq + 16u), load4(base + 64u * h + 48u + 16u * gq),
+                 load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
+  }
 
   stage_quants<T>(act, abytes, q, t0);
   for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += kThreads) {
@@ -160,47 +201,44 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
   }
   __syncthreads();
 
-  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
-  const uint32_t h = p >> 1, gq = p & 1u;
-  for (uint32_t g = team; g < nrows * nb; g += kThreads / 4u) {
+#pragma unroll
+  for (int it = 0; it < NI; it++) {
+    const uint32_t g = team + it * (kThreads / 4u);
+    if (g >= total) break;  // uniform over the team
     const uint32_t r = g / nb, b = g - r * nb;
-    const uint8_t* blk = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 210u;
-    // ql[64h+16gq..], ql[64h+32+16gq..], qh[32h+16gq..] (quantize/src/q6_k.rs:13-43)
-    const u32x4 A = load16_unaligned(blk + 64u * h + 16u * gq);
-    const u32x4 B = load16_unaligned(blk + 64u * h + 32u + 16u * gq);
-    const u32x4 C = load16_unaligned(blk + 128u + 32u * h + 16u * gq);
-    // scales[16] at 192 and d at 208, realigned from six aligned dwords
-    const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 3u);
-    const uint8_t* hb = blk + 192u - sh;
-    const u32x4 w03 = load16_a4(hb);
-    const uint32_t w4 = load4(hb + 16u), w5 = load4(hb + 20u);
-    const uint32_t X0 = __builtin_amdgcn_alignbyte(w03.y, w03.x, sh);
-    const uint32_t X1 = __builtin_amdgcn_alignbyte(w03.z, w03.y, sh);
-    const uint32_t X2 = __builtin_amdgcn_alignbyte(w03.w, w03.z, sh);
-    const uint32_t X3 = __builtin_amdgcn_alignbyte(w4, w03.w, sh);
-    const uint32_t X4 = __builtin_amdgcn_alignbyte(w5, w4, sh);
+    const uint32_t sh = 2u * (b & 1u);
+    const u32x4 a{__builtin_amdgcn_alignbyte(A[it].y, A[it].x, sh), __builtin_amdgcn_alignbyte(A[it].z, A[it].y, sh),
+                  __builtin_amdgcn_alignbyte(A[it].w, A[it].z, sh), __builtin_amdgcn_alignbyte(E[it].x, A[it].w, sh)};
+    const u32x4 bq{__builtin_amdgcn_alignbyte(B[it].y, B[it].x, sh), __builtin_amdgcn_alignbyte(B[it].z, B[it].y, sh),
+                   __builtin_amdgcn_alignbyte(B[it].w, B[it].z, sh), __builtin_amdgcn_alignbyte(E[it].y, B[it].w, sh)};
+    const u32x4 c{__builtin_amdgcn_alignbyte(C[it].y, C[it].x, sh), __builtin_amdgcn_alignbyte(C[it].z, C[it].y, sh),
+                  __builtin_amdgcn_alignbyte(C[it].w, C[it].z, sh), __builtin_amdgcn_alignbyte(E[it].z, C[it].w, sh)};
+    const uint32_t X0 = __builtin_amdgcn_alignbyte(W[it].y, W[it].x, sh);
+    const uint32_t X1 = __builtin_amdgcn_alignbyte(W[it].z, W[it].y, sh);
+    const uint32_t X2 = __builtin_amdgcn_alignbyte(W[it].w, W[it].z, sh);
+    const uint32_t X3 = __builtin_amdgcn_alignbyte(E[it].w, W[it].w, sh);
     const uint32_t slo = h ? X2 : X0, shi = h ? X3 : X1;
     // scale of run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
     const int32_t sc0 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq, 8);
     const int32_t sc1 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq + 16u, 8);
     const int32_t sc2 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq, 8);
     const int32_t sc3 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq + 16u, 8);
-    const float d = f16_lo(X4);
+    const float d = f16_lo(E[it].w >> (8u * sh));  // bytes 208..209
     uint32_t q0[4], q1[4], q2[4], q3[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
-      q0[k] = (A[k] & 0x0F0F0F0Fu) | ((C[k] << 4) & 0x30303030u);
-      q1[k] = (B[k] & 0x0F0F0F0Fu) | ((C[k] << 2) & 0x30303030u);
-      q2[k] = ((A[k] >> 4) & 0x0F0F0F0Fu) | (C[k] & 0x30303030u);
-      q3[k] = ((B[k] >> 4) & 0x0F0F0F0Fu) | ((C[k] >> 2) & 0x30303030u);
+      q0[k] = (a[k] & 0x0F0F0F0Fu) | ((c[k] << 4) & 0x30303030u);
+      q1[k] = (bq[k] & 0x0F0F0F0Fu) | ((c[k] << 2) & 0x30303030u);
+      q2[k] = ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0x30303030u);
+      q3[k] = ((bq[k] >> 4) & 0x0F0F0F0Fu) | ((c[k] >> 2) & 0x30303030u);
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const int8_t* a = act + t * abytes + b * 256u + 128u * h + 16u * gq;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+      const int8_t* av = act + t * abytes + b * 256u + 128u * h + 16u * gq;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(av);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(av + 32u);
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(av + 64u);
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(av + 96u);
       const int32_t* bb = bias + t * nbmax * 16u + b * 16u + 8u * h + gq;
       int32_t D0 = bb[0], D1 = bb[2], D2 = bb[4], D3 = bb[6];
 #pragma unroll
@@ -417,8 +455,8 @@ size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
 
 uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t total_rows) {
   if (type_id == 36u || type_id == 0u) return 32u;  // one row per 8-lane team
-  // enough rows that each 4-lane team decodes about two blocks
-  uint32_t R = (2u * 64u + nb - 1u) / nb;
+  // whole rows of at most NI blocks per 4-lane team
+  uint32_t R = static_cast<uint32_t>(NI) * (kThreads / 4u) / nb;
   if (R < 1u) R = 1u;
   (void)total_rows;
   return R;

@@ -54,6 +54,10 @@ hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, c
                        size_t width, size_t tokens, size_t t0, size_t tn, hipStream_t s,
                        int32_t* raw_i32);
 size_t gemv_max_tokens(uint32_t type_id, uint32_t nb);
+// Streaming decode GEMV for one or two tokens; false when the launch's shape
+// is outside what it handles (the caller then uses launch_gemv).
+bool launch_gemv_stream(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0,
+                        size_t tn, hipStream_t s, int32_t* raw, hipError_t* err);
 
 hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
                                  float* out, size_t out_len, hipStream_t s);

@@ -6,6 +6,8 @@ stated 1e-4 relative tolerance); every token of a batch identical to a
 single-token call. Shapes include the benchmark workloads at full size.
 """
 
+import os
+
 import numpy as np
 import pytest
 
@@ -21,6 +23,18 @@ def ctx():
     c = R.Context(0)
     yield c
     c.close()
+
+
+@pytest.fixture(params=["auto", "stream", "lds"])
+def variant(request):
+    """Both decode GEMV kernel families must give the CPU path's bits."""
+    old = os.environ.get("RUSTICIDE_HIP_GEMV")
+    os.environ["RUSTICIDE_HIP_GEMV"] = request.param
+    yield request.param
+    if old is None:
+        os.environ.pop("RUSTICIDE_HIP_GEMV", None)
+    else:
+        os.environ["RUSTICIDE_HIP_GEMV"] = old
 
 
 def bits(a):
@@ -90,17 +104,20 @@ def test_device_quantizers_match_the_oracle(ctx, kind):
 
 
 KQ_SHAPES = [
-    (12, 5632, 2048, [1]),      # Q4_K ffn_gate shape (benchmark workload)
+    (12, 5632, 2048, [1, 2]),   # Q4_K ffn_gate shape (benchmark workload)
     (12, 2048, 5632, [1, 2]),   # Q4_K ffn_down shape (22 blocks per row)
     (12, 37, 512, [1, 3, 8, 11]),
-    (14, 32000, 2048, [1]),     # Q6_K lm_head (benchmark workload)
+    (14, 32000, 2048, [1, 2]),  # Q6_K lm_head (benchmark workload)
+    (12, 64, 4096, [1, 2]),     # 16 blocks: one full pass
+    (14, 19, 8192, [1, 2]),     # 32 blocks: two passes
+    (12, 11, 256, [1, 2]),      # one block per row: 16 rows per wave
     (14, 2048, 5632, [1, 3]),   # Q6_K ffn_down: 4620-byte rows, padded stride
     (14, 45, 768, [1, 2, 9]),
 ]
 
 
 @pytest.mark.parametrize("type_id,rows,cols,token_counts", KQ_SHAPES)
-def test_kquant_gemv_is_bit_identical_to_the_cpu_path(ctx, type_id, rows, cols, token_counts):
+def test_kquant_gemv_is_bit_identical_to_the_cpu_path(ctx, variant, type_id, rows, cols, token_counts):
     data = synth.matrix(type_id, rows, cols, seed=rows + cols)
     m = R.Matrix.load(ctx, type_id, data, rows, cols)
     for tokens in token_counts:
@@ -144,11 +161,11 @@ def test_kquant_dot_within_1e4_of_dequantize_and_dot(ctx, type_id):
 # --------------------------------------------------------------- I2_S GEMV
 
 
-I2S_SHAPES = [(6912, 2560, [1]), (2560, 6912, [1, 2]), (33, 384, [1, 4, 9])]
+I2S_SHAPES = [(6912, 2560, [1, 2]), (2560, 6912, [1, 2]), (33, 384, [1, 4, 9]), (17, 8192, [1, 2])]
 
 
 @pytest.mark.parametrize("rows,cols,token_counts", I2S_SHAPES)
-def test_i2s_i32_accumulators_are_bit_exact(ctx, rows, cols, token_counts):
+def test_i2s_i32_accumulators_are_bit_exact(ctx, variant, rows, cols, token_counts):
     data = synth.i2s_matrix(rows, cols, seed=rows)
     m = R.Matrix.load(ctx, 36, data, rows, cols)
     assert m.ternary_scale == np.float32(0.02)
@@ -177,7 +194,7 @@ def test_i2s_code_three_and_hostile_bytes(ctx):
 # ------------------------------------------------------------ batch rules
 
 
-def test_one_batch_mixes_formats_and_matches_per_token_calls(ctx):
+def test_one_batch_mixes_formats_and_matches_per_token_calls(ctx, variant):
     # attention.rs:215-223 (Q/K/V in one batch) + matmul_tests.rs:237-271
     cols, tokens = 2048, 5
     specs = [(12, 2048), (12, 256), (14, 256), (36, 300), (14, 40)]
@@ -218,7 +235,7 @@ def test_no_ops_and_output_bounds(ctx):
     assert np.all(long[-3:] == 5.0)
 
 
-def test_an_input_narrower_than_the_rows_bounds_the_dot(ctx):
+def test_an_input_narrower_than_the_rows_bounds_the_dot(ctx, variant):
     # int_dot.rs:36-47 and ternary.rs:21-26: the shorter operand bounds the work
     rows, cols = 12, 1024
     for t in (12, 14, 36):
@@ -245,7 +262,7 @@ def test_dense_f32_rows_follow_the_eight_lane_dot(ctx):
         assert_same_bits(out, oracle_matmul(0, w, rows, cols, x, 2))
 
 
-def test_hostile_block_bytes_match_the_oracle(ctx):
+def test_hostile_block_bytes_match_the_oracle(ctx, variant):
     # the fuzz idea (rusticide-fuzz dequantize target): any bytes, incl. f16
     # inf/NaN scales, must compute what the CPU path computes
     rows, cols = 40, 512
