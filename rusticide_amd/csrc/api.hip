@@ -74,15 +74,18 @@ rh_status hip_fail(rh_ctx* ctx, hipError_t e, const char* what) {
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-// Decode (one or two tokens) runs the k-quants on the LDS-staged kernels and
-// I2_S on the streaming one, the faster of each pair on MI355X.
-// RUSTICIDE_HIP_GEMV=lds|stream forces one family for every format (both give
-// the same bits; the switch exists to test and time one against the other).
-bool use_stream(uint32_t type_id) {
+// Which GEMV kernel family serves a format: the LDS-staged kernels for the
+// k-quants and the streaming one for I2_S, the fastest of each on MI355X.
+// RUSTICIDE_HIP_GEMV=kq|stream|lds forces one family where it applies (all
+// give the same bits; the switch exists to test and time one against another).
+enum class Family { kPersistent, kStream, kLds };
+
+Family family(uint32_t type_id) {
   const char* v = std::getenv("RUSTICIDE_HIP_GEMV");
-  if (v && std::strcmp(v, "lds") == 0) return false;
-  if (v && std::strcmp(v, "stream") == 0) return true;
-  return type_id == RH_TYPE_I2_S;
+  if (v && std::strcmp(v, "lds") == 0) return Family::kLds;
+  if (v && std::strcmp(v, "stream") == 0) return Family::kStream;
+  if (v && std::strcmp(v, "kq") == 0 && type_id != RH_TYPE_I2_S) return Family::kPersistent;
+  return type_id == RH_TYPE_I2_S ? Family::kStream : Family::kLds;
 }
 
 // Grows scratch slot `i` to at least `bytes`.
@@ -163,10 +166,24 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (kind != RH_TYPE_F32) tmax = gemv_max_tokens(kind, nbmax);
       if (tmax == 0) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "rows too wide for the GEMV kernels");
       const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
-      if (kind != RH_TYPE_F32 && tokens <= 2 && use_stream(kind)) {
+      const Family fam = kind == RH_TYPE_F32 ? Family::kLds : family(kind);
+      if (fam == Family::kStream && tokens <= 2) {
         hipError_t e = hipSuccess;
         if (launch_gemv_stream(kind, g, q, tokens, 0, tokens, s, raw, &e)) {
           RH_HIP(ctx, e);
+          g = GemvJobs{};
+          nbmax = 0;
+          return RH_OK;
+        }
+      }
+      if (fam == Family::kPersistent) {
+        const uint32_t nbl = nbmax ? nbmax : 1u;
+        const size_t tk = gemv_kq_max_tokens(nbl);
+        if (tk) {
+          for (size_t t0 = 0; t0 < tokens; t0 += tk) {
+            const size_t tn = tokens - t0 < tk ? tokens - t0 : tk;
+            RH_HIP(ctx, launch_gemv_kq(kind, g, q, nbl, tokens, t0, tn, s));
+          }
           g = GemvJobs{};
           nbmax = 0;
           return RH_OK;

@@ -15,6 +15,8 @@
 //
 // I2_S: a team of 8 lanes walks a row 16 bytes at a time; the i32 dot is
 // order-free (wrapping) and is scaled once per row, as portable/ternary.rs:48-58.
+#include <cstdlib>
+
 #include "rh_device.h"
 #include "rh_internal.h"
 
@@ -46,12 +48,31 @@ __device__ __forceinline__ void stage_quants(int8_t* act, uint32_t bytes, const 
 // first, before the activation is staged and before the barrier, so every
 // resident workgroup has all of its rows in flight from its first cycles and
 // the decode of one workgroup overlaps the loads of the others.
-constexpr int NI = 2;
+// As stage_quants, for the k-quants: 16-byte chunk c of 256-byte block b is
+// stored at chunk c ^ (b & 15). The teams of a wave read the same chunk
+// offsets of different blocks at once; unswizzled those all land in the same
+// few LDS banks (a 256-byte block stride is a whole number of bank rows).
+template <int T>
+__device__ __forceinline__ void stage_quants_swizzled(int8_t* act, uint32_t bytes, const Q8Dev& q, size_t t0) {
+  for (uint32_t t = 0; t < static_cast<uint32_t>(T); t++) {
+    const int8_t* src = q.quants + (t0 + t) * q.qstride;
+    for (uint32_t i = threadIdx.x * 16u; i < bytes; i += kThreads * 16u) {
+      const uint32_t b = i >> 8, c = (i >> 4) & 15u;
+      *reinterpret_cast<u32x4*>(act + t * bytes + (b << 8) + ((c ^ (b & 15u)) << 4)) =
+          *reinterpret_cast<const u32x4*>(src + i);
+    }
+  }
+}
+
+// The address of activation byte k (a multiple of 16) of block b of token t.
+__device__ __forceinline__ const int8_t* swz(const int8_t* act_t, uint32_t b, uint32_t k) {
+  return act_t + (b << 8) + ((((k >> 4) ^ (b & 15u))) << 4);
+}
 
 // Q4_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
 //      terms [R][nbmax][T] f32
-template <int T>
+template <int T, int NI>
 __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
                                                        uint32_t nbmax, size_t tokens, size_t t0) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -68,19 +89,22 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
   const uint32_t total = nrows * nb;
   const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
 
+  // g = r*nb + b with g < 4*64: a float reciprocal divides exactly here
+  const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   u32x4 hd[NI], c0[NI], c1[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
     const uint32_t g = team + i * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;  // a spare team re-reads block 0
-    const uint32_t r = nb ? gg / nb : 0u, b = gg - r * nb;
-    const uint8_t* blk = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 144u;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - r * nb;
+    // matrices stay below 4 GiB and 2^24 rows: 24-bit multiplies, 32-bit offsets
+    const uint8_t* blk = J.w + (__umul24(row0 + r, static_cast<uint32_t>(J.stride)) + b * 144u);
     hd[i] = load16(blk);
     c0[i] = load16(blk + 16u + 16u * p);
     c1[i] = load16(blk + 80u + 16u * p);
   }
 
-  stage_quants<T>(act, abytes, q, t0);
+  stage_quants_swizzled<T>(act, abytes, q, t0);
   for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += kThreads) {
     const uint32_t t = i / (nbmax * 8u), k = i - t * nbmax * 8u;
     const size_t src = (t0 + t) * q.bstride + k;
@@ -95,7 +119,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
   for (int it = 0; it < NI; it++) {
     const uint32_t g = team + it * (kThreads / 4u);
     if (g >= total) break;  // uniform over the team
-    const uint32_t r = g / nb, b = g - r * nb;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - r * nb;
     const u32x4 h = hd[it];
     // 6-bit scales/mins of sub-blocks j0, j0+1, j0+4, j0+5 (ggml get_scale_min_k4,
     // quantize/src/q4_k.rs:17-25)
@@ -118,11 +142,12 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const int8_t* a = act + t * abytes + b * 256u + e0;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a + 32u * j0);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u * j0 + 32u);
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 32u * j0 + 128u);
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 32u * j0 + 160u);
+      const int8_t* at = act + t * abytes;
+      const uint32_t k0 = e0 + 32u * j0;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(swz(at, b, k0));
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 32u));
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 128u));
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 160u));
       int32_t D0 = 0, D1 = 0, D2 = 0, D3 = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -156,7 +181,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
 // Q6_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | bias [T][nbmax*16] i32
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
-template <int T>
+template <int T, int NI>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
                                                        uint32_t nbmax, size_t tokens, size_t t0) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -178,13 +203,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
   // bytes past a dword boundary: load aligned dwords, realign in registers.
   // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; W: scales at
   // 192; E: the fifth dwords of A, B, C and the dword holding d (q6_k.rs:13-43).
+  const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   u32x4 A[NI], B[NI], C[NI], W[NI], E[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
     const uint32_t g = team + i * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;
-    const uint32_t r = nb ? gg / nb : 0u, b = gg - r * nb;
-    const uint8_t* base = J.w + static_cast<size_t>(row0 + r) * J.stride + static_cast<size_t>(b) * 210u - 2u * (b & 1u);
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - r * nb;
+    const uint8_t* base = J.w + (__umul24(row0 + r, static_cast<uint32_t>(J.stride)) + b * 210u - 2u * (b & 1u));
     A[i] = load16_a4(base + 64u * h + 16u * gq);
     B[i] = load16_a4(base + 64u * h + 32u + 16u * gq);
     C[i] = load16_a4(base + 128u + 32u * h + 16u * gq);
@@ -193,7 +219,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
                  load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
   }
 
-  stage_quants<T>(act, abytes, q, t0);
+  stage_quants_swizzled<T>(act, abytes, q, t0);
   for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += kThreads) {
     const uint32_t t = i / (nbmax * 16u), k = i - t * nbmax * 16u;
     bias[i] = -32 * q.sums16[2u * (t0 + t) * q.bstride + k];
@@ -205,7 +231,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
   for (int it = 0; it < NI; it++) {
     const uint32_t g = team + it * (kThreads / 4u);
     if (g >= total) break;  // uniform over the team
-    const uint32_t r = g / nb, b = g - r * nb;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - r * nb;
     const uint32_t sh = 2u * (b & 1u);
     const u32x4 a{__builtin_amdgcn_alignbyte(A[it].y, A[it].x, sh), __builtin_amdgcn_alignbyte(A[it].z, A[it].y, sh),
                   __builtin_amdgcn_alignbyte(A[it].w, A[it].z, sh), __builtin_amdgcn_alignbyte(E[it].x, A[it].w, sh)};
@@ -234,11 +260,12 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const int8_t* av = act + t * abytes + b * 256u + 128u * h + 16u * gq;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(av);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(av + 32u);
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(av + 64u);
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(av + 96u);
+      const int8_t* at = act + t * abytes;
+      const uint32_t k0 = 128u * h + 16u * gq;
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(swz(at, b, k0));
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 32u));
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 64u));
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 96u));
       const int32_t* bb = bias + t * nbmax * 16u + b * 16u + 8u * h + gq;
       int32_t D0 = bb[0], D1 = bb[2], D2 = bb[4], D3 = bb[6];
 #pragma unroll
@@ -453,13 +480,72 @@ size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
   return 0;
 }
 
+// Blocks per 4-lane team in the k-quant kernels (1, 2 or 4), set per launch
+// by launch_t: the smallest that lets every workgroup of the grid be resident
+// at once, so no rows wait for a second generation of workgroups.
+// RUSTICIDE_HIP_GEMV_NI=1|2|4 forces it, for tuning.
+thread_local uint32_t g_blocks_per_team = 1u;
+
+uint32_t forced_blocks_per_team() {
+  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMV_NI")) {
+    if (v[0] == '1') return 1u;
+    if (v[0] == '2') return 2u;
+    if (v[0] == '4') return 4u;
+  }
+  return 0u;
+}
+
+uint32_t blocks_per_team(uint32_t type_id) {
+  (void)type_id;
+  return g_blocks_per_team;
+}
+
 uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t total_rows) {
   if (type_id == 36u || type_id == 0u) return 32u;  // one row per 8-lane team
   // whole rows of at most NI blocks per 4-lane team
-  uint32_t R = static_cast<uint32_t>(NI) * (kThreads / 4u) / nb;
+  uint32_t R = blocks_per_team(type_id) * (kThreads / 4u) / nb;
   if (R < 1u) R = 1u;
   (void)total_rows;
   return R;
+}
+
+template <int T, int NI>
+int resident_wgs_per_cu(uint32_t type_id, size_t lds) {
+  // measured once per kernel and LDS size bucket (1 KiB)
+  static int cache[2][64] = {};
+  const size_t bucket = lds / 1024u < 63u ? lds / 1024u : 63u;
+  int& c = cache[type_id == 12u ? 0 : 1][bucket];
+  if (c == 0) {
+    int n = 0;
+    const hipError_t e = type_id == 12u
+        ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_q4k_kernel<T, NI>, kThreads, (bucket + 1u) * 1024u)
+        : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_q6k_kernel<T, NI>, kThreads, (bucket + 1u) * 1024u);
+    c = (e == hipSuccess && n > 0) ? n : 1;
+  }
+  return c;
+}
+
+template <int T>
+uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_rows) {
+  if (const uint32_t forced = forced_blocks_per_team()) return forced;
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+      cus = 256;
+  }
+  for (uint32_t ni : {1u, 2u, 4u}) {
+    g_blocks_per_team = ni;
+    const uint32_t R = rows_per_wg(type_id, nb, total_rows);
+    const uint32_t wgs = (total_rows + R - 1u) / R;
+    const size_t lds = lds_bytes<T>(type_id, nb, R);
+    const int per_cu = ni == 1u ? resident_wgs_per_cu<T, 1>(type_id, lds)
+                     : ni == 2u ? resident_wgs_per_cu<T, 2>(type_id, lds)
+                                : resident_wgs_per_cu<T, 4>(type_id, lds);
+    if (wgs <= static_cast<uint32_t>(per_cu * cus)) return ni;
+  }
+  return 4u;
 }
 
 template <int T>
@@ -473,6 +559,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
   // Rows whose blocks the input does not reach still get an output (-0.0 for
   // the k-quants, as an empty f32 sum); size everything for at least one block.
   const uint32_t nbl = nbmax ? nbmax : 1u;
+  if (type_id == 12u || type_id == 14u) g_blocks_per_team = choose_blocks_per_team<T>(type_id, nbl, total_rows);
   const uint32_t R = rows_per_wg(type_id, nbl, total_rows);
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
@@ -486,10 +573,16 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     return hipGetLastError();
   }
   const size_t lds = lds_bytes<T>(type_id, nbl, R);
-  if (type_id == 12u)
-    hipLaunchKernelGGL(gemv_q4k_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
-  else if (type_id == 14u)
-    hipLaunchKernelGGL(gemv_q6k_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+  const uint32_t ni = blocks_per_team(type_id);
+  if (type_id == 12u) {
+    if (ni == 4u) hipLaunchKernelGGL((gemv_q4k_kernel<T, 4>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+    else if (ni == 2u) hipLaunchKernelGGL((gemv_q4k_kernel<T, 2>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+    else hipLaunchKernelGGL((gemv_q4k_kernel<T, 1>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+  } else if (type_id == 14u) {
+    if (ni == 4u) hipLaunchKernelGGL((gemv_q6k_kernel<T, 4>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+    else if (ni == 2u) hipLaunchKernelGGL((gemv_q6k_kernel<T, 2>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+    else hipLaunchKernelGGL((gemv_q6k_kernel<T, 1>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+  }
   else
     hipLaunchKernelGGL(gemv_i2s_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0,
                        raw);
@@ -499,9 +592,12 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
 }  // namespace
 
 size_t gemv_max_tokens(uint32_t type_id, uint32_t nb) {
-  // LDS per workgroup stays within 64 KiB.
+  // LDS per workgroup stays within 64 KiB at the largest tile (NI = 4)
   const uint32_t nbl = nb ? nb : 1u;
+  const uint32_t saved = g_blocks_per_team;
+  g_blocks_per_team = 4u;
   const uint32_t R = rows_per_wg(type_id, nbl, 0);
+  g_blocks_per_team = saved;
   size_t t = kMaxTokens;
   while (t > 1) {
     size_t need = 0;

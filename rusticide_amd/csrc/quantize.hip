@@ -44,7 +44,11 @@ __global__ __launch_bounds__(256) void quantize_super_kernel(const float* __rest
     uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(idx), off, 64));
     idx = o < idx ? o : idx;
   }
-  const float max = idx < 256u ? v[idx] : 0.0f;
+  // the owner of element idx broadcasts it (no dependent reload)
+  const uint32_t sel = idx & 3u;
+  const float mine = sel == 0 ? f[0] : sel == 1 ? f[1] : sel == 2 ? f[2] : f[3];
+  const float owned = __shfl(mine, static_cast<int>((idx >> 2) & 63u), 64);
+  const float max = idx < 256u ? owned : 0.0f;
   const float inverse = (max == 0.0f) ? 0.0f : __fdiv_rn(-127.0f, max);
   const float step = (max == 0.0f) ? 0.0f : __fdiv_rn(1.0f, inverse);
 
@@ -69,12 +73,116 @@ __global__ __launch_bounds__(256) void quantize_super_kernel(const float* __rest
   if (lane < 8u) q.scales[b0 + lane] = step;
 }
 
-// One workgroup per token: the row divisor in f64 with C's MAX semantics,
-// then the quants. A NaN element restarts the running maximum at the next
-// element (q8.rs:42-45), so the divisor depends on the elements after the
-// last NaN only; a trailing NaN makes it NaN.
-__global__ __launch_bounds__(256) void quantize_row_kernel(const float* __restrict__ x, size_t width,
-                                                           uint32_t n_blocks, Q8Dev q) {
+// One 1024-lane workgroup per token, four consecutive values per lane per
+// pass, all held in registers: the row divisor in f64 with C's MAX
+// semantics, then the quants. A NaN element restarts the running maximum at
+// the next element (q8.rs:42-45), so the divisor depends on the elements
+// after the last NaN only; a trailing NaN makes it NaN.
+constexpr uint32_t kRowThreads = 1024;
+constexpr uint32_t kRowPasses = 4;  // up to 16384 values per token
+
+__device__ __forceinline__ int block_max_i(int v, int* red) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const int o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  const uint32_t wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63u) == 0) red[wave] = v;
+  __syncthreads();
+  int m = red[0];
+  for (uint32_t w = 1; w < kRowThreads / 64u; w++) m = red[w] > m ? red[w] : m;
+  return m;
+}
+
+__device__ __forceinline__ float block_max_f(float v, float* red) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(v, off, 64);
+    v = o > v ? o : v;
+  }
+  const uint32_t wave = threadIdx.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63u) == 0) red[wave] = v;
+  __syncthreads();
+  float m = red[0];
+  for (uint32_t w = 1; w < kRowThreads / 64u; w++) m = red[w] > m ? red[w] : m;
+  return m;
+}
+
+__global__ __launch_bounds__(1024) void quantize_row_kernel(const float* __restrict__ x, size_t width,
+                                                            uint32_t n_blocks, Q8Dev q) {
+  __shared__ int s_i[kRowThreads / 64u];
+  __shared__ float s_f[kRowThreads / 64u];
+  const size_t t = blockIdx.x;
+  const float* v = x + t * width;
+  const uint32_t n = n_blocks * 32u;
+  const uint32_t lane = threadIdx.x & 63u;
+  float f[kRowPasses][4];
+  int last_nan = -1;
+#pragma unroll
+  for (uint32_t k = 0; k < kRowPasses; k++) {
+    const uint32_t base = 4u * threadIdx.x + 4u * kRowThreads * k;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t e = base + i;
+      f[k][i] = e < n ? v[e] : 0.0f;
+      if (e < n && f[k][i] != f[k][i]) last_nan = static_cast<int>(e);
+    }
+  }
+  const int p = block_max_i(last_nan, s_i);
+  float mag_max = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k < kRowPasses; k++)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t e = 4u * threadIdx.x + 4u * kRowThreads * k + i;
+      const float m = __builtin_fabsf(f[k][i]);
+      if (e < n && static_cast<int>(e) > p) mag_max = m > mag_max ? m : mag_max;
+    }
+  const float mm = block_max_f(mag_max, s_f);
+  double mx;
+  if (p < 0) {
+    mx = static_cast<double>(mm);
+    mx = 1e-5 > mx ? 1e-5 : mx;
+  } else if (p == static_cast<int>(n) - 1) {
+    mx = __builtin_nan("");
+  } else {
+    mx = static_cast<double>(mm);
+  }
+  const float divisor = static_cast<float>(127.0 / mx);
+
+#pragma unroll
+  for (uint32_t k = 0; k < kRowPasses; k++) {
+    const uint32_t base = 4u * threadIdx.x + 4u * kRowThreads * k;
+    if (4u * kRowThreads * k >= n) break;  // uniform
+    int32_t qv[4];
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float prod = f[k][i] * divisor;
+      qv[i] = round_row_to_i8(prod);
+      s += qv[i];
+    }
+    // a 32-block is 8 lanes of 4; lanes past n belong to whole blocks past n
+    int32_t s32 = s + __shfl_xor(s, 1, 64);
+    s32 += __shfl_xor(s32, 2, 64);
+    s32 += __shfl_xor(s32, 4, 64);
+    if (base < n) {
+      const uint32_t packed = (static_cast<uint32_t>(qv[0]) & 0xffu) | ((static_cast<uint32_t>(qv[1]) & 0xffu) << 8) |
+                              ((static_cast<uint32_t>(qv[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qv[3]) << 24);
+      *reinterpret_cast<uint32_t*>(q.quants + t * q.qstride + base) = packed;
+      if ((lane & 7u) == 0) {
+        q.sums[t * q.bstride + base / 32u] = s32;
+        q.scales[t * q.bstride + base / 32u] = divisor;
+      }
+    }
+  }
+}
+
+// Rows wider than the register-resident kernel holds: three passes over
+// global memory, one workgroup per token.
+__global__ __launch_bounds__(256) void quantize_row_wide_kernel(const float* __restrict__ x, size_t width,
+                                                                uint32_t n_blocks, Q8Dev q) {
   __shared__ int s_last_nan;
   __shared__ float s_max[4];
   __shared__ int s_nan_wave[4];
@@ -125,7 +233,6 @@ __global__ __launch_bounds__(256) void quantize_row_kernel(const float* __restri
   }
   const float divisor = static_cast<float>(127.0 / mx);
 
-  // quants and per-32 sums: one 32-block per 8 lanes, 4 values per lane
   for (uint32_t base = tid * 4u; base < n; base += 1024u) {
     int32_t qv[4];
     int32_t s = 0;
@@ -161,8 +268,12 @@ hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, cons
                                hipStream_t s) {
   const uint32_t n_blocks = static_cast<uint32_t>(width / 32u);
   if (n_blocks == 0 || tokens == 0) return hipSuccess;
-  hipLaunchKernelGGL(quantize_row_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, s, x,
-                     width, n_blocks, q);
+  if (n_blocks * 32u <= 4u * kRowThreads * kRowPasses)
+    hipLaunchKernelGGL(quantize_row_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(kRowThreads), 0, s, x,
+                       width, n_blocks, q);
+  else
+    hipLaunchKernelGGL(quantize_row_wide_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(256), 0, s, x,
+                       width, n_blocks, q);
   return hipGetLastError();
 }
 

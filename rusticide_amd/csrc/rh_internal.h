@@ -59,6 +59,12 @@ size_t gemv_max_tokens(uint32_t type_id, uint32_t nb);
 bool launch_gemv_stream(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0,
                         size_t tn, hipStream_t s, int32_t* raw, hipError_t* err);
 
+// Persistent k-quant GEMV (Q4_K, Q6_K) for up to gemv_kq_max_tokens tokens
+// per launch (0: the rows are too wide for it).
+size_t gemv_kq_max_tokens(uint32_t nb);
+hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, uint32_t nbmax, size_t tokens,
+                          size_t t0, size_t tn, hipStream_t s);
+
 hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
                                  float* out, size_t out_len, hipStream_t s);
 

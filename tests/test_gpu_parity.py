@@ -25,16 +25,22 @@ def ctx():
     c.close()
 
 
-@pytest.fixture(params=["auto", "stream", "lds"])
+@pytest.fixture(params=["auto", "kq", "stream", "lds-1", "lds-2", "lds-4"])
 def variant(request):
-    """Both decode GEMV kernel families must give the CPU path's bits."""
-    old = os.environ.get("RUSTICIDE_HIP_GEMV")
-    os.environ["RUSTICIDE_HIP_GEMV"] = request.param
-    yield request.param
-    if old is None:
-        os.environ.pop("RUSTICIDE_HIP_GEMV", None)
+    """Every decode GEMV kernel variant must give the CPU path's bits."""
+    family, _, ni = request.param.partition("-")
+    saved = {k: os.environ.get(k) for k in ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI")}
+    os.environ["RUSTICIDE_HIP_GEMV"] = family
+    if ni:
+        os.environ["RUSTICIDE_HIP_GEMV_NI"] = ni
     else:
-        os.environ["RUSTICIDE_HIP_GEMV"] = old
+        os.environ.pop("RUSTICIDE_HIP_GEMV_NI", None)
+    yield request.param
+    for k, v in saved.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
 
 
 def bits(a):
