@@ -74,18 +74,24 @@ rh_status hip_fail(rh_ctx* ctx, hipError_t e, const char* what) {
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-// Which GEMV kernel family serves a format: the LDS-staged kernels for the
-// k-quants and the streaming one for I2_S, the fastest of each on MI355X.
-// RUSTICIDE_HIP_GEMV=kq|stream|lds forces one family where it applies (all
-// give the same bits; the switch exists to test and time one against another).
-enum class Family { kPersistent, kStream, kLds };
+// Which GEMV kernel family serves a format. The default, kFused, is one
+// launch per format in which every workgroup quantizes the activation itself
+// (decode-sized batches; larger ones fall back to a quantize launch plus the
+// LDS-staged kernels). RUSTICIDE_HIP_GEMV=kq|stream|lds forces a family that
+// reads a separately quantized activation. All give the same bits; the switch
+// exists to test and time one against another.
+enum class Family { kFused, kPersistent, kStream, kLds };
 
 Family family(uint32_t type_id) {
   const char* v = std::getenv("RUSTICIDE_HIP_GEMV");
   if (v && std::strcmp(v, "lds") == 0) return Family::kLds;
   if (v && std::strcmp(v, "stream") == 0) return Family::kStream;
   if (v && std::strcmp(v, "kq") == 0 && type_id != RH_TYPE_I2_S) return Family::kPersistent;
-  return type_id == RH_TYPE_I2_S ? Family::kStream : Family::kLds;
+  return Family::kFused;
+}
+
+unsigned format_bit(uint32_t type_id) {
+  return type_id == RH_TYPE_Q4_K ? 1u : type_id == RH_TYPE_Q6_K ? 2u : type_id == RH_TYPE_I2_S ? 4u : 0u;
 }
 
 // Grows scratch slot `i` to at least `bytes`.
@@ -152,9 +158,11 @@ size_t rows_for(const rh_matrix* m, size_t out_len, size_t tokens) {
 
 // One grouped launch per format over `jobs`, against quantized activations
 // `super_q` / `row_q` (or the raw f32 inputs for dense rows).
+// `fused` holds, per format (bit 0 Q4_K, 1 Q6_K, 2 I2_S), whether its
+// launches quantize d_in themselves.
 rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t tokens, const rh_job* jobs,
                       size_t n_jobs, const Q8Dev& super_q, const Q8Dev& row_q, hipStream_t s,
-                      int32_t* raw) {
+                      int32_t* raw, unsigned fused) {
   rh_status st = RH_OK;
   const uint32_t kinds[4] = {RH_TYPE_Q4_K, RH_TYPE_Q6_K, RH_TYPE_I2_S, RH_TYPE_F32};
   for (uint32_t kind : kinds) {
@@ -165,6 +173,12 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       size_t tmax = kMaxTokens;
       if (kind != RH_TYPE_F32) tmax = gemv_max_tokens(kind, nbmax);
       if (tmax == 0) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "rows too wide for the GEMV kernels");
+      if (fused & format_bit(kind)) {
+        RH_HIP(ctx, launch_gemv_fused(kind, g, d_in, width, tokens, 0, tokens, s, raw));
+        g = GemvJobs{};
+        nbmax = 0;
+        return RH_OK;
+      }
       const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
       const Family fam = kind == RH_TYPE_F32 ? Family::kLds : family(kind);
       if (fam == Family::kStream && tokens <= 2) {
@@ -227,18 +241,37 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
 rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t tokens,
                     const rh_job* jobs, size_t n_jobs, hipStream_t s, int32_t* raw) {
   const size_t width = inputs_len / tokens;
-  bool need_super = false, need_row = false;
+  uint32_t nbmax[3] = {0, 0, 0};  // Q4_K, Q6_K, I2_S
   for (size_t i = 0; i < n_jobs; i++) {
     if (!jobs[i].weights) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a job has no matrix");
     if (!jobs[i].out && jobs[i].out_len) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a job has no output");
-    need_super |= is_kquant(jobs[i].weights->type_id);
-    need_row |= jobs[i].weights->type_id == RH_TYPE_I2_S;
+    const rh_matrix* m = jobs[i].weights;
+    const unsigned bit = format_bit(m->type_id);
+    if (!bit) continue;
+    const size_t cover = m->type_id == RH_TYPE_I2_S ? width / 128 : width / 256;
+    const uint32_t nb = static_cast<uint32_t>(m->nblocks < cover ? m->nblocks : cover);
+    uint32_t& n = nbmax[bit >> 1];
+    n = nb > n ? nb : n;
   }
+  // A format is fused when its family allows it and the batch fits one
+  // fused launch; otherwise its activation is quantized once here.
+  unsigned present = 0, fused = 0;
+  for (size_t i = 0; i < n_jobs; i++) present |= format_bit(jobs[i].weights->type_id);
+  const uint32_t kinds[3] = {RH_TYPE_Q4_K, RH_TYPE_Q6_K, RH_TYPE_I2_S};
+  for (int k = 0; k < 3; k++) {
+    const uint32_t kind = kinds[k];
+    const unsigned bit = format_bit(kind);
+    if (!(present & bit) || family(kind) != Family::kFused || !gemv_fused_ok(kind, width, tokens)) continue;
+    if (tokens > gemv_max_tokens(kind, nbmax[bit >> 1])) continue;
+    fused |= bit;
+  }
+  const bool need_super = (present & ~fused & 3u) != 0;
+  const bool need_row = (present & ~fused & 4u) != 0;
   rh_status st = ensure_q8(ctx, width, tokens);
   if (st != RH_OK) return st;
   if (need_super) RH_HIP(ctx, launch_quantize_super(d_in, width, tokens, ctx->super_q, s));
   if (need_row) RH_HIP(ctx, launch_quantize_row(d_in, width, tokens, ctx->row_q, s));
-  return launch_jobs(ctx, d_in, width, tokens, jobs, n_jobs, ctx->super_q, ctx->row_q, s, raw);
+  return launch_jobs(ctx, d_in, width, tokens, jobs, n_jobs, ctx->super_q, ctx->row_q, s, raw, fused);
 }
 
 }  // namespace
@@ -327,6 +360,13 @@ rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
     m->nblocks = cols / bs;
     m->row_bytes = m->nblocks * bb;
     m->stride = round_up(m->row_bytes, 16);
+    // the GEMV kernels address a matrix with 24-bit row indices and 32-bit
+    // byte offsets
+    if (rows >= (size_t{1} << 24) || m->stride >= (size_t{1} << 24) ||
+        rows * m->stride + kPad > size_t{0xffffffffu}) {
+      delete m;
+      return fail(ctx, RH_ERR_SHAPE_MISMATCH, "matrix exceeds 2^24 rows or 4 GiB of blocks");
+    }
     const size_t body = rows * m->row_bytes;
     if (type_id == RH_TYPE_I2_S) {
       // model/src/weights.rs:70-80,190-202: the trailer's leading f32
@@ -543,7 +583,7 @@ rh_status rh_dot_matrix_device(rh_ctx* ctx, const rh_matrix* m, const rh_q8* q, 
   RH_HIP(ctx, hipSetDevice(ctx->device));
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
   rh_job job{m, out, out_len};
-  return launch_jobs(ctx, nullptr, q->width, q->tokens, &job, 1, q->q, q->q, s, nullptr);
+  return launch_jobs(ctx, nullptr, q->width, q->tokens, &job, 1, q->q, q->q, s, nullptr, 0u);
 }
 
 rh_status rh_quantize(rh_ctx* ctx, int kind, const float* x, size_t len, int8_t* quants, float* scales,

@@ -69,12 +69,145 @@ __device__ __forceinline__ const int8_t* swz(const int8_t* act_t, uint32_t b, ui
   return act_t + (b << 8) + ((((k >> 4) ^ (b & 15u))) << 4);
 }
 
+// Q8Kind::SuperBlock quantization (portable/q8.rs:64-98) of the first nq
+// 256-value blocks of T tokens (x[t * width + ...]) straight into the LDS
+// tiles the k-quant kernels read: quants swizzled as stage_quants_swizzled
+// lays them out, d8[t][b] the block's step, and per token
+//   FMT 12: side[t][8b + j]  = the sum of 32-block j's quants;
+//   FMT 14: side[t][16b + k] = -32 * the sum of 16-run k's quants.
+// A 32-lane half-wave owns one block, 8 values per lane; a round covers K
+// blocks per half-wave. The kernels load the first round before their weight
+// loads: vector memory returns in issue order, so x loaded after the weights
+// could not be quantized until every weight had arrived.
+// Each block is reduced with DPP: amax over the magnitudes (q8.rs:12-25; a
+// NaN never enters it), then the first value whose magnitude is amax
+// (q8.rs:26-32) as the minimum of (index, sign) keys -- every candidate is
+// +-amax, so its sign is all the index selects. The arithmetic after that is
+// quantize_super_kernel's, so the bits are the same.
+template <int K>
+struct XRound {
+  float f[K][8];
+};
+
+struct XGeom {
+  const float* x;  // token t0
+  size_t width;
+  uint32_t nq;     // blocks quantized per token: min(nb, width / 256)
+  uint32_t total;  // T * nq
+  bool aligned;    // 16-byte loads are legal
+};
+
+template <int T>
+__device__ __forceinline__ XGeom x_geom(const float* x, size_t width, uint32_t nb) {
+  XGeom g;
+  g.x = x;
+  g.width = width;
+  g.nq = width / 256u < nb ? static_cast<uint32_t>(width / 256u) : nb;
+  g.total = static_cast<uint32_t>(T) * g.nq;
+  g.aligned = ((reinterpret_cast<uintptr_t>(x) | (width * 4u)) & 15u) == 0;
+  return g;
+}
+
+template <int K>
+__device__ __forceinline__ void load_x_round(XRound<K>& xr, const XGeom& g, uint32_t u0) {
+  const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
+#pragma unroll
+  for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
+    const uint32_t u = u0 + hw + k * (kThreads / 32u);
+    if (u >= g.total) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) xr.f[k][i] = 0.0f;
+      continue;
+    }
+    const uint32_t t = u / g.nq, b = u - t * g.nq;
+    const float* v = g.x + t * g.width + static_cast<size_t>(b) * 256u + 8u * hl;
+    if (g.aligned) {
+      const u32x4 lo = load16(reinterpret_cast<const uint8_t*>(v));
+      const u32x4 hi = load16(reinterpret_cast<const uint8_t*>(v + 4));
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        xr.f[k][i] = __uint_as_float(lo[i]);
+        xr.f[k][4 + i] = __uint_as_float(hi[i]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; i++) xr.f[k][i] = v[i];
+    }
+  }
+}
+
+template <int FMT, int K>
+__device__ __forceinline__ void quantize_x_round(const XRound<K>& xr, const XGeom& g, uint32_t u0, uint32_t nb,
+                                                 int8_t* act, float* d8, int32_t* side) {
+  const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
+  const uint32_t abytes = nb * 256u;
+#pragma unroll
+  for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
+    const uint32_t u = u0 + hw + k * (kThreads / 32u);
+    if (u >= g.total) break;  // uniform over the half-wave
+    const uint32_t t = u / g.nq, b = u - t * g.nq;
+    const float* f = xr.f[k];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float m = __builtin_fabsf(f[i]);
+      amax = m > amax ? m : amax;
+    }
+    amax = __uint_as_float(half_max_u32(__float_as_uint(amax)));
+    uint32_t key = 0xffffffffu;
+#pragma unroll
+    for (int i = 7; i >= 0; i--)
+      if (__builtin_fabsf(f[i]) == amax) key = 2u * (8u * hl + static_cast<uint32_t>(i)) + (__float_as_uint(f[i]) >> 31);
+    key = half_min_u32(key);
+    const float max = key == 0xffffffffu ? 0.0f : ((key & 1u) ? -amax : amax);
+    const float inverse = (max == 0.0f) ? 0.0f : __fdiv_rn(-127.0f, max);
+    const float step = (max == 0.0f) ? 0.0f : __fdiv_rn(1.0f, inverse);
+    uint32_t packed[2] = {0u, 0u};
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float prod = f[i] * inverse;
+      const int32_t qv = round_to_i8(prod);
+      s += qv;
+      packed[i >> 2] |= (static_cast<uint32_t>(qv) & 0xffu) << (8 * (i & 3));
+    }
+    // byte 8*hl of block b: chunk hl/2, stored at chunk (hl/2) ^ (b & 15)
+    uint32_t* dst = reinterpret_cast<uint32_t*>(act + t * abytes + (b << 8) + (((hl >> 1) ^ (b & 15u)) << 4) +
+                                                8u * (hl & 1u));
+    dst[0] = packed[0];
+    dst[1] = packed[1];
+    const int32_t s16 = s + static_cast<int32_t>(dpp<0xB1>(static_cast<uint32_t>(s)));
+    const int32_t s32 = s16 + static_cast<int32_t>(dpp<0x4E>(static_cast<uint32_t>(s16)));
+    if (FMT == 12) {
+      if ((hl & 3u) == 0) side[t * nb * 8u + b * 8u + (hl >> 2)] = s32;
+    } else {
+      if ((hl & 1u) == 0) side[t * nb * 16u + b * 16u + (hl >> 1)] = -32 * s16;
+    }
+    if (hl == 0) d8[t * nb + b] = step;
+  }
+}
+
+// The rounds after the first (which the kernel quantizes from its preload).
+template <int FMT, int K>
+__device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int8_t* act, float* d8,
+                                                int32_t* side) {
+  for (uint32_t u0 = static_cast<uint32_t>(K) * (kThreads / 32u); u0 < g.total;
+       u0 += static_cast<uint32_t>(K) * (kThreads / 32u)) {
+    XRound<K> xr;
+    load_x_round<K>(xr, g, u0);
+    quantize_x_round<FMT, K>(xr, g, u0, nb, act, d8, side);
+  }
+}
+
 // Q4_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
 //      terms [R][nbmax][T] f32
-template <int T, int NI>
-__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
-                                                       uint32_t nbmax, size_t tokens, size_t t0) {
+// FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
+// preloading FQ blocks per half-wave before the weights.
+template <int T, int NI, int FQ>
+__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
+                                                       size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
+                                                       size_t t0) {
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t abytes = nbmax * 256u;
   int8_t* act = reinterpret_cast<int8_t*>(lds);
@@ -91,6 +224,9 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
 
   // g = r*nb + b with g < 4*64: a float reciprocal divides exactly here
   const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
+  const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
+  XRound<FQ ? FQ : 1> xr;
+  if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
   u32x4 hd[NI], c0[NI], c1[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
@@ -104,12 +240,17 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
     c1[i] = load16(blk + 80u + 16u * p);
   }
 
-  stage_quants_swizzled<T>(act, abytes, q, t0);
-  for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += kThreads) {
-    const uint32_t t = i / (nbmax * 8u), k = i - t * nbmax * 8u;
-    const size_t src = (t0 + t) * q.bstride + k;
-    sums[i] = q.sums[src];
-    if ((k & 7u) == 0) d8[t * nbmax + k / 8u] = q.scales[src];
+  if (FQ) {
+    quantize_x_round<12, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, sums);
+    quantize_x_rest<12, FQ ? FQ : 1>(xg, nbmax, act, d8, sums);
+  } else {
+    stage_quants_swizzled<T>(act, abytes, q, t0);
+    for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += kThreads) {
+      const uint32_t t = i / (nbmax * 8u), k = i - t * nbmax * 8u;
+      const size_t src = (t0 + t) * q.bstride + k;
+      sums[i] = q.sums[src];
+      if ((k & 7u) == 0) d8[t * nbmax + k / 8u] = q.scales[src];
+    }
   }
   __syncthreads();
 
@@ -181,9 +322,12 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, u
 // Q6_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | bias [T][nbmax*16] i32
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
-template <int T, int NI>
-__global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, uint32_t R,
-                                                       uint32_t nbmax, size_t tokens, size_t t0) {
+// FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
+// preloading FQ blocks per half-wave before the weights.
+template <int T, int NI, int FQ>
+__global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
+                                                       size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
+                                                       size_t t0) {
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t abytes = nbmax * 256u;
   int8_t* act = reinterpret_cast<int8_t*>(lds);
@@ -204,6 +348,9 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
   // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; W: scales at
   // 192; E: the fifth dwords of A, B, C and the dword holding d (q6_k.rs:13-43).
   const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
+  const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
+  XRound<FQ ? FQ : 1> xr;
+  if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
   u32x4 A[NI], B[NI], C[NI], W[NI], E[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
@@ -219,11 +366,16 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, u
                  load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
   }
 
-  stage_quants_swizzled<T>(act, abytes, q, t0);
-  for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += kThreads) {
-    const uint32_t t = i / (nbmax * 16u), k = i - t * nbmax * 16u;
-    bias[i] = -32 * q.sums16[2u * (t0 + t) * q.bstride + k];
-    if ((k & 15u) == 0) d8[t * nbmax + k / 16u] = q.scales[(t0 + t) * q.bstride + k / 2u];
+  if (FQ) {
+    quantize_x_round<14, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, bias);
+    quantize_x_rest<14, FQ ? FQ : 1>(xg, nbmax, act, d8, bias);
+  } else {
+    stage_quants_swizzled<T>(act, abytes, q, t0);
+    for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += kThreads) {
+      const uint32_t t = i / (nbmax * 16u), k = i - t * nbmax * 16u;
+      bias[i] = -32 * q.sums16[2u * (t0 + t) * q.bstride + k];
+      if ((k & 15u) == 0) d8[t * nbmax + k / 16u] = q.scales[(t0 + t) * q.bstride + k / 2u];
+    }
   }
   __syncthreads();
 
@@ -383,6 +535,224 @@ __global__ __launch_bounds__(256) void gemv_i2s_kernel(GemvJobs jobs, Q8Dev q, u
   }
 }
 
+// I2_S x I8_S, fused -------------------------------------------------------
+// The workgroup quantizes its tokens itself (Q8Kind::Row, portable/q8.rs:38-49,
+// 99-105, the arithmetic of quantize_row_kernel). Each lane keeps 4
+// consecutive values of every 1024 in registers, loaded for the first token
+// before the weights. One workgroup reduction
+// gives the row's last NaN and its largest magnitude; without a NaN (the
+// usual case) that fixes the divisor, and only a row with a NaN needs a
+// second reduction, of the magnitudes after that NaN. The quants of the first
+// nkeep values then go to LDS with one sum per 32.
+constexpr uint32_t kFusedRowPasses = 8;  // rows of up to 8192 values
+
+// Workgroup maxima of (p, m) over its 4 waves; `slot` alternates between
+// calls so that one barrier per reduction suffices.
+__device__ __forceinline__ void wg_max_pair(int32_t& p, uint32_t& m, int32_t* red, uint32_t slot) {
+  p = half_max_i32(p);
+  m = half_max_u32(m);
+  p = max(__builtin_amdgcn_readlane(p, 0), __builtin_amdgcn_readlane(p, 32));
+  m = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 0)),
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 32)));
+  int32_t* r = red + slot * 2u * (kThreads / 64u);
+  if ((threadIdx.x & 63u) == 0) {
+    r[threadIdx.x >> 6] = p;
+    r[(kThreads / 64u) + (threadIdx.x >> 6)] = static_cast<int32_t>(m);
+  }
+  __syncthreads();
+  p = r[0];
+  m = static_cast<uint32_t>(r[kThreads / 64u]);
+  for (uint32_t w = 1; w < kThreads / 64u; w++) {
+    p = max(p, r[w]);
+    m = max(m, static_cast<uint32_t>(r[(kThreads / 64u) + w]));
+  }
+}
+
+struct RowX {
+  float f[kFusedRowPasses][4];
+};
+
+// Token t's values into registers: 4 consecutive values of every 1024.
+__device__ __forceinline__ void load_row_x(RowX& r, const float* __restrict__ v, uint32_t n, bool aligned) {
+#pragma unroll
+  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+    const uint32_t e = 4u * threadIdx.x + 4u * kThreads * k;  // n is a multiple of 32
+    if (e < n && aligned) {
+      const u32x4 q4 = load16(reinterpret_cast<const uint8_t*>(v + e));
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) r.f[k][i] = __uint_as_float(q4[i]);
+    } else {
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) r.f[k][i] = e < n ? v[e + i] : 0.0f;
+    }
+  }
+}
+
+// Token t from its registers into the LDS tiles; `slot` alternates the
+// reduction scratch between calls.
+__device__ __forceinline__ void quantize_row_regs(const RowX& r, uint32_t t, uint32_t n, uint32_t nkeep,
+                                                  int8_t* act, int32_t* qs32, float* divisor, int32_t* red,
+                                                  uint32_t& slot) {
+  const uint32_t lane = threadIdx.x & 63u;
+  int32_t last_nan = -1;
+  float all_max = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k < kFusedRowPasses; k++)
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) {
+      const uint32_t e = 4u * threadIdx.x + 4u * kThreads * k + i;
+      const float m = __builtin_fabsf(r.f[k][i]);
+      if (e < n && r.f[k][i] != r.f[k][i]) last_nan = static_cast<int32_t>(e);
+      all_max = m > all_max ? m : all_max;  // NaN never enters
+    }
+  int32_t p = last_nan;
+  uint32_t mb = __float_as_uint(all_max);
+  wg_max_pair(p, mb, red, slot);
+  slot ^= 1u;
+  // C's MAX from 1e-5 in f64: a NaN restarts the maximum at the next value
+  // (without the floor); a trailing NaN leaves it NaN
+  double mx;
+  if (p < 0) {
+    mx = static_cast<double>(__uint_as_float(mb));
+    mx = 1e-5 > mx ? 1e-5 : mx;
+  } else {
+    float after = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < kFusedRowPasses; k++)
+#pragma unroll
+      for (uint32_t i = 0; i < 4; i++) {
+        const uint32_t e = 4u * threadIdx.x + 4u * kThreads * k + i;
+        const float m = __builtin_fabsf(r.f[k][i]);
+        if (e < n && static_cast<int32_t>(e) > p) after = m > after ? m : after;
+      }
+    int32_t unused = -1;
+    uint32_t ab = __float_as_uint(after);
+    wg_max_pair(unused, ab, red, slot);
+    slot ^= 1u;
+    mx = p == static_cast<int32_t>(n) - 1 ? __builtin_nan("") : static_cast<double>(__uint_as_float(ab));
+  }
+  const float div = static_cast<float>(127.0 / mx);
+#pragma unroll
+  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+    const uint32_t base = 4u * threadIdx.x + 4u * kThreads * k;
+    int32_t qv[4];
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float prod = r.f[k][i] * div;
+      qv[i] = round_row_to_i8(prod);
+      s += qv[i];
+    }
+    // a 32-block is 8 lanes of 4 values
+    int32_t s32 = s + static_cast<int32_t>(dpp<0xB1>(static_cast<uint32_t>(s)));
+    s32 += static_cast<int32_t>(dpp<0x4E>(static_cast<uint32_t>(s32)));
+    s32 += static_cast<int32_t>(dpp<0x141>(static_cast<uint32_t>(s32)));
+    if (base < nkeep) {
+      *reinterpret_cast<uint32_t*>(act + t * nkeep + base) =
+          (static_cast<uint32_t>(qv[0]) & 0xffu) | ((static_cast<uint32_t>(qv[1]) & 0xffu) << 8) |
+          ((static_cast<uint32_t>(qv[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qv[3]) << 24);
+      if ((lane & 7u) == 0) qs32[t * (nkeep / 32u) + base / 32u] = s32;
+    }
+  }
+  if (threadIdx.x == 0) divisor[t] = div;
+}
+
+// LDS: act [T][nbmax*128] i8 | qs32 [T][nbmax*4] i32 | divisor [T] f32 |
+// reduction scratch. A team of lpr lanes (a power of two) owns a row; lane l
+// holds chunks l, l + lpr, ... (CPL of them) of 16 bytes, loaded before the
+// activation is quantized.
+template <int T, int CPL>
+__global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, const float* __restrict__ x,
+                                                             size_t width, uint32_t nq, uint32_t nbmax,
+                                                             uint32_t lpr, size_t tokens, size_t t0,
+                                                             int32_t* raw) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  const uint32_t nkeep = nbmax * 128u;
+  int8_t* act = reinterpret_cast<int8_t*>(lds);
+  int32_t* qs32 = reinterpret_cast<int32_t*>(lds + T * nkeep);
+  float* divisor = reinterpret_cast<float*>(qs32 + T * nbmax * 4u);
+  int32_t* red = reinterpret_cast<int32_t*>(divisor + T);  // [2 slots][2][waves]
+
+  const GemvJob& J = jobs.j[find_job(jobs)];
+  const uint32_t R = kThreads / lpr;
+  const uint32_t r = threadIdx.x / lpr, cl = threadIdx.x & (lpr - 1u);
+  const uint32_t row = (blockIdx.x - J.wg_begin) * R + r;
+  const bool live = row < J.rows;
+  const uint32_t nchunk = 2u * J.nb;
+  // token t0's values first: loads return in issue order (see load_x_round)
+  const float* xt = x + t0 * width;
+  const uint32_t n = nq * 32u;
+  const bool aligned = ((reinterpret_cast<uintptr_t>(xt) | (width * 4u)) & 15u) == 0;
+  RowX rx;
+  load_row_x(rx, xt, n, aligned);
+  u32x4 w[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = cl + static_cast<uint32_t>(i) * lpr;
+    w[i] = (live && c < nchunk) ? load16(J.w + __umul24(row, static_cast<uint32_t>(J.stride)) + 16u * c)
+                                : u32x4{0, 0, 0, 0};
+  }
+
+  uint32_t slot = 0;
+  quantize_row_regs(rx, 0u, n, nkeep, act, qs32, divisor, red, slot);
+  for (uint32_t t = 1; t < static_cast<uint32_t>(T); t++) {
+    load_row_x(rx, xt + t * width, n, aligned);
+    quantize_row_regs(rx, t, n, nkeep, act, qs32, divisor, red, slot);
+  }
+  __syncthreads();
+
+  uint32_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = cl + static_cast<uint32_t>(i) * lpr;
+    if (c >= nchunk) break;
+    uint32_t c6[4], c4[4], c2[4], c0[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      c6[k] = (w[i][k] >> 2) & 0x30303030u;  // code of shift 6, times 16
+      c4[k] = w[i][k] & 0x30303030u;         // shift 4, times 16
+      c2[k] = w[i][k] & 0x0C0C0C0Cu;         // shift 2, times 4
+      c0[k] = w[i][k] & 0x03030303u;         // shift 0
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const int8_t* a = act + t * nkeep + 128u * (c >> 1) + 16u * (c & 1u);
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+      int32_t P16 = 0, P4 = 0, P1 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        P16 = dot4(c6[k], a0[k], P16);
+        P16 = dot4(c4[k], a1[k], P16);
+        P4 = dot4(c2[k], a2[k], P4);
+        P1 = dot4(c0[k], a3[k], P1);
+      }
+      acc[t] += static_cast<uint32_t>(P1 + (P4 >> 2) + (P16 >> 4));
+    }
+  }
+  // ternary.rs:39,41: minus the sum of the quants of the row's blocks (wrapping)
+#pragma unroll
+  for (int t = 0; t < T; t++)
+    for (uint32_t k = cl; k < 4u * J.nb; k += lpr) acc[t] -= static_cast<uint32_t>(qs32[t * nbmax * 4u + k]);
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    uint32_t v = acc[t];
+    for (uint32_t off = lpr >> 1; off > 0; off >>= 1)
+      v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), static_cast<int>(off), 64));
+    const size_t idx = static_cast<size_t>(row) * tokens + t0 + t;
+    if (cl == 0 && live && idx < J.out_len) {
+      const int32_t dot = static_cast<int32_t>(v);
+      if (raw) raw[idx] = dot;
+      // ternary.rs:53-57: (dot as f32) / s * scale; 0 without a scale
+      else J.out[idx] = nq ? __fdiv_rn(static_cast<float>(dot), divisor[t]) * J.scale : 0.0f;
+    }
+  }
+}
+
 // Dense f32 ---------------------------------------------------------------
 // rusticide-simd/src/float.rs:23-36: eight fused lanes over the whole chunks,
 // the lanes added in order from -0.0, then the unfused tail (from -0.0).
@@ -480,12 +850,10 @@ size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
   return 0;
 }
 
-// Blocks per 4-lane team in the k-quant kernels (1, 2 or 4), set per launch
-// by launch_t: the smallest that lets every workgroup of the grid be resident
-// at once, so no rows wait for a second generation of workgroups.
+// Blocks per 4-lane team in the k-quant kernels (1, 2 or 4), chosen per
+// launch: the smallest that lets every workgroup of the grid be resident at
+// once, so no rows wait for a second generation of workgroups.
 // RUSTICIDE_HIP_GEMV_NI=1|2|4 forces it, for tuning.
-thread_local uint32_t g_blocks_per_team = 1u;
-
 uint32_t forced_blocks_per_team() {
   if (const char* v = std::getenv("RUSTICIDE_HIP_GEMV_NI")) {
     if (v[0] == '1') return 1u;
@@ -495,60 +863,88 @@ uint32_t forced_blocks_per_team() {
   return 0u;
 }
 
-uint32_t blocks_per_team(uint32_t type_id) {
-  (void)type_id;
-  return g_blocks_per_team;
+// Rows per workgroup: one per 8-lane team for I2_S and dense rows; for the
+// k-quants, whole rows of nb blocks over 64 teams of ni blocks each.
+uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
+  if (type_id == 36u || type_id == 0u) return 32u;
+  const uint32_t R = ni * (kThreads / 4u) / nb;
+  return R < 1u ? 1u : R;
 }
 
-uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t total_rows) {
-  if (type_id == 36u || type_id == 0u) return 32u;  // one row per 8-lane team
-  // whole rows of at most NI blocks per 4-lane team
-  uint32_t R = blocks_per_team(type_id) * (kThreads / 4u) / nb;
-  if (R < 1u) R = 1u;
-  (void)total_rows;
-  return R;
+template <int FMT, int T, int NI, int FQ>
+void* kq_kernel() {
+  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ>)
+                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ>);
 }
 
-template <int T, int NI>
-int resident_wgs_per_cu(uint32_t type_id, size_t lds) {
-  // measured once per kernel and LDS size bucket (1 KiB)
-  static int cache[2][64] = {};
-  const size_t bucket = lds / 1024u < 63u ? lds / 1024u : 63u;
-  int& c = cache[type_id == 12u ? 0 : 1][bucket];
-  if (c == 0) {
-    int n = 0;
-    const hipError_t e = type_id == 12u
-        ? hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_q4k_kernel<T, NI>, kThreads, (bucket + 1u) * 1024u)
-        : hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, gemv_q6k_kernel<T, NI>, kThreads, (bucket + 1u) * 1024u);
-    c = (e == hipSuccess && n > 0) ? n : 1;
+template <int FMT, int T, int FQ>
+void* kq_kernel_ni(uint32_t ni) {
+  return ni == 4u ? kq_kernel<FMT, T, 4, FQ>() : ni == 2u ? kq_kernel<FMT, T, 2, FQ>() : kq_kernel<FMT, T, 1, FQ>();
+}
+
+// fq: 0 (a separately quantized activation), 1 or 4 (fused, preload depth)
+template <int T>
+void* kq_kernel_for(uint32_t type_id, uint32_t ni, uint32_t fq) {
+  if (fq == 0u) return type_id == 12u ? kq_kernel_ni<12, T, 0>(ni) : kq_kernel_ni<14, T, 0>(ni);
+  if (fq == 1u) return type_id == 12u ? kq_kernel_ni<12, T, 1>(ni) : kq_kernel_ni<14, T, 1>(ni);
+  return type_id == 12u ? kq_kernel_ni<12, T, 4>(ni) : kq_kernel_ni<14, T, 4>(ni);
+}
+
+// Resident workgroups per CU of one kernel at an LDS size (1 KiB buckets).
+int resident_wgs_per_cu(const void* kernel, size_t lds) {
+  struct Entry {
+    const void* k;
+    size_t bucket;
+    int n;
+  };
+  static thread_local Entry cache[64];
+  static thread_local int used = 0;
+  const size_t bucket = lds / 1024u;
+  for (int i = 0; i < used; i++)
+    if (cache[i].k == kernel && cache[i].bucket == bucket) return cache[i].n;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kThreads, (bucket + 1u) * 1024u) != hipSuccess ||
+      n < 1)
+    n = 1;
+  if (used < 64) cache[used++] = Entry{kernel, bucket, n};
+  return n;
+}
+
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    cus = (hipGetDevice(&dev) == hipSuccess &&
+           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+              ? n
+              : 256;
   }
-  return c;
+  return cus;
+}
+
+// The 64 teams of a workgroup cover at most 64 * NI blocks: a row of nb
+// blocks needs NI >= nb / 64.
+uint32_t min_blocks_per_team(uint32_t nb) {
+  return nb <= 64u ? 1u : nb <= 128u ? 2u : 4u;
 }
 
 template <int T>
-uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_rows) {
-  if (const uint32_t forced = forced_blocks_per_team()) return forced;
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
-      cus = 256;
-  }
+uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_rows, uint32_t fq) {
+  const uint32_t floor_ni = min_blocks_per_team(nb);
+  if (const uint32_t forced = forced_blocks_per_team()) return forced > floor_ni ? forced : floor_ni;
   for (uint32_t ni : {1u, 2u, 4u}) {
-    g_blocks_per_team = ni;
-    const uint32_t R = rows_per_wg(type_id, nb, total_rows);
+    if (ni < floor_ni) continue;
+    const uint32_t R = rows_per_wg(type_id, nb, ni);
     const uint32_t wgs = (total_rows + R - 1u) / R;
-    const size_t lds = lds_bytes<T>(type_id, nb, R);
-    const int per_cu = ni == 1u ? resident_wgs_per_cu<T, 1>(type_id, lds)
-                     : ni == 2u ? resident_wgs_per_cu<T, 2>(type_id, lds)
-                                : resident_wgs_per_cu<T, 4>(type_id, lds);
-    if (wgs <= static_cast<uint32_t>(per_cu * cus)) return ni;
+    const int per_cu = resident_wgs_per_cu(kq_kernel_for<T>(type_id, ni, fq), lds_bytes<T>(type_id, nb, R));
+    if (wgs <= static_cast<uint32_t>(per_cu * device_cus())) return ni;
   }
   return 4u;
 }
 
-template <int T>
+// One grouped launch. FUSED: the k-quant kernels quantize x themselves
+// (T <= kMaxFusedTokens); otherwise they read the activation q holds.
+template <int T, bool FUSED>
 hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float* x, size_t width,
                     size_t tokens, size_t t0, hipStream_t s, int32_t* raw) {
   uint32_t nbmax = 0, total_rows = 0;
@@ -559,8 +955,15 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
   // Rows whose blocks the input does not reach still get an output (-0.0 for
   // the k-quants, as an empty f32 sum); size everything for at least one block.
   const uint32_t nbl = nbmax ? nbmax : 1u;
-  if (type_id == 12u || type_id == 14u) g_blocks_per_team = choose_blocks_per_team<T>(type_id, nbl, total_rows);
-  const uint32_t R = rows_per_wg(type_id, nbl, total_rows);
+  const bool kquant = type_id == 12u || type_id == 14u;
+  // fused: preload every block of a one-round activation, else 4 per half-wave
+  uint32_t fq = 0u;
+  if (FUSED) {
+    const size_t nq = width / 256u < nbmax ? width / 256u : nbmax;
+    fq = static_cast<size_t>(T) * nq <= kThreads / 32u ? 1u : 4u;
+  }
+  const uint32_t ni = kquant ? choose_blocks_per_team<T>(type_id, nbl, total_rows, fq) : 1u;
+  const uint32_t R = rows_per_wg(type_id, nbl, ni);
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     jobs.j[i].wg_begin = wgs;
@@ -573,19 +976,15 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     return hipGetLastError();
   }
   const size_t lds = lds_bytes<T>(type_id, nbl, R);
-  const uint32_t ni = blocks_per_team(type_id);
-  if (type_id == 12u) {
-    if (ni == 4u) hipLaunchKernelGGL((gemv_q4k_kernel<T, 4>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
-    else if (ni == 2u) hipLaunchKernelGGL((gemv_q4k_kernel<T, 2>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
-    else hipLaunchKernelGGL((gemv_q4k_kernel<T, 1>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
-  } else if (type_id == 14u) {
-    if (ni == 4u) hipLaunchKernelGGL((gemv_q6k_kernel<T, 4>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
-    else if (ni == 2u) hipLaunchKernelGGL((gemv_q6k_kernel<T, 2>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
-    else hipLaunchKernelGGL((gemv_q6k_kernel<T, 1>), dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0);
+  if (kquant) {
+    // the fused kernels quantize blocks [0, nbmax) of x, which width covers
+    const float* xin = FUSED ? x : nullptr;
+    void* k = kq_kernel_for<T>(type_id, ni, fq);
+    void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
+                    const_cast<uint32_t*>(&nbl), &tokens, &t0};
+    return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
   }
-  else
-    hipLaunchKernelGGL(gemv_i2s_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0,
-                       raw);
+  hipLaunchKernelGGL(gemv_i2s_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0, raw);
   return hipGetLastError();
 }
 
@@ -594,10 +993,8 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
 size_t gemv_max_tokens(uint32_t type_id, uint32_t nb) {
   // LDS per workgroup stays within 64 KiB at the largest tile (NI = 4)
   const uint32_t nbl = nb ? nb : 1u;
-  const uint32_t saved = g_blocks_per_team;
-  g_blocks_per_team = 4u;
-  const uint32_t R = rows_per_wg(type_id, nbl, 0);
-  g_blocks_per_team = saved;
+  if ((type_id == 12u || type_id == 14u) && nbl > 4u * (kThreads / 4u)) return 0;
+  const uint32_t R = rows_per_wg(type_id, nbl, 4u);
   size_t t = kMaxTokens;
   while (t > 1) {
     size_t need = 0;
@@ -620,14 +1017,70 @@ hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, c
                        size_t width, size_t tokens, size_t t0, size_t tn, hipStream_t s,
                        int32_t* raw) {
   switch (tn) {
-    case 1: return launch_t<1>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 2: return launch_t<2>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 3: return launch_t<3>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 4: return launch_t<4>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 5: return launch_t<5>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 6: return launch_t<6>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 7: return launch_t<7>(type_id, jobs, q, x, width, tokens, t0, s, raw);
-    case 8: return launch_t<8>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 1: return launch_t<1, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 2: return launch_t<2, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 3: return launch_t<3, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 4: return launch_t<4, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 5: return launch_t<5, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 6: return launch_t<6, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 7: return launch_t<7, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    case 8: return launch_t<8, false>(type_id, jobs, q, x, width, tokens, t0, s, raw);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+bool gemv_fused_ok(uint32_t type_id, size_t width, size_t tn) {
+  if (type_id == 12u || type_id == 14u) return tn >= 1 && tn <= kMaxFusedTokens;
+  if (type_id == 36u) return tn >= 1 && tn <= 2 && width / 32u * 32u <= 4u * kThreads * kFusedRowPasses;
+  return false;
+}
+
+namespace {
+
+template <int T>
+hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t tokens, size_t t0,
+                            hipStream_t s, int32_t* raw) {
+  uint32_t nbmax = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) nbmax = jobs.j[i].nb > nbmax ? jobs.j[i].nb : nbmax;
+  const uint32_t nbl = nbmax ? nbmax : 1u;
+  const uint32_t nq = static_cast<uint32_t>(width / 32u);
+  // two chunks per lane at most: nbl <= 64 (8192 values) gives lpr <= 64
+  const uint32_t nchunk = 2u * nbl;
+  uint32_t lpr = 8u;
+  while (lpr < 64u && 2u * lpr < nchunk) lpr <<= 1;
+  const uint32_t cpl = (nchunk + lpr - 1u) / lpr;
+  if (cpl > 2u) return hipErrorInvalidValue;
+  const uint32_t R = kThreads / lpr;
+  uint32_t wgs = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    jobs.j[i].wg_begin = wgs;
+    wgs += (jobs.j[i].rows + R - 1u) / R;
+  }
+  if (wgs == 0) return hipSuccess;
+  const size_t lds = T * nbl * 128u + T * nbl * 16u + T * 4u + 4u * (kThreads / 64u) * 4u;
+  if (cpl == 1u)
+    hipLaunchKernelGGL((gemv_i2s_fused_kernel<T, 1>), dim3(wgs), dim3(kThreads), lds, s, jobs, x, width, nq, nbl,
+                       lpr, tokens, t0, raw);
+  else
+    hipLaunchKernelGGL((gemv_i2s_fused_kernel<T, 2>), dim3(wgs), dim3(kThreads), lds, s, jobs, x, width, nq, nbl,
+                       lpr, tokens, t0, raw);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float* x, size_t width,
+                             size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw) {
+  if (!gemv_fused_ok(type_id, width, tn)) return hipErrorInvalidValue;
+  if (type_id == 36u)
+    return tn == 1 ? launch_i2s_fused<1>(jobs, x, width, tokens, t0, s, raw)
+                   : launch_i2s_fused<2>(jobs, x, width, tokens, t0, s, raw);
+  const Q8Dev none{};
+  switch (tn) {
+    case 1: return launch_t<1, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr);
+    case 2: return launch_t<2, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr);
+    case 3: return launch_t<3, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr);
+    case 4: return launch_t<4, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr);
     default: return hipErrorInvalidValue;
   }
 }

@@ -308,7 +308,8 @@ hipError_t launch_kq(GemvJobs jobs, const Q8Dev& q, uint32_t nbmax, size_t token
 }  // namespace
 
 size_t gemv_kq_max_tokens(uint32_t nb) {
-  if (nb == 0) return 0;
+  // a tile's teams cover kNI * kTeams blocks: wider rows go to the LDS kernels
+  if (nb == 0 || nb > static_cast<uint32_t>(kNI) * kTeams) return 0;
   for (uint32_t t = 4; t >= 1; t--)
     if (kq_lds_bytes(t, nb, kq_rows(nb)) <= 64u * 1024u) return t;
   return 0;

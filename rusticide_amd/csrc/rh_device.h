@@ -67,6 +67,39 @@ __device__ __forceinline__ int32_t quad_sum(int32_t v) {
   return v;
 }
 
+// One DPP lane permutation of v (every source lane is valid for the
+// patterns used here: quad_perm, row_half_mirror, row_mirror).
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp(uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(v), static_cast<int>(v), CTRL, 0xF, 0xF, false));
+}
+
+// Maximum / minimum over each aligned group of 32 lanes, left in every lane:
+// xor 1 and 2 (quad_perm), the 8-lane and 16-lane mirrors, then xor 16
+// (ds_swizzle in bit mode). Unsigned; non-negative floats compare as their bits.
+__device__ __forceinline__ uint32_t half_max_u32(uint32_t v) {
+  v = max(v, dpp<0xB1>(v));
+  v = max(v, dpp<0x4E>(v));
+  v = max(v, dpp<0x141>(v));
+  v = max(v, dpp<0x140>(v));
+  return max(v, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F)));
+}
+__device__ __forceinline__ uint32_t half_min_u32(uint32_t v) {
+  v = min(v, dpp<0xB1>(v));
+  v = min(v, dpp<0x4E>(v));
+  v = min(v, dpp<0x141>(v));
+  v = min(v, dpp<0x140>(v));
+  return min(v, static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F)));
+}
+__device__ __forceinline__ int32_t half_max_i32(int32_t v) {
+  v = max(v, static_cast<int32_t>(dpp<0xB1>(static_cast<uint32_t>(v))));
+  v = max(v, static_cast<int32_t>(dpp<0x4E>(static_cast<uint32_t>(v))));
+  v = max(v, static_cast<int32_t>(dpp<0x141>(static_cast<uint32_t>(v))));
+  v = max(v, static_cast<int32_t>(dpp<0x140>(static_cast<uint32_t>(v))));
+  return max(v, __builtin_amdgcn_ds_swizzle(v, 0x401F));
+}
+
 // Sum over aligned groups of 8 lanes; exact (wrapping) for integers.
 __device__ __forceinline__ uint32_t octet_sum(uint32_t v) {
   v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), 1, 64));

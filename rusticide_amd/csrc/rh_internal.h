@@ -10,6 +10,7 @@ namespace rh {
 
 constexpr int kMaxJobs = 8;       // matrices one GEMV launch can serve
 constexpr int kMaxTokens = 8;     // tokens one GEMV launch can serve
+constexpr size_t kMaxFusedTokens = 4;  // tokens a quantize-fused k-quant launch serves
 constexpr size_t kPad = 256;      // bytes of slack after every device matrix
 
 // The quantized activations of one batch on the device, laid out per token:
@@ -54,6 +55,13 @@ hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, c
                        size_t width, size_t tokens, size_t t0, size_t tn, hipStream_t s,
                        int32_t* raw_i32);
 size_t gemv_max_tokens(uint32_t type_id, uint32_t nb);
+// Single-launch decode GEMV: every workgroup quantizes the f32 activation of
+// its tokens into LDS itself (the same arithmetic as the quantize kernels).
+// gemv_fused_ok says whether a launch of tn tokens of `width` values fits it
+// (k-quants: tn <= kMaxFusedTokens; I2_S: tn <= 2, width <= 8192).
+bool gemv_fused_ok(uint32_t type_id, size_t width, size_t tn);
+hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float* x, size_t width,
+                             size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw);
 // Streaming decode GEMV for one or two tokens; false when the launch's shape
 // is outside what it handles (the caller then uses launch_gemv).
 bool launch_gemv_stream(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0,

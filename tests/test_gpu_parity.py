@@ -119,6 +119,8 @@ KQ_SHAPES = [
     (12, 11, 256, [1, 2]),      # one block per row: 16 rows per wave
     (14, 2048, 5632, [1, 3]),   # Q6_K ffn_down: 4620-byte rows, padded stride
     (14, 45, 768, [1, 2, 9]),
+    (12, 40, 25600, [1, 2]),    # 100 blocks per row: two blocks per team
+    (14, 24, 38400, [1, 2]),    # 150 blocks per row: four blocks per team
 ]
 
 
@@ -303,6 +305,10 @@ def test_load_errors_mirror_model_error(ctx):
     with pytest.raises(R.RusticideError) as e:
         R.Matrix.load(ctx, 2, np.zeros(18, np.uint8), 1, 32)
     assert e.value.kind == "MISSING_KERNEL"
+    # the kernels' 24-bit row / 32-bit offset addressing is checked at load
+    with pytest.raises(R.RusticideError) as e:
+        R.Matrix.load(ctx, 12, np.zeros(144, np.uint8), 1 << 24, 256)
+    assert e.value.kind == "SHAPE_MISMATCH" and "4 GiB" in str(e.value)
 
 
 # --------------------------------------------------------------- copy_row
