@@ -928,10 +928,15 @@ uint32_t min_blocks_per_team(uint32_t nb) {
   return nb <= 64u ? 1u : nb <= 128u ? 2u : 4u;
 }
 
+// The fused kernels take four blocks per team: measured on MI355X at the
+// TinyLlama / BitNet decode shapes, NI = 4 is the fastest or within 1%
+// everywhere (fewer, longer-lived workgroups amortize the quantize prologue).
+// The others take the smallest NI that keeps every workgroup resident.
 template <int T>
 uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_rows, uint32_t fq) {
   const uint32_t floor_ni = min_blocks_per_team(nb);
   if (const uint32_t forced = forced_blocks_per_team()) return forced > floor_ni ? forced : floor_ni;
+  if (fq) return 4u;
   for (uint32_t ni : {1u, 2u, 4u}) {
     if (ni < floor_ni) continue;
     const uint32_t R = rows_per_wg(type_id, nb, ni);
