@@ -26,7 +26,6 @@ struct rh_ctx {
   void* buf[8] = {};
   size_t cap[8] = {};
   Q8Dev super_q, row_q;
-  size_t gemm_min_tokens = SIZE_MAX;
 };
 
 struct rh_matrix {
@@ -54,7 +53,8 @@ namespace {
 
 enum Scratch { kIn = 0, kOut, kQuants, kScales, kSums, kSums16, kRaw, kRowQ };
 
-size_t g_gemm_min_tokens = SIZE_MAX;
+// Batches of this many tokens or more run the k-quants on the MFMA GEMM.
+size_t g_gemm_min_tokens = 9;
 
 rh_status fail(rh_ctx* ctx, rh_status st, const std::string& msg) {
   if (ctx) ctx->last_error = msg;
@@ -170,6 +170,13 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
     uint32_t nbmax = 0;
     auto flush = [&]() -> rh_status {
       if (g.n == 0) return RH_OK;
+      const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
+      if (is_kquant(kind) && tokens >= g_gemm_min_tokens) {
+        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, s));
+        g = GemvJobs{};
+        nbmax = 0;
+        return RH_OK;
+      }
       size_t tmax = kMaxTokens;
       if (kind != RH_TYPE_F32) tmax = gemv_max_tokens(kind, nbmax);
       if (tmax == 0) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "rows too wide for the GEMV kernels");
@@ -179,7 +186,6 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
         nbmax = 0;
         return RH_OK;
       }
-      const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
       const Family fam = kind == RH_TYPE_F32 ? Family::kLds : family(kind);
       if (fam == Family::kStream && tokens <= 2) {
         hipError_t e = hipSuccess;
@@ -262,6 +268,7 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
     const uint32_t kind = kinds[k];
     const unsigned bit = format_bit(kind);
     if (!(present & bit) || family(kind) != Family::kFused || !gemv_fused_ok(kind, width, tokens)) continue;
+    if (kind != RH_TYPE_I2_S && tokens >= g_gemm_min_tokens) continue;
     if (tokens > gemv_max_tokens(kind, nbmax[bit >> 1])) continue;
     fused |= bit;
   }

@@ -1,0 +1,394 @@
+// gemm.hip -- prefill GEMM on gfx950 matrix cores: Q4_K / Q6_K weights in
+// their native GGUF blocks against Q8_K-quantized activations of many tokens,
+// bit-identical to rusticide's CPU integer path.
+//
+// The CPU path (crates/rusticide-kernels/src/portable/int_dot.rs:142-204)
+// forms, per 256-weight super-block b of row r and token t, exact integers
+//   Q4_K: isum = sum_j sc_j * sum_l q*a, msum = sum_j m_j * bsum_j
+//   Q6_K: isum = sum_s sc_s * sum_l (q-32)*a
+// and one float term per block, added in block order. Here the integers come
+// from int8 MFMA (v_mfma_i32_32x32x32_i8), exact in i32:
+//   * the sub-block scale is folded into the weight, w = sc*q (Q4_K: 0..945;
+//     Q6_K: sc*(q-32), -4096..4064), split into two int8 planes w = 128*hi +
+//     lo (lo in 0..127). One accumulator takes the hi plane over the block's
+//     eight 32-deep steps, is shifted left by 7, then takes the lo plane:
+//     it ends holding isum;
+//   * the Q4_K min term needs only the block sums: with bsum = 128*bh + bl
+//     (bl in 0..127), msum = 128 * sum_j m_j*bh_j + sum_j m_j*bl_j, two MFMAs
+//     whose 32-deep operands carry the eight (m_j, bl_j) / (m_j, bh_j) pairs
+//     in one lane group and zeros elsewhere. Each lane gives A and B the same
+//     k for the same byte, so the order MFMA sums k in does not matter.
+// The float combine is the CPU path's, per block, in block order, one
+// accumulator per (row, token) in one lane.
+//
+// Tiles: a workgroup of 4 waves owns 64 rows x BN tokens; wave w computes rows
+// 32*(w&1).. and tokens (w>>1)*BN/2.. as BN/64 32x32 MFMA tiles. Per block:
+// weights are dequantized into LDS planes once per workgroup, the block's
+// activation tile and block-sum bytes are copied in, and the next block's raw
+// bytes are already in flight in registers while the MFMAs of this one run.
+#include <cstdlib>
+
+#include "rh_device.h"
+#include "rh_internal.h"
+
+namespace rh {
+
+namespace {
+
+constexpr uint32_t kThreads = 256;
+constexpr uint32_t kBM = 64;        // rows per workgroup
+constexpr uint32_t kStride = 272;   // LDS bytes per 256-byte row: +16 spreads the banks
+
+typedef int32_t v4i __attribute__((ext_vector_type(4)));
+typedef int32_t v16i __attribute__((ext_vector_type(16)));
+typedef int16_t s16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t gemm_job(const GemvJobs& jobs, uint32_t wg) {
+  uint32_t j = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < static_cast<uint32_t>(kMaxJobs); i++)
+    if (i < jobs.n && wg >= jobs.j[i].wg_begin) j = i;
+  return j;
+}
+
+// Raw bytes one thread holds for one block of its row (thread = row*4 + p).
+// Q4_K: w[0] header (d, dmin, scales[12]), w[1..2] qs[32p..32p+32).
+// Q6_K: the GEMV kernels' lane windows for h = p>>1, gq = p&1: w[0] ql at
+// 64h+16gq, w[1] ql at 64h+32+16gq, w[2] qh at 32h+16gq, w[3] scales, w[4]
+// the fifth dwords of those windows and of the scales (holding d).
+struct WRaw {
+  u32x4 w[5];
+};
+
+template <int FMT>
+__device__ __forceinline__ void load_wraw(WRaw& x, const uint8_t* row, uint32_t b, uint32_t p) {
+  if (FMT == 12) {
+    const uint8_t* blk = row + static_cast<size_t>(b) * 144u;
+    x.w[0] = load16(blk);
+    x.w[1] = load16(blk + 16u + 32u * p);
+    x.w[2] = load16(blk + 32u + 32u * p);
+  } else {
+    const uint32_t h = p >> 1, gq = p & 1u;
+    const uint8_t* base = row + static_cast<size_t>(b) * 210u - 2u * (b & 1u);
+    x.w[0] = load16_a4(base + 64u * h + 16u * gq);
+    x.w[1] = load16_a4(base + 64u * h + 32u + 16u * gq);
+    x.w[2] = load16_a4(base + 128u + 32u * h + 16u * gq);
+    x.w[3] = load16_a4(base + 192u);
+    x.w[4] = u32x4{load4(base + 64u * h + 16u * gq + 16u), load4(base + 64u * h + 48u + 16u * gq),
+                   load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
+  }
+}
+
+// 6-bit scale and min of Q4_K sub-block j from the header dwords
+// (ggml get_scale_min_k4, quantize/src/q4_k.rs:17-25).
+__device__ __forceinline__ void q4k_scale_min(const u32x4& hd, uint32_t j, uint32_t& sc, uint32_t& m) {
+  if (j < 4u) {
+    sc = bfe(hd.y, 8u * j, 6);
+    m = bfe(hd.z, 8u * j, 6);
+  } else {
+    const uint32_t jj = j - 4u;
+    sc = bfe(hd.w, 8u * jj, 4) | (bfe(hd.y, 8u * jj + 6u, 2) << 4);
+    m = bfe(hd.w, 8u * jj + 4u, 4) | (bfe(hd.z, 8u * jj + 6u, 2) << 4);
+  }
+}
+
+// Four unsigned nibble bytes q (0..15) times sc (0..63) as the hi/lo planes:
+// the products are formed two at a time in 16-bit lanes (< 2^16, no carry).
+__device__ __forceinline__ void split4_u(uint32_t q, uint32_t sc, uint32_t& hi, uint32_t& lo) {
+  const uint32_t pe = (q & 0x00FF00FFu) * sc;
+  const uint32_t po = ((q >> 8) & 0x00FF00FFu) * sc;
+  lo = (pe & 0x007F007Fu) | ((po & 0x007F007Fu) << 8);
+  hi = ((pe >> 7) & 0x00FF00FFu) | (((po >> 7) & 0x00FF00FFu) << 8);
+}
+
+// Four six-bit bytes q (0..63) as sc * (q - 32) (sc signed) in hi/lo planes:
+// w = 128*hi + lo, lo in 0..127, hi in -32..31 (two's complement bytes). The
+// products are formed two at a time in signed 16-bit lanes (|w| <= 4096).
+__device__ __forceinline__ void split4_s(uint32_t q, int32_t sc, uint32_t& hi, uint32_t& lo) {
+  const s16x2 scv{static_cast<int16_t>(sc), static_cast<int16_t>(sc)};
+  const s16x2 off{static_cast<int16_t>(-32 * sc), static_cast<int16_t>(-32 * sc)};
+  const uint32_t qe = q & 0x00FF00FFu, qo = (q >> 8) & 0x00FF00FFu;
+  const s16x2 we = __builtin_bit_cast(s16x2, qe) * scv + off;
+  const s16x2 wo = __builtin_bit_cast(s16x2, qo) * scv + off;
+  const uint32_t ue = __builtin_bit_cast(uint32_t, we), uo = __builtin_bit_cast(uint32_t, wo);
+  lo = (ue & 0x007F007Fu) | ((uo & 0x007F007Fu) << 8);
+  const s16x2 he = we >> static_cast<int16_t>(7), ho = wo >> static_cast<int16_t>(7);
+  hi = (__builtin_bit_cast(uint32_t, he) & 0x00FF00FFu) | ((__builtin_bit_cast(uint32_t, ho) & 0x00FF00FFu) << 8);
+}
+
+// LDS: hi [64][272] | lo [64][272] | act [BN][272] | mins [64][8] u8 |
+//      bsb [BN][16] (bl_0..7, bh_0..7) | rowd [64] float2 (d, dmin) | d8 [BN]
+template <int FMT, int BN>
+__global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, size_t tokens) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  int8_t* hiT = reinterpret_cast<int8_t*>(lds);
+  int8_t* loT = hiT + kBM * kStride;
+  int8_t* actT = loT + kBM * kStride;
+  uint8_t* minsT = reinterpret_cast<uint8_t*>(actT + BN * kStride);
+  uint8_t* bsT = minsT + kBM * 8u;
+  float2* rowd = reinterpret_cast<float2*>(bsT + BN * 16u);
+  float* d8T = reinterpret_cast<float*>(rowd + kBM);
+
+  const GemvJob& J = jobs.j[gemm_job(jobs, blockIdx.x)];
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * kBM;
+  const uint32_t tok0 = blockIdx.y * BN;
+  const uint32_t nb = J.nb;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t wm = wave & 1u, wn = wave >> 1;
+  constexpr int NT = BN / 64;  // 32x32 tiles per wave along tokens
+
+  // staging roles: one row quarter per thread for the weights, 16-byte
+  // chunks of the activation tile, one token's block sums for tid < BN
+  const uint32_t sr = tid >> 2, sp = tid & 3u;
+  const uint32_t srow = min(row0 + sr, J.rows - 1u);
+  const uint8_t* wrow = J.w + __umul24(srow, static_cast<uint32_t>(J.stride));
+  constexpr int ACH = BN * 16 / 256;  // activation chunks per thread
+  const size_t T = tokens;
+  const size_t stok = min(static_cast<size_t>(tok0 + (tid & (BN - 1))), T - 1);
+
+  WRaw wr;
+  u32x4 ar[ACH];
+  u32x4 sr0{}, sr1{};
+  float d8r = 0.0f;
+  auto prefetch = [&](uint32_t b) {
+    load_wraw<FMT>(wr, wrow, b, sp);
+#pragma unroll
+    for (int c = 0; c < ACH; c++) {
+      const uint32_t chunk = tid + static_cast<uint32_t>(c) * kThreads;
+      const uint32_t n = chunk >> 4, k = (chunk & 15u) * 16u;
+      const size_t tok = min(static_cast<size_t>(tok0 + n), T - 1);
+      ar[c] = load16(reinterpret_cast<const uint8_t*>(q.quants + tok * q.qstride + static_cast<size_t>(b) * 256u + k));
+    }
+    if (tid < static_cast<uint32_t>(BN)) {
+      const size_t o = stok * q.bstride + static_cast<size_t>(b) * 8u;
+      d8r = q.scales[o];
+      if (FMT == 12) {
+        sr0 = load16(reinterpret_cast<const uint8_t*>(q.sums + o));
+        sr1 = load16(reinterpret_cast<const uint8_t*>(q.sums + o + 4));
+      }
+    }
+  };
+
+  v16i acc_i[NT], acc_m[NT];
+  float y[NT][16];
+#pragma unroll
+  for (int t = 0; t < NT; t++)
+#pragma unroll
+    for (int i = 0; i < 16; i++) y[t][i] = -0.0f;
+
+  if (nb) prefetch(0);
+  for (uint32_t b = 0; b < nb; b++) {
+    // raw bytes -> LDS planes
+    if (FMT == 12) {
+      const u32x4 hd = wr.w[0];
+      uint32_t sc0, m0, sc1, m1;
+      q4k_scale_min(hd, 2u * sp, sc0, m0);
+      q4k_scale_min(hd, 2u * sp + 1u, sc1, m1);
+      // qs[32p + l]: low nibble -> k = 64p + l (sub-block 2p), high -> 64p + 32 + l
+      uint32_t h0[8], l0[8], h1[8], l1[8];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t v = wr.w[1 + (i >> 2)][i & 3];
+        split4_u(v & 0x0F0F0F0Fu, sc0, h0[i], l0[i]);
+        split4_u((v >> 4) & 0x0F0F0F0Fu, sc1, h1[i], l1[i]);
+      }
+      int8_t* hrow = hiT + sr * kStride + 64u * sp;
+      int8_t* lrow = loT + sr * kStride + 64u * sp;
+#pragma unroll
+      for (int i = 0; i < 8; i += 4) {
+        *reinterpret_cast<u32x4*>(hrow + 4 * i) = u32x4{h0[i], h0[i + 1], h0[i + 2], h0[i + 3]};
+        *reinterpret_cast<u32x4*>(lrow + 4 * i) = u32x4{l0[i], l0[i + 1], l0[i + 2], l0[i + 3]};
+        *reinterpret_cast<u32x4*>(hrow + 32 + 4 * i) = u32x4{h1[i], h1[i + 1], h1[i + 2], h1[i + 3]};
+        *reinterpret_cast<u32x4*>(lrow + 32 + 4 * i) = u32x4{l1[i], l1[i + 1], l1[i + 2], l1[i + 3]};
+      }
+      minsT[sr * 8u + 2u * sp] = static_cast<uint8_t>(m0);
+      minsT[sr * 8u + 2u * sp + 1u] = static_cast<uint8_t>(m1);
+      if (sp == 0) rowd[sr] = make_float2(f16_lo(hd.x), f16_hi(hd.x));
+      if (tid < static_cast<uint32_t>(BN)) {
+        // bsum_j = 128*bh_j + bl_j, bl_j in 0..127 (|bsum_j| <= 32*127)
+        const int32_t s8[8] = {static_cast<int32_t>(sr0.x), static_cast<int32_t>(sr0.y),
+                               static_cast<int32_t>(sr0.z), static_cast<int32_t>(sr0.w),
+                               static_cast<int32_t>(sr1.x), static_cast<int32_t>(sr1.y),
+                               static_cast<int32_t>(sr1.z), static_cast<int32_t>(sr1.w)};
+        uint32_t bl[2] = {0u, 0u}, bh[2] = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+          bl[j >> 2] |= (static_cast<uint32_t>(s8[j]) & 0x7fu) << (8 * (j & 3));
+          bh[j >> 2] |= (static_cast<uint32_t>(s8[j] >> 7) & 0xffu) << (8 * (j & 3));
+        }
+        *reinterpret_cast<u32x4*>(bsT + tid * 16u) = u32x4{bl[0], bl[1], bh[0], bh[1]};
+      }
+    } else {
+      const uint32_t h = sp >> 1, gq = sp & 1u;
+      const uint32_t sh = 2u * (b & 1u);
+      const u32x4 A = wr.w[0], B = wr.w[1], C = wr.w[2], W = wr.w[3], E = wr.w[4];
+      const u32x4 a{__builtin_amdgcn_alignbyte(A.y, A.x, sh), __builtin_amdgcn_alignbyte(A.z, A.y, sh),
+                    __builtin_amdgcn_alignbyte(A.w, A.z, sh), __builtin_amdgcn_alignbyte(E.x, A.w, sh)};
+      const u32x4 bq{__builtin_amdgcn_alignbyte(B.y, B.x, sh), __builtin_amdgcn_alignbyte(B.z, B.y, sh),
+                     __builtin_amdgcn_alignbyte(B.w, B.z, sh), __builtin_amdgcn_alignbyte(E.y, B.w, sh)};
+      const u32x4 c{__builtin_amdgcn_alignbyte(C.y, C.x, sh), __builtin_amdgcn_alignbyte(C.z, C.y, sh),
+                    __builtin_amdgcn_alignbyte(C.w, C.z, sh), __builtin_amdgcn_alignbyte(E.z, C.w, sh)};
+      const uint32_t X0 = __builtin_amdgcn_alignbyte(W.y, W.x, sh);
+      const uint32_t X1 = __builtin_amdgcn_alignbyte(W.z, W.y, sh);
+      const uint32_t X2 = __builtin_amdgcn_alignbyte(W.w, W.z, sh);
+      const uint32_t X3 = __builtin_amdgcn_alignbyte(E.w, W.w, sh);
+      const uint32_t slo = h ? X2 : X0, shi = h ? X3 : X1;
+      // run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
+      int32_t scr[4];
+      scr[0] = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq, 8);
+      scr[1] = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq + 16u, 8);
+      scr[2] = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq, 8);
+      scr[3] = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq + 16u, 8);
+      // element 128h + 32r + 16gq + l holds run r's value l (q6_k.rs:13-43)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const uint32_t qv = r == 0 ? (a[k] & 0x0F0F0F0Fu) | ((c[k] << 4) & 0x30303030u)
+                            : r == 1 ? (bq[k] & 0x0F0F0F0Fu) | ((c[k] << 2) & 0x30303030u)
+                            : r == 2 ? ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0x30303030u)
+                                     : ((bq[k] >> 4) & 0x0F0F0F0Fu) | ((c[k] >> 2) & 0x30303030u);
+          split4_s(qv, scr[r], hw[k], lw[k]);
+        }
+        const uint32_t k0 = 128u * h + 32u * static_cast<uint32_t>(r) + 16u * gq;
+        *reinterpret_cast<u32x4*>(hiT + sr * kStride + k0) = u32x4{hw[0], hw[1], hw[2], hw[3]};
+        *reinterpret_cast<u32x4*>(loT + sr * kStride + k0) = u32x4{lw[0], lw[1], lw[2], lw[3]};
+      }
+      if (sp == 0) rowd[sr] = make_float2(f16_lo(E.w >> (8u * sh)), 0.0f);
+    }
+#pragma unroll
+    for (int cch = 0; cch < ACH; cch++) {
+      const uint32_t chunk = tid + static_cast<uint32_t>(cch) * kThreads;
+      *reinterpret_cast<u32x4*>(actT + (chunk >> 4) * kStride + (chunk & 15u) * 16u) = ar[cch];
+    }
+    if (tid < static_cast<uint32_t>(BN)) d8T[tid] = d8r;
+    __syncthreads();
+    if (b + 1u < nb) prefetch(b + 1u);
+
+    const uint32_t arow = 32u * wm + (lane & 31u);
+    const uint32_t g = lane >> 5;  // the lane's 16-byte k group of a 32-deep step
+    uint32_t bcol[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) bcol[t] = static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc_i[t] = v16i{};
+    // hi plane over the block, then x128, then the lo plane
+#pragma unroll
+    for (uint32_t kk = 0; kk < 8u; kk++) {
+      const uint32_t ko = 32u * kk + 16u * g;
+      const v4i Ah = *reinterpret_cast<const v4i*>(hiT + arow * kStride + ko);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const v4i Bv = *reinterpret_cast<const v4i*>(actT + bcol[t] * kStride + ko);
+        acc_i[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah, Bv, acc_i[t], 0, 0, 0);
+      }
+    }
+    if (FMT == 12) {
+      // msum: (m_j, bh_j) then x128, then (m_j, bl_j), in lane group 0
+      const uint32_t mw0 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u) : 0u;
+      const uint32_t mw1 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u + 4u) : 0u;
+      const v4i Am{static_cast<int32_t>(mw0), static_cast<int32_t>(mw1), 0, 0};
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const u32x4 bs = *reinterpret_cast<const u32x4*>(bsT + bcol[t] * 16u);
+        const v4i Bh{g == 0 ? static_cast<int32_t>(bs.z) : 0, g == 0 ? static_cast<int32_t>(bs.w) : 0, 0, 0};
+        acc_m[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bh, v16i{}, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+#pragma unroll
+      for (int i = 0; i < 16; i++) acc_i[t][i] <<= 7;
+    if (FMT == 12) {
+      const uint32_t mw0 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u) : 0u;
+      const uint32_t mw1 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u + 4u) : 0u;
+      const v4i Am{static_cast<int32_t>(mw0), static_cast<int32_t>(mw1), 0, 0};
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc_m[t][i] <<= 7;
+        const u32x4 bs = *reinterpret_cast<const u32x4*>(bsT + bcol[t] * 16u);
+        const v4i Bl{g == 0 ? static_cast<int32_t>(bs.x) : 0, g == 0 ? static_cast<int32_t>(bs.y) : 0, 0, 0};
+        acc_m[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bl, acc_m[t], 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (uint32_t kk = 0; kk < 8u; kk++) {
+      const uint32_t ko = 32u * kk + 16u * g;
+      const v4i Al = *reinterpret_cast<const v4i*>(loT + arow * kStride + ko);
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        const v4i Bv = *reinterpret_cast<const v4i*>(actT + bcol[t] * kStride + ko);
+        acc_i[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al, Bv, acc_i[t], 0, 0, 0);
+      }
+    }
+    // the block's float term per (row, token), added in block order
+    // (D layout: lane n + 32*((m/4)%2), register 4*(m/8) + m%4)
+    float d8n[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) d8n[t] = d8T[bcol[t]];
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const uint32_t m = 32u * wm + 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
+      const float2 dd = rowd[m];
+#pragma unroll
+      for (int t = 0; t < NT; t++) {
+        float term;
+        if (FMT == 12) {
+          // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
+          const float neg = -(dd.y * static_cast<float>(acc_m[t][i]));
+          term = d8n[t] * __builtin_fmaf(dd.x, static_cast<float>(acc_i[t][i]), neg);
+        } else {
+          // int_dot.rs:203: (d * d8) * isum
+          const float s = dd.x * d8n[t];
+          term = s * static_cast<float>(acc_i[t][i]);
+        }
+        y[t][i] += term;
+      }
+    }
+    __syncthreads();
+  }
+
+  const uint32_t g = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const uint32_t m = 32u * wm + 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
+    const uint32_t row = row0 + m;
+    if (row >= J.rows) continue;
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const size_t tok = tok0 + static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
+      const size_t idx = static_cast<size_t>(row) * T + tok;
+      if (tok < T && idx < J.out_len) J.out[idx] = y[t][i];
+    }
+  }
+}
+
+template <int FMT, int BN>
+hipError_t launch_bn(GemvJobs jobs, const Q8Dev& q, size_t tokens, hipStream_t s) {
+  uint32_t wgs = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    jobs.j[i].wg_begin = wgs;
+    wgs += (jobs.j[i].rows + kBM - 1u) / kBM;
+  }
+  if (wgs == 0) return hipSuccess;
+  const uint32_t tiles = static_cast<uint32_t>((tokens + BN - 1) / BN);
+  const size_t lds = 2u * kBM * kStride + BN * kStride + kBM * 8u + BN * 16u + kBM * 8u + BN * 4u;
+  hipLaunchKernelGGL((gemm_kq_kernel<FMT, BN>), dim3(wgs, tiles), dim3(kThreads), lds, s, jobs, q, tokens);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, hipStream_t s) {
+  if (tokens == 0) return hipSuccess;
+  // RUSTICIDE_HIP_GEMM_BN=64|128 forces the token tile, for tuning
+  int bn = tokens >= 512 ? 128 : 64;
+  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMM_BN")) bn = v[0] == '1' ? 128 : 64;
+  if (type_id == 12u) return bn == 128 ? launch_bn<12, 128>(jobs, q, tokens, s) : launch_bn<12, 64>(jobs, q, tokens, s);
+  if (type_id == 14u) return bn == 128 ? launch_bn<14, 128>(jobs, q, tokens, s) : launch_bn<14, 64>(jobs, q, tokens, s);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace rh

@@ -73,6 +73,11 @@ size_t gemv_kq_max_tokens(uint32_t nb);
 hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, uint32_t nbmax, size_t tokens,
                           size_t t0, size_t tn, hipStream_t s);
 
+// Prefill GEMM on MFMA for the k-quants (Q4_K, Q6_K): every row of every job
+// against all `tokens` tokens of the quantized activation q, bit-identical to
+// the GEMV kernels (and so to the CPU path).
+hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, hipStream_t s);
+
 hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
                                  float* out, size_t out_len, hipStream_t s);
 

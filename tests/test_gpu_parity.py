@@ -166,6 +166,50 @@ def test_kquant_dot_within_1e4_of_dequantize_and_dot(ctx, type_id):
         assert abs(out[r] - ref) <= 1e-4 * max(1.0, float(np.abs(w).sum()))
 
 
+# ------------------------------------------------------ prefill GEMM (MFMA)
+
+
+GEMM_SHAPES = [
+    (12, 5632, 2048, [128, 512, 2048]),  # prefill on the ffn_gate shape: 128/512/2048 tokens
+    (12, 37, 512, [9, 77]),               # ragged rows and tokens
+    (14, 45, 768, [9, 70]),
+    (14, 2048, 5632, [64]),               # Q6_K ffn_down: 22 blocks, 4620-byte rows
+    (14, 32000, 2048, [64]),              # Q6_K lm_head over a 64-token prefill chunk
+    (12, 130, 25600, [16]),               # 100 blocks per row
+]
+
+
+@pytest.mark.parametrize("type_id,rows,cols,token_counts", GEMM_SHAPES)
+def test_prefill_gemm_is_bit_identical_to_the_cpu_path(ctx, type_id, rows, cols, token_counts):
+    # matmul_batch with many tokens (matmul.rs:229-248): the MFMA GEMM must give
+    # the CPU integer path's bits, token by token
+    assert R.lib().rh_gemm_min_tokens() <= min(token_counts)
+    data = synth.matrix(type_id, rows, cols, seed=rows + 3 * cols)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    for tokens in token_counts:
+        x = synth.normal_f32(tokens * cols, seed=100 + tokens)
+        want = oracle_matmul(type_id, data, rows, cols, x, tokens, threads=16)
+        out = np.full(rows * tokens, np.nan, np.float32)
+        R.matmul_batch(ctx, x, tokens, [(m, out)])
+        assert_same_bits(out, want, f"type={type_id} {rows}x{cols} tokens={tokens}")
+
+
+def test_prefill_gemm_batch_of_projections_and_hostile_bytes(ctx):
+    # Q/K/V in one batch (attention.rs:215-223) on the GEMM, plus random block
+    # bytes (f16 inf/NaN scales) that must compute what the CPU path computes
+    cols, tokens = 2048, 24
+    specs = [(12, 2048, synth.matrix(12, 2048, cols, seed=1)),
+             (12, 256, synth.matrix(12, 256, cols, seed=2)),
+             (14, 100, O.pseudo_random_bytes(100 * synth.row_bytes(14, cols), 7)),
+             (12, 64, O.pseudo_random_bytes(64 * synth.row_bytes(12, cols), 8))]
+    mats = [R.Matrix.load(ctx, t, d, rows, cols) for t, rows, d in specs]
+    x = synth.normal_f32(tokens * cols, seed=5)
+    outs = [np.full(rows * tokens, np.nan, np.float32) for _, rows, _ in specs]
+    R.matmul_batch(ctx, x, tokens, list(zip(mats, outs)))
+    for (t, rows, d), out in zip(specs, outs):
+        assert_same_bits(out, oracle_matmul(t, d, rows, cols, x, tokens), f"type {t} rows {rows}")
+
+
 # --------------------------------------------------------------- I2_S GEMV
 
 
