@@ -32,7 +32,10 @@ typedef enum rh_status {
     RH_ERR_INVALID_CONFIG = 5,   /* ModelError::InvalidConfig (cols == 0)  */
     RH_ERR_DEVICE = 6,           /* a HIP runtime error; see rh_last_error  */
     RH_ERR_OUT_OF_MEMORY = 7,
-    RH_ERR_NO_DEVICE = 8         /* no gfx950 device: the caller falls back */
+    RH_ERR_NO_DEVICE = 8,        /* no gfx950 device: the caller falls back */
+    RH_ERR_CONTEXT_FULL = 9,     /* ModelError::ContextFull                */
+    RH_ERR_CACHE_POSITION = 10,  /* ModelError::CachePosition              */
+    RH_ERR_NO_VALID_TOKENS = 11  /* SamplingError::NoValidTokens           */
 } rh_status;
 
 /* GGML type ids (crates/rusticide-quantize/src/format.rs:31-92), plus the
@@ -80,6 +83,7 @@ void *rh_stream(rh_ctx *ctx);
  * f32 as `widen` does (weights.rs:241-247). */
 rh_status rh_matrix_load(rh_ctx *ctx, uint32_t type_id, const void *data, size_t len,
                          size_t rows, size_t cols, rh_matrix **out);
+/* Frees the matrix; valid before or after its context is destroyed. */
 void rh_matrix_free(rh_matrix *m);
 size_t rh_matrix_rows(const rh_matrix *m);
 size_t rh_matrix_cols(const rh_matrix *m);
@@ -147,6 +151,82 @@ rh_status rh_ternary_dot_i32(rh_ctx *ctx, const rh_matrix *m, const float *input
  * batch size, crates/rusticide-kernels/src/matmul.rs:229-248). */
 size_t rh_gemm_min_tokens(void);
 void rh_set_gemm_min_tokens(size_t tokens);
+
+/* Test hooks for the float functions of the decoder kernels, none of which
+ * has a counterpart in the reference; they pin the kernels to the libm and
+ * IEEE operations behind rusticide's f32 code:
+ *   expf: the bits of the libm expf behind f32::exp (softmax, SiLU;
+ *         crates/rusticide-kernels/src/portable/{norm.rs:17-30,elementwise.rs:6-9});
+ *   sqrt: f32::sqrt, rounded to nearest (RMSNorm,
+ *         crates/rusticide-kernels/src/portable/norm.rs:8-14);
+ *   div:  f32 division, rounded to nearest.
+ * rh_sqrt_host runs the device's correction from the given starts (which must
+ * lie within one ulp of the result), or from the host's sqrt when start is
+ * NULL. rh_math_device evaluates one function elementwise on the device
+ * (b is read by RH_MATH_DIV only). */
+enum { RH_MATH_EXPF = 0, RH_MATH_SQRT = 1, RH_MATH_DIV = 2 };
+void rh_expf_host(const float *x, float *y, size_t n);
+void rh_sqrt_host(const float *x, const float *start, float *y, size_t n);
+rh_status rh_math_device(rh_ctx *ctx, uint32_t op, const float *a, const float *b, float *y, size_t n);
+/* Test hook: the RoPE angle table rh_decoder_new builds on the host,
+ * cos/sin of position * theta^(-2p/columns) per (position, pair)
+ * (crates/rusticide-kernels/src/portable/rope.rs:7-23). */
+void rh_rope_table_host(size_t positions, size_t columns, float theta, float *cos_out, float *sin_out);
+
+/* ---------------------------------------------------------------- decoder
+ * The callers of the quantized products, on the device: the llama-family
+ * Decoder (crates/rusticide-transformer/src/decoder.rs:17-136) and greedy
+ * generation (crates/rusticide-model/src/generate.rs:35-124). */
+
+/* DecoderConfig (crates/rusticide-transformer/src/config.rs:19-33) for the
+ * llama family (adjacent RoPE, SiLU, no biases or sub-norms). */
+typedef struct rh_decoder_config {
+    size_t embedding_length, block_count, feed_forward_length, head_count, head_count_kv, head_dim;
+    size_t context_length, vocab_size;
+    float rope_freq_base, rms_norm_eps;
+} rh_decoder_config;
+
+/* BlockWeights (transformer/src/weights.rs): matrices already loaded with
+ * rh_matrix_load (the decoder borrows them), norms as host f32 rows the
+ * decoder copies. */
+typedef struct rh_decoder_block {
+    const float *attn_norm;
+    const rh_matrix *attn_q, *attn_k, *attn_v, *attn_output;
+    const float *ffn_norm;
+    const rh_matrix *ffn_gate, *ffn_up, *ffn_down;
+} rh_decoder_block;
+
+/* DecoderWeights; output == NULL ties the output to token_embd. */
+typedef struct rh_decoder_weights {
+    const rh_matrix *token_embd;
+    const float *output_norm;
+    const rh_matrix *output;
+    const rh_decoder_block *blocks; /* block_count of them */
+} rh_decoder_weights;
+
+typedef struct rh_decoder rh_decoder;
+
+/* Decoder::new (decoder.rs:28-46): validates the config (config.rs:55-80;
+ * this build also needs head_dim <= 64), copies the norms, computes the RoPE
+ * angle table and allocates the f32 KV cache for context_length positions. */
+rh_status rh_decoder_new(rh_ctx *ctx, const rh_decoder_config *config, const rh_decoder_weights *weights,
+                         rh_decoder **out);
+void rh_decoder_free(rh_decoder *d);
+/* Model::reset (cache.rs:79-83). */
+void rh_decoder_reset(rh_decoder *d);
+/* Positions the cache holds. */
+size_t rh_decoder_position(const rh_decoder *d);
+/* Model::forward_batch (decoder.rs:57-107): tokens at positions
+ * start..start+n, the last token's logits into `logits` (logits_len values
+ * at most). Errors, checked before the cache changes: INVALID_CONFIG (no
+ * tokens, a token out of range), CONTEXT_FULL, CACHE_POSITION. */
+rh_status rh_decoder_forward_batch(rh_decoder *d, const uint32_t *tokens, size_t n, size_t start, float *logits,
+                                   size_t logits_len);
+/* generate (generate.rs:35-124) at temperature 0, without a tokenizer: reset,
+ * prefill in chunks of 64, then pick / forward up to max_tokens picks or the
+ * context end. The picks stay on the device between steps. */
+rh_status rh_decoder_generate_greedy(rh_decoder *d, const uint32_t *prompt, size_t n, size_t max_tokens,
+                                     uint32_t *out, size_t *n_out);
 
 #ifdef __cplusplus
 }

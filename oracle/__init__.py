@@ -267,3 +267,181 @@ def ternary_dot_matrix_i32(data, row_bytes_: int, inputs, tokens: int) -> np.nda
     lib().orc_ternary_dot_matrix_i32(_p(data), len(data), row_bytes_, _p(inputs), len(inputs),
                                      tokens, _p(out), len(out))
     return out
+
+
+# ------------------------------------------------------------------ decoder
+
+
+class _Matrix(ctypes.Structure):
+    _fields_ = [("type_id", ctypes.c_uint32), ("data", ctypes.c_void_p), ("rows", ctypes.c_size_t),
+                ("cols", ctypes.c_size_t)]
+
+
+class _Block(ctypes.Structure):
+    _fields_ = [("attn_norm", ctypes.c_void_p), ("attn_q", _Matrix), ("attn_k", _Matrix), ("attn_v", _Matrix),
+                ("attn_output", _Matrix), ("ffn_norm", ctypes.c_void_p), ("ffn_gate", _Matrix),
+                ("ffn_up", _Matrix), ("ffn_down", _Matrix)]
+
+
+class _DecoderWeights(ctypes.Structure):
+    _fields_ = [("token_embd", _Matrix), ("output_norm", ctypes.c_void_p), ("output", ctypes.POINTER(_Matrix)),
+                ("blocks", ctypes.POINTER(_Block))]
+
+
+class _DecoderConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in ("embedding_length", "block_count", "feed_forward_length",
+                                               "head_count", "head_count_kv", "head_dim", "context_length",
+                                               "vocab_size")] + [("rope_freq_base", ctypes.c_float),
+                                                                 ("rms_norm_eps", ctypes.c_float)]
+
+
+DECODER_ERRORS = {1: "NO_TOKENS", 2: "CONTEXT_FULL", 3: "TOKEN_RANGE", 4: "CACHE_POSITION",
+                  5: "NO_VALID_TOKENS", 6: "NO_MEMORY"}
+
+
+class DecoderError(RuntimeError):
+    def __init__(self, code: int):
+        self.kind = DECODER_ERRORS.get(code, str(code))
+        super().__init__(self.kind)
+
+
+def _dec_lib():
+    L = lib()
+    if not hasattr(L, "_dec_ready"):
+        P, S = ctypes.c_void_p, ctypes.c_size_t
+        L.orc_decoder_new.argtypes = [ctypes.POINTER(_DecoderConfig), ctypes.POINTER(_DecoderWeights), ctypes.c_int]
+        L.orc_decoder_new.restype = P
+        L.orc_decoder_free.argtypes = [P]
+        L.orc_decoder_reset.argtypes = [P]
+        L.orc_decoder_forward_batch.argtypes = [P, P, S, S, P]
+        L.orc_greedy.argtypes = [P, S, P]
+        L.orc_generate_greedy.argtypes = [P, P, S, S, P, P]
+        L.orc_normalize.argtypes = [P, P, S, ctypes.c_float, P]
+        L.orc_softmax.argtypes = [P, S]
+        L.orc_rope_adjacent.argtypes = [P, S, S, ctypes.c_float, S]
+        L.orc_rope_table.argtypes = [S, S, ctypes.c_float, P, P]
+        L.orc_expf_array.argtypes = [P, P, S]
+        L._dec_ready = True
+    return L
+
+
+def _mat(m, keep):
+    type_id, data, rows, cols = m
+    arr = np.ascontiguousarray(data).view(np.uint8).reshape(-1)
+    keep.append(arr)
+    return _Matrix(type_id, arr.ctypes.data, rows, cols)
+
+
+class Decoder:
+    """The reference decoder's forward pass on the CPU (rh_decoder.c) over a
+    model dict from rusticide_amd.synth.decoder_model."""
+
+    def __init__(self, model: dict, threads: int = 8):
+        L = _dec_lib()
+        c = model["config"]
+        self.config = c
+        self._keep = []
+        cfg = _DecoderConfig(*[c[k] for k in ("embedding_length", "block_count", "feed_forward_length",
+                                              "head_count", "head_count_kv", "head_dim", "context_length",
+                                              "vocab_size")], c["rope_freq_base"], c["rms_norm_eps"])
+        blocks = (_Block * len(model["blocks"]))()
+        for i, b in enumerate(model["blocks"]):
+            an = np.ascontiguousarray(b["attn_norm"], np.float32)
+            fn = np.ascontiguousarray(b["ffn_norm"], np.float32)
+            self._keep += [an, fn]
+            blocks[i] = _Block(an.ctypes.data, _mat(b["attn_q"], self._keep), _mat(b["attn_k"], self._keep),
+                               _mat(b["attn_v"], self._keep), _mat(b["attn_output"], self._keep), fn.ctypes.data,
+                               _mat(b["ffn_gate"], self._keep), _mat(b["ffn_up"], self._keep),
+                               _mat(b["ffn_down"], self._keep))
+        on = np.ascontiguousarray(model["output_norm"], np.float32)
+        self._keep.append(on)
+        out = None
+        if model.get("output") is not None:
+            out = _Matrix()
+            out = _mat(model["output"], self._keep)
+            self._out = out
+        w = _DecoderWeights(_mat(model["token_embd"], self._keep), on.ctypes.data,
+                            ctypes.pointer(out) if out is not None else None, blocks)
+        self._blocks, self._w, self._cfg = blocks, w, cfg
+        self.handle = L.orc_decoder_new(ctypes.byref(cfg), ctypes.byref(w), threads)
+        if not self.handle:
+            raise MemoryError("orc_decoder_new")
+
+    def forward_batch(self, tokens, start: int) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.zeros(self.config["vocab_size"], np.float32)
+        err = _dec_lib().orc_decoder_forward_batch(self.handle, t.ctypes.data, len(t), start, logits.ctypes.data)
+        if err:
+            raise DecoderError(err)
+        return logits
+
+    def forward(self, token: int, position: int) -> np.ndarray:
+        return self.forward_batch([token], position)
+
+    def reset(self) -> None:
+        _dec_lib().orc_decoder_reset(self.handle)
+
+    def generate_greedy(self, prompt, max_tokens: int) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(1, max_tokens), np.uint32)
+        n = ctypes.c_size_t()
+        err = _dec_lib().orc_generate_greedy(self.handle, p.ctypes.data, len(p), max_tokens, out.ctypes.data,
+                                             ctypes.byref(n))
+        if err:
+            raise DecoderError(err)
+        return out[: n.value]
+
+    def close(self) -> None:
+        if self.handle:
+            _dec_lib().orc_decoder_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def greedy(logits) -> int:
+    x = _f32(logits)
+    tok = ctypes.c_uint32()
+    err = _dec_lib().orc_greedy(x.ctypes.data, len(x), ctypes.byref(tok))
+    if err:
+        raise DecoderError(err)
+    return tok.value
+
+
+def normalize(x, weight, eps: float) -> np.ndarray:
+    x, w = _f32(x), _f32(weight)
+    out = np.zeros_like(x)
+    _dec_lib().orc_normalize(x.ctypes.data, w.ctypes.data, len(x), eps, out.ctypes.data)
+    return out
+
+
+def softmax(row) -> np.ndarray:
+    r = _f32(row).copy()
+    _dec_lib().orc_softmax(r.ctypes.data, len(r))
+    return r
+
+
+def rope_adjacent(row, position: int, theta: float, dim_pairs: int) -> np.ndarray:
+    r = _f32(row).copy()
+    _dec_lib().orc_rope_adjacent(r.ctypes.data, len(r), position, theta, dim_pairs)
+    return r
+
+
+def rope_table(positions: int, columns: int, theta: float):
+    pairs = columns // 2
+    c = np.zeros(positions * pairs, np.float32)
+    s = np.zeros(positions * pairs, np.float32)
+    _dec_lib().orc_rope_table(positions, columns, theta, c.ctypes.data, s.ctypes.data)
+    return c, s
+
+
+def expf(x) -> np.ndarray:
+    """libm's expf over an array (the function rusticide's f32::exp calls)."""
+    x = _f32(x)
+    y = np.empty_like(x)
+    _dec_lib().orc_expf_array(x.ctypes.data, y.ctypes.data, len(x))
+    return y

@@ -97,6 +97,71 @@ void orc_ternary_dot_matrix_i32(const uint8_t *data, size_t data_len, size_t row
                                 const float *inputs, size_t inputs_len, size_t tokens,
                                 int32_t *out, size_t out_len);
 
+/* ------------------------------------------------------------- decoder */
+
+/* DecoderConfig (crates/rusticide-transformer/src/config.rs:19-33), llama
+ * family: adjacent RoPE, SiLU, no biases or sub-norms. */
+typedef struct {
+    size_t embedding_length, block_count, feed_forward_length, head_count, head_count_kv, head_dim;
+    size_t context_length, vocab_size;
+    float rope_freq_base, rms_norm_eps;
+} orc_decoder_config;
+
+/* A weight matrix as Matrix holds it (model/src/weights.rs:17-38): GGML
+ * type id (0 = f32 rows) and its row-major bytes. */
+typedef struct {
+    uint32_t type_id;
+    const uint8_t *data;
+    size_t rows, cols;
+} orc_matrix;
+
+/* BlockWeights / DecoderWeights (transformer/src/weights.rs); output NULL
+ * is tied to token_embd. */
+typedef struct {
+    const float *attn_norm;
+    orc_matrix attn_q, attn_k, attn_v, attn_output;
+    const float *ffn_norm;
+    orc_matrix ffn_gate, ffn_up, ffn_down;
+} orc_block;
+
+typedef struct {
+    orc_matrix token_embd;
+    const float *output_norm;
+    const orc_matrix *output;
+    const orc_block *blocks;
+} orc_decoder_weights;
+
+typedef struct orc_decoder orc_decoder;
+
+/* Errors (ModelError / SamplingError kinds). */
+enum {
+    ORC_DEC_NO_TOKENS = 1,       /* InvalidConfig "no tokens to forward"   */
+    ORC_DEC_CONTEXT_FULL = 2,    /* ContextFull                            */
+    ORC_DEC_TOKEN_RANGE = 3,     /* InvalidConfig "token out of range"     */
+    ORC_DEC_CACHE_POSITION = 4,  /* CachePosition                          */
+    ORC_DEC_NO_VALID_TOKENS = 5, /* SamplingError::NoValidTokens           */
+    ORC_DEC_NO_MEMORY = 6
+};
+
+orc_decoder *orc_decoder_new(const orc_decoder_config *c, const orc_decoder_weights *w, int threads);
+void orc_decoder_free(orc_decoder *d);
+/* Model::reset (cache.rs:79-83). */
+void orc_decoder_reset(orc_decoder *d);
+/* Model::forward_batch (transformer/src/decoder.rs:57-107): logits
+ * [vocab_size] of the last token. */
+int orc_decoder_forward_batch(orc_decoder *d, const uint32_t *tokens, size_t n, size_t start, float *logits);
+/* Sampler::greedy_logits (sampling/src/sampler.rs:75-87). */
+int orc_greedy(const float *logits, size_t n, uint32_t *token);
+/* generate (model/src/generate.rs:35-124) at temperature 0. */
+int orc_generate_greedy(orc_decoder *d, const uint32_t *prompt, size_t n, size_t max_tokens, uint32_t *out,
+                        size_t *n_out);
+/* The f32 pieces, exposed for their known-answer tests. */
+void orc_normalize(const float *in, const float *weight, size_t n, float eps, float *out);
+void orc_softmax(float *row, size_t n);
+void orc_rope_adjacent(float *row, size_t len, size_t position, float theta, size_t dim_pairs);
+void orc_rope_table(size_t positions, size_t columns, float theta, float *cos_out, float *sin_out);
+void orc_expf_array(const float *x, float *y, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

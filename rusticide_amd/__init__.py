@@ -17,6 +17,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 
 import numpy as np
 
@@ -123,6 +124,7 @@ class Context:
         if st != 0:
             raise RusticideError(st, f"rh_init({device})")
         self.handle = h
+        self._children = weakref.WeakSet()  # matrices, activations, decoders
 
     def check(self, status: int) -> None:
         if status != 0:
@@ -133,6 +135,9 @@ class Context:
         return lib().rh_stream(self.handle)
 
     def close(self) -> None:
+        # everything made on this context goes first
+        for child in list(self._children):
+            child.free()
         if self.handle:
             lib().rh_destroy(self.handle)
             self.handle = None
@@ -170,6 +175,7 @@ class Matrix:
 
     def __init__(self, ctx: Context, handle):
         self.ctx, self.handle = ctx, handle
+        ctx._children.add(self)
 
     @classmethod
     def load(cls, ctx: Context, type_id: int, data, rows: int, cols: int) -> "Matrix":
@@ -227,6 +233,7 @@ class Q8:
         h = ctypes.c_void_p()
         ctx.check(lib().rh_q8_new(ctx.handle, ctypes.byref(h)))
         self.ctx, self.handle = ctx, h
+        ctx._children.add(self)
 
     def quantize(self, inputs, tokens: int, kind: int, stream: int = 0) -> "Q8":
         """Q8Input::quantize of every token of a device tensor `inputs`."""
@@ -279,3 +286,122 @@ def matmul_batch_device(ctx: Context, inputs, tokens: int, jobs, stream: int = 0
     """Device-resident form: `inputs` and outputs are torch device tensors."""
     ctx.check(lib().rh_matmul_batch_device(ctx.handle, _ptr(inputs), inputs.numel(), tokens, _jobs(jobs),
                                            len(jobs), stream or None))
+
+
+# ------------------------------------------------------------------ decoder
+
+STATUS.update({9: "CONTEXT_FULL", 10: "CACHE_POSITION", 11: "NO_VALID_TOKENS"})
+
+
+class _DecoderConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_size_t) for n in ("embedding_length", "block_count", "feed_forward_length",
+                                               "head_count", "head_count_kv", "head_dim", "context_length",
+                                               "vocab_size")] + [("rope_freq_base", ctypes.c_float),
+                                                                 ("rms_norm_eps", ctypes.c_float)]
+
+
+class _DecoderBlock(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("attn_norm", "attn_q", "attn_k", "attn_v", "attn_output",
+                                               "ffn_norm", "ffn_gate", "ffn_up", "ffn_down")]
+
+
+class _DecoderWeights(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in ("token_embd", "output_norm", "output", "blocks")]
+
+
+def _dec_lib() -> ctypes.CDLL:
+    L = lib()
+    if not hasattr(L, "_dec_ready"):
+        P, S, St = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        L.rh_decoder_new.argtypes = [P, ctypes.POINTER(_DecoderConfig), ctypes.POINTER(_DecoderWeights),
+                                     ctypes.POINTER(ctypes.c_void_p)]
+        L.rh_decoder_new.restype = St
+        L.rh_decoder_free.argtypes = [P]
+        L.rh_decoder_reset.argtypes = [P]
+        L.rh_decoder_position.argtypes = [P]
+        L.rh_decoder_position.restype = S
+        L.rh_decoder_forward_batch.argtypes = [P, P, S, S, P, S]
+        L.rh_decoder_forward_batch.restype = St
+        L.rh_decoder_generate_greedy.argtypes = [P, P, S, S, P, ctypes.POINTER(ctypes.c_size_t)]
+        L.rh_decoder_generate_greedy.restype = St
+        L._dec_ready = True
+    return L
+
+
+class Decoder:
+    """The llama-family Decoder on the device (rh_decoder_*): a model dict of
+    rusticide_amd.synth.decoder_model's shape, its matrices uploaded to HBM."""
+
+    def __init__(self, ctx: Context, model: dict):
+        L = _dec_lib()
+        c = model["config"]
+        self.ctx, self.config = ctx, c
+        self._mats, self._keep = [], []
+
+        def load(m):
+            t, data, rows, cols = m
+            mat = Matrix.load(ctx, t, data, rows, cols)
+            self._mats.append(mat)
+            return mat.handle.value if isinstance(mat.handle, ctypes.c_void_p) else mat.handle
+
+        def vec(v):
+            a = np.ascontiguousarray(v, np.float32)
+            self._keep.append(a)
+            return a.ctypes.data
+
+        blocks = (_DecoderBlock * len(model["blocks"]))()
+        for i, b in enumerate(model["blocks"]):
+            blocks[i] = _DecoderBlock(vec(b["attn_norm"]), load(b["attn_q"]), load(b["attn_k"]), load(b["attn_v"]),
+                                      load(b["attn_output"]), vec(b["ffn_norm"]), load(b["ffn_gate"]),
+                                      load(b["ffn_up"]), load(b["ffn_down"]))
+        out = load(model["output"]) if model.get("output") is not None else None
+        w = _DecoderWeights(load(model["token_embd"]), vec(model["output_norm"]), out, ctypes.addressof(blocks))
+        cfg = _DecoderConfig(*[c[k] for k in ("embedding_length", "block_count", "feed_forward_length",
+                                              "head_count", "head_count_kv", "head_dim", "context_length",
+                                              "vocab_size")], c["rope_freq_base"], c["rms_norm_eps"])
+        h = ctypes.c_void_p()
+        ctx.check(L.rh_decoder_new(ctx.handle, ctypes.byref(cfg), ctypes.byref(w), ctypes.byref(h)))
+        self.handle = h
+        self._blocks = blocks
+        ctx._children.add(self)
+
+    def forward_batch(self, tokens, start: int) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, np.uint32)
+        logits = np.zeros(self.config["vocab_size"], np.float32)
+        self.ctx.check(_dec_lib().rh_decoder_forward_batch(self.handle, t.ctypes.data, len(t), start,
+                                                           logits.ctypes.data, len(logits)))
+        return logits
+
+    def forward(self, token: int, position: int) -> np.ndarray:
+        return self.forward_batch([token], position)
+
+    def reset(self) -> None:
+        _dec_lib().rh_decoder_reset(self.handle)
+
+    @property
+    def position(self) -> int:
+        return _dec_lib().rh_decoder_position(self.handle)
+
+    def generate_greedy(self, prompt, max_tokens: int) -> np.ndarray:
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(1, max_tokens), np.uint32)
+        n = ctypes.c_size_t()
+        self.ctx.check(_dec_lib().rh_decoder_generate_greedy(self.handle, p.ctypes.data, len(p), max_tokens,
+                                                             out.ctypes.data, ctypes.byref(n)))
+        return out[: n.value]
+
+    def free(self) -> None:
+        if self.handle:
+            _dec_lib().rh_decoder_free(self.handle)
+            self.handle = None
+        for m in self._mats:
+            m.free()
+        self._mats = []
+
+    close = free
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -30,6 +30,7 @@ struct rh_ctx {
 
 struct rh_matrix {
   rh_ctx* ctx = nullptr;
+  int device = 0;  // freeing needs no live context
   uint32_t type_id = 0;
   size_t rows = 0, cols = 0;
   size_t row_bytes = 0;  // bytes of one row's data (f32 for dense)
@@ -42,6 +43,7 @@ struct rh_matrix {
 
 struct rh_q8 {
   rh_ctx* ctx = nullptr;
+  int device = 0;
   int kind = 0;
   size_t width = 0, tokens = 0;
   Q8Dev q;
@@ -283,6 +285,12 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
 
 }  // namespace
 
+namespace rh {
+int ctx_device(const rh_ctx* ctx) { return ctx->device; }
+const uint8_t* matrix_data(const rh_matrix* m) { return m->data; }
+size_t matrix_stride(const rh_matrix* m) { return m->stride; }
+}  // namespace rh
+
 extern "C" {
 
 const char* rh_adapter_name(void) { return "hip-gfx950"; }
@@ -332,6 +340,7 @@ rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
   rh_matrix* m = new (std::nothrow) rh_matrix();
   if (!m) return fail(ctx, RH_ERR_OUT_OF_MEMORY, "host allocation failed");
   m->ctx = ctx;
+  m->device = ctx->device;
   m->type_id = type_id;
   m->rows = rows;
   m->cols = cols;
@@ -420,10 +429,12 @@ rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
   return RH_OK;
 }
 
+// Frees without touching the context, which may already be destroyed: work
+// queued on any stream may still read the matrix, so the device drains first.
 void rh_matrix_free(rh_matrix* m) {
   if (!m) return;
-  hipSetDevice(m->ctx->device);
-  hipStreamSynchronize(m->ctx->stream);
+  hipSetDevice(m->device);
+  hipDeviceSynchronize();
   hipFree(m->data);
   delete m;
 }
@@ -527,13 +538,14 @@ rh_status rh_q8_new(rh_ctx* ctx, rh_q8** out) {
   *out = new (std::nothrow) rh_q8();
   if (!*out) return fail(ctx, RH_ERR_OUT_OF_MEMORY, "host allocation failed");
   (*out)->ctx = ctx;
+  (*out)->device = ctx->device;
   return RH_OK;
 }
 
 void rh_q8_free(rh_q8* q) {
   if (!q) return;
   if (q->mem) {
-    hipSetDevice(q->ctx->device);
+    hipSetDevice(q->device);
     hipDeviceSynchronize();
     hipFree(q->mem);
   }

@@ -1,0 +1,659 @@
+// model.hip -- the decoder forward pass around the quantized matrix products,
+// on the device: Decoder::forward_batch and greedy generation
+// (crates/rusticide-transformer/src/decoder.rs:57-136,
+//  crates/rusticide-model/src/generate.rs:35-124).
+//
+// Every projection goes through rh_matmul_batch_device (the fused decode
+// GEMV, or the MFMA GEMM for prefill chunks); the kernels here do what lies
+// between them, each following the reference's arithmetic step for step:
+//   * RMSNorm: squares summed in order from -0.0 by one lane, then
+//     x / sqrt(mean + eps) * w (portable/norm.rs:8-14, transformer norm.rs:10-14);
+//   * RoPE, adjacent pairs: fma(lo, cos, -(hi*sin)), fma(hi, cos, lo*sin)
+//     (portable/rope.rs:7-23) with cos/sin from a table the host computes
+//     with its libm at decoder creation, the same calls the CPU path makes;
+//   * attention per (token, head): the eight-lane fused dot over the head
+//     (rusticide-simd/src/float.rs:23-36) / sqrt(head_dim), max-subtracted
+//     softmax summed in order from 0.0, then mix_rows' fused accumulation in
+//     row order (float.rs:52-62, attention.rs:41-57);
+//   * SiLU * up, residual adds (portable/elementwise.rs);
+//   * greedy pick: NaN as -inf, total order, the last maximum wins
+//     (sampling/src/sampler.rs:75-87, filters.rs:37-43).
+// exp is rh::expf_ref (rh_math.h), which returns the bits of the libm expf
+// the CPU path calls.
+#include <cmath>
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/rusticide_hip.h"
+#include "rh_device.h"
+#include "rh_internal.h"
+#include "rh_math.h"
+
+namespace rh {
+namespace {
+
+constexpr uint32_t kNormThreads = 256;
+
+
+// Token rows of token_embd into hidden (Matrix::copy_row, weights.rs:120-150).
+__global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint8_t* data, size_t stride,
+                                                    const uint32_t* tokens, uint32_t width, float* hidden) {
+  const uint32_t t = blockIdx.y;
+  const uint8_t* row = data + static_cast<size_t>(tokens[t]) * stride;
+  float* out = hidden + static_cast<size_t>(t) * width;
+  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < width; e += gridDim.x * 256u) {
+    float v;
+    if (type_id == 0u) {
+      v = reinterpret_cast<const float*>(row)[e];
+    } else if (type_id == 12u) {  // quantize/src/q4_k.rs:32-66
+      const uint32_t b = e / 256u, l = e % 256u;
+      const uint8_t* blk = row + static_cast<size_t>(b) * 144u;
+      const float d = f16_lo(load4(blk)), dmin = f16_hi(load4(blk));
+      const uint32_t j = l / 32u, li = l % 32u;
+      const uint8_t* s = blk + 4;
+      uint32_t sc, m;
+      if (j < 4u) {
+        sc = s[j] & 63u;
+        m = s[j + 4u] & 63u;
+      } else {
+        sc = (s[j + 4u] & 0x0Fu) | ((s[j - 4u] >> 6) << 4);
+        m = (s[j + 4u] >> 4) | ((s[j] >> 6) << 4);
+      }
+      const uint8_t qb = blk[16u + 32u * (j / 2u) + li];
+      const uint32_t qv = (j & 1u) ? (qb >> 4) : (qb & 0x0Fu);
+      const float ds = d * static_cast<float>(sc), dm = dmin * static_cast<float>(m);
+      const float prod = ds * static_cast<float>(qv);
+      v = prod - dm;
+    } else {  // Q6_K, quantize/src/q6_k.rs:13-43
+      const uint32_t b = e / 256u, l = e % 256u;
+      const uint8_t* blk = row + static_cast<size_t>(b) * 210u;
+      const float d = f16_lo(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
+      const uint32_t hh = l / 128u, rr = (l % 128u) / 32u, li = l % 32u;
+      const uint8_t low = blk[64u * hh + 32u * (rr & 1u) + li];
+      const uint8_t high = blk[128u + 32u * hh + li];
+      const uint32_t nib = rr < 2u ? (low & 0x0Fu) : (low >> 4);
+      const int32_t qv = static_cast<int32_t>(nib | (((high >> (2u * rr)) & 3u) << 4)) - 32;
+      const float sc = static_cast<float>(static_cast<int8_t>(blk[192u + 8u * hh + 2u * rr + li / 16u]));
+      const float ds = d * sc;
+      v = ds * static_cast<float>(qv);
+    }
+    out[e] = v;
+  }
+}
+
+// hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t]),
+// then normed[t] = normalize(hidden[t], weight) for tokens t >= norm_from.
+// One workgroup per token.
+__global__ __launch_bounds__(256) void add_norm_kernel(float* hidden, const float* delta, uint32_t n, uint32_t width,
+                                                       const float* weight, float eps, uint32_t norm_from,
+                                                       float* normed) {
+  extern __shared__ __align__(16) float sq[];
+  __shared__ float s_rms;
+  const uint32_t t = blockIdx.x;
+  float* h = hidden + static_cast<size_t>(t) * width;
+  for (uint32_t e = threadIdx.x; e < width; e += kNormThreads) {
+    float v = h[e];
+    if (delta) {
+      v += delta[static_cast<size_t>(e) * n + t];
+      h[e] = v;
+    }
+    const float s = v * v;
+    sq[e] = s;
+  }
+  if (t < norm_from) return;  // uniform over the workgroup
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    // the squares summed in order from -0.0 (f32 Sum), one lane
+    float sum = -0.0f;
+    uint32_t e = 0;
+    for (; e + 4u <= width; e += 4u) {
+      const float4 v4 = *reinterpret_cast<const float4*>(sq + e);
+      sum += v4.x;
+      sum += v4.y;
+      sum += v4.z;
+      sum += v4.w;
+    }
+    for (; e < width; e++) sum += sq[e];
+    const float mean = __fdiv_rn(sum, static_cast<float>(width));
+    s_rms = sqrt_rn(mean + eps);
+  }
+  __syncthreads();
+  const float rms = s_rms;
+  float* o = normed + static_cast<size_t>(t - norm_from) * width;
+  for (uint32_t e = threadIdx.x; e < width; e += kNormThreads) {
+    const float v = __fdiv_rn(h[e], rms);
+    o[e] = v * weight[e];
+  }
+}
+
+// q/k/v from the projections (stored by weight row, x[e*n + t]): q rotated
+// into token-major rows, k rotated and v copied into the cache at positions
+// start + t. One thread per rotation pair (q, k) or value element (v).
+__global__ __launch_bounds__(256) void qkv_post_kernel(const float* qr, const float* kr, const float* vr, uint32_t n,
+                                                       uint32_t width, uint32_t kv, uint32_t head_dim,
+                                                       const float* rcos, const float* rsin, uint32_t start,
+                                                       float* q, float* kcache, float* vcache) {
+  const uint32_t t = blockIdx.y;
+  const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t pairs = head_dim / 2u;
+  const uint32_t pos = start + t;
+  const uint32_t qp = width / 2u, kp = kv / 2u;
+  if (i < qp + kp) {
+    const bool is_q = i < qp;
+    const uint32_t e = 2u * (is_q ? i : i - qp);
+    const float* src = is_q ? qr : kr;
+    const float lo = src[static_cast<size_t>(e) * n + t], hi = src[static_cast<size_t>(e + 1u) * n + t];
+    const uint32_t p = (e % head_dim) / 2u;
+    const float c = rcos[static_cast<size_t>(pos) * pairs + p], s = rsin[static_cast<size_t>(pos) * pairs + p];
+    const float hs = hi * s, ls = lo * s;
+    const float nlo = __builtin_fmaf(lo, c, -hs), nhi = __builtin_fmaf(hi, c, ls);
+    float* dst = is_q ? q + static_cast<size_t>(t) * width : kcache + static_cast<size_t>(pos) * kv;
+    dst[e] = nlo;
+    dst[e + 1u] = nhi;
+  } else if (i < qp + kp + kv) {
+    const uint32_t e = i - qp - kp;
+    vcache[static_cast<size_t>(pos) * kv + e] = vr[static_cast<size_t>(e) * n + t];
+  }
+}
+
+// One wave per (query head, token): scores over cached rows 0..=start+t,
+// softmax, then the weighted sum of value rows (attention.rs:41-57,189-207).
+__global__ __launch_bounds__(64) void attention_kernel(const float* q, const float* kcache, const float* vcache,
+                                                       uint32_t width, uint32_t kv, uint32_t head_dim,
+                                                       uint32_t group, float scale, uint32_t start, float* mixed) {
+  extern __shared__ float sh[];  // q head [64] | weights [rows]
+  float* qh = sh;
+  float* w = sh + 64;
+  const uint32_t h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+  const uint32_t rows = start + t + 1u;
+  const uint32_t off = (h / group) * head_dim;
+  if (lane < head_dim) qh[lane] = q[static_cast<size_t>(t) * width + h * head_dim + lane];
+  __syncthreads();
+  // dot (float.rs:23-36): eight fused lanes over whole chunks, lanes summed
+  // in order from -0.0, then the unfused tail summed from -0.0
+  const uint32_t chunks = head_dim / 8u;
+  float mx = -INFINITY;
+  for (uint32_t i = lane; i < rows; i += 64u) {
+    const float* kr = kcache + static_cast<size_t>(i) * kv + off;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = 0; c < chunks; c++)
+#pragma unroll
+      for (int l = 0; l < 8; l++) acc[l] = __builtin_fmaf(qh[8u * c + l], kr[8u * c + l], acc[l]);
+    float tail = -0.0f;
+    for (uint32_t e = 8u * chunks; e < head_dim; e++) {
+      const float p = qh[e] * kr[e];
+      tail += p;
+    }
+    float s = -0.0f;
+#pragma unroll
+    for (int l = 0; l < 8; l++) s += acc[l];
+    const float score = __fdiv_rn(s + tail, scale);
+    w[i] = score;
+    mx = fmaxf(mx, score);
+  }
+  // max over the lanes (exact in any order)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  for (uint32_t i = lane; i < rows; i += 64u) w[i] = expf_ref(w[i] - mx);
+  __syncthreads();
+  __shared__ float s_sum;
+  if (lane == 0) {
+    float sum = 0.0f;  // portable/norm.rs: `let mut sum = 0.0`
+    for (uint32_t i = 0; i < rows; i++) sum += w[i];
+    s_sum = sum;
+  }
+  __syncthreads();
+  const float sum = s_sum;
+  for (uint32_t i = lane; i < rows; i += 64u) w[i] = __fdiv_rn(w[i], sum);
+  __syncthreads();
+  // mix_rows (float.rs:52-62): out starts at 0.0, each row fused in order
+  if (lane < head_dim) {
+    float acc = 0.0f;
+    const float* vr = vcache + off + lane;
+    for (uint32_t i = 0; i < rows; i++) acc = __builtin_fmaf(vr[static_cast<size_t>(i) * kv], w[i], acc);
+    mixed[static_cast<size_t>(t) * width + h * head_dim + lane] = acc;
+  }
+}
+
+// hf[t][e] = silu(gate) * up, both stored by weight row (x[e*n + t])
+// (feed_forward.rs:51-66, portable/elementwise.rs:6-9).
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const float* up, uint32_t n, uint32_t len,
+                                                       float* hf) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x;
+  if (i >= static_cast<size_t>(n) * len) return;
+  const uint32_t t = static_cast<uint32_t>(i / len), e = static_cast<uint32_t>(i % len);
+  const float g = gate[static_cast<size_t>(e) * n + t];
+  const float den = 1.0f + expf_ref(-g);
+  const float s = __fdiv_rn(g, den);
+  hf[i] = s * up[static_cast<size_t>(e) * n + t];
+}
+
+// f32::total_cmp's order as an i32 key.
+__device__ __forceinline__ int32_t total_key(float f) {
+  const int32_t b = __float_as_int(f);
+  return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
+}
+
+// Greedy pick over the logits: NaN as -inf, max by total order, the last
+// maximum wins; out[0] = token, out[1] = 1 when some logit is finite. When
+// `tokens` is given the token is also appended at tokens[count[0]] (the
+// generation's record), count[0] advanced, and count[1] set for good once a
+// pick finds no finite logit.
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint32_t n, uint32_t* out,
+                                                      uint32_t* tokens, uint32_t* count) {
+  __shared__ int32_t skey[16];
+  __shared__ uint32_t sidx[16];
+  __shared__ uint32_t sfin[16];
+  int32_t best = INT32_MIN;
+  uint32_t bi = 0, fin = 0;
+  bool have = false;
+  for (uint32_t i = threadIdx.x; i < n; i += 1024u) {
+    const float v = logits[i];
+    fin |= __builtin_isfinite(v) ? 1u : 0u;
+    const int32_t k = total_key(v != v ? -INFINITY : v);
+    if (!have || k >= best) {
+      best = k;
+      bi = i;
+      have = true;
+    }
+  }
+  // (key, index) maximum: a larger key, or an equal key at a larger index
+  for (int o = 32; o > 0; o >>= 1) {
+    const int32_t ok = __shfl_xor(best, o, 64);
+    const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, 64));
+    const bool oh = __shfl_xor(have ? 1 : 0, o, 64) != 0;
+    fin |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(fin), o, 64));
+    if (oh && (!have || ok > best || (ok == best && oi > bi))) {
+      best = ok;
+      bi = oi;
+      have = true;
+    }
+  }
+  const uint32_t wv = threadIdx.x >> 6;
+  if ((threadIdx.x & 63u) == 0) {
+    skey[wv] = have ? best : INT32_MIN;
+    sidx[wv] = have ? bi : 0u;
+    sfin[wv] = fin | (have ? 2u : 0u);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int32_t b = INT32_MIN;
+    uint32_t idx = 0, f = 0;
+    bool any = false;
+    for (uint32_t w = 0; w < 16u; w++) {
+      f |= sfin[w] & 1u;
+      if (!(sfin[w] & 2u)) continue;
+      if (!any || skey[w] > b || (skey[w] == b && sidx[w] > idx)) {
+        b = skey[w];
+        idx = sidx[w];
+        any = true;
+      }
+    }
+    out[0] = idx;
+    out[1] = f;
+    if (tokens) {
+      tokens[count[0]] = idx;
+      count[0] = count[0] + 1u;
+      if (!f) count[1] = 1u;
+    }
+  }
+}
+
+// the float functions of the kernels above, one per element (test hook)
+__global__ __launch_bounds__(256) void math_kernel(uint32_t op, const float* a, const float* b, float* y, size_t n) {
+  const size_t i = static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x;
+  if (i >= n) return;
+  if (op == RH_MATH_EXPF) y[i] = expf_ref(a[i]);
+  else if (op == RH_MATH_SQRT) y[i] = sqrt_rn(a[i]);
+  else y[i] = __fdiv_rn(a[i], b[i]);
+}
+
+}  // namespace
+}  // namespace rh
+
+using namespace rh;
+
+struct rh_decoder {
+  rh_ctx* ctx = nullptr;
+  int device = 0;  // freeing needs no live context
+  hipStream_t stream = nullptr;
+  rh_decoder_config c{};
+  struct Block {
+    const rh_matrix *q, *k, *v, *o, *gate, *up, *down;
+    float *attn_norm, *ffn_norm;
+  };
+  std::vector<Block> blocks;
+  const rh_matrix* token_embd = nullptr;
+  const rh_matrix* output = nullptr;
+  float* output_norm = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr;
+  float *keys = nullptr, *values = nullptr;
+  size_t kv = 0;
+  size_t cached = 0;  // positions stored in every layer
+  // activations for up to `cap` tokens
+  size_t cap = 0;
+  float *hidden = nullptr, *normed = nullptr, *delta = nullptr, *qr = nullptr, *kr = nullptr, *vr = nullptr;
+  float *q = nullptr, *mixed = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
+  float* logits = nullptr;
+  uint32_t* tokens = nullptr;  // the chunk's token ids
+  uint32_t* pick = nullptr;    // argmax: [token, any finite]
+  uint32_t* record = nullptr;  // generated tokens
+  uint32_t* count = nullptr;   // [recorded, a pick found no finite logit]
+  size_t record_cap = 0;
+};
+
+namespace {
+
+constexpr size_t kPrefillChunk = 64;  // model/src/generate.rs:70
+
+template <typename T>
+hipError_t dmalloc(T** p, size_t n) {
+  return hipMalloc(reinterpret_cast<void**>(p), (n ? n : 1) * sizeof(T));
+}
+
+void free_acts(rh_decoder* d) {
+  for (void* p : {static_cast<void*>(d->hidden), static_cast<void*>(d->normed), static_cast<void*>(d->delta),
+                  static_cast<void*>(d->qr), static_cast<void*>(d->kr), static_cast<void*>(d->vr),
+                  static_cast<void*>(d->q), static_cast<void*>(d->mixed), static_cast<void*>(d->gate),
+                  static_cast<void*>(d->up), static_cast<void*>(d->hf), static_cast<void*>(d->tokens)})
+    if (p) hipFree(p);
+  d->hidden = d->normed = d->delta = d->qr = d->kr = d->vr = d->q = d->mixed = d->gate = d->up = d->hf = nullptr;
+  d->tokens = nullptr;
+  d->cap = 0;
+}
+
+hipError_t ensure_acts(rh_decoder* d, size_t n) {
+  if (d->cap >= n) return hipSuccess;
+  hipError_t e = hipStreamSynchronize(d->stream);
+  if (e != hipSuccess) return e;
+  free_acts(d);
+  const size_t w = d->c.embedding_length, f = d->c.feed_forward_length, kv = d->kv;
+  if ((e = dmalloc(&d->hidden, n * w)) != hipSuccess || (e = dmalloc(&d->normed, n * w)) != hipSuccess ||
+      (e = dmalloc(&d->delta, n * w)) != hipSuccess || (e = dmalloc(&d->qr, n * w)) != hipSuccess ||
+      (e = dmalloc(&d->kr, n * kv)) != hipSuccess || (e = dmalloc(&d->vr, n * kv)) != hipSuccess ||
+      (e = dmalloc(&d->q, n * w)) != hipSuccess || (e = dmalloc(&d->mixed, n * w)) != hipSuccess ||
+      (e = dmalloc(&d->gate, n * f)) != hipSuccess || (e = dmalloc(&d->up, n * f)) != hipSuccess ||
+      (e = dmalloc(&d->hf, n * f)) != hipSuccess || (e = dmalloc(&d->tokens, n)) != hipSuccess) {
+    free_acts(d);
+    return e;
+  }
+  d->cap = n;
+  return hipSuccess;
+}
+
+rh_status mm(rh_decoder* d, const float* in, size_t n, size_t width, std::initializer_list<rh_job> jobs) {
+  std::vector<rh_job> v(jobs);
+  return rh_matmul_batch_device(d->ctx, in, n * width, n, v.data(), v.size(), d->stream);
+}
+
+#define RHD(expr)                                   \
+  do {                                              \
+    hipError_t e_ = (expr);                         \
+    if (e_ != hipSuccess) return RH_ERR_DEVICE;     \
+  } while (0)
+#define RHS(expr)                                   \
+  do {                                              \
+    rh_status s_ = (expr);                          \
+    if (s_ != RH_OK) return s_;                     \
+  } while (0)
+
+// Decoder::forward_on_pool (decoder.rs:74-107) for n tokens whose ids are
+// already in d->tokens, at positions start..start+n; leaves the last token's
+// logits in d->logits.
+rh_status forward_device(rh_decoder* d, size_t n, size_t start) {
+  const rh_decoder_config& c = d->c;
+  const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
+  const uint32_t f = static_cast<uint32_t>(c.feed_forward_length), hd = static_cast<uint32_t>(c.head_dim);
+  const uint32_t nn = static_cast<uint32_t>(n);
+  hipStream_t s = d->stream;
+  const rh_matrix* E = d->token_embd;
+  hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, nn), dim3(256), 0, s, rh_matrix_type(E),
+                     matrix_data(E), matrix_stride(E), d->tokens, w, d->hidden);
+  RHD(hipGetLastError());
+  const float scale = ::sqrtf(static_cast<float>(c.head_dim));
+  const size_t norm_lds = static_cast<size_t>(w) * 4u;
+  const float* pending = nullptr;  // the residual the next norm adds first
+  for (size_t l = 0; l < d->blocks.size(); l++) {
+    const rh_decoder::Block& b = d->blocks[l];
+    hipLaunchKernelGGL(add_norm_kernel, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+                       b.attn_norm, c.rms_norm_eps, 0u, d->normed);
+    RHD(hipGetLastError());
+    RHS(mm(d, d->normed, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
+    float* kc = d->keys + l * c.context_length * kv;
+    float* vc = d->values + l * c.context_length * kv;
+    const uint32_t work = w / 2u + kv / 2u + kv;
+    hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn, w,
+                       kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
+    RHD(hipGetLastError());
+    const size_t att_lds = (64u + start + n) * 4u;
+    hipLaunchKernelGGL(attention_kernel, dim3(static_cast<uint32_t>(c.head_count), nn), dim3(64), att_lds, s, d->q,
+                       kc, vc, w, kv, hd, static_cast<uint32_t>(c.head_count / c.head_count_kv), scale,
+                       static_cast<uint32_t>(start), d->mixed);
+    RHD(hipGetLastError());
+    RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
+    hipLaunchKernelGGL(add_norm_kernel, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, d->delta, nn, w,
+                       b.ffn_norm, c.rms_norm_eps, 0u, d->normed);
+    RHD(hipGetLastError());
+    RHS(mm(d, d->normed, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
+    const size_t total = n * f;
+    hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255u) / 256u)), dim3(256), 0, s, d->gate,
+                       d->up, nn, f, d->hf);
+    RHD(hipGetLastError());
+    RHS(mm(d, d->hf, n, f, {{b.down, d->delta, n * w}}));
+    pending = d->delta;
+  }
+  // the last residual for every token, then the last token's output norm
+  hipLaunchKernelGGL(add_norm_kernel, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+                     d->output_norm, c.rms_norm_eps, nn - 1u, d->normed);
+  RHD(hipGetLastError());
+  const rh_matrix* out = d->output ? d->output : d->token_embd;
+  RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
+  d->cached = start + n;
+  return RH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void rh_rope_table_host(size_t positions, size_t columns, float theta, float* cos_out, float* sin_out) {
+  const size_t pairs = columns / 2;
+  for (size_t pos = 0; pos < positions; pos++)
+    for (size_t p = 0; p < pairs; p++) {
+      const float exponent = -static_cast<float>(2 * p) / static_cast<float>(columns);
+      const float angle = static_cast<float>(pos) * ::powf(theta, exponent);
+      cos_out[pos * pairs + p] = ::cosf(angle);
+      sin_out[pos * pairs + p] = ::sinf(angle);
+    }
+}
+
+void rh_expf_host(const float* x, float* y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = expf_ref(x[i]);
+}
+
+void rh_sqrt_host(const float* x, const float* start, float* y, size_t n) {
+  for (size_t i = 0; i < n; i++) y[i] = start ? sqrt_fix(x[i], start[i]) : sqrt_rn(x[i]);
+}
+
+rh_status rh_math_device(rh_ctx* ctx, uint32_t op, const float* a, const float* b, float* y, size_t n) {
+  const bool binary = op == RH_MATH_DIV;
+  if (!ctx || op > RH_MATH_DIV || (n && (!a || !y || (binary && !b)))) return RH_ERR_INVALID_ARGUMENT;
+  if (n == 0) return RH_OK;
+  if (hipSetDevice(ctx_device(ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  hipStream_t s = static_cast<hipStream_t>(rh_stream(ctx));
+  float *da = nullptr, *db = nullptr, *dy = nullptr;
+  if (dmalloc(&da, n) != hipSuccess || dmalloc(&dy, n) != hipSuccess || (binary && dmalloc(&db, n) != hipSuccess)) {
+    hipFree(da);
+    hipFree(dy);
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  hipError_t e = hipMemcpyAsync(da, a, n * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess && binary) e = hipMemcpyAsync(db, b, n * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(math_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0, s, op, da, db, dy,
+                       n);
+    e = hipGetLastError();
+  }
+  if (e == hipSuccess) e = hipMemcpyAsync(y, dy, n * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  hipFree(da);
+  hipFree(db);
+  hipFree(dy);
+  return e == hipSuccess ? RH_OK : RH_ERR_DEVICE;
+}
+
+rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_decoder_weights* weights,
+                         rh_decoder** out) {
+  if (!ctx || !config || !weights || !out || !weights->token_embd || !weights->output_norm || !weights->blocks)
+    return RH_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  const rh_decoder_config& c = *config;
+  // DecoderConfig::validate (transformer/src/config.rs:55-80), plus this
+  // kernel set's limits: head_dim <= 64, f32/Q4_K/Q6_K embedding rows
+  if (c.head_count == 0 || c.head_count_kv == 0 || c.head_count % c.head_count_kv != 0 || c.head_dim == 0 ||
+      c.head_dim % 2 != 0 || c.head_count * c.head_dim != c.embedding_length || c.block_count == 0 ||
+      c.feed_forward_length == 0 || c.context_length == 0 || c.vocab_size == 0 || c.head_dim > 64)
+    return RH_ERR_INVALID_CONFIG;
+  const uint32_t et = rh_matrix_type(weights->token_embd);
+  if ((et != RH_TYPE_F32 && et != RH_TYPE_Q4_K && et != RH_TYPE_Q6_K) ||
+      rh_matrix_cols(weights->token_embd) != c.embedding_length || rh_matrix_rows(weights->token_embd) < c.vocab_size)
+    return RH_ERR_SHAPE_MISMATCH;
+  if (hipSetDevice(ctx_device(ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  rh_decoder* d = new (std::nothrow) rh_decoder();
+  if (!d) return RH_ERR_OUT_OF_MEMORY;
+  d->ctx = ctx;
+  d->device = ctx_device(ctx);
+  d->stream = static_cast<hipStream_t>(rh_stream(ctx));
+  d->c = c;
+  d->kv = c.head_count_kv * c.head_dim;
+  d->token_embd = weights->token_embd;
+  d->output = weights->output;
+  const size_t w = c.embedding_length;
+  auto upload = [&](const float* host, float** dev) -> bool {
+    return dmalloc(dev, w) == hipSuccess &&
+           hipMemcpy(*dev, host, w * 4, hipMemcpyHostToDevice) == hipSuccess;
+  };
+  bool ok = upload(weights->output_norm, &d->output_norm);
+  for (size_t l = 0; ok && l < c.block_count; l++) {
+    const rh_decoder_block& b = weights->blocks[l];
+    rh_decoder::Block x{b.attn_q, b.attn_k, b.attn_v, b.attn_output, b.ffn_gate, b.ffn_up, b.ffn_down, nullptr,
+                        nullptr};
+    ok = b.attn_q && b.attn_k && b.attn_v && b.attn_output && b.ffn_gate && b.ffn_up && b.ffn_down &&
+         b.attn_norm && b.ffn_norm && upload(b.attn_norm, &x.attn_norm) && upload(b.ffn_norm, &x.ffn_norm);
+    d->blocks.push_back(x);
+  }
+  // RoPE angles for every position, with the host libm (portable/rope.rs:7-23)
+  const size_t pairs = c.head_dim / 2;
+  std::vector<float> hc(c.context_length * pairs), hs(c.context_length * pairs);
+  rh_rope_table_host(c.context_length, c.head_dim, c.rope_freq_base, hc.data(), hs.data());
+  ok = ok && dmalloc(&d->rope_cos, hc.size()) == hipSuccess && dmalloc(&d->rope_sin, hs.size()) == hipSuccess &&
+       hipMemcpy(d->rope_cos, hc.data(), hc.size() * 4, hipMemcpyHostToDevice) == hipSuccess &&
+       hipMemcpy(d->rope_sin, hs.data(), hs.size() * 4, hipMemcpyHostToDevice) == hipSuccess;
+  const size_t cache = c.block_count * c.context_length * d->kv;
+  ok = ok && dmalloc(&d->keys, cache) == hipSuccess && dmalloc(&d->values, cache) == hipSuccess &&
+       dmalloc(&d->logits, c.vocab_size) == hipSuccess && dmalloc(&d->pick, 2) == hipSuccess &&
+       dmalloc(&d->count, 2) == hipSuccess;
+  if (!ok) {
+    rh_decoder_free(d);
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  *out = d;
+  return RH_OK;
+}
+
+void rh_decoder_free(rh_decoder* d) {
+  if (!d) return;
+  // the context (and its stream) may already be destroyed: drain the device
+  hipSetDevice(d->device);
+  hipDeviceSynchronize();
+  free_acts(d);
+  for (auto& b : d->blocks) {
+    if (b.attn_norm) hipFree(b.attn_norm);
+    if (b.ffn_norm) hipFree(b.ffn_norm);
+  }
+  for (void* p : {static_cast<void*>(d->output_norm), static_cast<void*>(d->rope_cos),
+                  static_cast<void*>(d->rope_sin), static_cast<void*>(d->keys), static_cast<void*>(d->values),
+                  static_cast<void*>(d->logits), static_cast<void*>(d->pick), static_cast<void*>(d->record),
+                  static_cast<void*>(d->count)})
+    if (p) hipFree(p);
+  delete d;
+}
+
+void rh_decoder_reset(rh_decoder* d) {
+  if (d) d->cached = 0;
+}
+
+size_t rh_decoder_position(const rh_decoder* d) { return d ? d->cached : 0; }
+
+rh_status rh_decoder_forward_batch(rh_decoder* d, const uint32_t* tokens, size_t n, size_t start, float* logits,
+                                   size_t logits_len) {
+  if (!d || (!tokens && n) || (!logits && logits_len)) return RH_ERR_INVALID_ARGUMENT;
+  // decoder.rs:111-136: the batch is checked before anything changes
+  if (n == 0) return RH_ERR_INVALID_CONFIG;
+  if (start + n > d->c.context_length || start + n < start) return RH_ERR_CONTEXT_FULL;
+  for (size_t i = 0; i < n; i++)
+    if (tokens[i] >= d->c.vocab_size) return RH_ERR_INVALID_CONFIG;
+  if (start != d->cached) return RH_ERR_CACHE_POSITION;  // cache.rs:56-61
+  if (hipSetDevice(ctx_device(d->ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  if (ensure_acts(d, n) != hipSuccess) return RH_ERR_OUT_OF_MEMORY;
+  RHD(hipMemcpyAsync(d->tokens, tokens, n * 4, hipMemcpyHostToDevice, d->stream));
+  RHS(forward_device(d, n, start));
+  const size_t m = logits_len < d->c.vocab_size ? logits_len : d->c.vocab_size;
+  if (m) RHD(hipMemcpyAsync(logits, d->logits, m * 4, hipMemcpyDeviceToHost, d->stream));
+  RHD(hipStreamSynchronize(d->stream));
+  return RH_OK;
+}
+
+rh_status rh_decoder_generate_greedy(rh_decoder* d, const uint32_t* prompt, size_t n, size_t max_tokens,
+                                     uint32_t* out, size_t* n_out) {
+  if (!d || !n_out || (!prompt && n) || (!out && max_tokens)) return RH_ERR_INVALID_ARGUMENT;
+  *n_out = 0;
+  // generate.rs:45-48
+  if (n >= d->c.context_length) return RH_ERR_CONTEXT_FULL;
+  if (n == 0) return RH_ERR_INVALID_CONFIG;
+  for (size_t i = 0; i < n; i++)
+    if (prompt[i] >= d->c.vocab_size) return RH_ERR_INVALID_CONFIG;
+  if (hipSetDevice(ctx_device(d->ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  if (ensure_acts(d, n < kPrefillChunk ? n : kPrefillChunk) != hipSuccess) return RH_ERR_OUT_OF_MEMORY;
+  if (d->record_cap < max_tokens) {
+    RHD(hipStreamSynchronize(d->stream));
+    if (d->record) hipFree(d->record);
+    d->record = nullptr;
+    d->record_cap = 0;
+    if (dmalloc(&d->record, max_tokens) != hipSuccess) return RH_ERR_OUT_OF_MEMORY;
+    d->record_cap = max_tokens;
+  }
+  hipStream_t s = d->stream;
+  // prefill (generate.rs:70-81): reset, then chunks of 64
+  d->cached = 0;
+  for (size_t st = 0; st < n; st += kPrefillChunk) {
+    const size_t m = n - st < kPrefillChunk ? n - st : kPrefillChunk;
+    RHD(hipMemcpyAsync(d->tokens, prompt + st, m * 4, hipMemcpyHostToDevice, s));
+    RHS(forward_device(d, m, st));
+  }
+  RHD(hipMemsetAsync(d->count, 0, 8, s));
+  // decode_loop (generate.rs:83-111): pick, then forward the pick; the pick
+  // stays on the device and feeds the next step's embedding
+  size_t position = n;
+  size_t emitted = 0;
+  for (size_t i = 0; i < max_tokens; i++) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, d->logits, static_cast<uint32_t>(d->c.vocab_size),
+                       d->pick, d->record, d->count);
+    RHD(hipGetLastError());
+    emitted++;
+    if (position == d->c.context_length) break;
+    RHD(hipMemcpyAsync(d->tokens, d->pick, 4, hipMemcpyDeviceToDevice, s));
+    RHS(forward_device(d, 1, position));
+    position++;
+  }
+  uint32_t flag[2] = {0, 0};
+  if (emitted) RHD(hipMemcpyAsync(out, d->record, emitted * 4, hipMemcpyDeviceToHost, s));
+  RHD(hipMemcpyAsync(flag, d->count, 8, hipMemcpyDeviceToHost, s));
+  RHD(hipStreamSynchronize(s));
+  if (flag[1]) return RH_ERR_NO_VALID_TOKENS;  // sampler.rs:84-85
+  *n_out = emitted;
+  return RH_OK;
+}
+
+}  // extern "C"

@@ -78,6 +78,18 @@ hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q
 // the GEMV kernels (and so to the CPU path).
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, hipStream_t s);
 
+}  // namespace rh
+
+struct rh_ctx;
+struct rh_matrix;
+
+namespace rh {
+
+// Internal views of the ABI's opaque handles (api.hip).
+int ctx_device(const rh_ctx* ctx);
+const uint8_t* matrix_data(const rh_matrix* m);
+size_t matrix_stride(const rh_matrix* m);
+
 hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
                                  float* out, size_t out_len, hipStream_t s);
 

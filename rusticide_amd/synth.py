@@ -90,3 +90,86 @@ def matrix(type_id: int, rows: int, cols: int, seed: int) -> np.ndarray:
     if type_id == 36:
         return i2s_matrix(rows, cols, seed)
     raise ValueError(type_id)
+
+
+# ------------------------------------------------------- random-init decoders
+
+def pack_q4k_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """Packs 6-bit scales/mins [n, 8] into the 12 Q4_K scale bytes
+    (the inverse of ggml get_scale_min_k4, quantize/src/q4_k.rs:17-25)."""
+    sc = sc.astype(np.uint8)
+    m = m.astype(np.uint8)
+    out = np.zeros((sc.shape[0], 12), np.uint8)
+    out[:, 0:4] = (sc[:, 0:4] & 63) | ((sc[:, 4:8] >> 4) << 6)
+    out[:, 4:8] = (m[:, 0:4] & 63) | ((m[:, 4:8] >> 4) << 6)
+    out[:, 8:12] = (sc[:, 4:8] & 0x0F) | ((m[:, 4:8] & 0x0F) << 4)
+    return out
+
+
+def q4k_centered(rows: int, cols: int, seed: int, sigma: float = 0.02) -> np.ndarray:
+    """Q4_K rows whose weights are roughly N(0, sigma)-sized and centred:
+    nibbles uniform 0..15, sub-block scales uniform 1..8, mins round(7.5*sc),
+    d = dmin = f16(sigma / 20 * |N(1, 0.1)|)."""
+    nblocks = rows * cols // 256
+    rng = _rng(seed)
+    blocks = rng.integers(0, 256, size=(nblocks, 144), dtype=np.uint8)
+    sc = rng.integers(1, 9, size=(nblocks, 8), dtype=np.int32)
+    m = np.rint(7.5 * sc).astype(np.int32)
+    blocks[:, 4:16] = pack_q4k_scales(sc, m)
+    d = (np.abs(rng.normal(1.0, 0.1, nblocks)) * (sigma / 20.0)).astype(np.float16)
+    blocks[:, 0:2] = d.view(np.uint8).reshape(nblocks, 2)
+    blocks[:, 2:4] = d.view(np.uint8).reshape(nblocks, 2)
+    return blocks.reshape(-1)
+
+
+def q6k_centered(rows: int, cols: int, seed: int, sigma: float = 0.02) -> np.ndarray:
+    """Q6_K rows with N(0, sigma)-sized weights: 6-bit values uniform (centred
+    by the -32 offset), int8 scales uniform +-(1..16), d = f16(sigma / 157)."""
+    nblocks = rows * cols // 256
+    rng = _rng(seed)
+    blocks = rng.integers(0, 256, size=(nblocks, 210), dtype=np.uint8)
+    mag = rng.integers(1, 17, size=(nblocks, 16), dtype=np.int32)
+    sign = np.where(rng.random((nblocks, 16)) < 0.5, -1, 1)
+    blocks[:, 192:208] = (mag * sign).astype(np.int8).view(np.uint8)
+    d = (np.abs(rng.normal(1.0, 0.1, nblocks)) * (sigma / 157.0)).astype(np.float16)
+    blocks[:, 208:210] = d.view(np.uint8).reshape(nblocks, 2)
+    return blocks.reshape(-1)
+
+
+TINYLLAMA = dict(embedding_length=2048, block_count=22, feed_forward_length=5632, head_count=32,
+                 head_count_kv=4, head_dim=64, context_length=2048, vocab_size=32000,
+                 rope_freq_base=10000.0, rms_norm_eps=1e-5)
+
+
+def decoder_model(config: dict, seed: int) -> dict:
+    """A random-init llama-family decoder in the Q4_K_M tensor mix: Q4_K for
+    token_embd, attention and gate/up; Q6_K for the output and for ffn_down
+    in even layers (Q4_K in odd ones); f32 norms 1 + 0.05*N(0, 1).
+
+    Returns {"config": config, "token_embd", "output_norm", "output", "blocks"}
+    where a matrix is (type_id, bytes, rows, cols)."""
+    c = config
+    width, kv = c["embedding_length"], c["head_count_kv"] * c["head_dim"]
+    ffn, vocab = c["feed_forward_length"], c["vocab_size"]
+    rng = _rng(seed)
+    seeds = iter(rng.integers(0, 2 ** 31, size=16 + 16 * c["block_count"]).tolist())
+
+    def mat(type_id, rows, cols):
+        gen = q4k_centered if type_id == 12 else q6k_centered
+        return (type_id, gen(rows, cols, next(seeds)), rows, cols)
+
+    def norm():
+        return (1.0 + 0.05 * _rng(next(seeds)).standard_normal(width)).astype(np.float32)
+
+    blocks = []
+    for layer in range(c["block_count"]):
+        blocks.append({
+            "attn_norm": norm(),
+            "attn_q": mat(12, width, width), "attn_k": mat(12, kv, width), "attn_v": mat(12, kv, width),
+            "attn_output": mat(12, width, width),
+            "ffn_norm": norm(),
+            "ffn_gate": mat(12, ffn, width), "ffn_up": mat(12, ffn, width),
+            "ffn_down": mat(14 if layer % 2 == 0 else 12, width, ffn),
+        })
+    return {"config": dict(c), "token_embd": mat(12, vocab, width), "output_norm": norm(),
+            "output": mat(14, vocab, width), "blocks": blocks}

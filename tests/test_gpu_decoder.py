@@ -1,0 +1,168 @@
+"""The device decoder against the CPU restatement of rusticide's decoder.
+
+Bar: end-to-end greedy tokens from random-init models
+identical to the CPU path. The products are bit-identical by construction;
+the f32 glue follows the reference's operation order, so logits are compared
+bit for bit as well, with the largest difference reported if they ever part.
+"""
+
+import numpy as np
+import pytest
+
+import oracle as O
+import rusticide_amd as R
+from rusticide_amd import synth
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(embedding_length=256, block_count=2, feed_forward_length=512, head_count=4, head_count_kv=2,
+             head_dim=64, context_length=160, vocab_size=320, rope_freq_base=10000.0, rms_norm_eps=1e-5)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = R.Context(0)
+    yield c
+    c.close()
+
+
+def same_bits(a, b):
+    return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
+
+
+def diff(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def test_small_decoder_logits_match_the_cpu_path(ctx):
+    model = synth.decoder_model(SMALL, seed=11)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
+    rng = np.random.default_rng(3)
+    tokens = rng.integers(0, SMALL["vocab_size"], 70).astype(np.uint32)
+    # a 64-token prefill chunk, a ragged one, then single tokens
+    for start, chunk in ((0, tokens[:64]), (64, tokens[64:69]), (69, tokens[69:70])):
+        g = gpu.forward_batch(chunk, start)
+        c = cpu.forward_batch(chunk, start)
+        assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
+    assert gpu.position == 70
+    gpu.close()
+    cpu.close()
+
+
+def test_small_decoder_batch_equals_token_by_token(ctx):
+    # decoder_batch_tests.rs:50-66: a batch's last logits equal those of the
+    # same tokens fed one at a time
+    model = synth.decoder_model(SMALL, seed=12)
+    gpu = R.Decoder(ctx, model)
+    tokens = [5, 17, 300, 2, 99, 41, 7]
+    batch = gpu.forward_batch(tokens, 0)
+    gpu.reset()
+    for i, t in enumerate(tokens):
+        single = gpu.forward(t, i)
+    assert same_bits(batch, single), diff(batch, single)
+    gpu.close()
+
+
+def test_small_decoder_greedy_generation_matches(ctx):
+    model = synth.decoder_model(SMALL, seed=13)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
+    prompt = np.random.default_rng(4).integers(0, SMALL["vocab_size"], 70).astype(np.uint32)
+    want = cpu.generate_greedy(prompt, 40)
+    got = gpu.generate_greedy(prompt, 40)
+    assert np.array_equal(got, want), (got, want)
+    # generation stops at the context end (generate.rs:102-104)
+    near = np.arange(150, dtype=np.uint32) % SMALL["vocab_size"]
+    got = gpu.generate_greedy(near, 40)
+    want = cpu.generate_greedy(near, 40)
+    assert len(got) == len(want) == 11 and np.array_equal(got, want)
+    gpu.close()
+    cpu.close()
+
+
+def test_decoder_errors_mirror_model_error(ctx):
+    # decoder.rs:111-136, cache.rs:35-65, generate.rs:45-48
+    model = synth.decoder_model(SMALL, seed=14)
+    gpu = R.Decoder(ctx, model)
+    with pytest.raises(R.RusticideError) as e:
+        gpu.forward_batch([1, 2], SMALL["context_length"] - 1)
+    assert e.value.kind == "CONTEXT_FULL"
+    with pytest.raises(R.RusticideError) as e:
+        gpu.forward_batch([SMALL["vocab_size"]], 0)
+    assert e.value.kind == "INVALID_CONFIG"
+    gpu.forward_batch([1, 2, 3], 0)
+    with pytest.raises(R.RusticideError) as e:
+        gpu.forward_batch([4], 5)
+    assert e.value.kind == "CACHE_POSITION"
+    with pytest.raises(R.RusticideError) as e:
+        gpu.generate_greedy(np.zeros(SMALL["context_length"], np.uint32), 4)
+    assert e.value.kind == "CONTEXT_FULL"
+    gpu.close()
+
+
+def test_tinyllama_shaped_greedy_decode_matches_the_cpu_path(ctx):
+    # 22 layers, hidden 2048, 32/4 heads of 64, FFN 5632, vocab 32000,
+    # Q4_K_M mix; 64-token random prompt, then 128 greedy tokens
+    model = synth.decoder_model(synth.TINYLLAMA, seed=2026)
+    prompt = np.random.default_rng(7).integers(0, 32000, 64).astype(np.uint32)
+    gpu = R.Decoder(ctx, model)
+    cpu = O.Decoder(model, threads=16)
+    g = gpu.forward_batch(prompt, 0)
+    c = cpu.forward_batch(prompt, 0)
+    assert same_bits(g, c), f"prefill logits: max |diff| {diff(g, c)}"
+    want = cpu.generate_greedy(prompt, 128)
+    got = gpu.generate_greedy(prompt, 128)
+    assert len(got) == 128
+    assert np.array_equal(got, want), f"first mismatch at {np.flatnonzero(got != want)[:1]}"
+    gpu.close()
+    cpu.close()
+
+
+def _device_math(ctx, op, a, b=None):
+    import ctypes
+    L = R.lib()
+    L.rh_math_device.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p,
+                                 ctypes.c_void_p, ctypes.c_size_t]
+    a = np.ascontiguousarray(a, np.float32)
+    b = None if b is None else np.ascontiguousarray(b, np.float32)
+    y = np.empty_like(a)
+    ctx.check(L.rh_math_device(ctx.handle, op, a.ctypes.data, None if b is None else b.ctypes.data,
+                               y.ctypes.data, len(a)))
+    return y
+
+
+def _assert_same(y, want, x):
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(y), nan)
+    bad = np.flatnonzero(y[~nan].view(np.uint32) != want[~nan].view(np.uint32))
+    assert bad.size == 0, f"{bad.size} mismatches, e.g. x={x[~nan][bad[:3]]}"
+
+
+def test_device_expf_matches_libm(ctx):
+    # the expf of the softmax and SiLU kernels, on the device, against libm's
+    # (every 4099th bit pattern plus the special cases)
+    x = np.arange(0, 1 << 32, 4099, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([x, np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 88.72283, 88.72284, -103.97207,
+                                     -103.97208, -87.3366, 1e-45], np.float32)])
+    _assert_same(_device_math(ctx, 0, x), O.expf(x), x)
+
+
+def test_device_sqrt_is_rounded_to_nearest(ctx):
+    # RMSNorm's square root on the device against IEEE sqrt (numpy's), every
+    # 1021st positive float plus the special cases
+    x = np.arange(0, 0x7F800000, 1021, dtype=np.uint32).view(np.float32)
+    x = np.concatenate([x, np.array([0.0, -0.0, np.inf, -1.0, np.nan, 1e-5, 2 ** -64, 2 ** -126], np.float32)])
+    with np.errstate(invalid="ignore"):
+        want = np.sqrt(x)
+    _assert_same(_device_math(ctx, 1, x), want, x)
+
+
+def test_device_division_is_rounded_to_nearest(ctx):
+    rng = np.random.default_rng(5)
+    a = rng.integers(0, 0x7F800000, 1 << 22, dtype=np.uint32).view(np.float32)
+    b = rng.integers(0, 0x7F800000, 1 << 22, dtype=np.uint32).view(np.float32)
+    a[::2] = -a[::2]
+    x = np.concatenate([a, np.float32([1.0, -127.0, 0.0, 1.0, np.inf])])
+    y = np.concatenate([b, np.float32([3.0, 0.37, 0.0, 0.0, np.inf])])
+    with np.errstate(all="ignore"):
+        want = x / y
+    _assert_same(_device_math(ctx, 2, x, y), want, x)
