@@ -17,6 +17,14 @@ GEMV kernel, measured with HIP events on the stream it is launched on.
 summary in profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy of
 known size), when that summary covers the workload.
 
+`also.e2e_decode` is the metric's second half: greedy decode of a random-init
+TinyLlama-1.1B-shaped model in the Q4_K_M mix (22 layers, 2048 hidden, 32/4
+heads of 64, FFN 5632, vocab 32000; Q6_K lm_head and even-layer ffn_down),
+a 64-token prompt then 128 greedy tokens (generate.rs:35-124), f32 KV cache.
+tok/s = 128 / decode wall time, where decode time is a 129-token generation
+less a 1-token one (both include the same prefill). The CPU oracle decodes a
+few of the same tokens on the host cores beside it and must pick the same ones.
+
 Prints one JSON line on stdout; progress goes to stderr.
 """
 
@@ -182,6 +190,86 @@ def measure_cpu(res: dict, seconds: float):
     }
 
 
+def decode_bytes_per_token(model: dict, position: int) -> int:
+    """Compulsory HBM bytes of one decode step: every layer matrix, the output
+    matrix, the norms, one embedding row and the f32 KV rows read at
+    `position` cached positions."""
+    from rusticide_amd import synth
+    c = model["config"]
+
+    def mbytes(m):
+        t, _, rows, cols = m
+        return rows * synth.row_bytes(t, cols)
+
+    total = 0
+    for b in model["blocks"]:
+        total += sum(mbytes(b[k]) for k in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up",
+                                            "ffn_down"))
+        total += 4 * 2 * c["embedding_length"]
+    out = model["output"] if model.get("output") is not None else model["token_embd"]
+    total += mbytes(out) + 4 * c["embedding_length"]
+    t, _, _, cols = model["token_embd"]
+    total += synth.row_bytes(t, cols)
+    kv = c["head_count_kv"] * c["head_dim"]
+    total += c["block_count"] * position * kv * 4 * 2
+    return total
+
+
+def measure_decode(ctx, reps: int, prompt_len: int = 64, new_tokens: int = 128):
+    """Greedy decode of the TinyLlama-shaped model on the device."""
+    import rusticide_amd as R
+    from rusticide_amd import synth
+
+    t0 = time.perf_counter()
+    model = synth.decoder_model(synth.TINYLLAMA, seed=7)
+    dec = R.Decoder(ctx, model)
+    log(f"[bench] e2e: model built and uploaded in {time.perf_counter() - t0:.1f} s")
+    prompt = np.random.default_rng(1).integers(0, synth.TINYLLAMA["vocab_size"], prompt_len).astype(np.uint32)
+    tokens = dec.generate_greedy(prompt, new_tokens + 1)  # warm-up
+    decode_s, prefill_s = [], []
+    for _ in range(reps):
+        t = time.perf_counter()
+        dec.generate_greedy(prompt, 1)
+        t1 = time.perf_counter() - t
+        t = time.perf_counter()
+        got = dec.generate_greedy(prompt, new_tokens + 1)
+        tn = time.perf_counter() - t
+        assert np.array_equal(got, tokens), "greedy decode is not deterministic"
+        decode_s.append(tn - t1)
+        prefill_s.append(t1)
+    dec.close()
+    d = float(np.median(decode_s))
+    per_token = decode_bytes_per_token(model, prompt_len + new_tokens // 2)
+    return {
+        "model": model, "prompt": prompt, "tokens": tokens[:new_tokens],
+        "tok_s": new_tokens / d, "us_per_token": d / new_tokens * 1e6,
+        "prefill_ms": float(np.median(prefill_s)) * 1e3, "bytes_per_token": per_token,
+        "gbs": per_token / (d / new_tokens) / 1e9,
+    }
+
+
+def measure_cpu_decode(res: dict, tokens: int = 8):
+    """The oracle's decoder on the host cores: the same prompt's prefill, then
+    `tokens` greedy steps, which must pick the device's tokens."""
+    import oracle as O
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    cpu = O.Decoder(res["model"], threads=threads)
+    t = time.perf_counter()
+    got = cpu.generate_greedy(res["prompt"], 1)
+    t1 = time.perf_counter() - t
+    t = time.perf_counter()
+    got = cpu.generate_greedy(res["prompt"], tokens + 1)
+    tn = time.perf_counter() - t
+    cpu.close()
+    d = max(tn - t1, 1e-9)
+    return {
+        "tok_s": round(tokens / d, 3), "cores": threads, "kind": "port",
+        "sample": f"64-token prefill then {tokens} greedy steps, {threads} threads; "
+                  f"same tokens as the GPU: {bool(np.array_equal(got[:tokens], res['tokens'][:tokens]))}",
+    }
+
+
 def traffic_for(name: str):
     """HBM bytes per launch of the workload's kernel from the committed counter summary."""
     try:
@@ -233,6 +321,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc", action="store_true", help="run the short sequence rocprofv3 --pmc profiles")
+    ap.add_argument("--decode-reps", type=int, default=5, help="timed 64+128-token generations (0 skips)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -260,9 +349,17 @@ def main() -> int:
             f"warm {r['warm_kernel_us']:.2f} us = {r['warm_kernel_gbs']:.0f} GB/s; "
             f"pre-quantized GEMV alone {r['prequantized_gemv_us']:.2f} us")
     h = results[HEADLINE]
+    e2e = None
+    if args.decode_reps > 0:
+        e2e = measure_decode(ctx, args.decode_reps)
+        log(f"[bench] e2e decode: {e2e['tok_s']:.1f} tok/s ({e2e['us_per_token']:.1f} us/token, "
+            f"{e2e['gbs']:.0f} GB/s of compulsory bytes), prefill 64 tokens {e2e['prefill_ms']:.2f} ms")
     cpu = None if args.no_cpu else measure_cpu(h, args.cpu_seconds)
     if cpu:
         log(f"[bench] cpu baseline: {cpu['value']} GB/s ({cpu['sample']})")
+    cpu_decode = None if (args.no_cpu or e2e is None) else measure_cpu_decode(e2e)
+    if cpu_decode:
+        log(f"[bench] cpu decode: {cpu_decode['tok_s']} tok/s ({cpu_decode['sample']})")
     also = {
         n: {"workload": r["desc"], "step_gbs": round(r["step_gbs"], 1), "kernel_us": round(r["kernel_us"], 3),
             "kernel_gbs": round(r["kernel_gbs"], 1), "hbm_frac": round(r["kernel_gbs"] / HBM_PEAK_GBS, 4),
@@ -270,6 +367,16 @@ def main() -> int:
             "kernel": r["kernel"], "hbm_traffic_bytes": traffic_for(n)}
         for n, r in results.items() if n != HEADLINE
     }
+    if e2e is not None:
+        also["e2e_decode"] = {
+            "workload": "TinyLlama-1.1B-shaped Q4_K_M random-init model, 64-token prompt + 128 greedy tokens, "
+                        "batch 1, f32 KV cache",
+            "tok_s": round(e2e["tok_s"], 1), "us_per_token": round(e2e["us_per_token"], 1),
+            "prefill_64_ms": round(e2e["prefill_ms"], 3),
+            "bytes_per_token": e2e["bytes_per_token"], "compulsory_gbs": round(e2e["gbs"], 1),
+            "hbm_frac": round(e2e["gbs"] / HBM_PEAK_GBS, 4),
+            "cpu_oracle": cpu_decode,
+        }
     line = {
         "metric": METRIC,
         "value": round(h["step_gbs"], 2),

@@ -23,6 +23,7 @@
 #include <cmath>
 #include <cstring>
 #include <new>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/rusticide_hip.h"
@@ -34,6 +35,58 @@ namespace rh {
 namespace {
 
 constexpr uint32_t kNormThreads = 256;
+
+// ((s + p[0]) + p[1]) + ... on one lane, from 16-byte aligned LDS. The sum is
+// a chain of dependent adds; each batch of 28 values is loaded while the
+// previous batch is added (the scheduling barriers keep the compiler from
+// sinking the loads below the adds), so LDS latency does not stall the chain.
+// Two batches in flight stay under the 15 outstanding LDS reads a wait can
+// name, so the adds wait for their own batch only.
+constexpr uint32_t kSumBatch4 = 7;  // float4 per batch
+constexpr uint32_t kSumBatch = 4u * kSumBatch4;
+
+__device__ __forceinline__ void load_batch(const float* p, float4 (&v)[kSumBatch4]) {
+#pragma unroll
+  for (uint32_t j = 0; j < kSumBatch4; j++) v[j] = reinterpret_cast<const float4*>(p)[j];
+}
+
+__device__ __forceinline__ float add_batch(float s, const float4 (&v)[kSumBatch4]) {
+#pragma unroll
+  for (uint32_t j = 0; j < kSumBatch4; j++) {
+    s += v[j].x;
+    s += v[j].y;
+    s += v[j].z;
+    s += v[j].w;
+  }
+  return s;
+}
+
+__device__ __forceinline__ float ordered_sum(const float* p, uint32_t n, float s) {
+  uint32_t i = 0;
+  if (n >= kSumBatch) {
+    float4 a[kSumBatch4], b[kSumBatch4];
+    load_batch(p, a);
+    for (i = kSumBatch; i + 2u * kSumBatch <= n; i += 2u * kSumBatch) {
+      load_batch(p + i, b);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add_batch(s, a);
+      load_batch(p + i + kSumBatch, a);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add_batch(s, b);
+    }
+    if (i + kSumBatch <= n) {
+      load_batch(p + i, b);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add_batch(s, a);
+      s = add_batch(s, b);
+      i += kSumBatch;
+    } else {
+      s = add_batch(s, a);
+    }
+  }
+  for (; i < n; i++) s += p[i];
+  return s;
+}
 
 
 // Token rows of token_embd into hidden (Matrix::copy_row, weights.rs:120-150).
@@ -84,47 +137,79 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint
 
 // hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t]),
 // then normed[t] = normalize(hidden[t], weight) for tokens t >= norm_from.
-// One workgroup per token.
-__global__ __launch_bounds__(256) void add_norm_kernel(float* hidden, const float* delta, uint32_t n, uint32_t width,
-                                                       const float* weight, float eps, uint32_t norm_from,
-                                                       float* normed) {
+// One workgroup per token; each thread keeps its PER elements (e = tid +
+// 256k) in registers from the first load to the last store, so every global
+// load is issued up front.
+constexpr uint32_t kMaxNormPer = 32;  // widths up to 256 * 32 = 8192
+
+template <uint32_t PER>
+__global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restrict__ hidden,
+                                                                const float* __restrict__ delta, uint32_t n,
+                                                                uint32_t width, const float* __restrict__ weight,
+                                                                float eps, uint32_t norm_from,
+                                                                float* __restrict__ normed) {
   extern __shared__ __align__(16) float sq[];
   __shared__ float s_rms;
-  const uint32_t t = blockIdx.x;
+  const uint32_t t = blockIdx.x, tid = threadIdx.x;
   float* h = hidden + static_cast<size_t>(t) * width;
-  for (uint32_t e = threadIdx.x; e < width; e += kNormThreads) {
-    float v = h[e];
-    if (delta) {
-      v += delta[static_cast<size_t>(e) * n + t];
-      h[e] = v;
+  const bool norm = t >= norm_from;  // uniform over the workgroup
+  float v[PER], wt[PER], dl[PER];
+#pragma unroll
+  for (uint32_t k = 0; k < PER; k++) {
+    const uint32_t e = tid + k * kNormThreads;
+    if (e < width) {
+      v[k] = h[e];
+      if (delta) dl[k] = delta[static_cast<size_t>(e) * n + t];
+      if (norm) wt[k] = weight[e];
     }
-    const float s = v * v;
-    sq[e] = s;
   }
-  if (t < norm_from) return;  // uniform over the workgroup
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    // the squares summed in order from -0.0 (f32 Sum), one lane
-    float sum = -0.0f;
-    uint32_t e = 0;
-    for (; e + 4u <= width; e += 4u) {
-      const float4 v4 = *reinterpret_cast<const float4*>(sq + e);
-      sum += v4.x;
-      sum += v4.y;
-      sum += v4.z;
-      sum += v4.w;
+  if (delta) {
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++) {
+      const uint32_t e = tid + k * kNormThreads;
+      if (e < width) {
+        v[k] += dl[k];
+        h[e] = v[k];
+      }
     }
-    for (; e < width; e++) sum += sq[e];
+  }
+  if (!norm) return;
+#pragma unroll
+  for (uint32_t k = 0; k < PER; k++) {
+    const uint32_t e = tid + k * kNormThreads;
+    if (e < width) {
+      const float s = v[k] * v[k];
+      sq[e] = s;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    // the squares summed in order from -0.0 (f32 Sum), one lane
+    const float sum = ordered_sum(sq, width, -0.0f);
     const float mean = __fdiv_rn(sum, static_cast<float>(width));
     s_rms = sqrt_rn(mean + eps);
   }
   __syncthreads();
   const float rms = s_rms;
   float* o = normed + static_cast<size_t>(t - norm_from) * width;
-  for (uint32_t e = threadIdx.x; e < width; e += kNormThreads) {
-    const float v = __fdiv_rn(h[e], rms);
-    o[e] = v * weight[e];
+#pragma unroll
+  for (uint32_t k = 0; k < PER; k++) {
+    const uint32_t e = tid + k * kNormThreads;
+    if (e < width) {
+      const float x = __fdiv_rn(v[k], rms);
+      o[e] = x * wt[k];
+    }
   }
+}
+
+using AddNormFn = void (*)(float*, const float*, uint32_t, uint32_t, const float*, float, uint32_t, float*);
+
+// The add_norm_kernel instance for a row width (<= 256 * kMaxNormPer).
+AddNormFn add_norm_for(uint32_t width) {
+  if (width <= 4u * kNormThreads) return add_norm_kernel<4>;
+  if (width <= 8u * kNormThreads) return add_norm_kernel<8>;
+  if (width <= 16u * kNormThreads) return add_norm_kernel<16>;
+  return add_norm_kernel<kMaxNormPer>;
 }
 
 // q/k/v from the projections (stored by weight row, x[e*n + t]): q rotated
@@ -157,33 +242,102 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const float* qr, const fl
   }
 }
 
-// One wave per (query head, token): scores over cached rows 0..=start+t,
-// softmax, then the weighted sum of value rows (attention.rs:41-57,189-207).
-__global__ __launch_bounds__(64) void attention_kernel(const float* q, const float* kcache, const float* vcache,
-                                                       uint32_t width, uint32_t kv, uint32_t head_dim,
-                                                       uint32_t group, float scale, uint32_t start, float* mixed) {
-  extern __shared__ float sh[];  // q head [64] | weights [rows]
-  float* qh = sh;
-  float* w = sh + 64;
-  const uint32_t h = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+constexpr uint32_t kAttnThreads = 256;
+constexpr uint32_t kVTile = 64;  // value rows per LDS tile
+constexpr size_t kMaxAttentionLds = 65536;  // bytes of dynamic LDS per workgroup
+
+// LDS floats attention_kernel needs for `rows` cached rows: the query head,
+// a reduction area, the weights, and two value tiles.
+inline size_t attention_lds_floats(size_t rows) { return 128u + ((rows + 3u) & ~size_t{3}) + 2u * kVTile * 64u; }
+
+// Value rows r0..r0+count of one kv head into registers, one tile's share
+// per thread (HD = 64: 16 float4 per row, 16 threads a row).
+template <uint32_t HD>
+struct VTileRegs {
+  static constexpr uint32_t kPer = HD ? kVTile * HD / 4u / kAttnThreads : kVTile * 64u / kAttnThreads;
+  using T = typename std::conditional<HD != 0, float4, float>::type;
+  T v[kPer];
+  __device__ __forceinline__ void load(const float* vcache, uint32_t kv, uint32_t off, uint32_t hd, uint32_t r0,
+                                       uint32_t count) {
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; k++) {
+      const uint32_t f = threadIdx.x + k * kAttnThreads;
+      if constexpr (HD != 0) {
+        const uint32_t r = f / (HD / 4u), c = f % (HD / 4u);
+        if (r < count)
+          v[k] = *reinterpret_cast<const T*>(vcache + static_cast<size_t>(r0 + r) * kv + off + 4u * c);
+      } else {
+        const uint32_t r = f / hd, c = f % hd;
+        if (r < count && f < kVTile * hd) v[k] = vcache[static_cast<size_t>(r0 + r) * kv + off + c];
+      }
+    }
+  }
+  __device__ __forceinline__ void store(float* tile, uint32_t hd, uint32_t count) const {
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; k++) {
+      const uint32_t f = threadIdx.x + k * kAttnThreads;
+      if constexpr (HD != 0) {
+        if (f / (HD / 4u) < count) reinterpret_cast<T*>(tile)[f] = v[k];
+      } else {
+        if (f / hd < count && f < kVTile * hd) tile[f] = v[k];
+      }
+    }
+  }
+};
+
+// One workgroup per (query head, token): scores over cached rows
+// 0..=start+t, softmax, then the weighted sum of value rows
+// (attention.rs:41-57,189-207). HD = 64 specializes head_dim; HD = 0 reads
+// it at run time (any even head_dim <= 64).
+template <uint32_t HD>
+__global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q, const float* kcache,
+                                                                 const float* vcache, uint32_t width, uint32_t kv,
+                                                                 uint32_t head_dim, uint32_t group, float scale,
+                                                                 uint32_t start, float* mixed) {
+  extern __shared__ __align__(16) float sh[];
+  const uint32_t hd = HD ? HD : head_dim;
+  const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t rows = start + t + 1u;
-  const uint32_t off = (h / group) * head_dim;
-  if (lane < head_dim) qh[lane] = q[static_cast<size_t>(t) * width + h * head_dim + lane];
+  float* qh = sh;          // [64]
+  float* red = sh + 64;    // [64]
+  float* w = sh + 128;     // [rows rounded up to 4]
+  float* vt = w + ((rows + 3u) & ~3u);  // [2][kVTile * 64]
+  const uint32_t off = (h / group) * hd;
+  if (tid < hd) qh[tid] = q[static_cast<size_t>(t) * width + h * hd + tid];
   __syncthreads();
   // dot (float.rs:23-36): eight fused lanes over whole chunks, lanes summed
-  // in order from -0.0, then the unfused tail summed from -0.0
-  const uint32_t chunks = head_dim / 8u;
+  // in order from -0.0, then the unfused tail summed from -0.0. One cached
+  // row per thread, its loads issued before the arithmetic.
   float mx = -INFINITY;
-  for (uint32_t i = lane; i < rows; i += 64u) {
+  for (uint32_t i = tid; i < rows; i += kAttnThreads) {
     const float* kr = kcache + static_cast<size_t>(i) * kv + off;
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    for (uint32_t c = 0; c < chunks; c++)
-#pragma unroll
-      for (int l = 0; l < 8; l++) acc[l] = __builtin_fmaf(qh[8u * c + l], kr[8u * c + l], acc[l]);
     float tail = -0.0f;
-    for (uint32_t e = 8u * chunks; e < head_dim; e++) {
-      const float p = qh[e] * kr[e];
-      tail += p;
+    if constexpr (HD == 64u) {
+      float4 k4[16];
+#pragma unroll
+      for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const float4*>(kr)[c];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        const float4 a = k4[2 * c], b = k4[2 * c + 1];
+        acc[0] = __builtin_fmaf(qh[8 * c + 0], a.x, acc[0]);
+        acc[1] = __builtin_fmaf(qh[8 * c + 1], a.y, acc[1]);
+        acc[2] = __builtin_fmaf(qh[8 * c + 2], a.z, acc[2]);
+        acc[3] = __builtin_fmaf(qh[8 * c + 3], a.w, acc[3]);
+        acc[4] = __builtin_fmaf(qh[8 * c + 4], b.x, acc[4]);
+        acc[5] = __builtin_fmaf(qh[8 * c + 5], b.y, acc[5]);
+        acc[6] = __builtin_fmaf(qh[8 * c + 6], b.z, acc[6]);
+        acc[7] = __builtin_fmaf(qh[8 * c + 7], b.w, acc[7]);
+      }
+    } else {
+      const uint32_t chunks = hd / 8u;
+      for (uint32_t c = 0; c < chunks; c++)
+#pragma unroll
+        for (int l = 0; l < 8; l++) acc[l] = __builtin_fmaf(qh[8u * c + l], kr[8u * c + l], acc[l]);
+      for (uint32_t e = 8u * chunks; e < hd; e++) {
+        const float p = qh[e] * kr[e];
+        tail += p;
+      }
     }
     float s = -0.0f;
 #pragma unroll
@@ -192,28 +346,50 @@ __global__ __launch_bounds__(64) void attention_kernel(const float* q, const flo
     w[i] = score;
     mx = fmaxf(mx, score);
   }
-  // max over the lanes (exact in any order)
+  // max over the workgroup (exact in any order)
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  for (uint32_t i = lane; i < rows; i += 64u) w[i] = expf_ref(w[i] - mx);
+  if (lane == 0) red[wave] = mx;
   __syncthreads();
-  __shared__ float s_sum;
-  if (lane == 0) {
-    float sum = 0.0f;  // portable/norm.rs: `let mut sum = 0.0`
-    for (uint32_t i = 0; i < rows; i++) sum += w[i];
-    s_sum = sum;
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (uint32_t i = tid; i < rows; i += kAttnThreads) w[i] = expf_ref(w[i] - mx);
+  __syncthreads();
+  if (tid == 0) red[4] = ordered_sum(w, rows, 0.0f);  // portable/norm.rs: `let mut sum = 0.0`
+  __syncthreads();
+  const float sum = red[4];
+  for (uint32_t i = tid; i < rows; i += kAttnThreads) w[i] = __fdiv_rn(w[i], sum);
+  // mix_rows (float.rs:52-62): out starts at 0.0, each row fused in order.
+  // Value tiles are staged through LDS by every thread, a tile ahead of
+  // the first wave's chain of fused adds.
+  const uint32_t tiles = (rows + kVTile - 1u) / kVTile;
+  VTileRegs<HD> regs;
+  regs.load(vcache, kv, off, hd, 0u, rows < kVTile ? rows : kVTile);
+  regs.store(vt, hd, rows < kVTile ? rows : kVTile);
+  __syncthreads();
+  float acc = 0.0f;
+  for (uint32_t tile = 0; tile < tiles; tile++) {
+    const uint32_t r0 = tile * kVTile;
+    const uint32_t count = rows - r0 < kVTile ? rows - r0 : kVTile;
+    const bool more = tile + 1u < tiles;
+    const uint32_t nr0 = r0 + kVTile, ncount = more ? (rows - nr0 < kVTile ? rows - nr0 : kVTile) : 0u;
+    if (more) regs.load(vcache, kv, off, hd, nr0, ncount);
+    if (wave == 0 && lane < hd) {
+      const float* cur = vt + (tile & 1u) * kVTile * 64u;
+      const float* wr = w + r0;
+      uint32_t r = 0;
+      for (; r + 16u <= count; r += 16u) {
+        float v[16];
+#pragma unroll
+        for (int k = 0; k < 16; k++) v[k] = cur[(r + k) * hd + lane];
+#pragma unroll
+        for (int k = 0; k < 16; k++) acc = __builtin_fmaf(v[k], wr[r + k], acc);
+      }
+      for (; r < count; r++) acc = __builtin_fmaf(cur[r * hd + lane], wr[r], acc);
+    }
+    if (more) regs.store(vt + ((tile + 1u) & 1u) * kVTile * 64u, hd, ncount);
+    __syncthreads();
   }
-  __syncthreads();
-  const float sum = s_sum;
-  for (uint32_t i = lane; i < rows; i += 64u) w[i] = __fdiv_rn(w[i], sum);
-  __syncthreads();
-  // mix_rows (float.rs:52-62): out starts at 0.0, each row fused in order
-  if (lane < head_dim) {
-    float acc = 0.0f;
-    const float* vr = vcache + off + lane;
-    for (uint32_t i = 0; i < rows; i++) acc = __builtin_fmaf(vr[static_cast<size_t>(i) * kv], w[i], acc);
-    mixed[static_cast<size_t>(t) * width + h * head_dim + lane] = acc;
-  }
+  if (wave == 0 && lane < hd) mixed[static_cast<size_t>(t) * width + h * hd + lane] = acc;
 }
 
 // hf[t][e] = silu(gate) * up, both stored by weight row (x[e*n + t])
@@ -248,14 +424,25 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint3
   int32_t best = INT32_MIN;
   uint32_t bi = 0, fin = 0;
   bool have = false;
-  for (uint32_t i = threadIdx.x; i < n; i += 1024u) {
-    const float v = logits[i];
-    fin |= __builtin_isfinite(v) ? 1u : 0u;
-    const int32_t k = total_key(v != v ? -INFINITY : v);
-    if (!have || k >= best) {
-      best = k;
-      bi = i;
-      have = true;
+  // each thread visits its indices in increasing order, eight loads at once
+  for (uint32_t base = threadIdx.x; base < n; base += 8u * 1024u) {
+    float v[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8u; j++) {
+      const uint32_t i = base + j * 1024u;
+      if (i < n) v[j] = logits[i];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 8u; j++) {
+      const uint32_t i = base + j * 1024u;
+      if (i >= n) break;
+      fin |= __builtin_isfinite(v[j]) ? 1u : 0u;
+      const int32_t k = total_key(v[j] != v[j] ? -INFINITY : v[j]);
+      if (!have || k >= best) {
+        best = k;
+        bi = i;
+        have = true;
+      }
     }
   }
   // (key, index) maximum: a larger key, or an equal key at a larger index
@@ -399,9 +586,9 @@ rh_status mm(rh_decoder* d, const float* in, size_t n, size_t width, std::initia
   } while (0)
 
 // Decoder::forward_on_pool (decoder.rs:74-107) for n tokens whose ids are
-// already in d->tokens, at positions start..start+n; leaves the last token's
+// in device memory at `tokens`, at positions start..start+n; leaves the last token's
 // logits in d->logits.
-rh_status forward_device(rh_decoder* d, size_t n, size_t start) {
+rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t start) {
   const rh_decoder_config& c = d->c;
   const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
   const uint32_t f = static_cast<uint32_t>(c.feed_forward_length), hd = static_cast<uint32_t>(c.head_dim);
@@ -409,14 +596,15 @@ rh_status forward_device(rh_decoder* d, size_t n, size_t start) {
   hipStream_t s = d->stream;
   const rh_matrix* E = d->token_embd;
   hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, nn), dim3(256), 0, s, rh_matrix_type(E),
-                     matrix_data(E), matrix_stride(E), d->tokens, w, d->hidden);
+                     matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
   RHD(hipGetLastError());
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
   const size_t norm_lds = static_cast<size_t>(w) * 4u;
+  const AddNormFn norm_fn = add_norm_for(w);
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
     const rh_decoder::Block& b = d->blocks[l];
-    hipLaunchKernelGGL(add_norm_kernel, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+    hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
                        b.attn_norm, c.rms_norm_eps, 0u, d->normed);
     RHD(hipGetLastError());
     RHS(mm(d, d->normed, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
@@ -426,13 +614,14 @@ rh_status forward_device(rh_decoder* d, size_t n, size_t start) {
     hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn, w,
                        kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
     RHD(hipGetLastError());
-    const size_t att_lds = (64u + start + n) * 4u;
-    hipLaunchKernelGGL(attention_kernel, dim3(static_cast<uint32_t>(c.head_count), nn), dim3(64), att_lds, s, d->q,
-                       kc, vc, w, kv, hd, static_cast<uint32_t>(c.head_count / c.head_count_kv), scale,
+    const size_t att_lds = attention_lds_floats(start + n) * 4u;
+    hipLaunchKernelGGL(hd == 64u ? attention_kernel<64> : attention_kernel<0>,
+                       dim3(static_cast<uint32_t>(c.head_count), nn), dim3(kAttnThreads), att_lds, s, d->q, kc, vc,
+                       w, kv, hd, static_cast<uint32_t>(c.head_count / c.head_count_kv), scale,
                        static_cast<uint32_t>(start), d->mixed);
     RHD(hipGetLastError());
     RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
-    hipLaunchKernelGGL(add_norm_kernel, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, d->delta, nn, w,
+    hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, d->delta, nn, w,
                        b.ffn_norm, c.rms_norm_eps, 0u, d->normed);
     RHD(hipGetLastError());
     RHS(mm(d, d->normed, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
@@ -444,7 +633,7 @@ rh_status forward_device(rh_decoder* d, size_t n, size_t start) {
     pending = d->delta;
   }
   // the last residual for every token, then the last token's output norm
-  hipLaunchKernelGGL(add_norm_kernel, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+  hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
                      d->output_norm, c.rms_norm_eps, nn - 1u, d->normed);
   RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
@@ -510,10 +699,14 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
   *out = nullptr;
   const rh_decoder_config& c = *config;
   // DecoderConfig::validate (transformer/src/config.rs:55-80), plus this
-  // kernel set's limits: head_dim <= 64, f32/Q4_K/Q6_K embedding rows
+  // kernel set's limits: head_dim <= 64, embedding_length <= 8192, attention
+  // weights for the whole context in LDS (context_length <= 8064),
+  // f32/Q4_K/Q6_K embedding rows
   if (c.head_count == 0 || c.head_count_kv == 0 || c.head_count % c.head_count_kv != 0 || c.head_dim == 0 ||
       c.head_dim % 2 != 0 || c.head_count * c.head_dim != c.embedding_length || c.block_count == 0 ||
-      c.feed_forward_length == 0 || c.context_length == 0 || c.vocab_size == 0 || c.head_dim > 64)
+      c.feed_forward_length == 0 || c.context_length == 0 || c.vocab_size == 0 || c.head_dim > 64 ||
+      c.embedding_length > kMaxNormPer * kNormThreads ||
+      attention_lds_floats(c.context_length) * 4u > kMaxAttentionLds)
     return RH_ERR_INVALID_CONFIG;
   const uint32_t et = rh_matrix_type(weights->token_embd);
   if ((et != RH_TYPE_F32 && et != RH_TYPE_Q4_K && et != RH_TYPE_Q6_K) ||
@@ -598,7 +791,7 @@ rh_status rh_decoder_forward_batch(rh_decoder* d, const uint32_t* tokens, size_t
   if (hipSetDevice(ctx_device(d->ctx)) != hipSuccess) return RH_ERR_DEVICE;
   if (ensure_acts(d, n) != hipSuccess) return RH_ERR_OUT_OF_MEMORY;
   RHD(hipMemcpyAsync(d->tokens, tokens, n * 4, hipMemcpyHostToDevice, d->stream));
-  RHS(forward_device(d, n, start));
+  RHS(forward_device(d, d->tokens, n, start));
   const size_t m = logits_len < d->c.vocab_size ? logits_len : d->c.vocab_size;
   if (m) RHD(hipMemcpyAsync(logits, d->logits, m * 4, hipMemcpyDeviceToHost, d->stream));
   RHD(hipStreamSynchronize(d->stream));
@@ -630,7 +823,7 @@ rh_status rh_decoder_generate_greedy(rh_decoder* d, const uint32_t* prompt, size
   for (size_t st = 0; st < n; st += kPrefillChunk) {
     const size_t m = n - st < kPrefillChunk ? n - st : kPrefillChunk;
     RHD(hipMemcpyAsync(d->tokens, prompt + st, m * 4, hipMemcpyHostToDevice, s));
-    RHS(forward_device(d, m, st));
+    RHS(forward_device(d, d->tokens, m, st));
   }
   RHD(hipMemsetAsync(d->count, 0, 8, s));
   // decode_loop (generate.rs:83-111): pick, then forward the pick; the pick
@@ -643,8 +836,7 @@ rh_status rh_decoder_generate_greedy(rh_decoder* d, const uint32_t* prompt, size
     RHD(hipGetLastError());
     emitted++;
     if (position == d->c.context_length) break;
-    RHD(hipMemcpyAsync(d->tokens, d->pick, 4, hipMemcpyDeviceToDevice, s));
-    RHS(forward_device(d, 1, position));
+    RHS(forward_device(d, d->pick, 1, position));
     position++;
   }
   uint32_t flag[2] = {0, 0};
