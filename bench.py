@@ -17,6 +17,11 @@ GEMV kernel, measured with HIP events on the stream it is launched on.
 summary in profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy of
 known size), when that summary covers the workload.
 
+`also.prefill_gemm` is the MFMA path at the prefill shapes: Q4_K 5632x2048
+weights against 128, 512 and 2048 tokens (the whole matmul_batch step and the
+GEMM kernel alone on pre-quantized activations), as int8 MFMA utilisation
+against the 5.0 POPS dense peak, counting 2*rows*cols*tokens operations.
+
 `also.e2e_decode` is the metric's second half: greedy decode of a random-init
 TinyLlama-1.1B-shaped model in the Q4_K_M mix (22 layers, 2048 hidden, 32/4
 heads of 64, FFN 5632, vocab 32000; Q6_K lm_head and even-layer ffn_down),
@@ -190,6 +195,49 @@ def measure_cpu(res: dict, seconds: float):
     }
 
 
+INT8_PEAK_TOPS = 5000.0
+
+
+def measure_gemm(ctx, token_counts=(128, 512, 2048), reps: int = 20):
+    """Prefill GEMM (k-quant MFMA path) on the ffn_gate shape in Q4_K."""
+    import rusticide_amd as R
+    from rusticide_amd import hip as H
+    from rusticide_amd import synth
+
+    rows, cols = 5632, 2048
+    data = synth.matrix(12, rows, cols, seed=1)
+    mats = [R.Matrix.load(ctx, 12, data, rows, cols) for _ in range(4)]
+    stream = ctx.stream
+    res = []
+    for T in token_counts:
+        x = H.DeviceArray.from_numpy(synth.normal_f32(T * cols, seed=2))
+        out = H.DeviceArray(rows * T)
+        q8 = R.Q8(ctx).quantize(x, T, R.SUPER_BLOCK)
+
+        def timed(fn):
+            for i in range(3):
+                fn(i)
+            a, b = H.Event(), H.Event()
+            a.record(stream)
+            for i in range(reps):
+                fn(i)
+            b.record(stream)
+            H.synchronize()
+            return 1e3 * a.elapsed_ms(b) / reps
+
+        k_us = timed(lambda i: R.dot_matrix_device(mats[i % 4], q8, out))
+        s_us = timed(lambda i: R.matmul_batch_device(ctx, x, T, [(mats[i % 4], out)]))
+        ops = 2.0 * rows * cols * T
+        res.append({"tokens": T, "gemm_kernel_us": round(k_us, 2), "step_us": round(s_us, 2),
+                    "kernel_tops": round(ops / k_us / 1e6, 1),
+                    "mfma_frac": round(ops / k_us / 1e6 / INT8_PEAK_TOPS, 4),
+                    "step_tokens_per_s": round(T / s_us * 1e6)})
+        q8.free()
+    for m in mats:
+        m.free()
+    return res
+
+
 def decode_bytes_per_token(model: dict, position: int) -> int:
     """Compulsory HBM bytes of one decode step: every layer matrix, the output
     matrix, the norms, one embedding row and the f32 KV rows read at
@@ -283,8 +331,8 @@ def traffic_for(name: str):
 
 def pmc_probe(steps: int) -> int:
     """A short, fixed sequence for `rocprofv3 --pmc` runs: the headline step on
-    rotating copies, then device-to-device copies of a known size (the
-    calibration for the counters)."""
+    rotating copies, the prefill GEMM at 2048 tokens, then device-to-device
+    copies of a known size (the calibration for the counters)."""
     import rusticide_amd as R
     from rusticide_amd import hip as H
     from rusticide_amd import synth
@@ -301,6 +349,18 @@ def pmc_probe(steps: int) -> int:
         for m in mats:
             m.free()
         log(f"[pmc] {name}: {steps} steps")
+    # the prefill GEMM at 2048 tokens, for its MFMA / VALU / LDS counters
+    rows, cols, T = 5632, 2048, 2048
+    m = R.Matrix.load(ctx, 12, synth.matrix(12, rows, cols, seed=1), rows, cols)
+    x = H.DeviceArray.from_numpy(synth.normal_f32(T * cols, seed=2))
+    out = H.DeviceArray(rows * T)
+    q8 = R.Q8(ctx).quantize(x, T, R.SUPER_BLOCK)
+    for _ in range(5):
+        R.dot_matrix_device(m, q8, out)
+    H.synchronize()
+    q8.free()
+    m.free()
+    log(f"[pmc] prefill GEMM Q4_K {rows}x{cols} x {T} tokens: 5 launches")
     n = 256 * 2 ** 20
     a, b = H.DeviceArray(n // 4), H.DeviceArray(n // 4)
     a.fill_bytes(1)
@@ -322,6 +382,7 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc", action="store_true", help="run the short sequence rocprofv3 --pmc profiles")
     ap.add_argument("--decode-reps", type=int, default=5, help="timed 64+128-token generations (0 skips)")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -349,6 +410,11 @@ def main() -> int:
             f"warm {r['warm_kernel_us']:.2f} us = {r['warm_kernel_gbs']:.0f} GB/s; "
             f"pre-quantized GEMV alone {r['prequantized_gemv_us']:.2f} us")
     h = results[HEADLINE]
+    gemm = None if args.no_gemm else measure_gemm(ctx)
+    if gemm:
+        for g in gemm:
+            log(f"[bench] prefill GEMM Q4_K 5632x2048 x {g['tokens']} tokens: kernel {g['gemm_kernel_us']} us "
+                f"({g['kernel_tops']} TOPS, {100 * g['mfma_frac']:.1f}% of int8 peak), step {g['step_us']} us")
     e2e = None
     if args.decode_reps > 0:
         e2e = measure_decode(ctx, args.decode_reps)
@@ -367,6 +433,10 @@ def main() -> int:
             "kernel": r["kernel"], "hbm_traffic_bytes": traffic_for(n)}
         for n, r in results.items() if n != HEADLINE
     }
+    if gemm is not None:
+        also["prefill_gemm"] = {"workload": "Q4_K 5632x2048 (TinyLlama ffn_gate) x N tokens, int8 MFMA, "
+                                            "bit-identical to the CPU path", "by_tokens": gemm,
+                                "peak_tops": INT8_PEAK_TOPS}
     if e2e is not None:
         also["e2e_decode"] = {
             "workload": "TinyLlama-1.1B-shaped Q4_K_M random-init model, 64-token prompt + 128 greedy tokens, "

@@ -321,6 +321,9 @@ def _dec_lib():
         L.orc_rope_adjacent.argtypes = [P, S, S, ctypes.c_float, S]
         L.orc_rope_table.argtypes = [S, S, ctypes.c_float, P, P]
         L.orc_expf_array.argtypes = [P, P, S]
+        L.orc_silu_array.argtypes = [P, P, S]
+        L.orc_dot_rows.argtypes = [P, S, P, S, S, S, ctypes.c_float, P]
+        L.orc_mix_rows.argtypes = [P, S, P, S, S, S, P, S]
         L._dec_ready = True
     return L
 
@@ -437,6 +440,32 @@ def rope_table(positions: int, columns: int, theta: float):
     s = np.zeros(positions * pairs, np.float32)
     _dec_lib().orc_rope_table(positions, columns, theta, c.ctypes.data, s.ctypes.data)
     return c, s
+
+
+def silu(x) -> np.ndarray:
+    """portable/elementwise.rs:6-9 over an array."""
+    x = _f32(x)
+    y = np.zeros_like(x)
+    _dec_lib().orc_silu_array(x.ctypes.data, y.ctypes.data, len(x))
+    return y
+
+
+def dot_rows(query, rows, row_stride: int, offset: int, scale: float, n_out: int) -> np.ndarray:
+    """float.rs:38-58 over the whole row_stride-wide rows of `rows`, at most n_out of them."""
+    q, r = _f32(query), _f32(rows)
+    nrows = min(n_out, len(r) // max(row_stride, 1))
+    out = np.zeros(n_out, np.float32)
+    _dec_lib().orc_dot_rows(q.ctypes.data, len(q), r.ctypes.data, nrows, row_stride, offset, scale, out.ctypes.data)
+    return out
+
+
+def mix_rows(weights, rows, row_stride: int, offset: int, out) -> np.ndarray:
+    """float.rs:60-68 into a copy of `out`."""
+    w, r = _f32(weights), _f32(rows)
+    o = _f32(out).copy()
+    nrows = len(r) // max(row_stride, 1)
+    _dec_lib().orc_mix_rows(w.ctypes.data, len(w), r.ctypes.data, nrows, row_stride, offset, o.ctypes.data, len(o))
+    return o
 
 
 def expf(x) -> np.ndarray:

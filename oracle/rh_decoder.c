@@ -167,6 +167,41 @@ static float silu(float v)
     return v / den;
 }
 
+void orc_silu_array(const float *x, float *y, size_t n)
+{
+    for (size_t i = 0; i < n; i++) y[i] = silu(x[i]);
+}
+
+/* rusticide-simd/src/float.rs:38-58 dot_rows: out[i] = dot(query,
+ * rows_i[offset..offset+qlen]) / scale over nrows stride-wide rows (a zero
+ * stride counts as one); a window past the row, or whose end overflows,
+ * scores dot(query, []) / scale. */
+void orc_dot_rows(const float *query, size_t qlen, const float *rows, size_t nrows, size_t stride, size_t offset,
+                  float scale, float *out)
+{
+    if (stride == 0) stride = 1;
+    const size_t end = offset + qlen;
+    const int fits = end >= offset && end <= stride;
+    for (size_t i = 0; i < nrows; i++) {
+        const float *row = rows + i * stride;
+        out[i] = (fits ? orc_dot_f32(query, qlen, row + offset, qlen) : orc_dot_f32(query, 0, row, 0)) / scale;
+    }
+}
+
+/* float.rs:60-68 mix_rows: for rows i = 0.. in order, out[e] = fma(rows_i[offset
+ * + e], weights[i], out[e]); min(nw, nrows) rows, windows past the row (or
+ * whose end overflows) skipped, a zero stride counted as one. */
+void orc_mix_rows(const float *weights, size_t nw, const float *rows, size_t nrows, size_t stride, size_t offset,
+                  float *out, size_t n)
+{
+    if (stride == 0) stride = 1;
+    const size_t end = offset + n;
+    if (end < offset || end > stride) return;
+    const size_t m = nw < nrows ? nw : nrows;
+    for (size_t i = 0; i < m; i++)
+        for (size_t e = 0; e < n; e++) out[e] = fmaf(rows[i * stride + offset + e], weights[i], out[e]);
+}
+
 /* layout.rs:9-27: out[row * tokens + token] -> one row per token. */
 static void to_token_major(const float *by_row, size_t rows, size_t tokens, float *by_token)
 {
@@ -244,12 +279,11 @@ int orc_decoder_forward_batch(orc_decoder *d, const uint32_t *tokens, size_t n, 
             for (size_t h = 0; h < heads; h++) {
                 size_t rows = start + t + 1, off = (h / group) * hd;
                 const float *qh = q + t * width + h * hd;
-                for (size_t i = 0; i < rows; i++) scores[i] = orc_dot_f32(qh, hd, kc + i * kv + off, hd) / scale;
+                orc_dot_rows(qh, hd, kc, rows, kv, off, scale, scores);
                 orc_softmax(scores, rows);
                 float *mh = mixed + t * width + h * hd;
                 for (size_t e = 0; e < hd; e++) mh[e] = 0.0f;
-                for (size_t i = 0; i < rows; i++)
-                    for (size_t e = 0; e < hd; e++) mh[e] = fmaf(vc[i * kv + off + e], scores[i], mh[e]);
+                orc_mix_rows(scores, rows, vc, rows, kv, off, mh, hd);
             }
         orc_job oj = mat_job(&b->attn_output, orows, n * width);
         orc_matmul_batch(mixed, n * width, n, &oj, 1, d->threads);

@@ -161,6 +161,11 @@ void orc_softmax(float *row, size_t n);
 void orc_rope_adjacent(float *row, size_t len, size_t position, float theta, size_t dim_pairs);
 void orc_rope_table(size_t positions, size_t columns, float theta, float *cos_out, float *sin_out);
 void orc_expf_array(const float *x, float *y, size_t n);
+void orc_silu_array(const float *x, float *y, size_t n);
+void orc_dot_rows(const float *query, size_t qlen, const float *rows, size_t nrows, size_t stride, size_t offset,
+                  float scale, float *out);
+void orc_mix_rows(const float *weights, size_t nw, const float *rows, size_t nrows, size_t stride, size_t offset,
+                  float *out, size_t n);
 
 #ifdef __cplusplus
 }

@@ -144,3 +144,57 @@ def test_generation_prefills_in_chunks_and_stops_at_the_context(tiny):
     assert np.array_equal(got, np.array(seq, np.uint32))
     with pytest.raises(O.DecoderError):
         d.generate_greedy(list(range(16)), 3)
+
+
+def test_dot_rows_known_answers():
+    # float.rs:91-112: stride windows, offsets past the row or overflowing
+    rows = [1.0, 2.0, 9.0, 3.0, 4.0, 9.0]
+    assert O.dot_rows([1.0, 1.0], rows, 3, 0, 2.0, 2).tolist() == [1.5, 3.5]
+    assert O.dot_rows([1.0], rows, 3, 2, 1.0, 2).tolist() == [9.0, 9.0]
+    assert O.dot_rows([1.0], [1.0, 2.0], 2, 5, 1.0, 1).tolist() == [0.0]
+    assert O.dot_rows([1.0], [1.0, 2.0], 2, 2 ** 64 - 1, 1.0, 1).tolist() == [0.0]
+
+
+def test_dot_rows_scores_each_head_window_of_a_wide_row():
+    # float.rs:160-172 shape: 48 values as two 24-wide rows, 12-wide heads
+    rows = np.arange(1, 49, dtype=np.float32)
+    q = np.ones(12, np.float32)
+    for offset in (0, 12):
+        want = [float(np.sum(rows[i * 24 + offset:i * 24 + offset + 12])) for i in range(2)]
+        assert O.dot_rows(q, rows, 24, offset, 1.0, 2).tolist() == want
+
+
+def test_mix_rows_known_answers():
+    # float.rs:115-151
+    rows = [1.0, 2.0, 9.0, 3.0, 4.0, 9.0]
+    assert O.mix_rows([2.0, 0.5], rows, 3, 0, [10.0, 20.0]).tolist() == [13.5, 26.0]
+    assert O.mix_rows([1.0, 1.0], rows, 3, 2, [0.0]).tolist() == [18.0]
+    assert O.mix_rows([1.0], [1.0, 2.0], 2, 5, [5.0]).tolist() == [5.0]
+    assert O.mix_rows([1.0], [1.0, 2.0], 2, 2 ** 64 - 1, [5.0]).tolist() == [5.0]
+    assert O.mix_rows([1.0], [1.0, 2.0], 0, 0, [5.0]).tolist() == [6.0]
+
+
+def test_mix_rows_is_fused_in_row_order():
+    # float.rs:126-142: each product fused into its slot (one rounding), rows
+    # in order; an unfused or reordered sum differs on these values
+    rows = (np.arange(1, 49, dtype=np.float32) / np.float32(7.0)).astype(np.float32)
+    w = np.float32([0.3, 0.7])
+    for offset in (0, 12):
+        want = np.zeros(12, np.float64)
+        for i in range(2):
+            seg = rows[i * 24 + offset:i * 24 + offset + 12].astype(np.float64)
+            want = (seg * np.float64(w[i]) + want).astype(np.float32).astype(np.float64)  # exact product, one rounding
+        got = O.mix_rows(w, rows, 24, offset, np.zeros(12, np.float32))
+        assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32))
+
+
+def test_silu_known_answers():
+    # elementwise.rs:43-56: silu(0) = 0; silu(2) = 2 / (1 + exp(-2)) in f32
+    assert O.silu([0.0]).tolist() == [0.0]
+    e = O.expf([-2.0])[0]
+    want = np.float32(2.0) / (np.float32(1.0) + e)
+    assert O.silu([2.0, 2.0]).view(np.uint32).tolist() == [np.float32(want).view(np.uint32)] * 2
+    # SiLU is x * sigmoid(x): odd part plus x/2, checked in f64 on a spread
+    x = np.linspace(-20, 20, 4001, dtype=np.float32)
+    ref = x.astype(np.float64) / (1.0 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(O.silu(x) - ref) / np.maximum(np.abs(ref), 1e-30)) < 4e-7
