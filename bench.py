@@ -18,9 +18,10 @@ summary in profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy of
 known size), when that summary covers the workload.
 
 `also.prefill_gemm` is the MFMA path at the prefill shapes: Q4_K 5632x2048
-weights against 128, 512 and 2048 tokens (the whole matmul_batch step and the
-GEMM kernel alone on pre-quantized activations), as int8 MFMA utilisation
-against the 5.0 POPS dense peak, counting 2*rows*cols*tokens operations.
+and I2_S 6912x2560 weights against 128, 512 and 2048 tokens (the whole
+matmul_batch step and the GEMM kernel alone on pre-quantized activations), as
+int8 MFMA utilisation against the 5.0 POPS dense peak, counting
+2*rows*cols*tokens operations.
 
 `also.e2e_decode` is the metric's second half: greedy decode of a random-init
 TinyLlama-1.1B-shaped model in the Q4_K_M mix (22 layers, 2048 hidden, 32/4
@@ -198,43 +199,51 @@ def measure_cpu(res: dict, seconds: float):
 INT8_PEAK_TOPS = 5000.0
 
 
+GEMM_WORKLOADS = (
+    (12, 5632, 2048, "Q4_K 5632x2048 (TinyLlama ffn_gate)"),
+    (36, 6912, 2560, "I2_S 6912x2560 (BitNet 2B4T up/gate)"),
+)
+
+
 def measure_gemm(ctx, token_counts=(128, 512, 2048), reps: int = 20):
-    """Prefill GEMM (k-quant MFMA path) on the ffn_gate shape in Q4_K."""
+    """Prefill GEMMs (int8 MFMA): the k-quant path on the ffn_gate shape in
+    Q4_K and the ternary path on the BitNet up/gate shape."""
     import rusticide_amd as R
     from rusticide_amd import hip as H
     from rusticide_amd import synth
 
-    rows, cols = 5632, 2048
-    data = synth.matrix(12, rows, cols, seed=1)
-    mats = [R.Matrix.load(ctx, 12, data, rows, cols) for _ in range(4)]
     stream = ctx.stream
     res = []
-    for T in token_counts:
-        x = H.DeviceArray.from_numpy(synth.normal_f32(T * cols, seed=2))
-        out = H.DeviceArray(rows * T)
-        q8 = R.Q8(ctx).quantize(x, T, R.SUPER_BLOCK)
+    for type_id, rows, cols, desc in GEMM_WORKLOADS:
+        data = synth.i2s_matrix(rows, cols, seed=1) if type_id == 36 else synth.matrix(type_id, rows, cols, seed=1)
+        mats = [R.Matrix.load(ctx, type_id, data, rows, cols) for _ in range(4)]
+        kind = R.ROW if type_id == 36 else R.SUPER_BLOCK
+        for T in token_counts:
+            x = H.DeviceArray.from_numpy(synth.normal_f32(T * cols, seed=2))
+            out = H.DeviceArray(rows * T)
+            q8 = R.Q8(ctx).quantize(x, T, kind)
 
-        def timed(fn):
-            for i in range(3):
-                fn(i)
-            a, b = H.Event(), H.Event()
-            a.record(stream)
-            for i in range(reps):
-                fn(i)
-            b.record(stream)
-            H.synchronize()
-            return 1e3 * a.elapsed_ms(b) / reps
+            def timed(fn):
+                for i in range(3):
+                    fn(i)
+                a, b = H.Event(), H.Event()
+                a.record(stream)
+                for i in range(reps):
+                    fn(i)
+                b.record(stream)
+                H.synchronize()
+                return 1e3 * a.elapsed_ms(b) / reps
 
-        k_us = timed(lambda i: R.dot_matrix_device(mats[i % 4], q8, out))
-        s_us = timed(lambda i: R.matmul_batch_device(ctx, x, T, [(mats[i % 4], out)]))
-        ops = 2.0 * rows * cols * T
-        res.append({"tokens": T, "gemm_kernel_us": round(k_us, 2), "step_us": round(s_us, 2),
-                    "kernel_tops": round(ops / k_us / 1e6, 1),
-                    "mfma_frac": round(ops / k_us / 1e6 / INT8_PEAK_TOPS, 4),
-                    "step_tokens_per_s": round(T / s_us * 1e6)})
-        q8.free()
-    for m in mats:
-        m.free()
+            k_us = timed(lambda i: R.dot_matrix_device(mats[i % 4], q8, out))
+            s_us = timed(lambda i: R.matmul_batch_device(ctx, x, T, [(mats[i % 4], out)]))
+            ops = 2.0 * rows * cols * T
+            res.append({"workload": desc, "tokens": T, "gemm_kernel_us": round(k_us, 2), "step_us": round(s_us, 2),
+                        "kernel_tops": round(ops / k_us / 1e6, 1),
+                        "mfma_frac": round(ops / k_us / 1e6 / INT8_PEAK_TOPS, 4),
+                        "step_tokens_per_s": round(T / s_us * 1e6)})
+            q8.free()
+        for m in mats:
+            m.free()
     return res
 
 
@@ -413,7 +422,7 @@ def main() -> int:
     gemm = None if args.no_gemm else measure_gemm(ctx)
     if gemm:
         for g in gemm:
-            log(f"[bench] prefill GEMM Q4_K 5632x2048 x {g['tokens']} tokens: kernel {g['gemm_kernel_us']} us "
+            log(f"[bench] prefill GEMM {g['workload']} x {g['tokens']} tokens: kernel {g['gemm_kernel_us']} us "
                 f"({g['kernel_tops']} TOPS, {100 * g['mfma_frac']:.1f}% of int8 peak), step {g['step_us']} us")
     e2e = None
     if args.decode_reps > 0:
@@ -434,9 +443,8 @@ def main() -> int:
         for n, r in results.items() if n != HEADLINE
     }
     if gemm is not None:
-        also["prefill_gemm"] = {"workload": "Q4_K 5632x2048 (TinyLlama ffn_gate) x N tokens, int8 MFMA, "
-                                            "bit-identical to the CPU path", "by_tokens": gemm,
-                                "peak_tops": INT8_PEAK_TOPS}
+        also["prefill_gemm"] = {"workload": "int8 MFMA GEMMs x N tokens, bit-identical to the CPU path",
+                                "runs": gemm, "peak_tops": INT8_PEAK_TOPS}
     if e2e is not None:
         also["e2e_decode"] = {
             "workload": "TinyLlama-1.1B-shaped Q4_K_M random-init model, 64-token prompt + 128 greedy tokens, "

@@ -145,8 +145,9 @@ rh_status rh_quantize(rh_ctx *ctx, int kind, const float *x, size_t len, int8_t 
 rh_status rh_ternary_dot_i32(rh_ctx *ctx, const rh_matrix *m, const float *inputs,
                              size_t inputs_len, size_t tokens, int32_t *out, size_t out_len);
 
-/* Token count from which rh_matmul_batch* run k-quant matrices on the MFMA
- * GEMM instead of the GEMV kernels (both give the same bits); 9 by default.
+/* Token count from which rh_matmul_batch* run Q4_K, Q6_K and I2_S matrices on
+ * the MFMA GEMMs instead of the GEMV kernels (both give the same bits); 9 by
+ * default.
  * Process-wide. No counterpart in the reference (its row kernels serve every
  * batch size, crates/rusticide-kernels/src/matmul.rs:229-248). */
 size_t rh_gemm_min_tokens(void);

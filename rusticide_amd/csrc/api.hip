@@ -55,7 +55,7 @@ namespace {
 
 enum Scratch { kIn = 0, kOut, kQuants, kScales, kSums, kSums16, kRaw, kRowQ };
 
-// Batches of this many tokens or more run the k-quants on the MFMA GEMM.
+// Batches of this many tokens or more run Q4_K, Q6_K and I2_S on the MFMA GEMMs.
 size_t g_gemm_min_tokens = 9;
 
 rh_status fail(rh_ctx* ctx, rh_status st, const std::string& msg) {
@@ -175,6 +175,12 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
       if (is_kquant(kind) && tokens >= g_gemm_min_tokens) {
         RH_HIP(ctx, launch_gemm(kind, g, q, tokens, s));
+        g = GemvJobs{};
+        nbmax = 0;
+        return RH_OK;
+      }
+      if (kind == RH_TYPE_I2_S && tokens >= g_gemm_min_tokens) {
+        RH_HIP(ctx, launch_gemm_i2s(g, q, tokens, raw, s));
         g = GemvJobs{};
         nbmax = 0;
         return RH_OK;

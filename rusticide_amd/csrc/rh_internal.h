@@ -77,6 +77,9 @@ hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q
 // against all `tokens` tokens of the quantized activation q, bit-identical to
 // the GEMV kernels (and so to the CPU path).
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, hipStream_t s);
+// Prefill GEMM on int8 MFMA for I2_S against the I8_S activation q; with
+// `raw` the i32 dots go there instead of the scaled outputs.
+hipError_t launch_gemm_i2s(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, int32_t* raw, hipStream_t s);
 
 }  // namespace rh
 

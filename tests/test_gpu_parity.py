@@ -210,6 +210,62 @@ def test_prefill_gemm_batch_of_projections_and_hostile_bytes(ctx):
         assert_same_bits(out, oracle_matmul(t, d, rows, cols, x, tokens), f"type {t} rows {rows}")
 
 
+# ---------------------------------------------------- I2_S prefill GEMM (MFMA)
+
+
+I2S_GEMM_SHAPES = [
+    (6912, 2560, [64, 512]),   # BitNet 2B4T up/gate over a prefill chunk and a long prompt
+    (2560, 6912, [128]),       # down: 54 blocks per row
+    (33, 384, [9, 77, 300]),   # ragged rows and tokens, both token tiles
+    (130, 128, [16]),          # one block per row
+]
+
+
+@pytest.mark.parametrize("rows,cols,token_counts", I2S_GEMM_SHAPES)
+def test_i2s_prefill_gemm_is_bit_exact(ctx, rows, cols, token_counts):
+    # ternary.rs:11-57 on int8 MFMA: the i32 dots equal the CPU path's, and
+    # the scaled outputs its bits
+    assert R.lib().rh_gemm_min_tokens() <= min(token_counts)
+    data = synth.i2s_matrix(rows, cols, seed=rows + cols)
+    m = R.Matrix.load(ctx, 36, data, rows, cols)
+    rb = cols // 4
+    for tokens in token_counts:
+        x = synth.normal_f32(tokens * cols, seed=30 + tokens)
+        raw = ctx.ternary_dot_i32(m, x, tokens)
+        want = O.ternary_dot_matrix_i32(data[: rows * rb], rb, x, tokens)
+        assert np.array_equal(raw, want), f"{rows}x{cols} tokens={tokens}"
+        out = np.full(rows * tokens, np.nan, np.float32)
+        R.matmul_batch(ctx, x, tokens, [(m, out)])
+        assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, tokens, scale=0.02, threads=16),
+                         f"{rows}x{cols} tokens={tokens}")
+
+
+def test_i2s_prefill_gemm_every_code_and_hostile_activations(ctx):
+    # random packed bytes use code 3 (+2, i2_s.rs:96-104); activations with
+    # NaN, infinities and zeros exercise the I8_S rules (q8.rs:38-49,99-105);
+    # two ternary matrices share the launch
+    rows, cols, tokens = 96, 1024, 40
+    specs = []
+    for seed, scale in ((11, 0.75), (12, -3.0)):
+        body = O.pseudo_random_bytes(rows * cols // 4, seed)
+        data = np.concatenate([body, np.array([scale], np.float32).view(np.uint8), np.zeros(28, np.uint8)])
+        specs.append((data, scale))
+    mats = [R.Matrix.load(ctx, 36, d, rows, cols) for d, _ in specs]
+    x = synth.normal_f32(tokens * cols, seed=41).reshape(tokens, cols)
+    x[3, 17] = np.nan
+    x[5, :] = 0.0
+    x[7, 100] = np.inf
+    x[9, 1000] = -np.inf
+    x[11, -1] = np.nan
+    x = x.reshape(-1)
+    outs = [np.full(rows * tokens, np.nan, np.float32) for _ in mats]
+    R.matmul_batch(ctx, x, tokens, list(zip(mats, outs)))
+    for (d, scale), m, out in zip(specs, mats, outs):
+        raw = ctx.ternary_dot_i32(m, x, tokens)
+        assert np.array_equal(raw, O.ternary_dot_matrix_i32(d[: rows * cols // 4], cols // 4, x, tokens))
+        assert_same_bits(out, oracle_matmul(36, d, rows, cols, x, tokens, scale=scale), f"scale {scale}")
+
+
 # --------------------------------------------------------------- I2_S GEMV
 
 
