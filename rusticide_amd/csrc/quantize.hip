@@ -179,6 +179,95 @@ __global__ __launch_bounds__(1024) void quantize_row_kernel(const float* __restr
   }
 }
 
+// The same arithmetic with one wave per token (four tokens per workgroup):
+// lane l holds the 16-byte chunks l, l+64, ... of the row in registers, so
+// both reductions stay inside the wave and every load is issued at once. For
+// rows of at most 256*P values whose width is a multiple of 4, and batches of
+// 512 tokens or more.
+template <uint32_t P>
+__global__ __launch_bounds__(256) void quantize_row_wave_kernel(const float* __restrict__ x, size_t width,
+                                                                uint32_t n_blocks, size_t tokens, Q8Dev q) {
+  const size_t t = static_cast<size_t>(blockIdx.x) * 4u + (threadIdx.x >> 6);
+  if (t >= tokens) return;  // whole waves
+  const uint32_t lane = threadIdx.x & 63u;
+  const float* v = x + t * width;
+  const uint32_t n = n_blocks * 32u;  // a multiple of 32: chunks are all in or all out
+  // every load issued unconditionally (chunks past n read chunk 0 and are
+  // then zeroed), so the compiler emits no branch around them
+  float4 f[P];
+#pragma unroll
+  for (uint32_t k = 0; k < P; k++) {
+    const uint32_t base = 4u * (lane + 64u * k);
+    f[k] = *reinterpret_cast<const float4*>(v + (base < n ? base : 0u));
+  }
+  int last_nan = -1;
+#pragma unroll
+  for (uint32_t k = 0; k < P; k++) {
+    const uint32_t base = 4u * (lane + 64u * k);
+    const bool in = base < n;
+    if (!in) f[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    last_nan = (in && f[k].x != f[k].x) ? static_cast<int>(base) : last_nan;
+    last_nan = (in && f[k].y != f[k].y) ? static_cast<int>(base + 1u) : last_nan;
+    last_nan = (in && f[k].z != f[k].z) ? static_cast<int>(base + 2u) : last_nan;
+    last_nan = (in && f[k].w != f[k].w) ? static_cast<int>(base + 3u) : last_nan;
+  }
+  const int p = half_max_i32(last_nan);
+  const int pw = max(__builtin_amdgcn_readlane(p, 0), __builtin_amdgcn_readlane(p, 32));
+  float mag_max = 0.0f;
+#pragma unroll
+  for (uint32_t k = 0; k < P; k++) {
+    const uint32_t base = 4u * (lane + 64u * k);
+    const float e[4] = {f[k].x, f[k].y, f[k].z, f[k].w};
+#pragma unroll
+    for (uint32_t i = 0; i < 4u; i++) {
+      const float m = __builtin_fabsf(e[i]);
+      mag_max = (base + i < n && static_cast<int>(base + i) > pw && m > mag_max) ? m : mag_max;
+    }
+  }
+  // magnitudes are non-negative floats or +inf: their bits order like u32
+  const uint32_t mb = half_max_u32(__float_as_uint(mag_max));
+  const float mm = __uint_as_float(max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mb), 0)),
+                                       static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(mb), 32))));
+  double mx;
+  if (pw < 0) {
+    mx = static_cast<double>(mm);
+    mx = 1e-5 > mx ? 1e-5 : mx;
+  } else if (pw == static_cast<int>(n) - 1) {
+    mx = __builtin_nan("");
+  } else {
+    mx = static_cast<double>(mm);
+  }
+  const float divisor = static_cast<float>(127.0 / mx);
+#pragma unroll
+  for (uint32_t k = 0; k < P; k++) {
+    const uint32_t base = 4u * (lane + 64u * k);
+    if (64u * 4u * k >= n) break;  // uniform
+    const float e[4] = {f[k].x, f[k].y, f[k].z, f[k].w};
+    int32_t qv[4];
+    int32_t s = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float prod = e[i] * divisor;
+      qv[i] = round_row_to_i8(prod);
+      s += qv[i];
+    }
+    // a 32-block is the 8 lanes 8j..8j+7: quad sums, then the half-row mirror
+    uint32_t s32 = static_cast<uint32_t>(s);
+    s32 += dpp<0xB1>(s32);
+    s32 += dpp<0x4E>(s32);
+    s32 += dpp<0x141>(s32);
+    if (base < n) {
+      const uint32_t packed = (static_cast<uint32_t>(qv[0]) & 0xffu) | ((static_cast<uint32_t>(qv[1]) & 0xffu) << 8) |
+                              ((static_cast<uint32_t>(qv[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qv[3]) << 24);
+      *reinterpret_cast<uint32_t*>(q.quants + t * q.qstride + base) = packed;
+      if ((lane & 7u) == 0) {
+        q.sums[t * q.bstride + base / 32u] = static_cast<int32_t>(s32);
+        q.scales[t * q.bstride + base / 32u] = divisor;
+      }
+    }
+  }
+}
+
 // Rows wider than the register-resident kernel holds: three passes over
 // global memory, one workgroup per token.
 __global__ __launch_bounds__(256) void quantize_row_wide_kernel(const float* __restrict__ x, size_t width,
@@ -268,6 +357,19 @@ hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, cons
                                hipStream_t s) {
   const uint32_t n_blocks = static_cast<uint32_t>(width / 32u);
   if (n_blocks == 0 || tokens == 0) return hipSuccess;
+  const uint32_t n = n_blocks * 32u;
+  // one wave per token pays off once there are enough tokens to fill the
+  // chip; fewer tokens spread each row over a 1024-lane workgroup instead
+  if (width % 4u == 0 && n <= 256u * 32u && tokens >= 512u) {
+    const dim3 grid(static_cast<uint32_t>((tokens + 3u) / 4u));
+    if (n <= 256u * 8u)
+      hipLaunchKernelGGL(quantize_row_wave_kernel<8>, grid, dim3(256), 0, s, x, width, n_blocks, tokens, q);
+    else if (n <= 256u * 16u)
+      hipLaunchKernelGGL(quantize_row_wave_kernel<16>, grid, dim3(256), 0, s, x, width, n_blocks, tokens, q);
+    else
+      hipLaunchKernelGGL(quantize_row_wave_kernel<32>, grid, dim3(256), 0, s, x, width, n_blocks, tokens, q);
+    return hipGetLastError();
+  }
   if (n_blocks * 32u <= 4u * kRowThreads * kRowPasses)
     hipLaunchKernelGGL(quantize_row_kernel, dim3(static_cast<uint32_t>(tokens)), dim3(kRowThreads), 0, s, x,
                        width, n_blocks, q);

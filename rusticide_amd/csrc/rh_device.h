@@ -121,11 +121,9 @@ __device__ __forceinline__ int32_t round_to_i8(float v) {
 // Q8Kind::Row round_row_to_i8 (portable/q8.rs:128-130): ties to even, then a
 // saturating cast to [-128, 127] with NaN to 0.
 __device__ __forceinline__ int32_t round_row_to_i8(float v) {
-  float r = __builtin_rintf(v);
-  if (r != r) return 0;
-  if (r <= -128.0f) return -128;
-  if (r >= 127.0f) return 127;
-  return static_cast<int32_t>(r);
+  const float r = __builtin_rintf(v);
+  const float c = __builtin_fminf(__builtin_fmaxf(r, -128.0f), 127.0f);  // NaN r gives -128 here
+  return r != r ? 0 : static_cast<int32_t>(c);
 }
 
 }  // namespace rh

@@ -93,6 +93,12 @@ def quant_cases():
     sub = (rng.standard_normal(256) * 1e-40).astype(np.float32)
     cases.append(sub)
     cases.append(rng.standard_normal(300).astype(np.float32))  # partial blocks
+    cases.append(rng.standard_normal(8192).astype(np.float32))  # widest row the one-wave I8_S kernel holds
+    wide = rng.standard_normal(6912).astype(np.float32)  # BitNet down width, NaN and inf mid-row
+    wide[5000] = np.nan
+    wide[6000] = np.inf
+    cases.append(wide)
+    cases.append(rng.standard_normal(8224).astype(np.float32))  # past it: the workgroup kernel
     return cases
 
 
