@@ -293,6 +293,35 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
 
 namespace rh {
 int ctx_device(const rh_ctx* ctx) { return ctx->device; }
+
+rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& norm, size_t width, const rh_job* jobs,
+                             size_t n_jobs, hipStream_t s) {
+  if (!ctx || !hidden || !norm.weight || !jobs || n_jobs == 0) return RH_ERR_INVALID_ARGUMENT;
+  for (size_t i = 0; i < n_jobs; i++)
+    if (!jobs[i].weights || !is_kquant(jobs[i].weights->type_id) || (!jobs[i].out && jobs[i].out_len))
+      return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a norm-fused job is not a k-quant matrix with an output");
+  for (uint32_t kind : {static_cast<uint32_t>(RH_TYPE_Q4_K), static_cast<uint32_t>(RH_TYPE_Q6_K)}) {
+    GemvJobs g{};
+    for (size_t i = 0; i < n_jobs; i++) {
+      const rh_matrix* m = jobs[i].weights;
+      if (m->type_id != kind) continue;
+      const size_t rows = rows_for(m, jobs[i].out_len, 1);
+      if (rows == 0) continue;
+      if (g.n == static_cast<uint32_t>(kMaxJobs)) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "too many jobs");
+      const size_t cover = width / 256;
+      GemvJob& j = g.j[g.n++];
+      j.w = m->data;
+      j.stride = m->stride;
+      j.rows = static_cast<uint32_t>(rows);
+      j.nb = static_cast<uint32_t>(m->nblocks < cover ? m->nblocks : cover);
+      j.out = jobs[i].out;
+      j.out_len = jobs[i].out_len;
+      j.scale = m->scale;
+    }
+    if (g.n) RH_HIP(ctx, launch_gemv_fused(kind, g, hidden, width, 1, 0, 1, s, nullptr, &norm));
+  }
+  return RH_OK;
+}
 const uint8_t* matrix_data(const rh_matrix* m) { return m->data; }
 size_t matrix_stride(const rh_matrix* m) { return m->stride; }
 }  // namespace rh

@@ -19,6 +19,7 @@
 
 #include "rh_device.h"
 #include "rh_internal.h"
+#include "rh_math.h"
 
 namespace rh {
 
@@ -187,6 +188,81 @@ __device__ __forceinline__ void quantize_x_round(const XRound<K>& xr, const XGeo
   }
 }
 
+// The residual add and RMSNorm on a one-token preload that holds the whole
+// row (NormIn): each lane forms v = h + delta for its values and their
+// squares in LDS, one lane sums the squares in element order, then every
+// lane replaces its values with (v / rms) * weight -- the arithmetic of the
+// decoder's add_norm kernel, value for value. norm_load issues the delta and
+// weight loads with the activation's, before the matrix loads (loads return
+// in issue order); norm_apply runs after them.
+template <int K>
+struct NormRound {
+  float d[K][8];
+  float w[K][8];
+};
+
+template <int K>
+__device__ __forceinline__ void norm_load(NormRound<K>& nr, const XGeom& g, const NormIn& nrm) {
+  const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
+#pragma unroll
+  for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
+    const uint32_t u = hw + k * (kThreads / 32u);
+    const size_t e0 = static_cast<size_t>(u < g.total ? u : 0u) * 256u + 8u * hl;
+    const u32x4 w0 = load16(reinterpret_cast<const uint8_t*>(nrm.weight + e0));
+    const u32x4 w1 = load16(reinterpret_cast<const uint8_t*>(nrm.weight + e0 + 4));
+    u32x4 d0{}, d1{};
+    if (nrm.delta) {
+      d0 = load16(reinterpret_cast<const uint8_t*>(nrm.delta + e0));
+      d1 = load16(reinterpret_cast<const uint8_t*>(nrm.delta + e0 + 4));
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      nr.w[k][i] = __uint_as_float(w0[i]);
+      nr.w[k][4 + i] = __uint_as_float(w1[i]);
+      nr.d[k][i] = __uint_as_float(d0[i]);
+      nr.d[k][4 + i] = __uint_as_float(d1[i]);
+    }
+  }
+}
+
+template <int K>
+__device__ __forceinline__ void norm_apply(XRound<K>& xr, const NormRound<K>& nr, const XGeom& g, const NormIn& nrm,
+                                           float* sq, float* s_rms) {
+  const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
+#pragma unroll
+  for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
+    const uint32_t u = hw + k * (kThreads / 32u);
+    if (u >= g.total) continue;
+    const uint32_t e0 = u * 256u + 8u * hl;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      float v = xr.f[k][i];
+      if (nrm.delta) v += nr.d[k][i];
+      xr.f[k][i] = v;
+      const float s2 = v * v;
+      sq[e0 + i] = s2;
+      if (nrm.hidden_out && blockIdx.x == 0) nrm.hidden_out[e0 + i] = v;
+    }
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t n = g.total * 256u;
+    const float sum = ordered_sum(sq, n, -0.0f);
+    const float mean = __fdiv_rn(sum, static_cast<float>(n));
+    *s_rms = sqrt_rn(mean + nrm.eps);
+  }
+  __syncthreads();
+  const float rms = *s_rms;
+#pragma unroll
+  for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float xv = __fdiv_rn(xr.f[k][i], rms);
+      xr.f[k][i] = xv * nr.w[k][i];
+    }
+  }
+}
+
 // The rounds after the first (which the kernel quantizes from its preload).
 template <int FMT, int K>
 __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int8_t* act, float* d8,
@@ -204,10 +280,12 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
 //      terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ>
+// NORM (T = 1, the whole row in the preload): x is the hidden state and the
+// kernel applies the NormIn residual add and RMSNorm before quantizing.
+template <int T, int NI, int FQ, bool NORM>
 __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
-                                                       size_t t0) {
+                                                       size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t abytes = nbmax * 256u;
   int8_t* act = reinterpret_cast<int8_t*>(lds);
@@ -227,6 +305,8 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
   if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
+  NormRound<FQ ? FQ : 1> nr;
+  if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
   u32x4 hd[NI], c0[NI], c1[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
@@ -240,6 +320,8 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
     c1[i] = load16(blk + 80u + 16u * p);
   }
 
+  if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
+                                    reinterpret_cast<float*>(lds + nrm.lds_offset) + xg.total * 256u);
   if (FQ) {
     quantize_x_round<12, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, sums);
     quantize_x_rest<12, FQ ? FQ : 1>(xg, nbmax, act, d8, sums);
@@ -324,10 +406,10 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ>
+template <int T, int NI, int FQ, bool NORM>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
-                                                       size_t t0) {
+                                                       size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
   const uint32_t abytes = nbmax * 256u;
   int8_t* act = reinterpret_cast<int8_t*>(lds);
@@ -351,6 +433,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
   if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
+  NormRound<FQ ? FQ : 1> nr;
+  if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
   u32x4 A[NI], B[NI], C[NI], W[NI], E[NI];
 #pragma unroll
   for (int i = 0; i < NI; i++) {
@@ -366,6 +450,8 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
                  load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
   }
 
+  if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
+                                    reinterpret_cast<float*>(lds + nrm.lds_offset) + xg.total * 256u);
   if (FQ) {
     quantize_x_round<14, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, bias);
     quantize_x_rest<14, FQ ? FQ : 1>(xg, nbmax, act, d8, bias);
@@ -871,10 +957,17 @@ uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
   return R < 1u ? 1u : R;
 }
 
-template <int FMT, int T, int NI, int FQ>
+template <int FMT, int T, int NI, int FQ, bool NORM = false>
 void* kq_kernel() {
-  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ>)
-                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ>);
+  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM>)
+                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM>);
+}
+
+// The norm-fused decode kernels: one token, four blocks per team, the row
+// preloaded in one (FQ 1) or four (FQ 4) rounds.
+void* kq_norm_kernel(uint32_t type_id, uint32_t fq) {
+  if (type_id == 12u) return fq == 1u ? kq_kernel<12, 1, 4, 1, true>() : kq_kernel<12, 1, 4, 4, true>();
+  return fq == 1u ? kq_kernel<14, 1, 4, 1, true>() : kq_kernel<14, 1, 4, 4, true>();
 }
 
 template <int FMT, int T, int FQ>
@@ -951,7 +1044,7 @@ uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_ro
 // (T <= kMaxFusedTokens); otherwise they read the activation q holds.
 template <int T, bool FUSED>
 hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float* x, size_t width,
-                    size_t tokens, size_t t0, hipStream_t s, int32_t* raw) {
+                    size_t tokens, size_t t0, hipStream_t s, int32_t* raw, const NormIn* norm = nullptr) {
   uint32_t nbmax = 0, total_rows = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     nbmax = jobs.j[i].nb > nbmax ? jobs.j[i].nb : nbmax;
@@ -967,7 +1060,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     const size_t nq = width / 256u < nbmax ? width / 256u : nbmax;
     fq = static_cast<size_t>(T) * nq <= kThreads / 32u ? 1u : 4u;
   }
-  const uint32_t ni = kquant ? choose_blocks_per_team<T>(type_id, nbl, total_rows, fq) : 1u;
+  const uint32_t ni = norm ? 4u : kquant ? choose_blocks_per_team<T>(type_id, nbl, total_rows, fq) : 1u;
   const uint32_t R = rows_per_wg(type_id, nbl, ni);
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
@@ -980,13 +1073,23 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
                        tokens, t0);
     return hipGetLastError();
   }
-  const size_t lds = lds_bytes<T>(type_id, nbl, R);
+  size_t lds = lds_bytes<T>(type_id, nbl, R);
   if (kquant) {
     // the fused kernels quantize blocks [0, nbmax) of x, which width covers
     const float* xin = FUSED ? x : nullptr;
-    void* k = kq_kernel_for<T>(type_id, ni, fq);
+    NormIn nrm{};
+    void* k;
+    if (norm) {
+      // the squares of the row (and the rms) after the kernel's own LDS
+      nrm = *norm;
+      nrm.lds_offset = static_cast<uint32_t>((lds + 15u) / 16u * 16u);
+      lds = nrm.lds_offset + static_cast<size_t>(nbl) * 256u * 4u + 16u;
+      k = kq_norm_kernel(type_id, fq);
+    } else {
+      k = kq_kernel_for<T>(type_id, ni, fq);
+    }
     void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
-                    const_cast<uint32_t*>(&nbl), &tokens, &t0};
+                    const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};
     return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
   }
   hipLaunchKernelGGL(gemv_i2s_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0, raw);
@@ -1074,9 +1177,23 @@ hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t 
 
 }  // namespace
 
+bool norm_fusable(uint32_t type_id, size_t width, uint32_t nbmax) {
+  // the whole row in the preload: every block of x quantized, at most four
+  // rounds of eight half-waves
+  return (type_id == 12u || type_id == 14u) && width % 256u == 0 && width / 256u == nbmax && nbmax >= 1u &&
+         nbmax <= 4u * (kThreads / 32u);
+}
+
 hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float* x, size_t width,
-                             size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw) {
+                             size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw, const NormIn* norm) {
   if (!gemv_fused_ok(type_id, width, tn)) return hipErrorInvalidValue;
+  if (norm) {
+    uint32_t nbmax = 0;
+    for (uint32_t i = 0; i < jobs.n; i++) nbmax = jobs.j[i].nb > nbmax ? jobs.j[i].nb : nbmax;
+    if (tn != 1 || tokens != 1 || !norm_fusable(type_id, width, nbmax)) return hipErrorInvalidValue;
+    const Q8Dev none{};
+    return launch_t<1, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr, norm);
+  }
   if (type_id == 36u)
     return tn == 1 ? launch_i2s_fused<1>(jobs, x, width, tokens, t0, s, raw)
                    : launch_i2s_fused<2>(jobs, x, width, tokens, t0, s, raw);

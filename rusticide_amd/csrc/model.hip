@@ -21,9 +21,11 @@
 // exp is rh::expf_ref (rh_math.h), which returns the bits of the libm expf
 // the CPU path calls.
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <new>
 #include <type_traits>
+#include <utility>
 #include <vector>
 
 #include "../../include/rusticide_hip.h"
@@ -36,57 +38,6 @@ namespace {
 
 constexpr uint32_t kNormThreads = 256;
 
-// ((s + p[0]) + p[1]) + ... on one lane, from 16-byte aligned LDS. The sum is
-// a chain of dependent adds; each batch of 28 values is loaded while the
-// previous batch is added (the scheduling barriers keep the compiler from
-// sinking the loads below the adds), so LDS latency does not stall the chain.
-// Two batches in flight stay under the 15 outstanding LDS reads a wait can
-// name, so the adds wait for their own batch only.
-constexpr uint32_t kSumBatch4 = 7;  // float4 per batch
-constexpr uint32_t kSumBatch = 4u * kSumBatch4;
-
-__device__ __forceinline__ void load_batch(const float* p, float4 (&v)[kSumBatch4]) {
-#pragma unroll
-  for (uint32_t j = 0; j < kSumBatch4; j++) v[j] = reinterpret_cast<const float4*>(p)[j];
-}
-
-__device__ __forceinline__ float add_batch(float s, const float4 (&v)[kSumBatch4]) {
-#pragma unroll
-  for (uint32_t j = 0; j < kSumBatch4; j++) {
-    s += v[j].x;
-    s += v[j].y;
-    s += v[j].z;
-    s += v[j].w;
-  }
-  return s;
-}
-
-__device__ __forceinline__ float ordered_sum(const float* p, uint32_t n, float s) {
-  uint32_t i = 0;
-  if (n >= kSumBatch) {
-    float4 a[kSumBatch4], b[kSumBatch4];
-    load_batch(p, a);
-    for (i = kSumBatch; i + 2u * kSumBatch <= n; i += 2u * kSumBatch) {
-      load_batch(p + i, b);
-      __builtin_amdgcn_sched_barrier(0);
-      s = add_batch(s, a);
-      load_batch(p + i + kSumBatch, a);
-      __builtin_amdgcn_sched_barrier(0);
-      s = add_batch(s, b);
-    }
-    if (i + kSumBatch <= n) {
-      load_batch(p + i, b);
-      __builtin_amdgcn_sched_barrier(0);
-      s = add_batch(s, a);
-      s = add_batch(s, b);
-      i += kSumBatch;
-    } else {
-      s = add_batch(s, a);
-    }
-  }
-  for (; i < n; i++) s += p[i];
-  return s;
-}
 
 
 // Token rows of token_embd into hidden (Matrix::copy_row, weights.rs:120-150).
@@ -521,6 +472,8 @@ struct rh_decoder {
   // activations for up to `cap` tokens
   size_t cap = 0;
   float *hidden = nullptr, *normed = nullptr, *delta = nullptr, *qr = nullptr, *kr = nullptr, *vr = nullptr;
+  float* hidden2 = nullptr;  // the residual's other buffer on the norm-fused path
+  bool fuse_norm = false;    // one-token forwards fold each RMSNorm into the GEMV after it
   float *q = nullptr, *mixed = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
   float* logits = nullptr;
   uint32_t* tokens = nullptr;  // the chunk's token ids
@@ -540,6 +493,8 @@ hipError_t dmalloc(T** p, size_t n) {
 }
 
 void free_acts(rh_decoder* d) {
+  if (d->hidden2) hipFree(d->hidden2);
+  d->hidden2 = nullptr;
   for (void* p : {static_cast<void*>(d->hidden), static_cast<void*>(d->normed), static_cast<void*>(d->delta),
                   static_cast<void*>(d->qr), static_cast<void*>(d->kr), static_cast<void*>(d->vr),
                   static_cast<void*>(d->q), static_cast<void*>(d->mixed), static_cast<void*>(d->gate),
@@ -561,7 +516,8 @@ hipError_t ensure_acts(rh_decoder* d, size_t n) {
       (e = dmalloc(&d->kr, n * kv)) != hipSuccess || (e = dmalloc(&d->vr, n * kv)) != hipSuccess ||
       (e = dmalloc(&d->q, n * w)) != hipSuccess || (e = dmalloc(&d->mixed, n * w)) != hipSuccess ||
       (e = dmalloc(&d->gate, n * f)) != hipSuccess || (e = dmalloc(&d->up, n * f)) != hipSuccess ||
-      (e = dmalloc(&d->hf, n * f)) != hipSuccess || (e = dmalloc(&d->tokens, n)) != hipSuccess) {
+      (e = dmalloc(&d->hf, n * f)) != hipSuccess || (e = dmalloc(&d->tokens, n)) != hipSuccess ||
+      (e = dmalloc(&d->hidden2, w)) != hipSuccess) {
     free_acts(d);
     return e;
   }
@@ -588,7 +544,10 @@ rh_status mm(rh_decoder* d, const float* in, size_t n, size_t width, std::initia
 // Decoder::forward_on_pool (decoder.rs:74-107) for n tokens whose ids are
 // in device memory at `tokens`, at positions start..start+n; leaves the last token's
 // logits in d->logits.
+rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start);
+
 rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t start) {
+  if (n == 1 && d->fuse_norm) return forward_one_fused(d, tokens, start);
   const rh_decoder_config& c = d->c;
   const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
   const uint32_t f = static_cast<uint32_t>(c.feed_forward_length), hd = static_cast<uint32_t>(c.head_dim);
@@ -639,6 +598,70 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   const rh_matrix* out = d->output ? d->output : d->token_embd;
   RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
   d->cached = start + n;
+  return RH_OK;
+}
+
+// forward_device for one token with every RMSNorm folded into the fused GEMV
+// after it (NormIn): the residual h + delta is formed inside the QKV, gate/up
+// and output launches, the first workgroup of each writing it to the other
+// hidden buffer. Same arithmetic as the add_norm path, value for value.
+rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start) {
+  const rh_decoder_config& c = d->c;
+  const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
+  const uint32_t f = static_cast<uint32_t>(c.feed_forward_length), hd = static_cast<uint32_t>(c.head_dim);
+  hipStream_t s = d->stream;
+  const rh_matrix* E = d->token_embd;
+  hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, 1u), dim3(256), 0, s, rh_matrix_type(E),
+                     matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
+  RHD(hipGetLastError());
+  const float scale = ::sqrtf(static_cast<float>(c.head_dim));
+  float* h = d->hidden;
+  float* h2 = d->hidden2;
+  const float* pending = nullptr;  // the residual the next norm adds first
+  for (size_t l = 0; l < d->blocks.size(); l++) {
+    const rh_decoder::Block& b = d->blocks[l];
+    NormIn an{};
+    an.delta = pending;
+    an.weight = b.attn_norm;
+    an.eps = c.rms_norm_eps;
+    an.hidden_out = pending ? h2 : nullptr;
+    const rh_job qkv[3] = {{b.q, d->qr, w}, {b.k, d->kr, kv}, {b.v, d->vr, kv}};
+    RHS(matmul_norm_device(d->ctx, h, an, w, qkv, 3, s));
+    if (pending) std::swap(h, h2);
+    float* kc = d->keys + l * c.context_length * kv;
+    float* vc = d->values + l * c.context_length * kv;
+    const uint32_t work = w / 2u + kv / 2u + kv;
+    hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, 1u), dim3(256), 0, s, d->qr, d->kr, d->vr, 1u, w,
+                       kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
+    RHD(hipGetLastError());
+    const size_t att_lds = attention_lds_floats(start + 1) * 4u;
+    hipLaunchKernelGGL(hd == 64u ? attention_kernel<64> : attention_kernel<0>,
+                       dim3(static_cast<uint32_t>(c.head_count), 1u), dim3(kAttnThreads), att_lds, s, d->q, kc, vc,
+                       w, kv, hd, static_cast<uint32_t>(c.head_count / c.head_count_kv), scale,
+                       static_cast<uint32_t>(start), d->mixed);
+    RHD(hipGetLastError());
+    RHS(mm(d, d->mixed, 1, w, {{b.o, d->delta, w}}));
+    NormIn fn{};
+    fn.delta = d->delta;
+    fn.weight = b.ffn_norm;
+    fn.eps = c.rms_norm_eps;
+    fn.hidden_out = h2;
+    const rh_job gu[2] = {{b.gate, d->gate, f}, {b.up, d->up, f}};
+    RHS(matmul_norm_device(d->ctx, h, fn, w, gu, 2, s));
+    std::swap(h, h2);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((f + 255u) / 256u), dim3(256), 0, s, d->gate, d->up, 1u, f, d->hf);
+    RHD(hipGetLastError());
+    RHS(mm(d, d->hf, 1, f, {{b.down, d->delta, w}}));
+    pending = d->delta;
+  }
+  NormIn on{};
+  on.delta = pending;
+  on.weight = d->output_norm;
+  on.eps = c.rms_norm_eps;
+  const rh_matrix* out = d->output ? d->output : d->token_embd;
+  const rh_job lm = {out, d->logits, c.vocab_size};
+  RHS(matmul_norm_device(d->ctx, h, on, w, &lm, 1, s));
+  d->cached = start + 1;
   return RH_OK;
 }
 
@@ -751,6 +774,18 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
     rh_decoder_free(d);
     return RH_ERR_OUT_OF_MEMORY;
   }
+  // one-token forwards fold the norms into the GEMVs when every normed
+  // projection is a k-quant matrix that takes the whole row in its preload;
+  // RUSTICIDE_HIP_NORM_FUSE=0 keeps the separate norm kernels (same bits)
+  auto fusable = [&](const rh_matrix* m) {
+    const uint32_t t = rh_matrix_type(m);
+    return rh_matrix_cols(m) == w && norm_fusable(t, w, static_cast<uint32_t>(w / 256u));
+  };
+  bool fuse = fusable(d->output ? d->output : d->token_embd);
+  for (const rh_decoder::Block& b : d->blocks)
+    fuse = fuse && fusable(b.q) && fusable(b.k) && fusable(b.v) && fusable(b.gate) && fusable(b.up);
+  const char* env = std::getenv("RUSTICIDE_HIP_NORM_FUSE");
+  d->fuse_norm = fuse && !(env && env[0] == '0');
   *out = d;
   return RH_OK;
 }

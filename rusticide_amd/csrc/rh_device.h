@@ -126,4 +126,56 @@ __device__ __forceinline__ int32_t round_row_to_i8(float v) {
   return r != r ? 0 : static_cast<int32_t>(c);
 }
 
+// ((s + p[0]) + p[1]) + ... on one lane, from 16-byte aligned LDS. The sum is
+// a chain of dependent adds; each batch of 28 values is loaded while the
+// previous batch is added (the scheduling barriers keep the compiler from
+// sinking the loads below the adds), so LDS latency does not stall the chain.
+// Two batches in flight stay under the 15 outstanding LDS reads a wait can
+// name, so the adds wait for their own batch only.
+constexpr uint32_t kSumBatch4 = 7;  // float4 per batch
+constexpr uint32_t kSumBatch = 4u * kSumBatch4;
+
+__device__ __forceinline__ void load_batch(const float* p, float4 (&v)[kSumBatch4]) {
+#pragma unroll
+  for (uint32_t j = 0; j < kSumBatch4; j++) v[j] = reinterpret_cast<const float4*>(p)[j];
+}
+
+__device__ __forceinline__ float add_batch(float s, const float4 (&v)[kSumBatch4]) {
+#pragma unroll
+  for (uint32_t j = 0; j < kSumBatch4; j++) {
+    s += v[j].x;
+    s += v[j].y;
+    s += v[j].z;
+    s += v[j].w;
+  }
+  return s;
+}
+
+__device__ __forceinline__ float ordered_sum(const float* p, uint32_t n, float s) {
+  uint32_t i = 0;
+  if (n >= kSumBatch) {
+    float4 a[kSumBatch4], b[kSumBatch4];
+    load_batch(p, a);
+    for (i = kSumBatch; i + 2u * kSumBatch <= n; i += 2u * kSumBatch) {
+      load_batch(p + i, b);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add_batch(s, a);
+      load_batch(p + i + kSumBatch, a);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add_batch(s, b);
+    }
+    if (i + kSumBatch <= n) {
+      load_batch(p + i, b);
+      __builtin_amdgcn_sched_barrier(0);
+      s = add_batch(s, a);
+      s = add_batch(s, b);
+      i += kSumBatch;
+    } else {
+      s = add_batch(s, a);
+    }
+  }
+  for (; i < n; i++) s += p[i];
+  return s;
+}
+
 }  // namespace rh

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "../../include/rusticide_hip.h"
+
 namespace rh {
 
 constexpr int kMaxJobs = 8;       // matrices one GEMV launch can serve
@@ -44,6 +46,19 @@ struct GemvJobs {
   uint32_t n;
 };
 
+// The residual add and RMSNorm a fused one-token k-quant GEMV launch applies
+// to its activation before quantizing it: v = h + delta (h when delta is
+// null), x = (v / sqrt(mean(v*v) + eps)) * weight, the sum of squares in
+// element order (transformer/src/norm.rs:10-14, portable/norm.rs:8-14). The
+// launch's first workgroup writes v to hidden_out when that is set.
+struct NormIn {
+  const float* delta = nullptr;
+  const float* weight = nullptr;
+  float eps = 0.0f;
+  float* hidden_out = nullptr;
+  uint32_t lds_offset = 0;  // filled by the launcher
+};
+
 // Launchers (stream-ordered; they return the launch status).
 hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, const Q8Dev& q,
                                  hipStream_t s);
@@ -60,8 +75,12 @@ size_t gemv_max_tokens(uint32_t type_id, uint32_t nb);
 // gemv_fused_ok says whether a launch of tn tokens of `width` values fits it
 // (k-quants: tn <= kMaxFusedTokens; I2_S: tn <= 2, width <= 8192).
 bool gemv_fused_ok(uint32_t type_id, size_t width, size_t tn);
+// With `norm`, x is the hidden state h of one token and the k-quant kernels
+// form the normalized activation themselves (norm_fusable says when).
 hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float* x, size_t width,
-                             size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw);
+                             size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw,
+                             const NormIn* norm = nullptr);
+bool norm_fusable(uint32_t type_id, size_t width, uint32_t nbmax);
 // Streaming decode GEMV for one or two tokens; false when the launch's shape
 // is outside what it handles (the caller then uses launch_gemv).
 bool launch_gemv_stream(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0,
@@ -95,5 +114,12 @@ size_t matrix_stride(const rh_matrix* m);
 
 hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
                                  float* out, size_t out_len, hipStream_t s);
+
+// rh_matmul_batch_device for one token whose activation the k-quant
+// kernels form themselves from the hidden state: normalize(hidden + delta) *
+// weight (NormIn). Every job must be Q4_K or Q6_K with cols = width and
+// norm_fusable; the caller checks that once.
+rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& norm, size_t width, const rh_job* jobs,
+                             size_t n_jobs, hipStream_t s);
 
 }  // namespace rh

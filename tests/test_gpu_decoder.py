@@ -26,6 +26,18 @@ def ctx():
     c.close()
 
 
+@pytest.fixture(params=["fused", "separate"])
+def norm_path(request, monkeypatch):
+    # one-token forwards fold each RMSNorm into the GEMV after it unless
+    # RUSTICIDE_HIP_NORM_FUSE=0 (read when a decoder is created); both give
+    # the CPU path's bits
+    if request.param == "separate":
+        monkeypatch.setenv("RUSTICIDE_HIP_NORM_FUSE", "0")
+    else:
+        monkeypatch.delenv("RUSTICIDE_HIP_NORM_FUSE", raising=False)
+    return request.param
+
+
 def same_bits(a, b):
     return np.array_equal(np.asarray(a, np.float32).view(np.uint32), np.asarray(b, np.float32).view(np.uint32))
 
@@ -34,7 +46,7 @@ def diff(a, b):
     return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
 
 
-def test_small_decoder_logits_match_the_cpu_path(ctx):
+def test_small_decoder_logits_match_the_cpu_path(ctx, norm_path):
     model = synth.decoder_model(SMALL, seed=11)
     gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
     rng = np.random.default_rng(3)
@@ -49,7 +61,7 @@ def test_small_decoder_logits_match_the_cpu_path(ctx):
     cpu.close()
 
 
-def test_small_decoder_batch_equals_token_by_token(ctx):
+def test_small_decoder_batch_equals_token_by_token(ctx, norm_path):
     # decoder_batch_tests.rs:50-66: a batch's last logits equal those of the
     # same tokens fed one at a time
     model = synth.decoder_model(SMALL, seed=12)
@@ -63,7 +75,7 @@ def test_small_decoder_batch_equals_token_by_token(ctx):
     gpu.close()
 
 
-def test_small_decoder_greedy_generation_matches(ctx):
+def test_small_decoder_greedy_generation_matches(ctx, norm_path):
     model = synth.decoder_model(SMALL, seed=13)
     gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
     prompt = np.random.default_rng(4).integers(0, SMALL["vocab_size"], 70).astype(np.uint32)
@@ -99,7 +111,7 @@ def test_decoder_errors_mirror_model_error(ctx):
     gpu.close()
 
 
-def test_tinyllama_shaped_greedy_decode_matches_the_cpu_path(ctx):
+def test_tinyllama_shaped_greedy_decode_matches_the_cpu_path(ctx, norm_path):
     # 22 layers, hidden 2048, 32/4 heads of 64, FFN 5632, vocab 32000,
     # Q4_K_M mix; 64-token random prompt, then 128 greedy tokens
     model = synth.decoder_model(synth.TINYLLAMA, seed=2026)
