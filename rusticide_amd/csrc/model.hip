@@ -601,10 +601,10 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   return RH_OK;
 }
 
-// forward_device for one token with every RMSNorm folded into the fused GEMV
-// after it (NormIn): the residual h + delta is formed inside the QKV, gate/up
-// and output launches, the first workgroup of each writing it to the other
-// hidden buffer. Same arithmetic as the add_norm path, value for value.
+// forward_device for one token with the layers' RMSNorms folded into the
+// fused GEMV after them (NormIn): the residual h + delta is formed inside the
+// QKV and gate/up launches, the first workgroup of each writing it to the
+// other hidden buffer. Same arithmetic as the add_norm path, value for value.
 rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start) {
   const rh_decoder_config& c = d->c;
   const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
@@ -654,13 +654,14 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start)
     RHS(mm(d, d->hf, 1, f, {{b.down, d->delta, w}}));
     pending = d->delta;
   }
-  NormIn on{};
-  on.delta = pending;
-  on.weight = d->output_norm;
-  on.eps = c.rms_norm_eps;
+  // the output norm stays a kernel of its own: the output matrix's launch has
+  // more workgroups than fit on the chip at once, and each would repeat the
+  // ordered sum
+  hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), static_cast<size_t>(w) * 4u, s, h, pending, 1u,
+                     w, d->output_norm, c.rms_norm_eps, 0u, d->normed);
+  RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
-  const rh_job lm = {out, d->logits, c.vocab_size};
-  RHS(matmul_norm_device(d->ctx, h, on, w, &lm, 1, s));
+  RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
   d->cached = start + 1;
   return RH_OK;
 }
@@ -781,7 +782,7 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
     const uint32_t t = rh_matrix_type(m);
     return rh_matrix_cols(m) == w && norm_fusable(t, w, static_cast<uint32_t>(w / 256u));
   };
-  bool fuse = fusable(d->output ? d->output : d->token_embd);
+  bool fuse = true;
   for (const rh_decoder::Block& b : d->blocks)
     fuse = fuse && fusable(b.q) && fusable(b.k) && fusable(b.v) && fusable(b.gate) && fusable(b.up);
   const char* env = std::getenv("RUSTICIDE_HIP_NORM_FUSE");
