@@ -169,6 +169,14 @@ enum { RH_MATH_EXPF = 0, RH_MATH_SQRT = 1, RH_MATH_DIV = 2 };
 void rh_expf_host(const float *x, float *y, size_t n);
 void rh_sqrt_host(const float *x, const float *start, float *y, size_t n);
 rh_status rh_math_device(rh_ctx *ctx, uint32_t op, const float *a, const float *b, float *y, size_t n);
+/* Test hook with no reference counterpart: the ordered float sum the decoder
+ * kernels form for RMSNorm, ((init + values[0]) + values[1]) + ... one IEEE
+ * add at a time (the f32 `Sum` fold of
+ * crates/rusticide-kernels/src/portable/norm.rs:8-14), computed on the device
+ * by the same wave-parallel code; n <= 8192. `rounds` (may be NULL) receives
+ * the guessing rounds it took; 7 means it finished with the sequential chain. */
+rh_status rh_ordered_sum_device(rh_ctx *ctx, const float *values, size_t n, float init, float *sum,
+                                uint32_t *rounds);
 /* Test hook: the RoPE angle table rh_decoder_new builds on the host,
  * cos/sin of position * theta^(-2p/columns) per (position, pair)
  * (crates/rusticide-kernels/src/portable/rope.rs:7-23). */

@@ -234,22 +234,29 @@ __device__ __forceinline__ void norm_apply(XRound<K>& xr, const NormRound<K>& nr
     const uint32_t u = hw + k * (kThreads / 32u);
     if (u >= g.total) continue;
     const uint32_t e0 = u * 256u + 8u * hl;
+    float s2[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       float v = xr.f[k][i];
       if (nrm.delta) v += nr.d[k][i];
       xr.f[k][i] = v;
-      const float s2 = v * v;
-      sq[e0 + i] = s2;
+      s2[i] = v * v;
       if (nrm.hidden_out && blockIdx.x == 0) nrm.hidden_out[e0 + i] = v;
     }
+    // 8 consecutive values stay inside one 32-value chunk of the layout
+    float4* dst = reinterpret_cast<float4*>(sq + wave_sum_index(e0));
+    dst[0] = float4{s2[0], s2[1], s2[2], s2[3]};
+    dst[1] = float4{s2[4], s2[5], s2[6], s2[7]};
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 64u) {
+    // the squares summed in order from -0.0 (f32 Sum), by wave 0
     const uint32_t n = g.total * 256u;
-    const float sum = ordered_sum(sq, n, -0.0f);
-    const float mean = __fdiv_rn(sum, static_cast<float>(n));
-    *s_rms = sqrt_rn(mean + nrm.eps);
+    const float sum = ordered_sum_wave(sq, n, -0.0f);
+    if (threadIdx.x == 0) {
+      const float mean = __fdiv_rn(sum, static_cast<float>(n));
+      *s_rms = sqrt_rn(mean + nrm.eps);
+    }
   }
   __syncthreads();
   const float rms = *s_rms;
@@ -321,7 +328,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
   }
 
   if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
-                                    reinterpret_cast<float*>(lds + nrm.lds_offset) + xg.total * 256u);
+                                    reinterpret_cast<float*>(lds + nrm.lds_offset) + wave_sum_floats(xg.total * 256u));
   if (FQ) {
     quantize_x_round<12, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, sums);
     quantize_x_rest<12, FQ ? FQ : 1>(xg, nbmax, act, d8, sums);
@@ -451,7 +458,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
   }
 
   if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
-                                    reinterpret_cast<float*>(lds + nrm.lds_offset) + xg.total * 256u);
+                                    reinterpret_cast<float*>(lds + nrm.lds_offset) + wave_sum_floats(xg.total * 256u));
   if (FQ) {
     quantize_x_round<14, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, bias);
     quantize_x_rest<14, FQ ? FQ : 1>(xg, nbmax, act, d8, bias);
@@ -1083,7 +1090,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       // the squares of the row (and the rms) after the kernel's own LDS
       nrm = *norm;
       nrm.lds_offset = static_cast<uint32_t>((lds + 15u) / 16u * 16u);
-      lds = nrm.lds_offset + static_cast<size_t>(nbl) * 256u * 4u + 16u;
+      lds = nrm.lds_offset + static_cast<size_t>(wave_sum_floats(nbl * 256u)) * 4u + 16u;
       k = kq_norm_kernel(type_id, fq);
     } else {
       k = kq_kernel_for<T>(type_id, ni, fq);

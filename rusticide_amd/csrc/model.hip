@@ -130,15 +130,19 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
     const uint32_t e = tid + k * kNormThreads;
     if (e < width) {
       const float s = v[k] * v[k];
-      sq[e] = s;
+      sq[wave_sum_index(e)] = s;
     }
   }
+  // the rest of the last 32-value chunk holds the sum's identity
+  if (tid < ((width + 31u) & ~31u) - width) sq[wave_sum_index(width + tid)] = -0.0f;
   __syncthreads();
-  if (tid == 0) {
-    // the squares summed in order from -0.0 (f32 Sum), one lane
-    const float sum = ordered_sum(sq, width, -0.0f);
-    const float mean = __fdiv_rn(sum, static_cast<float>(width));
-    s_rms = sqrt_rn(mean + eps);
+  if (tid < 64u) {
+    // the squares summed in order from -0.0 (f32 Sum), by wave 0
+    const float sum = ordered_sum_wave(sq, width, -0.0f);
+    if (tid == 0) {
+      const float mean = __fdiv_rn(sum, static_cast<float>(width));
+      s_rms = sqrt_rn(mean + eps);
+    }
   }
   __syncthreads();
   const float rms = s_rms;
@@ -154,6 +158,9 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
 }
 
 using AddNormFn = void (*)(float*, const float*, uint32_t, uint32_t, const float*, float, uint32_t, float*);
+
+// Dynamic LDS of add_norm_kernel: the squares in the ordered sum's layout.
+size_t add_norm_lds(uint32_t width) { return static_cast<size_t>(wave_sum_floats(width)) * 4u; }
 
 // The add_norm_kernel instance for a row width (<= 256 * kMaxNormPer).
 AddNormFn add_norm_for(uint32_t width) {
@@ -447,6 +454,19 @@ __global__ __launch_bounds__(256) void math_kernel(uint32_t op, const float* a, 
   else y[i] = __fdiv_rn(a[i], b[i]);
 }
 
+// One wave: values[0..n) into the ordered sum's LDS layout, then the sum.
+__global__ __launch_bounds__(64) void ordered_sum_kernel(const float* values, uint32_t n, float init, float* out,
+                                                         uint32_t* rounds) {
+  extern __shared__ __align__(16) float buf[];
+  const uint32_t padded = (n + 31u) & ~31u;
+  for (uint32_t i = threadIdx.x; i < padded; i += 64u) buf[wave_sum_index(i)] = i < n ? values[i] : -0.0f;
+  __syncthreads();
+  const float s = ordered_sum_wave(buf, n, init, rounds);
+  if (threadIdx.x == 0) *out = s;
+}
+
+constexpr size_t kMaxOrderedSumTest = 8192;
+
 }  // namespace
 }  // namespace rh
 
@@ -558,7 +578,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                      matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
   RHD(hipGetLastError());
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
-  const size_t norm_lds = static_cast<size_t>(w) * 4u;
+  const size_t norm_lds = add_norm_lds(w);
   const AddNormFn norm_fn = add_norm_for(w);
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
@@ -657,7 +677,7 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start)
   // the output norm stays a kernel of its own: the output matrix's launch has
   // more workgroups than fit on the chip at once, and each would repeat the
   // ordered sum
-  hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), static_cast<size_t>(w) * 4u, s, h, pending, 1u,
+  hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), add_norm_lds(w), s, h, pending, 1u,
                      w, d->output_norm, c.rms_norm_eps, 0u, d->normed);
   RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
@@ -713,6 +733,37 @@ rh_status rh_math_device(rh_ctx* ctx, uint32_t op, const float* a, const float* 
   hipFree(da);
   hipFree(db);
   hipFree(dy);
+  return e == hipSuccess ? RH_OK : RH_ERR_DEVICE;
+}
+
+rh_status rh_ordered_sum_device(rh_ctx* ctx, const float* values, size_t n, float init, float* sum,
+                                uint32_t* rounds) {
+  if (!ctx || !sum || n > kMaxOrderedSumTest || (n && !values)) return RH_ERR_INVALID_ARGUMENT;
+  if (hipSetDevice(ctx_device(ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  hipStream_t s = static_cast<hipStream_t>(rh_stream(ctx));
+  float *dv = nullptr, *dout = nullptr;
+  uint32_t* dr = nullptr;
+  if (dmalloc(&dv, n + 1) != hipSuccess || dmalloc(&dout, 1) != hipSuccess ||
+      hipMalloc(reinterpret_cast<void**>(&dr), 4) != hipSuccess) {
+    hipFree(dv);
+    hipFree(dout);
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  hipError_t e = n ? hipMemcpyAsync(dv, values, n * 4, hipMemcpyHostToDevice, s) : hipSuccess;
+  if (e == hipSuccess) e = hipMemsetAsync(dr, 0, 4, s);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(ordered_sum_kernel, dim3(1), dim3(64), wave_sum_floats(static_cast<uint32_t>(n)) * 4u + 16u,
+                       s, dv, static_cast<uint32_t>(n), init, dout, dr);
+    e = hipGetLastError();
+  }
+  uint32_t r = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(sum, dout, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(&r, dr, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (rounds) *rounds = r;
+  hipFree(dv);
+  hipFree(dout);
+  hipFree(dr);
   return e == hipSuccess ? RH_OK : RH_ERR_DEVICE;
 }
 

@@ -178,4 +178,207 @@ __device__ __forceinline__ float ordered_sum(const float* p, uint32_t n, float s
   return s;
 }
 
+// Wave-parallel ordered sum ---------------------------------------------------
+//
+// ordered_sum's exact result, ((init + p[0]) + p[1]) + ... in float, from one
+// full wave: the values are cut into one run of 32-value chunks per lane, and
+// each lane adds its run as a chain from a guessed start. The result is
+// accepted only when every lane's chain is shown to start exactly where the
+// previous lane's ended (lane 0 starts at init): then, by induction over the
+// runs, the last lane's end is the sequential sum bit for bit. The guesses
+// only decide how fast that happens.
+//
+// Guesses: round 0 takes an approximate sum of every run; an exclusive prefix
+// sum (in double) of those gives approximate starts. Each round then chains
+// every run from three candidate starts -- the guess and the floats one ulp
+// either side -- and maps each chain's end to the candidate of the next lane
+// it equals (or to none). The maps compose (a byte permutation, v_perm_b32),
+// and a prefix scan of them tells every lane which of its candidates is the
+// true start. While the running sum stays in one binade, an add rounds to the
+// same grid whatever the start, except for ties to even, which depend on the
+// start's last bit: so a run's increment is nearly independent of its start,
+// the prefix sum of increments from one round puts the next round's guesses
+// within an ulp, and the three candidates absorb the ties. When a round
+// leaves some lane unresolved, the lanes before it are exact and the next
+// guesses come from their increments. After kWaveSumRounds rounds one chain
+// runs on from the last exact lane, so the result is exact in every case
+// (NaN, infinity and signed values included) and the cost is bounded.
+//
+// Layout: value i sits at float index 36*(i/32) + i%32 of p (16-byte aligned
+// LDS): the 16-byte reads of 16 consecutive lanes fall on distinct banks.
+// Indices from n up to the next multiple of 32 must hold -0.0, the exact
+// identity of float addition (x + -0.0 == x for every x, -0.0 included).
+constexpr uint32_t kWaveSumRounds = 6;
+
+__host__ __device__ constexpr uint32_t wave_sum_index(uint32_t i) { return (i >> 5) * 36u + (i & 31u); }
+__host__ __device__ constexpr uint32_t wave_sum_floats(uint32_t n) { return ((n + 31u) >> 5) * 36u; }
+
+__device__ __forceinline__ void load_chunk(const float* p, float4 (&v)[8]) {
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; j++) v[j] = reinterpret_cast<const float4*>(p)[j];
+}
+
+// Three chains over one chunk, in element order.
+__device__ __forceinline__ void chain3(float (&s)[3], const float4 (&v)[8]) {
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; j++) {
+    const float x[4] = {v[j].x, v[j].y, v[j].z, v[j].w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      s[0] += x[i];
+      s[1] += x[i];
+      s[2] += x[i];
+    }
+  }
+}
+
+__device__ __forceinline__ float chain1(float s, const float4 (&v)[8]) {
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; j++) {
+    s += v[j].x;
+    s += v[j].y;
+    s += v[j].z;
+    s += v[j].w;
+  }
+  return s;
+}
+
+// An approximate sum of one chunk (pairwise; only a guess).
+__device__ __forceinline__ float tree_chunk(const float4 (&v)[8]) {
+  float t[8];
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; j++) t[j] = (v[j].x + v[j].y) + (v[j].z + v[j].w);
+  return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
+}
+
+// DPP moves for a Hillis-Steele scan over the wave: row_shr:1/2/4/8 within
+// rows of 16 lanes, then row_bcast:15 (rows 1 and 3) and row_bcast:31 (rows 2
+// and 3). Lanes without a source, or outside ROWS, read `fill`.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t scan_dpp(uint32_t v, uint32_t fill) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(fill), static_cast<int>(v), CTRL, ROWS, 0xF, false));
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ double scan_dpp_f64(double v) {
+  const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
+  const uint64_t lo = scan_dpp<CTRL, ROWS>(static_cast<uint32_t>(b), 0u);
+  const uint64_t hi = scan_dpp<CTRL, ROWS>(static_cast<uint32_t>(b >> 32), 0u);
+  return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
+}
+
+// Inclusive prefix sum over the 64 lanes (approximate guesses only).
+__device__ __forceinline__ double wave_prefix_sum(double v) {
+  v += scan_dpp_f64<0x111, 0xF>(v);
+  v += scan_dpp_f64<0x112, 0xF>(v);
+  v += scan_dpp_f64<0x114, 0xF>(v);
+  v += scan_dpp_f64<0x118, 0xF>(v);
+  v += scan_dpp_f64<0x142, 0xA>(v);
+  v += scan_dpp_f64<0x143, 0xC>(v);
+  return v;
+}
+
+// A map from {0, 1, 2, 3} to itself as 4 bytes (byte i = image of i); 3 is
+// "none" and maps to itself. after(hi, lo) applies lo first: v_perm_b32
+// picks byte lo[i] of hi for every byte i.
+constexpr uint32_t kMapIdentity = 0x03020100u;
+__device__ __forceinline__ uint32_t map_after(uint32_t hi, uint32_t lo) { return __builtin_amdgcn_perm(hi, hi, lo); }
+
+// Inclusive prefix composition over the 64 lanes: lane k ends with
+// map_k o ... o map_0.
+__device__ __forceinline__ uint32_t wave_prefix_maps(uint32_t m) {
+  m = map_after(m, scan_dpp<0x111, 0xF>(m, kMapIdentity));
+  m = map_after(m, scan_dpp<0x112, 0xF>(m, kMapIdentity));
+  m = map_after(m, scan_dpp<0x114, 0xF>(m, kMapIdentity));
+  m = map_after(m, scan_dpp<0x118, 0xF>(m, kMapIdentity));
+  m = map_after(m, scan_dpp<0x142, 0xA>(m, kMapIdentity));
+  m = map_after(m, scan_dpp<0x143, 0xC>(m, kMapIdentity));
+  return m;
+}
+
+// Called by all 64 lanes of one wave with the same p, n and init; returns the
+// sum in every lane. `rounds`, when given, receives the rounds used (lane 0
+// writes it; kWaveSumRounds + 1 means the closing sequential chain ran).
+__device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, float init,
+                                                  uint32_t* rounds = nullptr) {
+  const uint32_t lane = __lane_id();
+  const uint32_t chunks = (n + 31u) >> 5;
+  if (chunks == 0) return init;
+  const uint32_t per = (chunks + 63u) >> 6;           // chunks per lane
+  const uint32_t lanes = (chunks + per - 1u) / per;   // lanes holding values
+  const uint32_t mine = lane < lanes ? min(per, chunks - lane * per) : 0u;
+  const float* run = p + (mine ? lane * per * 36u : 0u);
+
+  float4 v[8];
+  double d = 0.0;  // this lane's increment, as well as known
+  if (mine) {
+    load_chunk(run, v);
+    float t = tree_chunk(v);
+    for (uint32_t c = 1; c < mine; c++) {
+      float4 w[8];
+      load_chunk(run + c * 36u, w);
+      t += tree_chunk(w);
+    }
+    d = t;
+  }
+
+  uint32_t r = 0, first_bad = 0;
+  float end = init;
+  bool done = false;
+  while (true) {
+    r++;
+    const double before = __shfl_up(wave_prefix_sum(d), 1, 64);
+    const float g = lane == 0 ? init : static_cast<float>(static_cast<double>(init) + before);
+    const uint32_t gb = __float_as_uint(g);
+    const float cand[3] = {g, __uint_as_float(gb - 1u), __uint_as_float(gb + 1u)};
+    float s[3] = {cand[0], cand[1], cand[2]};
+    if (mine) {
+      chain3(s, v);
+      for (uint32_t c = 1; c < mine; c++) {
+        float4 w[8];
+        load_chunk(run + c * 36u, w);
+        chain3(s, w);
+      }
+    }
+    // which candidate of the next lane each end is: bits equal, one below,
+    // one above
+    const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(gb), 1, 64));
+    uint32_t map = 0x03000000u;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const uint32_t delta = __float_as_uint(s[i]) - next;
+      const uint32_t j = delta == 0u ? 0u : delta == 0xFFFFFFFFu ? 1u : delta == 1u ? 2u : 3u;
+      map |= j << (8 * i);
+    }
+    if (lane + 1u >= lanes) map = kMapIdentity;
+    const uint32_t upto = static_cast<uint32_t>(__shfl_up(static_cast<int>(wave_prefix_maps(map)), 1, 64));
+    const uint32_t state = lane == 0 ? 0u : (upto & 0xFFu);  // lane 0 starts at candidate 0, init
+    const float mine_end = state == 1u ? s[1] : state == 2u ? s[2] : s[0];
+    const uint64_t bad = __ballot(lane < lanes && state == 3u);
+    if (bad == 0) {
+      end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine_end), static_cast<int>(lanes - 1u)));
+      done = true;
+      break;
+    }
+    first_bad = static_cast<uint32_t>(__builtin_ctzll(bad));  // >= 1: lane 0 is always resolved
+    end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine_end), static_cast<int>(first_bad - 1u)));
+    if (r == kWaveSumRounds) break;
+    const float start = state == 1u ? cand[1] : state == 2u ? cand[2] : cand[0];
+    d = lane < first_bad ? static_cast<double>(mine_end) - static_cast<double>(start)
+                         : static_cast<double>(s[0]) - static_cast<double>(cand[0]);
+  }
+  if (!done) {
+    // `end` is the exact sum of the runs before lane first_bad
+    for (uint32_t c = first_bad * per; c < chunks; c++) {
+      float4 w[8];
+      load_chunk(p + c * 36u, w);
+      end = chain1(end, w);
+    }
+    r++;
+  }
+  if (rounds && lane == 0) *rounds = r;
+  return end;
+}
+
 }  // namespace rh

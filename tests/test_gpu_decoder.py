@@ -168,6 +168,85 @@ def test_device_sqrt_is_rounded_to_nearest(ctx):
     _assert_same(_device_math(ctx, 1, x), want, x)
 
 
+def _device_ordered_sum(ctx, values, init):
+    import ctypes
+    L = R.lib()
+    L.rh_ordered_sum_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float,
+                                        ctypes.c_void_p, ctypes.c_void_p]
+    v = np.ascontiguousarray(values, np.float32)
+    out = np.zeros(1, np.float32)
+    rounds = np.zeros(1, np.uint32)
+    ctx.check(L.rh_ordered_sum_device(ctx.handle, v.ctypes.data if v.size else None, v.size, float(init),
+                                      out.ctypes.data, rounds.ctypes.data))
+    return out[0], int(rounds[0])
+
+
+def _fold(values, init):
+    # ((init + v0) + v1) + ...: numpy's accumulate adds in order, one float32
+    # rounding per step
+    seq = np.concatenate([np.float32([init]), np.asarray(values, np.float32)])
+    with np.errstate(all="ignore"):
+        return np.add.accumulate(seq, dtype=np.float32)[-1]
+
+
+def _ordered_sum_cases():
+    rng = np.random.default_rng(11)
+    cases = []
+    for n in (0, 1, 2, 31, 32, 33, 63, 64, 65, 100, 2047, 2048, 2049, 2560, 4096, 5000, 8191, 8192):
+        v = rng.standard_normal(n).astype(np.float32)
+        cases.append(("squares", v * v, -0.0))
+    for _ in range(24):
+        n = int(rng.integers(1, 8193))
+        v = (rng.standard_normal(n) * np.exp(rng.uniform(-30, 30, n))).astype(np.float32)
+        cases.append(("wide squares", v * v, -0.0))
+        cases.append(("signed", rng.standard_normal(n).astype(np.float32) * np.float32(1e3), 0.0))
+        cases.append(("exp weights", rng.exponential(1.0, n).astype(np.float32), 0.0))
+    n = 2048
+    cases.append(("zeros from -0", np.zeros(n, np.float32), -0.0))
+    cases.append(("negative zeros from -0", np.full(n, -0.0, np.float32), -0.0))
+    cases.append(("zeros from +0", np.zeros(n, np.float32), 0.0))
+    cases.append(("ties", np.float32(2.0 ** -24) * rng.integers(0, 4, n).astype(np.float32) + np.float32(1.0), 0.0))
+    sub = rng.integers(1, 1 << 23, n, dtype=np.uint32).view(np.float32)
+    cases.append(("subnormals", sub, -0.0))
+    big = np.full(n, 3e37, np.float32)
+    cases.append(("overflow to inf", big, 0.0))
+    cases.append(("inf and -inf", np.float32([1.0, np.inf, 2.0, -np.inf, 3.0] * 10), 0.0))
+    with_nan = rng.standard_normal(n).astype(np.float32) ** 2
+    with_nan[1500] = np.nan
+    cases.append(("a NaN", with_nan, -0.0))
+    cancel = rng.standard_normal(n).astype(np.float32)
+    cancel = np.concatenate([cancel, -cancel[::-1]])
+    cases.append(("cancellation", cancel, 0.0))
+    cases.append(("init 1e30", rng.standard_normal(3000).astype(np.float32), 1e30))
+    return cases
+
+
+def test_device_ordered_sum_is_the_sequential_fold(ctx):
+    # the RMSNorm sum of squares (and any float sum the kernels must keep in
+    # element order) against a sequential float32 fold, bit for bit, NaN
+    # aside (any NaN)
+    for name, values, init in _ordered_sum_cases():
+        got, rounds = _device_ordered_sum(ctx, values, init)
+        want = _fold(values, init)
+        if np.isnan(want):
+            assert np.isnan(got), name
+            continue
+        assert got.view(np.uint32) == want.view(np.uint32), (name, values.size, got, want, rounds)
+
+
+def test_device_ordered_sum_settles_in_few_rounds(ctx):
+    # the speculative rounds, not the closing sequential chain, finish the
+    # RMSNorm-shaped sums (squares of hidden states, 2048 and 4096 wide)
+    rounds = []
+    rng = np.random.default_rng(12)
+    for n in (2048, 4096) * 16:
+        v = (rng.standard_normal(n) * rng.uniform(0.01, 10)).astype(np.float32)
+        got, r = _device_ordered_sum(ctx, v * v, -0.0)
+        assert got.view(np.uint32) == _fold(v * v, -0.0).view(np.uint32)
+        rounds.append(r)
+    assert max(rounds) <= 6 and np.mean(rounds) <= 3.5, rounds
+
+
 def test_device_division_is_rounded_to_nearest(ctx):
     rng = np.random.default_rng(5)
     a = rng.integers(0, 0x7F800000, 1 << 22, dtype=np.uint32).view(np.float32)
