@@ -188,21 +188,22 @@ __device__ __forceinline__ float ordered_sum(const float* p, uint32_t n, float s
 // runs, the last lane's end is the sequential sum bit for bit. The guesses
 // only decide how fast that happens.
 //
-// Guesses: round 0 takes an approximate sum of every run; an exclusive prefix
-// sum (in double) of those gives approximate starts. Each round then chains
-// every run from three candidate starts -- the guess and the floats one ulp
-// either side -- and maps each chain's end to the candidate of the next lane
-// it equals (or to none). The maps compose (a byte permutation, v_perm_b32),
-// and a prefix scan of them tells every lane which of its candidates is the
-// true start. While the running sum stays in one binade, an add rounds to the
-// same grid whatever the start, except for ties to even, which depend on the
-// start's last bit: so a run's increment is nearly independent of its start,
-// the prefix sum of increments from one round puts the next round's guesses
-// within an ulp, and the three candidates absorb the ties. When a round
-// leaves some lane unresolved, the lanes before it are exact and the next
-// guesses come from their increments. After kWaveSumRounds rounds one chain
-// runs on from the last exact lane, so the result is exact in every case
-// (NaN, infinity and signed values included) and the cost is bounded.
+// Guesses: an approximate sum of every run, then an exclusive prefix sum (in
+// double) of those, gives approximate starts; one chain per lane from there
+// gives each run's increment (end minus start). While the running sum stays
+// in one binade, an add rounds to the same grid whatever the start, except
+// for ties to even, which follow the start's last bit: so an increment is
+// nearly independent of where its run starts, and the prefix sum of the
+// increments puts every lane within an ulp of its true start. Each checking
+// round then chains every run from three candidate starts -- the guess and
+// the floats one ulp either side -- and maps each chain's end to the
+// candidate of the next lane it equals (or to none). The maps compose (a
+// byte permutation, v_perm_b32), and a prefix composition tells every lane
+// which of its candidates is the true start. A round that leaves some lane
+// unresolved has proved the lanes before it exact; the next guesses come
+// from their increments. After kWaveSumRounds checking rounds one chain runs
+// on from the last exact lane, so the result is exact in every case (NaN,
+// infinity and signed values included) and the cost is bounded.
 //
 // Layout: value i sits at float index 36*(i/32) + i%32 of p (16-byte aligned
 // LDS): the 16-byte reads of 16 consecutive lanes fall on distinct banks.
@@ -251,55 +252,74 @@ __device__ __forceinline__ float tree_chunk(const float4 (&v)[8]) {
   return ((t[0] + t[1]) + (t[2] + t[3])) + ((t[4] + t[5]) + (t[6] + t[7]));
 }
 
-// DPP moves for a Hillis-Steele scan over the wave: row_shr:1/2/4/8 within
-// rows of 16 lanes, then row_bcast:15 (rows 1 and 3) and row_bcast:31 (rows 2
-// and 3). Lanes without a source, or outside ROWS, read `fill`.
-template <int CTRL, int ROWS>
-__device__ __forceinline__ uint32_t scan_dpp(uint32_t v, uint32_t fill) {
+// DPP moves (GFX9 controls): row_shr:1/2/4/8 within rows of 16 lanes,
+// row_bcast:15 (into rows 1 and 3) and row_bcast:31 (into rows 2 and 3) for
+// a Hillis-Steele scan; wave_shr:1 (lane i reads lane i-1) and wave_shl:1
+// (lane i reads lane i+1) across the wave. Lanes without a source, or
+// outside ROWS, read `fill`.
+constexpr int kDppWaveShl1 = 0x130;
+constexpr int kDppWaveShr1 = 0x138;
+
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ uint32_t dpp_fill(uint32_t v, uint32_t fill) {
   return static_cast<uint32_t>(
       __builtin_amdgcn_update_dpp(static_cast<int>(fill), static_cast<int>(v), CTRL, ROWS, 0xF, false));
 }
 
-template <int CTRL, int ROWS>
-__device__ __forceinline__ double scan_dpp_f64(double v) {
+template <int CTRL, int ROWS = 0xF>
+__device__ __forceinline__ double dpp_fill0_f64(double v) {
   const uint64_t b = static_cast<uint64_t>(__double_as_longlong(v));
-  const uint64_t lo = scan_dpp<CTRL, ROWS>(static_cast<uint32_t>(b), 0u);
-  const uint64_t hi = scan_dpp<CTRL, ROWS>(static_cast<uint32_t>(b >> 32), 0u);
+  const uint64_t lo = dpp_fill<CTRL, ROWS>(static_cast<uint32_t>(b), 0u);
+  const uint64_t hi = dpp_fill<CTRL, ROWS>(static_cast<uint32_t>(b >> 32), 0u);
   return __longlong_as_double(static_cast<long long>((hi << 32) | lo));
 }
 
-// Inclusive prefix sum over the 64 lanes (approximate guesses only).
+// Inclusive prefix sum over the 64 lanes (approximate: it only makes
+// guesses).
 __device__ __forceinline__ double wave_prefix_sum(double v) {
-  v += scan_dpp_f64<0x111, 0xF>(v);
-  v += scan_dpp_f64<0x112, 0xF>(v);
-  v += scan_dpp_f64<0x114, 0xF>(v);
-  v += scan_dpp_f64<0x118, 0xF>(v);
-  v += scan_dpp_f64<0x142, 0xA>(v);
-  v += scan_dpp_f64<0x143, 0xC>(v);
+  v += dpp_fill0_f64<0x111>(v);
+  v += dpp_fill0_f64<0x112>(v);
+  v += dpp_fill0_f64<0x114>(v);
+  v += dpp_fill0_f64<0x118>(v);
+  v += dpp_fill0_f64<0x142, 0xA>(v);
+  v += dpp_fill0_f64<0x143, 0xC>(v);
   return v;
 }
 
+// Start guesses from increments: lane k gets init + the increments of lanes
+// 0..k-1, rounded to float; lane 0 gets init itself (the shift's fill), so
+// no lane-dependent branch surrounds the cross-lane moves.
+__device__ __forceinline__ float guess_starts(double d, float init) {
+  const float end = static_cast<float>(static_cast<double>(init) + wave_prefix_sum(d));
+  return __uint_as_float(dpp_fill<kDppWaveShr1>(__float_as_uint(end), __float_as_uint(init)));
+}
+
 // A map from {0, 1, 2, 3} to itself as 4 bytes (byte i = image of i); 3 is
-// "none" and maps to itself. after(hi, lo) applies lo first: v_perm_b32
+// "none" and maps to itself. map_after(hi, lo) applies lo first: v_perm_b32
 // picks byte lo[i] of hi for every byte i.
 constexpr uint32_t kMapIdentity = 0x03020100u;
 __device__ __forceinline__ uint32_t map_after(uint32_t hi, uint32_t lo) { return __builtin_amdgcn_perm(hi, hi, lo); }
 
-// Inclusive prefix composition over the 64 lanes: lane k ends with
-// map_k o ... o map_0.
-__device__ __forceinline__ uint32_t wave_prefix_maps(uint32_t m) {
-  m = map_after(m, scan_dpp<0x111, 0xF>(m, kMapIdentity));
-  m = map_after(m, scan_dpp<0x112, 0xF>(m, kMapIdentity));
-  m = map_after(m, scan_dpp<0x114, 0xF>(m, kMapIdentity));
-  m = map_after(m, scan_dpp<0x118, 0xF>(m, kMapIdentity));
-  m = map_after(m, scan_dpp<0x142, 0xA>(m, kMapIdentity));
-  m = map_after(m, scan_dpp<0x143, 0xC>(m, kMapIdentity));
-  return m;
+// Exclusive prefix composition over the 64 lanes: lane k gets
+// map_{k-1} o ... o map_0 (lane 0 the identity).
+__device__ __forceinline__ uint32_t wave_prefix_maps_excl(uint32_t m) {
+  m = map_after(m, dpp_fill<0x111>(m, kMapIdentity));
+  m = map_after(m, dpp_fill<0x112>(m, kMapIdentity));
+  m = map_after(m, dpp_fill<0x114>(m, kMapIdentity));
+  m = map_after(m, dpp_fill<0x118>(m, kMapIdentity));
+  m = map_after(m, dpp_fill<0x142, 0xA>(m, kMapIdentity));
+  m = map_after(m, dpp_fill<0x143, 0xC>(m, kMapIdentity));
+  return dpp_fill<kDppWaveShr1>(m, kMapIdentity);
 }
 
 // Called by all 64 lanes of one wave with the same p, n and init; returns the
-// sum in every lane. `rounds`, when given, receives the rounds used (lane 0
-// writes it; kWaveSumRounds + 1 means the closing sequential chain ran).
+// sum in every lane. `rounds`, when given, receives the checking rounds used
+// (lane 0 writes it; kWaveSumRounds + 1 means the closing sequential chain
+// ran). The cross-lane moves (DPP, ballot, readlane) read every lane, so
+// each runs as a statement of its own at the function's top level, never
+// inside a lane-dependent branch or a conditional expression: a C++ ?:
+// evaluates only the operand it picks, and a move run with some lanes off
+// reads fills in their place.
 __device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, float init,
                                                   uint32_t* rounds = nullptr) {
   const uint32_t lane = __lane_id();
@@ -322,14 +342,27 @@ __device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, fl
     }
     d = t;
   }
+  // one chain from the approximate start refines the increment
+  {
+    const float g = guess_starts(d, init);
+    float e = g;
+    if (mine) {
+      e = chain1(e, v);
+      for (uint32_t c = 1; c < mine; c++) {
+        float4 w[8];
+        load_chunk(run + c * 36u, w);
+        e = chain1(e, w);
+      }
+    }
+    d = static_cast<double>(e) - static_cast<double>(g);
+  }
 
   uint32_t r = 0, first_bad = 0;
   float end = init;
   bool done = false;
   while (true) {
     r++;
-    const double before = __shfl_up(wave_prefix_sum(d), 1, 64);
-    const float g = lane == 0 ? init : static_cast<float>(static_cast<double>(init) + before);
+    const float g = guess_starts(d, init);
     const uint32_t gb = __float_as_uint(g);
     const float cand[3] = {g, __uint_as_float(gb - 1u), __uint_as_float(gb + 1u)};
     float s[3] = {cand[0], cand[1], cand[2]};
@@ -343,7 +376,7 @@ __device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, fl
     }
     // which candidate of the next lane each end is: bits equal, one below,
     // one above
-    const uint32_t next = static_cast<uint32_t>(__shfl_down(static_cast<int>(gb), 1, 64));
+    const uint32_t next = dpp_fill<kDppWaveShl1>(gb, 0u);
     uint32_t map = 0x03000000u;
 #pragma unroll
     for (int i = 0; i < 3; i++) {
@@ -352,8 +385,9 @@ __device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, fl
       map |= j << (8 * i);
     }
     if (lane + 1u >= lanes) map = kMapIdentity;
-    const uint32_t upto = static_cast<uint32_t>(__shfl_up(static_cast<int>(wave_prefix_maps(map)), 1, 64));
-    const uint32_t state = lane == 0 ? 0u : (upto & 0xFFu);  // lane 0 starts at candidate 0, init
+    // lane 0 starts at candidate 0 (init); lane k at the image of 0 under
+    // the maps of the lanes before it
+    const uint32_t state = wave_prefix_maps_excl(map) & 0xFFu;
     const float mine_end = state == 1u ? s[1] : state == 2u ? s[2] : s[0];
     const uint64_t bad = __ballot(lane < lanes && state == 3u);
     if (bad == 0) {
