@@ -209,12 +209,15 @@ constexpr size_t kMaxAttentionLds = 65536;  // bytes of dynamic LDS per workgrou
 inline size_t attention_lds_floats(size_t rows) { return 128u + ((rows + 3u) & ~size_t{3}) + 2u * kVTile * 64u; }
 
 // Value rows r0..r0+count of one kv head into registers, one tile's share
-// per thread (HD = 64: 16 float4 per row, 16 threads a row).
+// per thread (HD = 64: 16 f32x4 per row, 16 threads a row).
 template <uint32_t HD>
 struct VTileRegs {
   static constexpr uint32_t kPer = HD ? kVTile * HD / 4u / kAttnThreads : kVTile * 64u / kAttnThreads;
-  using T = typename std::conditional<HD != 0, float4, float>::type;
+  using T = typename std::conditional<HD != 0, f32x4, float>::type;
   T v[kPer];
+  // Every thread loads unconditionally (rows past count re-read row
+  // count - 1, which store() drops): a load under a condition into this
+  // array would make the compiler keep it in scratch and wait for each load.
   __device__ __forceinline__ void load(const float* vcache, uint32_t kv, uint32_t off, uint32_t hd, uint32_t r0,
                                        uint32_t count) {
 #pragma unroll
@@ -222,11 +225,12 @@ struct VTileRegs {
       const uint32_t f = threadIdx.x + k * kAttnThreads;
       if constexpr (HD != 0) {
         const uint32_t r = f / (HD / 4u), c = f % (HD / 4u);
-        if (r < count)
-          v[k] = *reinterpret_cast<const T*>(vcache + static_cast<size_t>(r0 + r) * kv + off + 4u * c);
+        const uint32_t rr = r < count ? r : count - 1u;
+        v[k] = *reinterpret_cast<const T*>(vcache + static_cast<size_t>(r0 + rr) * kv + off + 4u * c);
       } else {
         const uint32_t r = f / hd, c = f % hd;
-        if (r < count && f < kVTile * hd) v[k] = vcache[static_cast<size_t>(r0 + r) * kv + off + c];
+        const uint32_t rr = r < count ? r : count - 1u;
+        v[k] = vcache[static_cast<size_t>(r0 + rr) * kv + off + c];
       }
     }
   }
@@ -242,6 +246,67 @@ struct VTileRegs {
     }
   }
 };
+
+// dot (float.rs:23-36) for head_dim 64: eight fused lanes over the eight
+// 8-wide chunks.
+__device__ __forceinline__ void lanes64(const float* qh, const f32x4 (&k4)[16], float (&acc)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; c++) {
+    const f32x4 a = k4[2 * c], b = k4[2 * c + 1];
+    acc[0] = __builtin_fmaf(qh[8 * c + 0], a.x, acc[0]);
+    acc[1] = __builtin_fmaf(qh[8 * c + 1], a.y, acc[1]);
+    acc[2] = __builtin_fmaf(qh[8 * c + 2], a.z, acc[2]);
+    acc[3] = __builtin_fmaf(qh[8 * c + 3], a.w, acc[3]);
+    acc[4] = __builtin_fmaf(qh[8 * c + 4], b.x, acc[4]);
+    acc[5] = __builtin_fmaf(qh[8 * c + 5], b.y, acc[5]);
+    acc[6] = __builtin_fmaf(qh[8 * c + 6], b.z, acc[6]);
+    acc[7] = __builtin_fmaf(qh[8 * c + 7], b.w, acc[7]);
+  }
+}
+
+// The dot's lanes summed in order from -0.0, plus the tail, over the scale
+// (attention.rs:189-207 divides each score by sqrt(head_dim)).
+__device__ __forceinline__ float score_from_lanes(const float (&acc)[8], float tail, float scale) {
+  float s = -0.0f;
+#pragma unroll
+  for (int l = 0; l < 8; l++) s += acc[l];
+  return __fdiv_rn(s + tail, scale);
+}
+
+// softmax (norm.rs:17-30) of the scores w[0..rows) in place, given each
+// thread's maximum of the scores it wrote: the maximum over the workgroup
+// (exact in any order), exp(x - max), the sum in order from 0.0 on one lane,
+// and the division. The caller synchronizes before reading w.
+__device__ __forceinline__ void softmax_rows(float* w, uint32_t rows, float mx, float* red) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (uint32_t i = tid; i < rows; i += kAttnThreads) w[i] = expf_ref(w[i] - mx);
+  __syncthreads();
+  if (tid == 0) red[4] = ordered_sum(w, rows, 0.0f);  // portable/norm.rs: `let mut sum = 0.0`
+  __syncthreads();
+  const float sum = red[4];
+  for (uint32_t i = tid; i < rows; i += kAttnThreads) w[i] = __fdiv_rn(w[i], sum);
+}
+
+// mix_rows (float.rs:52-62) over one staged value tile: output lane `lane`
+// adds rows 0..count of the tile in order, one fused multiply-add each.
+__device__ __forceinline__ float mix_tile(const float* cur, const float* wr, uint32_t count, uint32_t hd,
+                                          uint32_t lane, float acc) {
+  uint32_t r = 0;
+  for (; r + 16u <= count; r += 16u) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) v[k] = cur[(r + k) * hd + lane];
+#pragma unroll
+    for (int k = 0; k < 16; k++) acc = __builtin_fmaf(v[k], wr[r + k], acc);
+  }
+  for (; r < count; r++) acc = __builtin_fmaf(cur[r * hd + lane], wr[r], acc);
+  return acc;
+}
 
 // One workgroup per (query head, token): scores over cached rows
 // 0..=start+t, softmax, then the weighted sum of value rows
@@ -272,21 +337,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float tail = -0.0f;
     if constexpr (HD == 64u) {
-      float4 k4[16];
+      f32x4 k4[16];
 #pragma unroll
-      for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const float4*>(kr)[c];
-#pragma unroll
-      for (int c = 0; c < 8; c++) {
-        const float4 a = k4[2 * c], b = k4[2 * c + 1];
-        acc[0] = __builtin_fmaf(qh[8 * c + 0], a.x, acc[0]);
-        acc[1] = __builtin_fmaf(qh[8 * c + 1], a.y, acc[1]);
-        acc[2] = __builtin_fmaf(qh[8 * c + 2], a.z, acc[2]);
-        acc[3] = __builtin_fmaf(qh[8 * c + 3], a.w, acc[3]);
-        acc[4] = __builtin_fmaf(qh[8 * c + 4], b.x, acc[4]);
-        acc[5] = __builtin_fmaf(qh[8 * c + 5], b.y, acc[5]);
-        acc[6] = __builtin_fmaf(qh[8 * c + 6], b.z, acc[6]);
-        acc[7] = __builtin_fmaf(qh[8 * c + 7], b.w, acc[7]);
-      }
+      for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
+      lanes64(qh, k4, acc);
     } else {
       const uint32_t chunks = hd / 8u;
       for (uint32_t c = 0; c < chunks; c++)
@@ -297,25 +351,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
         tail += p;
       }
     }
-    float s = -0.0f;
-#pragma unroll
-    for (int l = 0; l < 8; l++) s += acc[l];
-    const float score = __fdiv_rn(s + tail, scale);
+    const float score = score_from_lanes(acc, tail, scale);
     w[i] = score;
     mx = fmaxf(mx, score);
   }
-  // max over the workgroup (exact in any order)
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (uint32_t i = tid; i < rows; i += kAttnThreads) w[i] = expf_ref(w[i] - mx);
-  __syncthreads();
-  if (tid == 0) red[4] = ordered_sum(w, rows, 0.0f);  // portable/norm.rs: `let mut sum = 0.0`
-  __syncthreads();
-  const float sum = red[4];
-  for (uint32_t i = tid; i < rows; i += kAttnThreads) w[i] = __fdiv_rn(w[i], sum);
+  softmax_rows(w, rows, mx, red);
   // mix_rows (float.rs:52-62): out starts at 0.0, each row fused in order.
   // Value tiles are staged through LDS by every thread, a tile ahead of
   // the first wave's chain of fused adds.
@@ -331,23 +371,158 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
     const bool more = tile + 1u < tiles;
     const uint32_t nr0 = r0 + kVTile, ncount = more ? (rows - nr0 < kVTile ? rows - nr0 : kVTile) : 0u;
     if (more) regs.load(vcache, kv, off, hd, nr0, ncount);
-    if (wave == 0 && lane < hd) {
-      const float* cur = vt + (tile & 1u) * kVTile * 64u;
-      const float* wr = w + r0;
-      uint32_t r = 0;
-      for (; r + 16u <= count; r += 16u) {
-        float v[16];
-#pragma unroll
-        for (int k = 0; k < 16; k++) v[k] = cur[(r + k) * hd + lane];
-#pragma unroll
-        for (int k = 0; k < 16; k++) acc = __builtin_fmaf(v[k], wr[r + k], acc);
-      }
-      for (; r < count; r++) acc = __builtin_fmaf(cur[r * hd + lane], wr[r], acc);
-    }
+    if (wave == 0 && lane < hd) acc = mix_tile(vt + (tile & 1u) * kVTile * 64u, w + r0, count, hd, lane, acc);
     if (more) regs.store(vt + ((tile + 1u) & 1u) * kVTile * 64u, hd, ncount);
     __syncthreads();
   }
   if (wave == 0 && lane < hd) mixed[static_cast<size_t>(t) * width + h * hd + lane] = acc;
+}
+
+// Value tile rows r0.. (below `rows`) of one kv head for head_dim 64, a
+// f32x4 per thread and k; row `start` comes from the projection `vnew`.
+// Loads are unconditional (rows past the end re-read row `start`, and
+// store_v_tile drops them) so the tile stays in registers.
+constexpr uint32_t kStepVTiles = 4;  // value tiles a step loads before its first wait
+constexpr uint32_t kTileF4 = kVTile * 64u / 4u / kAttnThreads;
+
+__device__ __forceinline__ void load_v_tile(f32x4 (&v)[kTileF4], const float* vcache, const float* vnew, uint32_t kv,
+                                            uint32_t off, uint32_t r0, uint32_t rows, uint32_t start) {
+#pragma unroll
+  for (uint32_t k = 0; k < kTileF4; k++) {
+    const uint32_t f = threadIdx.x + k * kAttnThreads, row = r0 + (f >> 4);
+    const uint32_t rr = row < rows ? row : start;
+    const float* src = rr == start ? vnew : vcache + static_cast<size_t>(rr) * kv + off;
+    v[k] = reinterpret_cast<const f32x4*>(src)[f & 15u];
+  }
+}
+
+__device__ __forceinline__ void store_v_tile(float* tile, const f32x4 (&v)[kTileF4], uint32_t r0, uint32_t rows) {
+#pragma unroll
+  for (uint32_t k = 0; k < kTileF4; k++) {
+    const uint32_t f = threadIdx.x + k * kAttnThreads;
+    if (r0 + (f >> 4) < rows) reinterpret_cast<f32x4*>(tile)[f] = v[k];
+  }
+}
+
+// One token at position `start` with head_dim 64: qkv_post_kernel and
+// attention_kernel in one launch, with their arithmetic. Each workgroup (one
+// per query head) rotates its q and its kv head's new key row itself, with
+// qkv_post_kernel's expressions, and takes the new value row from the
+// projection; the first workgroup of each kv head appends the new key and
+// value rows to the cache (no workgroup of the launch reads that row from
+// the cache). Every global load -- each thread's first cached key row, the
+// RoPE inputs, the new value row and up to kStepVTiles value tiles -- is
+// issued before the first wait, so the step waits on memory once.
+__global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
+    const float* qr, const float* kr, const float* vr, const float* rcos, const float* rsin, float* kcache,
+    float* vcache, uint32_t kv, uint32_t group, float scale, uint32_t start, float* mixed) {
+  constexpr uint32_t hd = 64u;
+  extern __shared__ __align__(16) float sh[];
+  const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t rows = start + 1u;
+  float* qh = sh;                        // [64]
+  float* red = sh + 64;                  // [64]
+  float* w = sh + 128;                   // [rows rounded up to 4]
+  float* vt = w + ((rows + 3u) & ~3u);   // [2][kVTile * 64]
+  float* knew = vt + kVTile * 64u;       // the rotated new key, in tile buffer 1 until the values need it
+  const uint32_t off = (h / group) * hd;
+  const bool appends = h % group == 0u;
+  const float* vnew = vr + off;
+
+  // this thread's first cached key row (row 0, unused, when it has none)
+  f32x4 k4[16];
+  const float* k0 = kcache + static_cast<size_t>(tid < start ? tid : 0u) * kv + off;
+#pragma unroll
+  for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(k0)[c];
+  // RoPE inputs (qkv_post_kernel): threads 0..31 the query's pairs, 32..63
+  // the new key's
+  float lo = 0.0f, hi = 0.0f, cs = 0.0f, sn = 0.0f;
+  const uint32_t pair = tid & 31u;
+  if (tid < 64u) {
+    const float* src = tid < 32u ? qr + static_cast<size_t>(h) * hd : kr + off;
+    lo = src[2u * pair];
+    hi = src[2u * pair + 1u];
+    cs = rcos[static_cast<size_t>(start) * (hd / 2u) + pair];
+    sn = rsin[static_cast<size_t>(start) * (hd / 2u) + pair];
+  }
+  const f32x4 vrow = reinterpret_cast<const f32x4*>(vnew)[tid & 15u];
+  f32x4 vtile[kStepVTiles][kTileF4];
+#pragma unroll
+  for (uint32_t t = 0; t < kStepVTiles; t++) load_v_tile(vtile[t], vcache, vnew, kv, off, t * kVTile, rows, start);
+
+  if (tid < 64u) {
+    const float hs = hi * sn, ls = lo * sn;
+    const float nlo = __builtin_fmaf(lo, cs, -hs), nhi = __builtin_fmaf(hi, cs, ls);
+    float* dst = tid < 32u ? qh : knew;
+    dst[2u * pair] = nlo;
+    dst[2u * pair + 1u] = nhi;
+  }
+  __syncthreads();
+  if (appends) {
+    if (tid < 16u)
+      reinterpret_cast<f32x4*>(kcache + static_cast<size_t>(start) * kv + off)[tid] =
+          reinterpret_cast<const f32x4*>(knew)[tid];
+    else if (tid >= 64u && tid < 80u)
+      reinterpret_cast<f32x4*>(vcache + static_cast<size_t>(start) * kv + off)[tid - 64u] = vrow;
+  }
+
+  float mx = -INFINITY;
+  for (uint32_t i = tid; i < rows; i += kAttnThreads) {
+    f32x4 kk[16];
+    if (i == start) {
+#pragma unroll
+      for (int c = 0; c < 16; c++) kk[c] = reinterpret_cast<const f32x4*>(knew)[c];
+    } else if (i == tid) {
+#pragma unroll
+      for (int c = 0; c < 16; c++) kk[c] = k4[c];
+    } else {
+#pragma unroll
+      for (int c = 0; c < 16; c++)
+        kk[c] = reinterpret_cast<const f32x4*>(kcache + static_cast<size_t>(i) * kv + off)[c];
+    }
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    lanes64(qh, kk, acc);
+    const float score = score_from_lanes(acc, -0.0f, scale);
+    w[i] = score;
+    mx = fmaxf(mx, score);
+  }
+  softmax_rows(w, rows, mx, red);
+
+  // mix_rows over the value tiles, staged through the two LDS buffers a tile
+  // ahead of wave 0's chain; tiles past kStepVTiles are loaded here
+  const uint32_t tiles = (rows + kVTile - 1u) / kVTile;
+  float acc = 0.0f;
+  store_v_tile(vt, vtile[0], 0u, rows);
+  __syncthreads();
+#pragma unroll
+  for (uint32_t t = 0; t < kStepVTiles; t++) {
+    if (t < tiles) {
+      const uint32_t r0 = t * kVTile, count = rows - r0 < kVTile ? rows - r0 : kVTile;
+      float* next = vt + ((t + 1u) & 1u) * kVTile * 64u;
+      if (t + 1u < tiles) {
+        if (t + 1u < kStepVTiles) {
+          store_v_tile(next, vtile[t + 1u < kStepVTiles ? t + 1u : 0u], r0 + kVTile, rows);
+        } else {
+          f32x4 v[kTileF4];
+          load_v_tile(v, vcache, vnew, kv, off, r0 + kVTile, rows, start);
+          store_v_tile(next, v, r0 + kVTile, rows);
+        }
+      }
+      if (wave == 0) acc = mix_tile(vt + (t & 1u) * kVTile * 64u, w + r0, count, hd, lane, acc);
+      __syncthreads();
+    }
+  }
+  for (uint32_t t = kStepVTiles; t < tiles; t++) {
+    const uint32_t r0 = t * kVTile, count = rows - r0 < kVTile ? rows - r0 : kVTile;
+    if (t + 1u < tiles) {
+      f32x4 v[kTileF4];
+      load_v_tile(v, vcache, vnew, kv, off, r0 + kVTile, rows, start);
+      store_v_tile(vt + ((t + 1u) & 1u) * kVTile * 64u, v, r0 + kVTile, rows);
+    }
+    if (wave == 0) acc = mix_tile(vt + (t & 1u) * kVTile * 64u, w + r0, count, hd, lane, acc);
+    __syncthreads();
+  }
+  if (wave == 0) mixed[static_cast<size_t>(h) * hd + lane] = acc;
 }
 
 // hf[t][e] = silu(gate) * up, both stored by weight row (x[e*n + t])
@@ -650,15 +825,20 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start)
     if (pending) std::swap(h, h2);
     float* kc = d->keys + l * c.context_length * kv;
     float* vc = d->values + l * c.context_length * kv;
-    const uint32_t work = w / 2u + kv / 2u + kv;
-    hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, 1u), dim3(256), 0, s, d->qr, d->kr, d->vr, 1u, w,
-                       kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
-    RHD(hipGetLastError());
     const size_t att_lds = attention_lds_floats(start + 1) * 4u;
-    hipLaunchKernelGGL(hd == 64u ? attention_kernel<64> : attention_kernel<0>,
-                       dim3(static_cast<uint32_t>(c.head_count), 1u), dim3(kAttnThreads), att_lds, s, d->q, kc, vc,
-                       w, kv, hd, static_cast<uint32_t>(c.head_count / c.head_count_kv), scale,
-                       static_cast<uint32_t>(start), d->mixed);
+    const uint32_t group = static_cast<uint32_t>(c.head_count / c.head_count_kv);
+    if (hd == 64u) {
+      hipLaunchKernelGGL(attention_step_kernel, dim3(static_cast<uint32_t>(c.head_count)), dim3(kAttnThreads),
+                         att_lds, s, d->qr, d->kr, d->vr, d->rope_cos, d->rope_sin, kc, vc, kv, group, scale,
+                         static_cast<uint32_t>(start), d->mixed);
+    } else {
+      const uint32_t work = w / 2u + kv / 2u + kv;
+      hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, 1u), dim3(256), 0, s, d->qr, d->kr, d->vr, 1u,
+                         w, kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
+      RHD(hipGetLastError());
+      hipLaunchKernelGGL(attention_kernel<0>, dim3(static_cast<uint32_t>(c.head_count), 1u), dim3(kAttnThreads),
+                         att_lds, s, d->q, kc, vc, w, kv, hd, group, scale, static_cast<uint32_t>(start), d->mixed);
+    }
     RHD(hipGetLastError());
     RHS(mm(d, d->mixed, 1, w, {{b.o, d->delta, w}}));
     NormIn fn{};

@@ -17,6 +17,10 @@ namespace rh {
 typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+// A native 4-float vector. HIP's float4 is a struct whose copies become
+// memcpy, which keeps register arrays of it in scratch when they live across
+// branches; arrays of this type stay in registers.
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
