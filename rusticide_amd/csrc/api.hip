@@ -322,6 +322,33 @@ rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& nor
   }
   return RH_OK;
 }
+bool gate_up_pairable(const rh_matrix* gate, const rh_matrix* up, size_t width) {
+  return gate && up && is_kquant(gate->type_id) && gate->type_id == up->type_id && gate->cols == width &&
+         up->cols == width && gate->rows == up->rows && gate->stride == up->stride &&
+         gate->nblocks == up->nblocks && gate->nblocks == width / 256 &&
+         norm_fusable(gate->type_id, width, static_cast<uint32_t>(width / 256));
+}
+
+rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn& norm, size_t width,
+                                  const rh_matrix* gate, const rh_matrix* up, float* out, size_t rows, hipStream_t s) {
+  if (!ctx || !hidden || !norm.weight || !out) return RH_ERR_INVALID_ARGUMENT;
+  if (!gate_up_pairable(gate, up, width) || rows > gate->rows)
+    return fail(ctx, RH_ERR_INVALID_ARGUMENT, "gate and up are not one k-quant shape");
+  if (rows == 0) return RH_OK;
+  GemvJobs g{};
+  GemvJob& j = g.j[g.n++];
+  j.w = gate->data;
+  j.w2 = up->data;
+  j.stride = gate->stride;
+  j.rows = static_cast<uint32_t>(rows);
+  j.nb = static_cast<uint32_t>(gate->nblocks);
+  j.out = out;
+  j.out_len = rows;
+  j.scale = gate->scale;
+  RH_HIP(ctx, launch_gemv_fused(gate->type_id, g, hidden, width, 1, 0, 1, s, nullptr, &norm));
+  return RH_OK;
+}
+
 const uint8_t* matrix_data(const rh_matrix* m) { return m->data; }
 size_t matrix_stride(const rh_matrix* m) { return m->stride; }
 }  // namespace rh

@@ -282,6 +282,59 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
   }
 }
 
+// The rows of a k-quant workgroup. PAIR (a gate/up launch): the workgroup
+// takes nh rows of the job's w from row0 on as its rows 0..nh-1, and the
+// same rows of w2 as its rows nh..2nh-1.
+struct WgRows {
+  uint32_t row0, nrows, nh;
+};
+
+template <bool PAIR>
+__device__ __forceinline__ WgRows wg_rows(const GemvJob& J, uint32_t R) {
+  const uint32_t per = PAIR ? R / 2u : R;
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * per;
+  const uint32_t nh = min(per, J.rows - row0);
+  return WgRows{row0, PAIR ? 2u * nh : nh, nh};
+}
+
+// Block b of workgroup row r (matrices stay below 4 GiB and 2^24 rows:
+// 24-bit multiplies, 32-bit offsets).
+template <bool PAIR>
+__device__ __forceinline__ const uint8_t* block_at(const GemvJob& J, const WgRows& g, uint32_t r, uint32_t boff) {
+  const bool second = PAIR && r >= g.nh;
+  const uint8_t* m = second ? J.w2 : J.w;
+  const uint32_t row = g.row0 + (second ? r - g.nh : r);
+  return m + (__umul24(row, static_cast<uint32_t>(J.stride)) + boff);
+}
+
+// Each row's block terms summed in block order from -0.0
+// (portable/int_dot/rows.rs:9-12,59) and written; PAIR writes
+// silu(gate) * up with silu_mul's expressions (portable/elementwise.rs:6-9).
+template <int T, bool PAIR>
+__device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, const float* terms, uint32_t nb,
+                                           uint32_t nbmax, size_t tokens, size_t t0) {
+  if constexpr (PAIR) {
+    static_assert(T == 1, "a gate/up pair serves one token");
+    for (uint32_t r = threadIdx.x; r < g.nh; r += kThreads) {
+      float gs = -0.0f, us = -0.0f;
+      for (uint32_t b = 0; b < nb; b++) gs += terms[r * nbmax + b];
+      for (uint32_t b = 0; b < nb; b++) us += terms[(r + g.nh) * nbmax + b];
+      const float den = 1.0f + expf_ref(-gs);
+      const float sg = __fdiv_rn(gs, den);
+      const size_t idx = static_cast<size_t>(g.row0 + r) * tokens + t0;
+      if (idx < J.out_len) J.out[idx] = sg * us;
+    }
+  } else {
+    for (uint32_t i = threadIdx.x; i < g.nrows * T; i += kThreads) {
+      const uint32_t r = i / T, t = i - r * T;
+      float s = -0.0f;
+      for (uint32_t b = 0; b < nb; b++) s += terms[(r * nbmax + b) * T + t];
+      const size_t idx = static_cast<size_t>(g.row0 + r) * tokens + t0 + t;
+      if (idx < J.out_len) J.out[idx] = s;
+    }
+  }
+}
+
 // Q4_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
 //      terms [R][nbmax][T] f32
@@ -289,7 +342,7 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
 // preloading FQ blocks per half-wave before the weights.
 // NORM (T = 1, the whole row in the preload): x is the hidden state and the
 // kernel applies the NormIn residual add and RMSNorm before quantizing.
-template <int T, int NI, int FQ, bool NORM>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false>
 __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
@@ -301,10 +354,9 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
   float* terms = reinterpret_cast<float*>(sums + T * nbmax * 8u);
 
   const GemvJob& J = jobs.j[find_job(jobs)];
-  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
-  const uint32_t nrows = min(R, J.rows - row0);
+  const WgRows wr = wg_rows<PAIR>(J, R);
   const uint32_t nb = J.nb;
-  const uint32_t total = nrows * nb;
+  const uint32_t total = wr.nrows * nb;
   const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
 
   // g = r*nb + b with g < 4*64: a float reciprocal divides exactly here
@@ -320,8 +372,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
     const uint32_t g = team + i * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;  // a spare team re-reads block 0
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - r * nb;
-    // matrices stay below 4 GiB and 2^24 rows: 24-bit multiplies, 32-bit offsets
-    const uint8_t* blk = J.w + (__umul24(row0 + r, static_cast<uint32_t>(J.stride)) + b * 144u);
+    const uint8_t* blk = block_at<PAIR>(J, wr, r, b * 144u);
     hd[i] = load16(blk);
     c0[i] = load16(blk + 16u + 16u * p);
     c1[i] = load16(blk + 80u + 16u * p);
@@ -399,13 +450,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
     }
   }
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < nrows * T; i += kThreads) {
-    const uint32_t r = i / T, t = i - r * T;
-    float s = -0.0f;
-    for (uint32_t b = 0; b < nb; b++) s += terms[(r * nbmax + b) * T + t];
-    const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
-    if (idx < J.out_len) J.out[idx] = s;
-  }
+  write_rows<T, PAIR>(J, wr, terms, nb, nbmax, tokens, t0);
 }
 
 // Q6_K x Q8_K --------------------------------------------------------------
@@ -413,7 +458,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ, bool NORM>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false>
 __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
@@ -425,10 +470,9 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
   float* terms = reinterpret_cast<float*>(bias + T * nbmax * 16u);
 
   const GemvJob& J = jobs.j[find_job(jobs)];
-  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R;
-  const uint32_t nrows = min(R, J.rows - row0);
+  const WgRows wr = wg_rows<PAIR>(J, R);
   const uint32_t nb = J.nb;
-  const uint32_t total = nrows * nb;
+  const uint32_t total = wr.nrows * nb;
   const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
   const uint32_t h = p >> 1, gq = p & 1u;
 
@@ -448,7 +492,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
     const uint32_t g = team + i * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - r * nb;
-    const uint8_t* base = J.w + (__umul24(row0 + r, static_cast<uint32_t>(J.stride)) + b * 210u - 2u * (b & 1u));
+    const uint8_t* base = block_at<PAIR>(J, wr, r, b * 210u - 2u * (b & 1u));
     A[i] = load16_a4(base + 64u * h + 16u * gq);
     B[i] = load16_a4(base + 64u * h + 32u + 16u * gq);
     C[i] = load16_a4(base + 128u + 32u * h + 16u * gq);
@@ -529,13 +573,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
     }
   }
   __syncthreads();
-  for (uint32_t i = threadIdx.x; i < nrows * T; i += kThreads) {
-    const uint32_t r = i / T, t = i - r * T;
-    float s = -0.0f;
-    for (uint32_t b = 0; b < nb; b++) s += terms[(r * nbmax + b) * T + t];
-    const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
-    if (idx < J.out_len) J.out[idx] = s;
-  }
+  write_rows<T, PAIR>(J, wr, terms, nb, nbmax, tokens, t0);
 }
 
 // I2_S x I8_S --------------------------------------------------------------
@@ -964,15 +1002,19 @@ uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
   return R < 1u ? 1u : R;
 }
 
-template <int FMT, int T, int NI, int FQ, bool NORM = false>
+template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false>
 void* kq_kernel() {
-  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM>)
-                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM>);
+  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR>)
+                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR>);
 }
 
 // The norm-fused decode kernels: one token, four blocks per team, the row
-// preloaded in one (FQ 1) or four (FQ 4) rounds.
-void* kq_norm_kernel(uint32_t type_id, uint32_t fq) {
+// preloaded in one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
+void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair) {
+  if (pair) {
+    if (type_id == 12u) return fq == 1u ? kq_kernel<12, 1, 4, 1, true, true>() : kq_kernel<12, 1, 4, 4, true, true>();
+    return fq == 1u ? kq_kernel<14, 1, 4, 1, true, true>() : kq_kernel<14, 1, 4, 4, true, true>();
+  }
   if (type_id == 12u) return fq == 1u ? kq_kernel<12, 1, 4, 1, true>() : kq_kernel<12, 1, 4, 4, true>();
   return fq == 1u ? kq_kernel<14, 1, 4, 1, true>() : kq_kernel<14, 1, 4, 4, true>();
 }
@@ -1069,10 +1111,15 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
   }
   const uint32_t ni = norm ? 4u : kquant ? choose_blocks_per_team<T>(type_id, nbl, total_rows, fq) : 1u;
   const uint32_t R = rows_per_wg(type_id, nbl, ni);
+  // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
+  const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
+  if (pair && (!norm || !kquant || R < 2u)) return hipErrorInvalidValue;
+  const uint32_t per = pair ? R / 2u : R;
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
+    if (i > 0 && jobs.j[i].w2) return hipErrorInvalidValue;
     jobs.j[i].wg_begin = wgs;
-    wgs += (jobs.j[i].rows + R - 1u) / R;
+    wgs += (jobs.j[i].rows + per - 1u) / per;
   }
   if (wgs == 0) return hipSuccess;
   if (type_id == 0u) {
@@ -1091,7 +1138,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       nrm = *norm;
       nrm.lds_offset = static_cast<uint32_t>((lds + 15u) / 16u * 16u);
       lds = nrm.lds_offset + static_cast<size_t>(wave_sum_floats(nbl * 256u)) * 4u + 16u;
-      k = kq_norm_kernel(type_id, fq);
+      k = kq_norm_kernel(type_id, fq, pair);
     } else {
       k = kq_kernel_for<T>(type_id, ni, fq);
     }

@@ -846,11 +846,16 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start)
     fn.weight = b.ffn_norm;
     fn.eps = c.rms_norm_eps;
     fn.hidden_out = h2;
-    const rh_job gu[2] = {{b.gate, d->gate, f}, {b.up, d->up, f}};
-    RHS(matmul_norm_device(d->ctx, h, fn, w, gu, 2, s));
+    if (gate_up_pairable(b.gate, b.up, w)) {
+      // gate and up rows side by side in one launch, which writes silu(gate) * up
+      RHS(matmul_norm_silu_device(d->ctx, h, fn, w, b.gate, b.up, d->hf, f, s));
+    } else {
+      const rh_job gu[2] = {{b.gate, d->gate, f}, {b.up, d->up, f}};
+      RHS(matmul_norm_device(d->ctx, h, fn, w, gu, 2, s));
+      hipLaunchKernelGGL(silu_mul_kernel, dim3((f + 255u) / 256u), dim3(256), 0, s, d->gate, d->up, 1u, f, d->hf);
+      RHD(hipGetLastError());
+    }
     std::swap(h, h2);
-    hipLaunchKernelGGL(silu_mul_kernel, dim3((f + 255u) / 256u), dim3(256), 0, s, d->gate, d->up, 1u, f, d->hf);
-    RHD(hipGetLastError());
     RHS(mm(d, d->hf, 1, f, {{b.down, d->delta, w}}));
     pending = d->delta;
   }

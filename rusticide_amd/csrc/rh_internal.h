@@ -39,6 +39,10 @@ struct GemvJob {
   size_t out_len;
   float scale;          // I2_S tensor scale
   uint32_t wg_begin;    // first workgroup of this job in the grid
+  // A second matrix of w's shape and stride (the up projection beside the
+  // gate one): the norm-fused k-quant launch then writes silu(w x) * (w2 x)
+  // to out instead of w x.
+  const uint8_t* w2;
 };
 
 struct GemvJobs {
@@ -121,5 +125,12 @@ hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t 
 // norm_fusable; the caller checks that once.
 rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& norm, size_t width, const rh_job* jobs,
                              size_t n_jobs, hipStream_t s);
+// The feed-forward's first half for one token in one launch:
+// out[r] = silu(gate_r . x) * (up_r . x) for rows r < rows, x the normalized
+// activation as above (feed_forward.rs:51-66). gate and up must be k-quant
+// matrices of one type, shape and stride (gate_up_pairable says when).
+bool gate_up_pairable(const rh_matrix* gate, const rh_matrix* up, size_t width);
+rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn& norm, size_t width,
+                                  const rh_matrix* gate, const rh_matrix* up, float* out, size_t rows, hipStream_t s);
 
 }  // namespace rh
