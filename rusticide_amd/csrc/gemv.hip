@@ -282,6 +282,15 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
   }
 }
 
+// Blocks per team whose weight loads a k-quant kernel issues before its
+// activation prologue; the rest go out one per block computed, `ahead`
+// blocks in front. A wave whose loads all go out at once stalls on issue
+// once its CU's memory queue is full, which holds back the prologue and every
+// dot behind it; the norm-fused kernels, whose prologue is longer, still
+// issue every block first.
+template <int NI, bool NORM>
+constexpr int issue_ahead() { return NORM ? NI : (NI < 2 ? NI : 2); }
+
 // The rows of a k-quant workgroup. PAIR (a gate/up launch): the workgroup
 // takes nh rows of the job's w from row0 on as its rows 0..nh-1, and the
 // same rows of w2 as its rows nh..2nh-1.
@@ -317,8 +326,8 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
     static_assert(T == 1, "a gate/up pair serves one token");
     for (uint32_t r = threadIdx.x; r < g.nh; r += kThreads) {
       float gs = -0.0f, us = -0.0f;
-      for (uint32_t b = 0; b < nb; b++) gs += terms[r * nbmax + b];
-      for (uint32_t b = 0; b < nb; b++) us += terms[(r + g.nh) * nbmax + b];
+      for (uint32_t b = 0; b < nb; b++) gs += terms[__umul24(r, nbmax) + b];
+      for (uint32_t b = 0; b < nb; b++) us += terms[__umul24(r + g.nh, nbmax) + b];
       const float den = 1.0f + expf_ref(-gs);
       const float sg = __fdiv_rn(gs, den);
       const size_t idx = static_cast<size_t>(g.row0 + r) * tokens + t0;
@@ -328,7 +337,7 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
     for (uint32_t i = threadIdx.x; i < g.nrows * T; i += kThreads) {
       const uint32_t r = i / T, t = i - r * T;
       float s = -0.0f;
-      for (uint32_t b = 0; b < nb; b++) s += terms[(r * nbmax + b) * T + t];
+      for (uint32_t b = 0; b < nb; b++) s += terms[(__umul24(r, nbmax) + b) * T + t];
       const size_t idx = static_cast<size_t>(g.row0 + r) * tokens + t0 + t;
       if (idx < J.out_len) J.out[idx] = s;
     }
@@ -367,16 +376,18 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
   NormRound<FQ ? FQ : 1> nr;
   if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
   u32x4 hd[NI], c0[NI], c1[NI];
-#pragma unroll
-  for (int i = 0; i < NI; i++) {
-    const uint32_t g = team + i * (kThreads / 4u);
+  auto issue = [&](int i) {
+    const uint32_t g = team + static_cast<uint32_t>(i) * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;  // a spare team re-reads block 0
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - r * nb;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
     const uint8_t* blk = block_at<PAIR>(J, wr, r, b * 144u);
     hd[i] = load16(blk);
     c0[i] = load16(blk + 16u + 16u * p);
     c1[i] = load16(blk + 80u + 16u * p);
-  }
+  };
+  constexpr int ahead = issue_ahead<NI, NORM>();
+#pragma unroll
+  for (int i = 0; i < ahead; i++) issue(i);
 
   if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
                                     reinterpret_cast<float*>(lds + nrm.lds_offset) + wave_sum_floats(xg.total * 256u));
@@ -398,9 +409,10 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
   const bool min_lane = (p & 1u) == 0;
 #pragma unroll
   for (int it = 0; it < NI; it++) {
+    if (it + ahead < NI) issue(it + ahead);
     const uint32_t g = team + it * (kThreads / 4u);
     if (g >= total) break;  // uniform over the team
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - r * nb;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
     const u32x4 h = hd[it];
     // 6-bit scales/mins of sub-blocks j0, j0+1, j0+4, j0+5 (ggml get_scale_min_k4,
     // quantize/src/q4_k.rs:17-25)
@@ -437,15 +449,18 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
         D2 = dot4(lo1[k], a2[k], D2);
         D3 = dot4(hi1[k], a3[k], D3);
       }
-      int32_t isum = sc0 * D0 + sc1 * D1 + sc2 * D2 + sc3 * D3;
+      // 24-bit multiplies are exact here: |D| < 2^17, sums of 32 quants < 2^12,
+      // scales and mins below 64
+      int32_t isum = __mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3);
       const int32_t* S = sums + t * nbmax * 8u + b * 8u + j0;
-      int32_t msum = min_lane ? (m0 * S[0] + m1 * S[1] + m2 * S[4] + m3 * S[5]) : 0;
+      int32_t msum =
+          min_lane ? (__mul24(m0, S[0]) + __mul24(m1, S[1]) + __mul24(m2, S[4]) + __mul24(m3, S[5])) : 0;
       isum = quad_sum(isum);
       msum = quad_sum(msum);
       if (p == 0) {
         // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
         const float neg = -(dmin * static_cast<float>(msum));
-        terms[(r * nbmax + b) * T + t] = d8[t * nbmax + b] * __builtin_fmaf(d, static_cast<float>(isum), neg);
+        terms[(__umul24(r, nbmax) + b) * T + t] = d8[t * nbmax + b] * __builtin_fmaf(d, static_cast<float>(isum), neg);
       }
     }
   }
@@ -487,11 +502,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
   NormRound<FQ ? FQ : 1> nr;
   if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
   u32x4 A[NI], B[NI], C[NI], W[NI], E[NI];
-#pragma unroll
-  for (int i = 0; i < NI; i++) {
-    const uint32_t g = team + i * (kThreads / 4u);
+  auto issue = [&](int i) {
+    const uint32_t g = team + static_cast<uint32_t>(i) * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - r * nb;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
     const uint8_t* base = block_at<PAIR>(J, wr, r, b * 210u - 2u * (b & 1u));
     A[i] = load16_a4(base + 64u * h + 16u * gq);
     B[i] = load16_a4(base + 64u * h + 32u + 16u * gq);
@@ -499,7 +513,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
     W[i] = load16_a4(base + 192u);
     E[i] = u32x4{load4(base + 64u * h + 16u * gq + 16u), load4(base + 64u * h + 48u + 16u * gq),
                  load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
-  }
+  };
+  constexpr int ahead = issue_ahead<NI, NORM>();
+#pragma unroll
+  for (int i = 0; i < ahead; i++) issue(i);
 
   if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
                                     reinterpret_cast<float*>(lds + nrm.lds_offset) + wave_sum_floats(xg.total * 256u));
@@ -518,9 +535,10 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
 
 #pragma unroll
   for (int it = 0; it < NI; it++) {
+    if (it + ahead < NI) issue(it + ahead);
     const uint32_t g = team + it * (kThreads / 4u);
     if (g >= total) break;  // uniform over the team
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - r * nb;
+    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
     const uint32_t sh = 2u * (b & 1u);
     const u32x4 a{__builtin_amdgcn_alignbyte(A[it].y, A[it].x, sh), __builtin_amdgcn_alignbyte(A[it].z, A[it].y, sh),
                   __builtin_amdgcn_alignbyte(A[it].w, A[it].z, sh), __builtin_amdgcn_alignbyte(E[it].x, A[it].w, sh)};
@@ -564,11 +582,12 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
         D2 = dot4(q2[k], a2[k], D2);
         D3 = dot4(q3[k], a3[k], D3);
       }
-      int32_t isum = quad_sum(sc0 * D0 + sc1 * D1 + sc2 * D2 + sc3 * D3);
+      // |D| < 2^20 and |scale| <= 128: the 24-bit multiplies are exact
+      int32_t isum = quad_sum(__mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3));
       if (p == 0) {
         // int_dot.rs:203: read_f16_le(block, 208) * span.scales[0] * lossy(sum)
         const float dd = d * d8[t * nbmax + b];
-        terms[(r * nbmax + b) * T + t] = dd * static_cast<float>(isum);
+        terms[(__umul24(r, nbmax) + b) * T + t] = dd * static_cast<float>(isum);
       }
     }
   }
@@ -990,6 +1009,7 @@ uint32_t forced_blocks_per_team() {
     if (v[0] == '1') return 1u;
     if (v[0] == '2') return 2u;
     if (v[0] == '4') return 4u;
+    if (v[0] == '8') return 8u;
   }
   return 0u;
 }
@@ -1021,6 +1041,9 @@ void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair) {
 
 template <int FMT, int T, int FQ>
 void* kq_kernel_ni(uint32_t ni) {
+  // eight blocks per team: one-token fused launches only
+  if constexpr (T == 1 && FQ != 0)
+    if (ni == 8u) return kq_kernel<FMT, T, 8, FQ>();
   return ni == 4u ? kq_kernel<FMT, T, 4, FQ>() : ni == 2u ? kq_kernel<FMT, T, 2, FQ>() : kq_kernel<FMT, T, 1, FQ>();
 }
 
@@ -1072,13 +1095,27 @@ uint32_t min_blocks_per_team(uint32_t nb) {
 
 // The fused kernels take four blocks per team: measured on MI355X at the
 // TinyLlama / BitNet decode shapes, NI = 4 is the fastest or within 1%
-// everywhere (fewer, longer-lived workgroups amortize the quantize prologue).
+// everywhere (fewer, longer-lived workgroups amortize the quantize prologue),
+// except for one-token launches of three or more workgroups per CU, which
+// take eight (Q6_K 32000x2048: 12.5 us against 13.1 us).
 // The others take the smallest NI that keeps every workgroup resident.
 template <int T>
 uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_rows, uint32_t fq) {
   const uint32_t floor_ni = min_blocks_per_team(nb);
-  if (const uint32_t forced = forced_blocks_per_team()) return forced > floor_ni ? forced : floor_ni;
-  if (fq) return 4u;
+  if (uint32_t forced = forced_blocks_per_team()) {
+    if (forced == 8u && (T != 1 || !fq)) forced = 4u;  // eight: one-token fused kernels only
+    return forced > floor_ni ? forced : floor_ni;
+  }
+  if (fq) {
+    // every workgroup quantizes the whole activation: when four blocks per
+    // team would give three or more workgroups per CU (a 32000-row output
+    // matrix), eight halve that repeated work; smaller launches keep four so
+    // the grid still covers the chip
+    if (T == 1 && (total_rows + rows_per_wg(type_id, nb, 4u) - 1u) / rows_per_wg(type_id, nb, 4u) >=
+                      3u * static_cast<uint32_t>(device_cus()))
+      return 8u;
+    return 4u;
+  }
   for (uint32_t ni : {1u, 2u, 4u}) {
     if (ni < floor_ni) continue;
     const uint32_t R = rows_per_wg(type_id, nb, ni);
