@@ -285,11 +285,10 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
 // Blocks per team whose weight loads a k-quant kernel issues before its
 // activation prologue; the rest go out one per block computed, `ahead`
 // blocks in front. A wave whose loads all go out at once stalls on issue
-// once its CU's memory queue is full, which holds back the prologue and every
-// dot behind it; the norm-fused kernels, whose prologue is longer, still
-// issue every block first.
+// once its CU's memory queue is full, which holds back the prologue (the
+// quantize, and the norm in the norm-fused kernels) and every dot behind it.
 template <int NI, bool NORM>
-constexpr int issue_ahead() { return NORM ? NI : (NI < 2 ? NI : 2); }
+constexpr int issue_ahead() { return NI < 2 ? NI : 2; }
 
 // The rows of a k-quant workgroup. PAIR (a gate/up launch): the workgroup
 // takes nh rows of the job's w from row0 on as its rows 0..nh-1, and the
