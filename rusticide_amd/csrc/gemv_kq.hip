@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvJobs jobs, Q8Dev q, Ti
   const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
 
   // the first tile's weights are requested before anything else
-  Raw cur[kNI], nxt[kNI];
+  Raw bufa[kNI], bufb[kNI];
   auto issue = [&](Raw (&buf)[kNI], uint32_t gt) {
     if (gt >= geo.tiles) return;  // uniform
     const GemvJob& J = jobs.j[tile_job(jobs, gt)];
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvJobs jobs, Q8Dev q, Ti
     }
   };
   uint32_t gt = blockIdx.x;
-  issue(cur, gt);
+  issue(bufa, gt);
 
   // stage the activation once per workgroup; chunk c of block b goes to
   // chunk c ^ (b & 15) so the teams of a wave read distinct LDS banks
@@ -132,7 +132,10 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvJobs jobs, Q8Dev q, Ti
   const uint32_t j0 = 2u * (p >> 1), e0 = 16u * (p & 1u);  // Q4_K lane roles
   const bool min_lane = (p & 1u) == 0;
 
-  for (uint32_t k = 0; gt < geo.tiles; k++, gt += gridDim.x) {
+  // one tile from the register set `cur`, after the next tile's loads go
+  // into `nxt`; the two sets alternate (a copy between them would wait for
+  // the loads just issued)
+  auto tile = [&](const Raw (&cur)[kNI], Raw (&nxt)[kNI], uint32_t k, uint32_t gt) {
     issue(nxt, gt + gridDim.x);
     const GemvJob& J = jobs.j[tile_job(jobs, gt)];
     const uint32_t row0 = (gt - J.wg_begin) * R;
@@ -182,9 +185,10 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvJobs jobs, Q8Dev q, Ti
             D2 = dot4(lo1[i], a2[i], D2);
             D3 = dot4(hi1[i], a3[i], D3);
           }
-          int32_t isum = sc0 * D0 + sc1 * D1 + sc2 * D2 + sc3 * D3;
+          int32_t isum = __mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3);
           const int32_t* S = side + t * nbmax * 16u + b * 8u + j0;
-          int32_t msum = min_lane ? (m0 * S[0] + m1 * S[1] + m2 * S[4] + m3 * S[5]) : 0;
+          int32_t msum =
+              min_lane ? (__mul24(m0, S[0]) + __mul24(m1, S[1]) + __mul24(m2, S[4]) + __mul24(m3, S[5])) : 0;
           isum = quad_sum(isum);
           msum = quad_sum(msum);
           if (p == 0) {
@@ -240,7 +244,7 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvJobs jobs, Q8Dev q, Ti
             D2 = dot4(q2[i], a2[i], D2);
             D3 = dot4(q3[i], a3[i], D3);
           }
-          const int32_t isum = quad_sum(sc0 * D0 + sc1 * D1 + sc2 * D2 + sc3 * D3);
+          const int32_t isum = quad_sum(__mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3));
           if (p == 0) {
             // int_dot.rs:203: read_f16_le(block, 208) * span.scales[0] * lossy(sum)
             const float dd = d * d8[t * nbmax + b];
@@ -258,8 +262,11 @@ __global__ __launch_bounds__(256) void gemv_kq_kernel(GemvJobs jobs, Q8Dev q, Ti
       const size_t idx = static_cast<size_t>(row0 + r) * tokens + t0 + t;
       if (idx < J.out_len) J.out[idx] = s;
     }
-#pragma unroll
-    for (int i = 0; i < kNI; i++) cur[i] = nxt[i];
+  };
+  for (uint32_t k = 0; gt < geo.tiles; k += 2u, gt += 2u * gridDim.x) {
+    tile(bufa, bufb, k, gt);
+    if (gt + gridDim.x >= geo.tiles) break;
+    tile(bufb, bufa, k + 1u, gt + gridDim.x);
   }
 }
 
