@@ -1002,7 +1002,7 @@ size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
 // Blocks per 4-lane team in the k-quant kernels (1, 2 or 4), chosen per
 // launch: the smallest that lets every workgroup of the grid be resident at
 // once, so no rows wait for a second generation of workgroups.
-// RUSTICIDE_HIP_GEMV_NI=1|2|4 forces it, for tuning.
+// RUSTICIDE_HIP_GEMV_NI=1|2|4|8 forces it, for tuning.
 uint32_t forced_blocks_per_team() {
   if (const char* v = std::getenv("RUSTICIDE_HIP_GEMV_NI")) {
     if (v[0] == '1') return 1u;
