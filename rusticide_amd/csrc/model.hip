@@ -273,14 +273,28 @@ __device__ __forceinline__ float score_from_lanes(const float (&acc)[8], float t
   return __fdiv_rn(s + tail, scale);
 }
 
+// f32 order as unsigned keys, for DPP maxima: a larger float, a larger key;
+// NaN maps to 0, below every number, and back to a NaN.
+__device__ __forceinline__ uint32_t max_key(float f) {
+  const uint32_t b = __float_as_uint(f);
+  return f != f ? 0u : (b >> 31) ? ~b : (b | 0x80000000u);
+}
+__device__ __forceinline__ float max_key_float(uint32_t k) {
+  return __uint_as_float((k >> 31) ? (k & 0x7fffffffu) : ~k);
+}
+
 // softmax (norm.rs:17-30) of the scores w[0..rows) in place, given each
 // thread's maximum of the scores it wrote: the maximum over the workgroup
 // (exact in any order), exp(x - max), the sum in order from 0.0 on one lane,
 // and the division. The caller synchronizes before reading w.
 __device__ __forceinline__ void softmax_rows(float* w, uint32_t rows, float mx, float* red) {
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  // the maximum over each half-wave as an order-preserving key (DPP), then
+  // the two halves; NaN keys are the smallest, so NaN scores drop out as
+  // fmaxf drops them
+  mx = max_key_float(half_max_u32(max_key(mx)));
+  mx = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
+             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)));
   if (lane == 0) red[wave] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -429,13 +443,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
   const bool appends = h % group == 0u;
   const float* vnew = vr + off;
 
-  // this thread's first cached key row (row 0, unused, when it has none)
-  f32x4 k4[16];
-  const float* k0 = kcache + static_cast<size_t>(tid < start ? tid : 0u) * kv + off;
-#pragma unroll
-  for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(k0)[c];
   // RoPE inputs (qkv_post_kernel): threads 0..31 the query's pairs, 32..63
-  // the new key's
+  // the new key's. Issued first: loads return in order, and the rotation and
+  // the barrier after it need only these.
   float lo = 0.0f, hi = 0.0f, cs = 0.0f, sn = 0.0f;
   const uint32_t pair = tid & 31u;
   if (tid < 64u) {
@@ -445,6 +455,11 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
     cs = rcos[static_cast<size_t>(start) * (hd / 2u) + pair];
     sn = rsin[static_cast<size_t>(start) * (hd / 2u) + pair];
   }
+  // this thread's first cached key row (row 0, unused, when it has none)
+  f32x4 k4[16];
+  const float* k0 = kcache + static_cast<size_t>(tid < start ? tid : 0u) * kv + off;
+#pragma unroll
+  for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(k0)[c];
   const f32x4 vrow = reinterpret_cast<const f32x4*>(vnew)[tid & 15u];
   f32x4 vtile[kStepVTiles][kTileF4];
 #pragma unroll
