@@ -157,6 +157,39 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
     }
 
 
+def measure_stream_read(ctx, nbytes: int, copies: int, steps: int, warmup: int) -> float:
+    """GB/s of a plain streaming read (rh_stream_read_device) of `nbytes` per
+    launch, rotated over the same number of copies as the headline: the
+    measured ceiling the GEMV kernel is compared with."""
+    import ctypes
+    import rusticide_amd as R
+    from rusticide_amd import hip as H
+
+    L = R.lib()
+    L.rh_stream_read_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_size_t,
+                                        ctypes.c_size_t, ctypes.c_void_p]
+    n = (nbytes + 15) // 16 * 16
+    bufs = [H.DeviceArray(n // 4) for _ in range(copies)]
+    for b in bufs:
+        b.fill_bytes(0x3C)
+    ptrs = (ctypes.c_void_p * copies)(*[b.ptr.value for b in bufs])
+    sink = H.DeviceArray(2048, dtype=np.uint32)
+    # the launches are queued from C: a Python call per launch would take
+    # longer than the ~9 us read and leave the GPU idle between launches
+    ctx.check(L.rh_stream_read_device(ctx.handle, ptrs, copies, n, warmup, sink.ptr))
+    H.synchronize()
+    start, end = H.Event(), H.Event()
+    start.record(ctx.stream)
+    ctx.check(L.rh_stream_read_device(ctx.handle, ptrs, copies, n, steps, sink.ptr))
+    end.record(ctx.stream)
+    H.synchronize()
+    us = 1e3 * start.elapsed_ms(end) / steps
+    for b in bufs:
+        b.free()
+    sink.free()
+    return n / (us * 1e-6) / 1e9
+
+
 def measure_cpu(res: dict, seconds: float):
     """The oracle (a C restatement of the reference CPU path) on this host's cores."""
     import oracle as O
@@ -192,7 +225,8 @@ def measure_cpu(res: dict, seconds: float):
     return {
         "value": round(res["bytes"] / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
         "sample": (f"{n} full {rows}x{cols} GEMVs incl. activation quantization, "
-                   f"{threads} threads, {el:.2f} s wall on {cpu}; bit-identical to the GPU: {same}"),
+                   f"{threads} threads ({os.cpu_count()} visible), {el:.2f} s wall on {cpu}; "
+                   f"bit-identical to the GPU: {same}"),
     }
 
 
@@ -419,6 +453,10 @@ def main() -> int:
             f"warm {r['warm_kernel_us']:.2f} us = {r['warm_kernel_gbs']:.0f} GB/s; "
             f"pre-quantized GEMV alone {r['prequantized_gemv_us']:.2f} us")
     h = results[HEADLINE]
+    stream_gbs = measure_stream_read(ctx, h["bytes"], h["copies"], args.steps, args.warmup)
+    log(f"[bench] streaming read of the same bytes per launch: {stream_gbs:.0f} GB/s "
+        f"({100 * stream_gbs / HBM_PEAK_GBS:.1f}% of 8 TB/s); the GEMV kernel reaches "
+        f"{100 * h['kernel_gbs'] / stream_gbs:.1f}% of it")
     gemm = None if args.no_gemm else measure_gemm(ctx)
     if gemm:
         for g in gemm:
@@ -476,6 +514,8 @@ def main() -> int:
                      "traffic": traffic_for(HEADLINE),
                      "kernel": h["kernel"], "kernel_avg_us": round(h["kernel_us"], 3),
                      "warm_cache_resident_gbs": round(h["warm_kernel_gbs"], 1),
+                     "stream_read_gbs": round(stream_gbs, 1),
+                     "frac_of_stream_read": round(h["kernel_gbs"] / stream_gbs, 4),
                      "prequantized_gemv_us": round(h["prequantized_gemv_us"], 3)},
         "cpu_baseline": cpu,
         "also": also,

@@ -169,6 +169,15 @@ enum { RH_MATH_EXPF = 0, RH_MATH_SQRT = 1, RH_MATH_DIV = 2 };
 void rh_expf_host(const float *x, float *y, size_t n);
 void rh_sqrt_host(const float *x, const float *start, float *y, size_t n);
 rh_status rh_math_device(rh_ctx *ctx, uint32_t op, const float *a, const float *b, float *y, size_t n);
+/* Bench hook with no reference counterpart: `launches` plain streaming reads
+ * of `bytes` (a multiple of 16) of device memory, launch i reading
+ * buffers[i % n_buffers] (16-byte aligned device pointers), queued on the
+ * context's stream, asynchronous. It is the measured bandwidth ceiling the
+ * GEMV kernels are compared with; `sink` (device memory of
+ * RH_STREAM_READ_SINK_WORDS words) receives one word per workgroup. */
+enum { RH_STREAM_READ_SINK_WORDS = 2048 };
+rh_status rh_stream_read_device(rh_ctx *ctx, const void *const *buffers, size_t n_buffers, size_t bytes,
+                                size_t launches, uint32_t *sink);
 /* Test hook with no reference counterpart: the ordered float sum the decoder
  * kernels form for RMSNorm, ((init + values[0]) + values[1]) + ... one IEEE
  * add at a time (the f32 `Sum` fold of
