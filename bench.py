@@ -30,6 +30,9 @@ a 64-token prompt then 128 greedy tokens (generate.rs:35-124), f32 KV cache.
 tok/s = 128 / decode wall time, where decode time is a 129-token generation
 less a 1-token one (both include the same prefill). The CPU oracle decodes a
 few of the same tokens on the host cores beside it and must pick the same ones.
+The model reaches the device as a GGUF file (rusticide_amd.gguf writes it):
+`gguf_load` times its parse (rh_gguf_parse) and the upload of its tensors to
+HBM (rh_gguf_model_load, host memory to device).
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -311,10 +314,33 @@ def measure_decode(ctx, reps: int, prompt_len: int = 64, new_tokens: int = 128):
     import rusticide_amd as R
     from rusticide_amd import synth
 
+    from rusticide_amd import gguf as G
+
     t0 = time.perf_counter()
     model = synth.decoder_model(synth.TINYLLAMA, seed=7)
-    dec = R.Decoder(ctx, model)
-    log(f"[bench] e2e: model built and uploaded in {time.perf_counter() - t0:.1f} s")
+    data = G.decoder_gguf(model)
+    log(f"[bench] e2e: model and its {len(data) / 1e6:.0f} MB GGUF file built in {time.perf_counter() - t0:.1f} s")
+    # the file's way onto the device: parse (a copy of the bytes and the
+    # table checks), then every tensor checked and uploaded
+    parse_s, upload_s = [], []
+    for _ in range(3):
+        t = time.perf_counter()
+        f = G.GgufFile(data)
+        parse_s.append(time.perf_counter() - t)
+        t = time.perf_counter()
+        gm = G.GgufModel(ctx, f)
+        upload_s.append(time.perf_counter() - t)
+        gm.free()
+        f.close()
+    f = G.GgufFile(data)
+    gm = G.GgufModel(ctx, f)
+    dec = gm.decoder()
+    load = {"file_bytes": len(data), "tensors": f.tensor_count, "parse_ms": float(np.median(parse_s)) * 1e3,
+            "upload_ms": float(np.median(upload_s)) * 1e3}
+    load["upload_gbs"] = len(data) / (load["upload_ms"] * 1e-3) / 1e9
+    del data
+    log(f"[bench] e2e: GGUF parse {load['parse_ms']:.1f} ms, upload {load['upload_ms']:.1f} ms "
+        f"({load['upload_gbs']:.1f} GB/s host to HBM)")
     prompt = np.random.default_rng(1).integers(0, synth.TINYLLAMA["vocab_size"], prompt_len).astype(np.uint32)
     tokens = dec.generate_greedy(prompt, new_tokens + 1)  # warm-up
     decode_s, prefill_s = [], []
@@ -329,13 +355,15 @@ def measure_decode(ctx, reps: int, prompt_len: int = 64, new_tokens: int = 128):
         decode_s.append(tn - t1)
         prefill_s.append(t1)
     dec.close()
+    gm.free()
+    f.close()
     d = float(np.median(decode_s))
     per_token = decode_bytes_per_token(model, prompt_len + new_tokens // 2)
     return {
         "model": model, "prompt": prompt, "tokens": tokens[:new_tokens],
         "tok_s": new_tokens / d, "us_per_token": d / new_tokens * 1e6,
         "prefill_ms": float(np.median(prefill_s)) * 1e3, "bytes_per_token": per_token,
-        "gbs": per_token / (d / new_tokens) / 1e9,
+        "gbs": per_token / (d / new_tokens) / 1e9, "gguf_load": load,
     }
 
 
@@ -491,6 +519,7 @@ def main() -> int:
             "prefill_64_ms": round(e2e["prefill_ms"], 3),
             "bytes_per_token": e2e["bytes_per_token"], "compulsory_gbs": round(e2e["gbs"], 1),
             "hbm_frac": round(e2e["gbs"] / HBM_PEAK_GBS, 4),
+            "gguf_load": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in e2e["gguf_load"].items()},
             "cpu_oracle": cpu_decode,
         }
     line = {

@@ -35,7 +35,11 @@ typedef enum rh_status {
     RH_ERR_NO_DEVICE = 8,        /* no gfx950 device: the caller falls back */
     RH_ERR_CONTEXT_FULL = 9,     /* ModelError::ContextFull                */
     RH_ERR_CACHE_POSITION = 10,  /* ModelError::CachePosition              */
-    RH_ERR_NO_VALID_TOKENS = 11  /* SamplingError::NoValidTokens           */
+    RH_ERR_NO_VALID_TOKENS = 11, /* SamplingError::NoValidTokens           */
+    RH_ERR_GGUF = 12,            /* GgufError: rh_gguf_error says which     */
+    RH_ERR_MISSING_METADATA = 13, /* ModelError::MissingMetadata            */
+    RH_ERR_MISSING_TENSOR = 14,  /* ModelError::MissingTensor               */
+    RH_ERR_UNKNOWN_ARCHITECTURE = 15 /* ModelError::UnknownArchitecture    */
 } rh_status;
 
 /* GGML type ids (crates/rusticide-quantize/src/format.rs:31-92), plus the
@@ -69,7 +73,8 @@ typedef struct rh_job {
  * RH_ERR_NO_DEVICE tells the caller to keep the CPU adapter. */
 rh_status rh_init(int device, rh_ctx **out);
 void rh_destroy(rh_ctx *ctx);
-/* The message of the last failed call on this context ("" if none). */
+/* The message of the last failed call on this context ("" if none); with
+ * NULL, of the last failed call this thread made without a context. */
 const char *rh_last_error(const rh_ctx *ctx);
 /* Adapter name, as `Adapter::name` (adapter.rs:40-45): "hip-gfx950". */
 const char *rh_adapter_name(void);
@@ -247,6 +252,97 @@ rh_status rh_decoder_forward_batch(rh_decoder *d, const uint32_t *tokens, size_t
  * context end. The picks stay on the device between steps. */
 rh_status rh_decoder_generate_greedy(rh_decoder *d, const uint32_t *prompt, size_t n, size_t max_tokens,
                                      uint32_t *out, size_t *n_out);
+
+/* ------------------------------------------------------------------- GGUF
+ * GGUF v3 files held in memory (crates/rusticide-io/src/gguf) and the upload
+ * of their tensors to HBM (crates/rusticide-model/src/weights.rs:40-98,
+ * crates/rusticide-transformer/src/{hyperparameters.rs,loader.rs}). */
+
+/* GgufError (crates/rusticide-io/src/error.rs:9-108), kind by kind. */
+enum {
+    RH_GGUF_OK = 0,
+    RH_GGUF_INVALID_MAGIC = 1,
+    RH_GGUF_UNSUPPORTED_VERSION = 2,     /* value: the version            */
+    RH_GGUF_UNSUPPORTED_TENSOR_TYPE = 3, /* name, value: the type id       */
+    RH_GGUF_CAST_OVERFLOW = 4,
+    RH_GGUF_INVALID_ALIGNMENT = 5,
+    RH_GGUF_DUPLICATE_KEY = 6,           /* name: the key                  */
+    RH_GGUF_DUPLICATE_TENSOR = 7,        /* name                           */
+    RH_GGUF_TOO_MANY_DIMENSIONS = 8,     /* value: the declared count      */
+    RH_GGUF_SHAPE_OVERFLOW = 9,          /* name                           */
+    RH_GGUF_MISALIGNED_TENSOR = 10,      /* name, value: the offset        */
+    RH_GGUF_OVERLAPPING_TENSORS = 11,    /* name, other: the two, in data order */
+    RH_GGUF_UNEXPECTED_EOF = 12,
+    RH_GGUF_TENSOR_NOT_FOUND = 13,       /* name                           */
+    RH_GGUF_INVALID_VALUE_TYPE = 14,     /* value: the type tag            */
+    RH_GGUF_METADATA_TOO_LARGE = 15,     /* value: the element limit       */
+    RH_GGUF_NESTING_TOO_DEEP = 16        /* value: the depth limit         */
+};
+typedef struct rh_gguf_error {
+    uint32_t kind;
+    uint64_t value;
+    char name[128];  /* NUL-terminated, truncated */
+    char other[128]; /* the second tensor of OVERLAPPING_TENSORS */
+} rh_gguf_error;
+
+typedef struct rh_gguf rh_gguf;
+
+/* GgufFile::from_bytes (gguf/file.rs:39-62): parses a GGUF v3 file and keeps a
+ * copy of its bytes. On RH_ERR_GGUF, *err (when given) says what failed. */
+rh_status rh_gguf_parse(const void *bytes, size_t len, rh_gguf **out, rh_gguf_error *err);
+void rh_gguf_free(rh_gguf *g);
+/* Metadata::len, GgufFile::tensor_count. */
+size_t rh_gguf_metadata_count(const rh_gguf *g);
+size_t rh_gguf_tensor_count(const rh_gguf *g);
+/* tensor_names()[index] (sorted) and its TensorInfo:
+ * the shape outermost first ([1] for a scalar; at most 4 dimensions), the
+ * GGML type id and the offset in the data section. The name stays valid
+ * until rh_gguf_free (gguf/tensor_info.rs:15-62). */
+rh_status rh_gguf_tensor_at(const rh_gguf *g, size_t index, const char **name, uint32_t *type_id,
+                            size_t *n_dims, uint64_t shape[4], uint64_t *offset);
+/* The index of a tensor name; RH_ERR_MISSING_TENSOR when absent. */
+rh_status rh_gguf_tensor_find(const rh_gguf *g, const char *name, size_t *index);
+/* GgufFile::quantized_tensor / layout (gguf/load.rs:47-79): the tensor's bytes
+ * inside the held file (blocks and any trailer; F32/F16 values), valid until
+ * rh_gguf_free. RH_ERR_GGUF with TENSOR_NOT_FOUND, UNSUPPORTED_TENSOR_TYPE,
+ * CAST_OVERFLOW or UNEXPECTED_EOF. */
+rh_status rh_gguf_tensor_data(const rh_gguf *g, const char *name, const uint8_t **data, size_t *len,
+                              rh_gguf_error *err);
+/* Metadata::get: the value type tag of a key (0..12 as in the file; arrays
+ * are 9); RH_ERR_MISSING_METADATA when absent. */
+rh_status rh_gguf_meta_type(const rh_gguf *g, const char *key, uint32_t *value_type);
+/* Metadata::arch_unsigned (gguf/metadata.rs:117-125): u32, u64, or a
+ * non-negative i32/i64, as u64. */
+rh_status rh_gguf_meta_uint(const rh_gguf *g, const char *key, uint64_t *out);
+/* Metadata::arch_float (gguf/metadata.rs:128-134): f32, or f64 narrowed. */
+rh_status rh_gguf_meta_float(const rh_gguf *g, const char *key, float *out);
+/* A string value, its invalid UTF-8 replaced by U+FFFD (Cursor::string,
+ * gguf/cursor.rs:57-60): `*len` bytes (when `len` is given; the value may
+ * hold NULs) followed by a NUL, valid until rh_gguf_free. */
+rh_status rh_gguf_meta_string(const rh_gguf *g, const char *key, const char **out, size_t *len);
+
+/* DecoderConfig::from_source (crates/rusticide-transformer/src/hyperparameters.rs:80-135) for the llama
+ * family (crates/rusticide-llama/src/variant.rs:41-49): the llama.* keys,
+ * head_count_kv defaulting to head_count, rope.freq_base to 10000 and the
+ * RMS epsilon to 1e-5, vocab_size from token_embd.weight. Errors:
+ * MISSING_METADATA without general.architecture and UNKNOWN_ARCHITECTURE
+ * when it is not "llama" (crates/rusticide-model/src/registry.rs:39-55),
+ * MISSING_METADATA, MISSING_TENSOR, INVALID_CONFIG; the message names the
+ * key or tensor, or gives the reason (rh_last_error of `ctx`, which may be
+ * NULL). */
+rh_status rh_gguf_decoder_config(rh_ctx *ctx, const rh_gguf *g, rh_decoder_config *out);
+
+/* A decoder's weights uploaded from a GGUF file: DecoderWeights::from_source
+ * (crates/rusticide-transformer/src/loader.rs:19-93) for the llama family. Every matrix is checked against
+ * its expected shape and uploaded with rh_matrix_load; norms are read as
+ * f32. output.weight is optional (tied to token_embd). Bias and sub-norm
+ * tensors are rejected (MISSING_KERNEL): this decoder has neither. */
+typedef struct rh_gguf_model rh_gguf_model;
+rh_status rh_gguf_model_load(rh_ctx *ctx, const rh_gguf *g, rh_gguf_model **out);
+const rh_decoder_config *rh_gguf_model_config(const rh_gguf_model *m);
+/* rh_decoder_new over the model's weights; free the decoder first. */
+rh_status rh_gguf_model_decoder(rh_gguf_model *m, rh_decoder **out);
+void rh_gguf_model_free(rh_gguf_model *m);
 
 #ifdef __cplusplus
 }

@@ -45,10 +45,14 @@ static orc_job mat_job(const orc_matrix *m, float *out, size_t out_len)
         j.data_len = m->rows * m->cols;
         j.width = m->cols;
     } else {
-        j.kind = ORC_BLOCKS;
+        j.kind = m->type_id == 36 ? ORC_TERNARY : ORC_BLOCKS;
         j.type_id = m->type_id;
         j.width = mat_row_bytes(m);
         j.data_len = m->rows * j.width;
+        /* Matrix::load (model/src/weights.rs:70-80): an I2_S matrix's scale
+         * opens the trailer after its rows, which the caller passes along */
+        if (m->type_id == 36)
+            orc_i2s_scale((const uint8_t *)m->data + j.data_len, 32, &j.scale);
     }
     j.data = m->data;
     j.out = out;

@@ -290,7 +290,8 @@ def matmul_batch_device(ctx: Context, inputs, tokens: int, jobs, stream: int = 0
 
 # ------------------------------------------------------------------ decoder
 
-STATUS.update({9: "CONTEXT_FULL", 10: "CACHE_POSITION", 11: "NO_VALID_TOKENS"})
+STATUS.update({9: "CONTEXT_FULL", 10: "CACHE_POSITION", 11: "NO_VALID_TOKENS", 12: "GGUF", 13: "MISSING_METADATA",
+               14: "MISSING_TENSOR", 15: "UNKNOWN_ARCHITECTURE"})
 
 
 class _DecoderConfig(ctypes.Structure):

@@ -349,6 +349,16 @@ rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn
   return RH_OK;
 }
 
+// Calls made without a context keep their message per thread
+// (rh_last_error(NULL)).
+thread_local std::string t_last_error;
+
+rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg) {
+  if (ctx) return fail(ctx, st, msg);
+  t_last_error = msg;
+  return st;
+}
+
 const uint8_t* matrix_data(const rh_matrix* m) { return m->data; }
 size_t matrix_stride(const rh_matrix* m) { return m->stride; }
 }  // namespace rh
@@ -386,7 +396,7 @@ void rh_destroy(rh_ctx* ctx) {
   delete ctx;
 }
 
-const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->last_error.c_str() : ""; }
+const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->last_error.c_str() : rh::t_last_error.c_str(); }
 
 void* rh_stream(rh_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
 

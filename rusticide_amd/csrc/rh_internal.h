@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <string>
+
 #include "../../include/rusticide_hip.h"
 
 namespace rh {
@@ -113,6 +115,8 @@ namespace rh {
 
 // Internal views of the ABI's opaque handles (api.hip).
 int ctx_device(const rh_ctx* ctx);
+// Records `msg` as the context's rh_last_error and returns `st`.
+rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg);
 const uint8_t* matrix_data(const rh_matrix* m);
 size_t matrix_stride(const rh_matrix* m);
 
