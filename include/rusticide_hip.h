@@ -276,7 +276,9 @@ enum {
     RH_GGUF_TENSOR_NOT_FOUND = 13,       /* name                           */
     RH_GGUF_INVALID_VALUE_TYPE = 14,     /* value: the type tag            */
     RH_GGUF_METADATA_TOO_LARGE = 15,     /* value: the element limit       */
-    RH_GGUF_NESTING_TOO_DEEP = 16        /* value: the depth limit         */
+    RH_GGUF_NESTING_TOO_DEEP = 16,       /* value: the depth limit         */
+    RH_GGUF_NOT_A_FILE = 17,             /* name: the path                 */
+    RH_GGUF_IO = 18                      /* name: the path, value: errno   */
 };
 typedef struct rh_gguf_error {
     uint32_t kind;
@@ -290,6 +292,11 @@ typedef struct rh_gguf rh_gguf;
 /* GgufFile::from_bytes (gguf/file.rs:39-62): parses a GGUF v3 file and keeps a
  * copy of its bytes. On RH_ERR_GGUF, *err (when given) says what failed. */
 rh_status rh_gguf_parse(const void *bytes, size_t len, rh_gguf **out, rh_gguf_error *err);
+/* GgufFile::load (gguf/file.rs:62-77): maps the file read-only (nothing is
+ * copied; the mapping lasts until rh_gguf_free) and parses it. RH_ERR_GGUF
+ * with NOT_A_FILE for a directory, device or pipe, IO when it cannot be
+ * opened or mapped, else as rh_gguf_parse. */
+rh_status rh_gguf_open(const char *path, rh_gguf **out, rh_gguf_error *err);
 void rh_gguf_free(rh_gguf *g);
 /* Metadata::len, GgufFile::tensor_count. */
 size_t rh_gguf_metadata_count(const rh_gguf *g);
@@ -333,10 +340,14 @@ rh_status rh_gguf_meta_string(const rh_gguf *g, const char *key, const char **ou
 rh_status rh_gguf_decoder_config(rh_ctx *ctx, const rh_gguf *g, rh_decoder_config *out);
 
 /* A decoder's weights uploaded from a GGUF file: DecoderWeights::from_source
- * (crates/rusticide-transformer/src/loader.rs:19-93) for the llama family. Every matrix is checked against
- * its expected shape and uploaded with rh_matrix_load; norms are read as
- * f32. output.weight is optional (tied to token_embd). Bias and sub-norm
- * tensors are rejected (MISSING_KERNEL): this decoder has neither. */
+ * (crates/rusticide-transformer/src/loader.rs:19-93) for the llama family.
+ * Every matrix is checked against its expected shape and format as
+ * rh_matrix_load checks it, in the reference's order, before any byte moves;
+ * then all go up in one pass through two pinned staging buffers of the
+ * context (host threads fill one while the DMA engine drains the other).
+ * Norms are read as f32. output.weight is optional (tied to token_embd).
+ * Bias and sub-norm tensors are rejected (MISSING_KERNEL): this decoder has
+ * neither. Calls on one context must not overlap. */
 typedef struct rh_gguf_model rh_gguf_model;
 rh_status rh_gguf_model_load(rh_ctx *ctx, const rh_gguf *g, rh_gguf_model **out);
 const rh_decoder_config *rh_gguf_model_config(const rh_gguf_model *m);

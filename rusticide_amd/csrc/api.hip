@@ -6,11 +6,13 @@
 // (crates/rusticide-kernels/src/matmul.rs:229-248) becomes: quantize each
 // activation kind once per batch on the device, then one grouped GEMV launch
 // per weight format covering every matrix of that format.
+#include <algorithm>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <new>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "../../include/rusticide_hip.h"
@@ -26,6 +28,9 @@ struct rh_ctx {
   void* buf[8] = {};
   size_t cap[8] = {};
   Q8Dev super_q, row_q;
+  // pinned staging for matrix uploads, made on the first one
+  uint8_t* stage[2] = {};
+  hipEvent_t stage_done[2] = {};
 };
 
 struct rh_matrix {
@@ -361,52 +366,11 @@ rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg) {
 
 const uint8_t* matrix_data(const rh_matrix* m) { return m->data; }
 size_t matrix_stride(const rh_matrix* m) { return m->stride; }
-}  // namespace rh
 
-extern "C" {
-
-const char* rh_adapter_name(void) { return "hip-gfx950"; }
-
-rh_status rh_init(int device, rh_ctx** out) {
-  if (!out) return RH_ERR_INVALID_ARGUMENT;
-  *out = nullptr;
-  int n = 0;
-  if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return RH_ERR_NO_DEVICE;
-  hipDeviceProp_t prop;
-  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return RH_ERR_NO_DEVICE;
-  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RH_ERR_NO_DEVICE;
-  rh_ctx* ctx = new (std::nothrow) rh_ctx();
-  if (!ctx) return RH_ERR_OUT_OF_MEMORY;
-  ctx->device = device;
-  if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
-    delete ctx;
-    return RH_ERR_DEVICE;
-  }
-  *out = ctx;
-  return RH_OK;
-}
-
-void rh_destroy(rh_ctx* ctx) {
-  if (!ctx) return;
-  hipSetDevice(ctx->device);
-  hipStreamSynchronize(ctx->stream);
-  for (void* b : ctx->buf)
-    if (b) hipFree(b);
-  hipStreamDestroy(ctx->stream);
-  delete ctx;
-}
-
-const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->last_error.c_str() : rh::t_last_error.c_str(); }
-
-void* rh_stream(rh_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
-
-size_t rh_gemm_min_tokens(void) { return g_gemm_min_tokens; }
-void rh_set_gemm_min_tokens(size_t tokens) { g_gemm_min_tokens = tokens; }
-
-rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t len, size_t rows,
-                         size_t cols, rh_matrix** out) {
+rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t len, size_t rows, size_t cols,
+                         PendingUpload* out) {
   if (!ctx || !out || (!data && len)) return RH_ERR_INVALID_ARGUMENT;
-  *out = nullptr;
+  out->m = nullptr;
   if (cols == 0) return fail(ctx, RH_ERR_INVALID_CONFIG, "a weight matrix has no columns");
   RH_HIP(ctx, hipSetDevice(ctx->device));
   rh_matrix* m = new (std::nothrow) rh_matrix();
@@ -416,7 +380,6 @@ rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
   m->type_id = type_id;
   m->rows = rows;
   m->cols = cols;
-  std::vector<float> widened;
   const uint8_t* src = static_cast<const uint8_t*>(data);
   size_t bs = 0, bb = 0;
   if (type_id == RH_TYPE_F32 || type_id == RH_TYPE_F16) {
@@ -426,15 +389,18 @@ rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
       return fail(ctx, RH_ERR_SHAPE_MISMATCH, "data too short for rows x cols");
     }
     if (type_id == RH_TYPE_F16) {  // widen (model/src/weights.rs:241-247)
-      widened.resize(rows * cols);
-      for (size_t i = 0; i < rows * cols; i++) {
-        uint16_t h;
-        std::memcpy(&h, src + 2 * i, 2);
-        _Float16 f;
-        std::memcpy(&f, &h, 2);
-        widened[i] = static_cast<float>(f);
+      try {
+        out->widened.resize(rows * cols);
+      } catch (const std::bad_alloc&) {
+        delete m;
+        return fail(ctx, RH_ERR_OUT_OF_MEMORY, "host allocation failed");
       }
-      src = reinterpret_cast<const uint8_t*>(widened.data());
+      for (size_t i = 0; i < rows * cols; i++) {
+        _Float16 f;
+        std::memcpy(&f, src + 2 * i, 2);
+        out->widened[i] = static_cast<float>(f);
+      }
+      src = reinterpret_cast<const uint8_t*>(out->widened.data());
       m->type_id = RH_TYPE_F32;
     }
     m->row_bytes = cols * 4;
@@ -483,21 +449,182 @@ rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
     delete m;
     return hip_fail(ctx, e, "hipMalloc(matrix)");
   }
-  e = hipMemsetAsync(m->data, 0, m->bytes, ctx->stream);
-  if (e == hipSuccess && rows) {
-    if (m->stride == m->row_bytes)
-      e = hipMemcpyAsync(m->data, src, rows * m->row_bytes, hipMemcpyHostToDevice, ctx->stream);
-    else
-      e = hipMemcpy2DAsync(m->data, m->stride, src, m->row_bytes, m->row_bytes, rows,
-                           hipMemcpyHostToDevice, ctx->stream);
+  out->m = m;
+  out->src = src;
+  return RH_OK;
+}
+
+namespace {
+
+constexpr size_t kStageBytes = size_t{32} << 20;  // per pinned staging buffer
+constexpr size_t kCopySlice = size_t{2} << 20;    // least bytes one host thread copies
+
+// Bytes [lo, hi) of a matrix's device image: row r's data at r * stride,
+// zeros in the gaps between rows and after the last one.
+void image_range(const rh_matrix* m, const uint8_t* src, size_t lo, size_t hi, uint8_t* dst) {
+  const size_t body = m->rows * m->stride;
+  size_t pos = lo;
+  while (pos < hi) {
+    if (pos >= body) {
+      std::memset(dst + (pos - lo), 0, hi - pos);
+      return;
+    }
+    if (m->stride == m->row_bytes) {  // rows back to back: one copy
+      const size_t e = hi < body ? hi : body;
+      std::memcpy(dst + (pos - lo), src + pos, e - pos);
+      pos = e;
+      continue;
+    }
+    const size_t r = pos / m->stride, in = pos - r * m->stride;
+    const size_t end = std::min(hi, (r + 1) * m->stride);
+    if (in < m->row_bytes) {
+      const size_t e = std::min(end, r * m->stride + m->row_bytes);
+      std::memcpy(dst + (pos - lo), src + r * m->row_bytes + in, e - pos);
+      pos = e;
+    }
+    if (pos < end) {
+      std::memset(dst + (pos - lo), 0, end - pos);
+      pos = end;
+    }
   }
-  if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
-  if (e != hipSuccess) {
-    hipFree(m->data);
-    delete m;
-    return hip_fail(ctx, e, "upload");
+}
+
+// image_range over up to 8 host threads, each at least kCopySlice bytes.
+void image_range_parallel(const rh_matrix* m, const uint8_t* src, size_t lo, size_t hi, uint8_t* dst) {
+  const size_t n = hi - lo;
+  size_t threads = std::min<size_t>(8, std::max<size_t>(1, std::thread::hardware_concurrency()));
+  threads = std::min(threads, std::max<size_t>(1, n / kCopySlice));
+  if (threads <= 1) {
+    image_range(m, src, lo, hi, dst);
+    return;
   }
-  *out = m;
+  const size_t part = round_up((n + threads - 1) / threads, 4096);
+  std::vector<std::thread> pool;
+  for (size_t t = 1; t < threads && lo + t * part < hi; t++) {
+    const size_t a = lo + t * part, b = std::min(hi, a + part);
+    pool.emplace_back(image_range, m, src, a, b, dst + (a - lo));
+  }
+  image_range(m, src, lo, std::min(hi, lo + part), dst);
+  for (auto& th : pool) th.join();
+}
+
+struct Dma {
+  uint8_t* dst;
+  size_t off, len;
+};
+
+}  // namespace
+
+// Every matrix's image goes through two pinned buffers: while the DMA engine
+// copies one to HBM, host threads fill the other from the (pageable) source
+// bytes. One synchronization at the end.
+rh_status matrix_upload(rh_ctx* ctx, PendingUpload* p, size_t n) {
+  if (!ctx || (!p && n)) return RH_ERR_INVALID_ARGUMENT;
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  if (!ctx->stage[0]) {
+    for (int b = 0; b < 2; b++) {
+      RH_HIP(ctx, hipHostMalloc(reinterpret_cast<void**>(&ctx->stage[b]), kStageBytes, hipHostMallocDefault));
+      RH_HIP(ctx, hipEventCreateWithFlags(&ctx->stage_done[b], hipEventDisableTiming));
+      RH_HIP(ctx, hipEventRecord(ctx->stage_done[b], ctx->stream));
+    }
+  }
+  int cur = 0;
+  size_t fill = 0;
+  std::vector<Dma> dmas;
+  auto flush = [&]() -> rh_status {
+    for (const Dma& d : dmas)
+      RH_HIP(ctx, hipMemcpyAsync(d.dst, ctx->stage[cur] + d.off, d.len, hipMemcpyHostToDevice, ctx->stream));
+    RH_HIP(ctx, hipEventRecord(ctx->stage_done[cur], ctx->stream));
+    dmas.clear();
+    cur ^= 1;
+    fill = 0;
+    // the other buffer's copies must be done before it is refilled
+    RH_HIP(ctx, hipEventSynchronize(ctx->stage_done[cur]));
+    return RH_OK;
+  };
+  // the buffer about to be filled first may still feed a previous call's
+  // copies only if that call failed midway; wait for it anyway
+  RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  for (size_t i = 0; i < n; i++) {
+    rh_matrix* m = p[i].m;
+    for (size_t off = 0; off < m->bytes;) {
+      const size_t take = std::min(m->bytes - off, kStageBytes - fill);
+      image_range_parallel(m, p[i].src, off, off + take, ctx->stage[cur] + fill);
+      dmas.push_back({m->data + off, fill, take});
+      fill += take;
+      off += take;
+      if (fill == kStageBytes) {
+        rh_status st = flush();
+        if (st != RH_OK) return st;
+      }
+    }
+  }
+  if (fill) {
+    rh_status st = flush();
+    if (st != RH_OK) return st;
+  }
+  RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+  return RH_OK;
+}
+}  // namespace rh
+
+extern "C" {
+
+const char* rh_adapter_name(void) { return "hip-gfx950"; }
+
+rh_status rh_init(int device, rh_ctx** out) {
+  if (!out) return RH_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= device || device < 0) return RH_ERR_NO_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return RH_ERR_NO_DEVICE;
+  if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RH_ERR_NO_DEVICE;
+  rh_ctx* ctx = new (std::nothrow) rh_ctx();
+  if (!ctx) return RH_ERR_OUT_OF_MEMORY;
+  ctx->device = device;
+  if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
+    delete ctx;
+    return RH_ERR_DEVICE;
+  }
+  *out = ctx;
+  return RH_OK;
+}
+
+void rh_destroy(rh_ctx* ctx) {
+  if (!ctx) return;
+  hipSetDevice(ctx->device);
+  hipStreamSynchronize(ctx->stream);
+  for (void* b : ctx->buf)
+    if (b) hipFree(b);
+  for (int b = 0; b < 2; b++) {
+    if (ctx->stage[b]) hipHostFree(ctx->stage[b]);
+    if (ctx->stage_done[b]) hipEventDestroy(ctx->stage_done[b]);
+  }
+  hipStreamDestroy(ctx->stream);
+  delete ctx;
+}
+
+const char* rh_last_error(const rh_ctx* ctx) { return ctx ? ctx->last_error.c_str() : rh::t_last_error.c_str(); }
+
+void* rh_stream(rh_ctx* ctx) { return ctx ? static_cast<void*>(ctx->stream) : nullptr; }
+
+size_t rh_gemm_min_tokens(void) { return g_gemm_min_tokens; }
+void rh_set_gemm_min_tokens(size_t tokens) { g_gemm_min_tokens = tokens; }
+
+rh_status rh_matrix_load(rh_ctx* ctx, uint32_t type_id, const void* data, size_t len, size_t rows,
+                         size_t cols, rh_matrix** out) {
+  if (!ctx || !out || (!data && len)) return RH_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  PendingUpload p;
+  rh_status st = matrix_prepare(ctx, type_id, data, len, rows, cols, &p);
+  if (st != RH_OK) return st;
+  st = matrix_upload(ctx, &p, 1);
+  if (st != RH_OK) {
+    rh_matrix_free(p.m);
+    return st;
+  }
+  *out = p.m;
   return RH_OK;
 }
 

@@ -15,9 +15,16 @@
 // DecoderWeights::from_source for the llama family
 // (crates/rusticide-transformer/src/{hyperparameters.rs,loader.rs},
 // crates/rusticide-model/src/weights.rs:40-98,216-239): shapes are checked
-// before each upload, matrices go through rh_matrix_load (which validates
-// their formats and the I2_S trailer), norms are read as f32.
+// before each allocation, matrices get rh_matrix_load's checks (formats,
+// the I2_S trailer) and are uploaded together through pinned staging
+// buffers once all are checked; norms are read as f32.
+#include <fcntl.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
 #include <algorithm>
+#include <cerrno>
 #include <cstring>
 #include <new>
 #include <string>
@@ -288,18 +295,26 @@ bool byte_len(const TensorInfo& t, uint64_t* len, Err* err) {
 }  // namespace
 
 struct rh_gguf {
-  std::vector<uint8_t> data;
+  // the file: a copy held here, or a read-only mapping of it
+  std::vector<uint8_t> owned;
+  void* map = nullptr;
+  const uint8_t* bytes = nullptr;
+  size_t size = 0;
   std::unordered_map<std::string, Value> meta;
   std::vector<TensorInfo> tensors;  // sorted by name
   std::unordered_map<std::string, size_t> index;
   size_t data_start = 0;
+
+  ~rh_gguf() {
+    if (map) munmap(map, size);
+  }
 };
 
 namespace {
 
 // GgufFile::from_bytes (file.rs:39-62).
 bool parse_file(rh_gguf* g, Err* err) {
-  Cursor c{g->data.data(), g->data.size()};
+  Cursor c{g->bytes, g->size};
   // Header::parse (header.rs:20-36)
   if (c.n < 24) {
     *err = make_err(RH_GGUF_UNEXPECTED_EOF);
@@ -419,7 +434,7 @@ bool parse_file(rh_gguf* g, Err* err) {
     return false;
   }
   const uint64_t start = (pos + alignment - 1) & ~(alignment - 1);
-  if (start > g->data.size()) {
+  if (start > g->size) {
     *err = make_err(RH_GGUF_UNEXPECTED_EOF);
     return false;
   }
@@ -436,11 +451,11 @@ bool tensor_bytes(const rh_gguf* g, const TensorInfo& t, const uint8_t** data, s
   uint64_t n;
   if (!byte_len(t, &n, err)) return false;
   const uint64_t start = g->data_start;
-  if (t.offset > UINT64_MAX - start || start + t.offset > UINT64_MAX - n || start + t.offset + n > g->data.size()) {
+  if (t.offset > UINT64_MAX - start || start + t.offset > UINT64_MAX - n || start + t.offset + n > g->size) {
     *err = make_err(RH_GGUF_UNEXPECTED_EOF);
     return false;
   }
-  *data = g->data.data() + start + t.offset;
+  *data = g->bytes + start + t.offset;
   *len = static_cast<size_t>(n);
   return true;
 }
@@ -473,6 +488,7 @@ struct rh_gguf_model {
   rh_ctx* ctx = nullptr;
   rh_decoder_config config{};
   std::vector<rh_matrix*> matrices;  // owned
+  std::vector<rh::PendingUpload> pending;  // checked and allocated, not yet uploaded
   std::vector<std::vector<float>> norms;
   std::vector<rh_decoder_block> blocks;
   rh_decoder_weights weights{};
@@ -493,7 +509,8 @@ rh_status check_shape(rh_ctx* ctx, const rh_gguf* g, const std::string& name, co
   return RH_OK;
 }
 
-// Matrix::load (weights.rs:48-98) onto the device.
+// Matrix::load (weights.rs:48-98): checked and allocated on the device; the
+// bytes go up with every other matrix's once all are checked.
 rh_status load_matrix(rh_gguf_model* m, const rh_gguf* g, const std::string& name, size_t rows, size_t cols,
                       const rh_matrix** out) {
   const TensorInfo* t = nullptr;
@@ -504,11 +521,12 @@ rh_status load_matrix(rh_gguf_model* m, const rh_gguf* g, const std::string& nam
   size_t len = 0;
   Err err;
   if (!tensor_bytes(g, *t, &data, &len, &err)) return model_fail(m->ctx, RH_ERR_GGUF, "tensor " + name + ": bad extent");
-  rh_matrix* mat = nullptr;
-  st = rh_matrix_load(m->ctx, t->type_id, data, len, rows, cols, &mat);
+  rh::PendingUpload p;
+  st = rh::matrix_prepare(m->ctx, t->type_id, data, len, rows, cols, &p);
   if (st != RH_OK) return st;
-  m->matrices.push_back(mat);
-  *out = mat;
+  m->matrices.push_back(p.m);
+  *out = p.m;
+  m->pending.push_back(std::move(p));
   return RH_OK;
 }
 
@@ -548,7 +566,63 @@ rh_status rh_gguf_parse(const void* bytes, size_t len, rh_gguf** out, rh_gguf_er
   rh_gguf* g = new (std::nothrow) rh_gguf();
   if (!g) return RH_ERR_OUT_OF_MEMORY;
   try {
-    g->data.assign(static_cast<const uint8_t*>(bytes), static_cast<const uint8_t*>(bytes) + len);
+    g->owned.assign(static_cast<const uint8_t*>(bytes), static_cast<const uint8_t*>(bytes) + len);
+    g->bytes = g->owned.data();
+    g->size = len;
+    Err e;
+    if (!parse_file(g, &e)) {
+      report(e, err);
+      delete g;
+      return RH_ERR_GGUF;
+    }
+  } catch (const std::bad_alloc&) {
+    delete g;
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  report(Err{}, err);
+  *out = g;
+  return RH_OK;
+}
+
+rh_status rh_gguf_open(const char* path, rh_gguf** out, rh_gguf_error* err) {
+  if (!path || !out) return RH_ERR_INVALID_ARGUMENT;
+  *out = nullptr;
+  // non-blocking, so that a pipe without a writer is refused rather than waited on
+  const int fd = open(path, O_RDONLY | O_CLOEXEC | O_NONBLOCK);
+  if (fd < 0) {
+    report(make_err(RH_GGUF_IO, static_cast<uint64_t>(errno), path), err);
+    return RH_ERR_GGUF;
+  }
+  struct stat st;
+  if (fstat(fd, &st) != 0) {
+    report(make_err(RH_GGUF_IO, static_cast<uint64_t>(errno), path), err);
+    close(fd);
+    return RH_ERR_GGUF;
+  }
+  if (!S_ISREG(st.st_mode)) {  // a directory, device or pipe could be read without end
+    report(make_err(RH_GGUF_NOT_A_FILE, 0, path), err);
+    close(fd);
+    return RH_ERR_GGUF;
+  }
+  rh_gguf* g = new (std::nothrow) rh_gguf();
+  if (!g) {
+    close(fd);
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  g->size = static_cast<size_t>(st.st_size);
+  if (g->size) {
+    void* p = mmap(nullptr, g->size, PROT_READ, MAP_PRIVATE, fd, 0);
+    if (p == MAP_FAILED) {
+      report(make_err(RH_GGUF_IO, static_cast<uint64_t>(errno), path), err);
+      close(fd);
+      delete g;
+      return RH_ERR_GGUF;
+    }
+    g->map = p;
+    g->bytes = static_cast<const uint8_t*>(p);
+  }
+  close(fd);
+  try {
     Err e;
     if (!parse_file(g, &e)) {
       report(e, err);
@@ -754,6 +828,10 @@ rh_status rh_gguf_model_load(rh_ctx* ctx, const rh_gguf* g, rh_gguf_model** out)
       st = load_matrix(m, g, "output.weight", c.vocab_size, e, &m->weights.output);
     if (st == RH_OK) st = load_matrix(m, g, "token_embd.weight", c.vocab_size, e, &m->weights.token_embd);
     if (st == RH_OK) st = load_vector(m, g, "output_norm.weight", e, &m->weights.output_norm);
+    // every tensor checked and allocated: the bytes go up in one pipelined pass
+    if (st == RH_OK) st = rh::matrix_upload(ctx, m->pending.data(), m->pending.size());
+    m->pending.clear();
+    m->pending.shrink_to_fit();
   } catch (const std::bad_alloc&) {
     st = RH_ERR_OUT_OF_MEMORY;
   }

@@ -7,6 +7,7 @@
 #include <stdint.h>
 
 #include <string>
+#include <vector>
 
 #include "../../include/rusticide_hip.h"
 
@@ -119,6 +120,21 @@ int ctx_device(const rh_ctx* ctx);
 rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg);
 const uint8_t* matrix_data(const rh_matrix* m);
 size_t matrix_stride(const rh_matrix* m);
+
+// A matrix checked and allocated on the device (Matrix::load_on's checks,
+// model/src/weights.rs:53-98) whose image is not uploaded yet: `src` holds
+// its rows back to back (`widened` owns them for an F16 source).
+struct PendingUpload {
+  rh_matrix* m = nullptr;
+  const uint8_t* src = nullptr;
+  std::vector<float> widened;
+};
+rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t len, size_t rows, size_t cols,
+                         PendingUpload* out);
+// Uploads the images of `n` prepared matrices (rows at their HBM stride,
+// zeros elsewhere) and waits for the copies. On failure the matrices stay
+// allocated for the caller to free.
+rh_status matrix_upload(rh_ctx* ctx, PendingUpload* p, size_t n);
 
 hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
                                  float* out, size_t out_len, hipStream_t s);

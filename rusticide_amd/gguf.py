@@ -39,7 +39,8 @@ KINDS = {
     1: "InvalidMagic", 2: "UnsupportedVersion", 3: "UnsupportedTensorType", 4: "CastOverflow",
     5: "InvalidAlignment", 6: "DuplicateKey", 7: "DuplicateTensor", 8: "TooManyDimensions",
     9: "ShapeOverflow", 10: "MisalignedTensor", 11: "OverlappingTensors", 12: "UnexpectedEof",
-    13: "TensorNotFound", 14: "InvalidValueType", 15: "MetadataTooLarge", 16: "NestingTooDeep",
+    13: "TensorNotFound", 14: "InvalidValueType", 15: "MetadataTooLarge", 16: "NestingTooDeep", 17: "NotAFile",
+    18: "Io",
 }
 
 # ------------------------------------------------------------------ writer
@@ -191,6 +192,8 @@ def _gguf_lib() -> ctypes.CDLL:
         L.rh_gguf_parse.argtypes = [P, S, ctypes.POINTER(P), PE]
         L.rh_gguf_parse.restype = St
         L.rh_gguf_free.argtypes = [P]
+        L.rh_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(P), PE]
+        L.rh_gguf_open.restype = St
         for n in ("rh_gguf_metadata_count", "rh_gguf_tensor_count"):
             getattr(L, n).argtypes = [P]
             getattr(L, n).restype = S
@@ -241,14 +244,20 @@ class GgufFile:
 
     @classmethod
     def load(cls, path) -> "GgufFile":
-        """GgufFile::load (gguf/file.rs:72-80): a regular file only; a
-        directory, device or pipe is NotAFile, a read error is OSError."""
-        if not os.path.isfile(path):
-            if os.path.exists(path):
-                raise GgufError("NotAFile", name=str(path))
-            raise FileNotFoundError(path)
-        with open(path, "rb") as f:
-            return cls(f.read())
+        """GgufFile::load (gguf/file.rs:62-77) by rh_gguf_open: the file is
+        mapped, not copied. A directory, device or pipe is NotAFile; a file
+        that cannot be opened is Io, with its errno as `value`."""
+        L = _gguf_lib()
+        self = cls.__new__(cls)
+        self.handle = None
+        h, err = ctypes.c_void_p(), _Error()
+        st = L.rh_gguf_open(os.fsencode(path), ctypes.byref(h), ctypes.byref(err))
+        if st == 12:
+            raise GgufError._from(err)
+        if st != 0:
+            raise RusticideError(st, "rh_gguf_open")
+        self.handle = h
+        return self
 
     def _h(self):
         if not self.handle:

@@ -35,6 +35,8 @@ def hip() -> ctypes.CDLL:
         H.hipEventRecord.argtypes = [P, P]
         H.hipEventSynchronize.argtypes = [P]
         H.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), P, P]
+        H.hipHostMalloc.argtypes = [ctypes.POINTER(P), S, ctypes.c_uint]
+        H.hipHostFree.argtypes = [P]
         H.hipGetErrorString.argtypes = [ctypes.c_int]
         H.hipGetErrorString.restype = ctypes.c_char_p
         _hip = H
@@ -117,6 +119,26 @@ class Event:
     def __del__(self):
         try:
             hip().hipEventDestroy(self.h)
+        except Exception:
+            pass
+
+
+class PinnedHost:
+    """`n` bytes of page-locked host memory (hipHostMalloc)."""
+
+    def __init__(self, n: int):
+        self.n = int(n)
+        self.ptr = ctypes.c_void_p()
+        check(hip().hipHostMalloc(ctypes.byref(self.ptr), max(1, self.n), 0), "hipHostMalloc")
+
+    def free(self) -> None:
+        if self.ptr:
+            hip().hipHostFree(self.ptr)
+            self.ptr = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
         except Exception:
             pass
 

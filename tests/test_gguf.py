@@ -8,6 +8,7 @@ String decoding is pinned independently: Python's bytes.decode("utf-8",
 String::from_utf8_lossy, so random byte strings must decode alike.
 """
 
+import errno
 import os
 import struct
 
@@ -361,15 +362,38 @@ def test_offsets_are_relative_to_the_data_section():
     assert np.array_equal(np.frombuffer(f.tensor_bytes("second"), np.float32), [2.0, 3.0])
 
 
-def test_load_reads_regular_files_only(tmp_path):
+def test_load_maps_regular_files_only(tmp_path):
+    # file_tests.rs:194-230
     p = tmp_path / "m.gguf"
-    p.write_bytes(Writer().tensor("a", [1], F32, bytes(4)).build())
-    assert GgufFile.load(p).tensor_names() == ["a"]
-    with pytest.raises(FileNotFoundError):
-        GgufFile.load(tmp_path / "missing.gguf")
-    for special in (tmp_path, "/dev/zero"):
+    p.write_bytes(Writer().tensor("a", [1], F32, bytes([9] * 4)).build())
+    f = GgufFile.load(p)
+    assert f.tensor_names() == ["a"] and f.tensor_bytes("a") == bytes([9] * 4)
+    f.close()
+    e = pytest.raises(GgufError, GgufFile.load, tmp_path / "missing.gguf").value
+    assert (e.gguf_kind, e.value) == ("Io", errno.ENOENT)
+    fifo = tmp_path / "pipe"
+    os.mkfifo(fifo)
+    for special in (tmp_path, "/dev/zero", fifo):
         if os.path.exists(special):
             assert pytest.raises(GgufError, GgufFile.load, special).value.gguf_kind == "NotAFile"
+    # an empty file and a truncated one fail as their bytes would
+    (tmp_path / "empty.gguf").write_bytes(b"")
+    assert pytest.raises(GgufError, GgufFile.load, tmp_path / "empty.gguf").value.gguf_kind == "UnexpectedEof"
+    (tmp_path / "short.gguf").write_bytes(Writer().build()[:-8])
+    assert pytest.raises(GgufError, GgufFile.load, tmp_path / "short.gguf").value.gguf_kind == "UnexpectedEof"
+
+
+def test_a_mapped_file_reads_like_parsed_bytes(tmp_path):
+    from rusticide_amd import synth
+    model = synth.decoder_model(dict(embedding_length=256, block_count=1, feed_forward_length=512, head_count=4,
+                                     head_count_kv=2, head_dim=64, context_length=64, vocab_size=64,
+                                     rope_freq_base=10000.0, rms_norm_eps=1e-5), seed=3)
+    data = G.decoder_gguf(model)
+    (tmp_path / "m.gguf").write_bytes(data)
+    a, b = GgufFile(data), GgufFile.load(tmp_path / "m.gguf")
+    assert a.tensor_names() == b.tensor_names() and a.decoder_config() == b.decoder_config()
+    for name in a.tensor_names():
+        assert a.tensor_info(name) == b.tensor_info(name) and a.tensor_bytes(name) == b.tensor_bytes(name)
 
 
 # ------------------------------------------------------------ decoder config
