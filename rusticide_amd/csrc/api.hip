@@ -25,8 +25,8 @@ struct rh_ctx {
   hipStream_t stream = nullptr;
   std::string last_error;
   // scratch, grown on demand
-  void* buf[8] = {};
-  size_t cap[8] = {};
+  void* buf[9] = {};
+  size_t cap[9] = {};
   Q8Dev super_q, row_q;
   // pinned staging for matrix uploads, made on the first one
   uint8_t* stage[2] = {};
@@ -58,7 +58,8 @@ struct rh_q8 {
 
 namespace {
 
-enum Scratch { kIn = 0, kOut, kQuants, kScales, kSums, kSums16, kRaw, kRowQ };
+enum Scratch { kIn = 0, kOut, kQuants, kScales, kSums, kSums16, kRaw, kRowQ, kTerms, kScratchSlots };
+static_assert(kScratchSlots == sizeof(rh_ctx::cap) / sizeof(size_t), "one scratch slot per Scratch value");
 
 // Batches of this many tokens or more run Q4_K, Q6_K and I2_S on the MFMA GEMMs.
 size_t g_gemm_min_tokens = 9;
@@ -179,7 +180,13 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (g.n == 0) return RH_OK;
       const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
       if (is_kquant(kind) && tokens >= g_gemm_min_tokens) {
-        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, s));
+        float* terms = nullptr;
+        if (const size_t tb = gemm_split_bytes(kind, g, tokens)) {
+          rh_status es = ensure(ctx, kTerms, tb);
+          if (es != RH_OK) return es;
+          terms = static_cast<float*>(ctx->buf[kTerms]);
+        }
+        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, terms, s));
         g = GemvJobs{};
         nbmax = 0;
         return RH_OK;

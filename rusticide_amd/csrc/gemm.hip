@@ -26,6 +26,14 @@
 // weights are dequantized into LDS planes once per workgroup, the block's
 // activation tile and block-sum bytes are copied in, and the next block's raw
 // bytes are already in flight in registers while the MFMAs of this one run.
+//
+// Split K: when the row and token tiles give too few workgroups to fill the
+// chip (a 64-token prefill of a 2048-row matrix is 32 of them), blockIdx.z
+// takes a segment of seg_len blocks. Segment 0 forms the in-order sum over its
+// blocks as usual; every later segment stores each of its blocks' float terms,
+// and gemm_combine_kernel continues segment 0's sum with them in block order.
+// That is the unsplit sequence of float additions, so the bits do not change.
+#include <algorithm>
 #include <cstdlib>
 
 #include "rh_device.h"
@@ -118,8 +126,17 @@ __device__ __forceinline__ void split4_s(uint32_t q, int32_t sc, uint32_t& hi, u
 
 // LDS: hi [64][272] | lo [64][272] | act [BN][272] | mins [64][8] u8 |
 //      bsb [BN][16] (bl_0..7, bh_0..7) | rowd [64] float2 (d, dmin) | d8 [BN]
-template <int FMT, int BN>
-__global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, size_t tokens) {
+// Terms of a split launch: plane 0 holds segment 0's sums, plane 1 + b -
+// seg_len the term of block b >= seg_len; each plane is [rows_pad][tokens]
+// over the launch's 64-row tiles.
+struct SplitTerms {
+  float* terms;       // nullptr: no split
+  uint32_t seg_len;   // blocks per segment
+  uint32_t rows_pad;  // 64 x the launch's workgroups along rows
+};
+
+template <int FMT, int BN, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, size_t tokens, SplitTerms split) {
   extern __shared__ __align__(16) uint8_t lds[];
   int8_t* hiT = reinterpret_cast<int8_t*>(lds);
   int8_t* loT = hiT + kBM * kStride;
@@ -133,6 +150,10 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
   const uint32_t row0 = (blockIdx.x - J.wg_begin) * kBM;
   const uint32_t tok0 = blockIdx.y * BN;
   const uint32_t nb = J.nb;
+  const uint32_t seg = SPLIT ? blockIdx.z : 0u;
+  const uint32_t b_begin = SPLIT ? seg * split.seg_len : 0u;
+  const uint32_t b_end = SPLIT ? min(nb, b_begin + split.seg_len) : nb;
+  const bool store_terms = SPLIT && seg > 0u;
   const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
   const uint32_t wm = wave & 1u, wn = wave >> 1;
   constexpr int NT = BN / 64;  // 32x32 tiles per wave along tokens
@@ -176,8 +197,8 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
 #pragma unroll
     for (int i = 0; i < 16; i++) y[t][i] = -0.0f;
 
-  if (nb) prefetch(0);
-  for (uint32_t b = 0; b < nb; b++) {
+  if (b_begin < b_end) prefetch(b_begin);
+  for (uint32_t b = b_begin; b < b_end; b++) {
     // raw bytes -> LDS planes
     if (FMT == 12) {
       const u32x4 hd = wr.w[0];
@@ -264,7 +285,7 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
     }
     if (tid < static_cast<uint32_t>(BN)) d8T[tid] = d8r;
     __syncthreads();
-    if (b + 1u < nb) prefetch(b + 1u);
+    if (b + 1u < b_end) prefetch(b + 1u);
 
     const uint32_t arow = 32u * wm + (lane & 31u);
     const uint32_t g = lane >> 5;  // the lane's 16-byte k group of a 32-deep step
@@ -328,6 +349,8 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
     float d8n[NT];
 #pragma unroll
     for (int t = 0; t < NT; t++) d8n[t] = d8T[bcol[t]];
+    float* plane = store_terms ? split.terms + static_cast<size_t>(1u + b - split.seg_len) * split.rows_pad * T
+                               : nullptr;
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const uint32_t m = 32u * wm + 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
@@ -344,11 +367,17 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
           const float s = dd.x * d8n[t];
           term = s * static_cast<float>(acc_i[t][i]);
         }
-        y[t][i] += term;
+        if (store_terms) {
+          const size_t tok = tok0 + static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
+          if (tok < T) plane[static_cast<size_t>(blockIdx.x * kBM + m) * T + tok] = term;
+        } else {
+          y[t][i] += term;
+        }
       }
     }
     __syncthreads();
   }
+  if (store_terms) return;
 
   const uint32_t g = lane >> 5;
 #pragma unroll
@@ -359,35 +388,137 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
 #pragma unroll
     for (int t = 0; t < NT; t++) {
       const size_t tok = tok0 + static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
+      if (SPLIT) {  // segment 0 of a split launch: plane 0
+        if (tok < T) split.terms[static_cast<size_t>(blockIdx.x * kBM + m) * T + tok] = y[t][i];
+        continue;
+      }
       const size_t idx = static_cast<size_t>(row) * T + tok;
       if (tok < T && idx < J.out_len) J.out[idx] = y[t][i];
     }
   }
 }
 
-template <int FMT, int BN>
-hipError_t launch_bn(GemvJobs jobs, const Q8Dev& q, size_t tokens, hipStream_t s) {
+// The end of a split launch: per (row, token), segment 0's sum plus the later
+// blocks' terms, one addition at a time in block order.
+// Each thread owns four consecutive (row, token) slots (a plane holds a
+// multiple of 64 of them) and keeps eight planes of loads in flight; the
+// additions stay one plane at a time, in block order.
+__global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const float* __restrict__ terms,
+                                                           uint32_t planes, uint32_t rows_pad, size_t tokens) {
+  const size_t n = static_cast<size_t>(rows_pad) * tokens;
+  const size_t idx = (static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x) * 4u;
+  if (idx >= n) return;
+  f32x4 y = *reinterpret_cast<const f32x4*>(terms + idx);
+  uint32_t p = 1;
+  for (; p + 8u <= planes; p += 8u) {
+    f32x4 v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = *reinterpret_cast<const f32x4*>(terms + static_cast<size_t>(p + k) * n + idx);
+#pragma unroll
+    for (int k = 0; k < 8; k++) y += v[k];
+  }
+  for (; p < planes; p++) y += *reinterpret_cast<const f32x4*>(terms + static_cast<size_t>(p) * n + idx);
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const uint32_t grow = static_cast<uint32_t>((idx + e) / tokens);
+    const size_t tok = idx + e - static_cast<size_t>(grow) * tokens;
+    const GemvJob& J = jobs.j[gemm_job(jobs, grow / kBM)];
+    const uint32_t row = grow - J.wg_begin * kBM;
+    const size_t o = static_cast<size_t>(row) * tokens + tok;
+    if (row < J.rows && o < J.out_len) J.out[o] = y[e];
+  }
+}
+
+int token_tile(size_t tokens) {
+  // RUSTICIDE_HIP_GEMM_BN=64|128 forces the token tile, for tuning
+  int bn = tokens >= 512 ? 128 : 64;
+  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMM_BN")) bn = v[0] == '1' ? 128 : 64;
+  return bn;
+}
+
+// Workgroups along rows, with each job's first one recorded in wg_begin.
+uint32_t row_tiles(GemvJobs& jobs) {
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     jobs.j[i].wg_begin = wgs;
     wgs += (jobs.j[i].rows + kBM - 1u) / kBM;
   }
+  return wgs;
+}
+
+struct SplitPlan {
+  uint32_t segs = 1, seg_len = 0, planes = 0, rows_pad = 0;
+};
+
+// Splits K when the launch has fewer than kSplitBelow workgroups, aiming at
+// kSplitTarget; every job must have the same block count. Below 2 blocks, or
+// with RUSTICIDE_HIP_GEMM_SPLIT=0, nothing is split.
+constexpr uint32_t kSplitBelow = 128, kSplitTarget = 512;
+
+SplitPlan plan_split(GemvJobs jobs, size_t tokens) {
+  SplitPlan p;
+  const uint32_t wgs = row_tiles(jobs);
+  if (wgs == 0 || jobs.n == 0) return p;
+  const uint32_t nb = jobs.j[0].nb;
+  for (uint32_t i = 1; i < jobs.n; i++)
+    if (jobs.j[i].nb != nb) return p;
+  const char* env = std::getenv("RUSTICIDE_HIP_GEMM_SPLIT");
+  if (env && env[0] == '0') return p;
+  const size_t tiles = (tokens + token_tile(tokens) - 1) / token_tile(tokens);
+  const size_t base = static_cast<size_t>(wgs) * tiles;
+  if (nb < 2 || base >= kSplitBelow) return p;
+  const uint32_t want = static_cast<uint32_t>(std::min<size_t>(nb, (kSplitTarget + base - 1) / base));
+  if (want < 2) return p;
+  p.seg_len = (nb + want - 1) / want;
+  p.segs = (nb + p.seg_len - 1) / p.seg_len;
+  if (p.segs < 2) return SplitPlan{};
+  p.planes = 1 + nb - p.seg_len;
+  p.rows_pad = wgs * kBM;
+  return p;
+}
+
+template <int FMT, int BN>
+hipError_t launch_bn(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPlan& plan, float* terms,
+                     hipStream_t s) {
+  const uint32_t wgs = row_tiles(jobs);
   if (wgs == 0) return hipSuccess;
   const uint32_t tiles = static_cast<uint32_t>((tokens + BN - 1) / BN);
   const size_t lds = 2u * kBM * kStride + BN * kStride + kBM * 8u + BN * 16u + kBM * 8u + BN * 4u;
-  hipLaunchKernelGGL((gemm_kq_kernel<FMT, BN>), dim3(wgs, tiles), dim3(kThreads), lds, s, jobs, q, tokens);
+  const bool split = plan.segs > 1 && terms;
+  if (!split) {
+    hipLaunchKernelGGL((gemm_kq_kernel<FMT, BN, false>), dim3(wgs, tiles), dim3(kThreads), lds, s, jobs, q, tokens,
+                       SplitTerms{nullptr, 0u, 0u});
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL((gemm_kq_kernel<FMT, BN, true>), dim3(wgs, tiles, plan.segs), dim3(kThreads), lds, s, jobs, q,
+                     tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad});
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const size_t n = static_cast<size_t>(plan.rows_pad) * tokens;  // a multiple of 64
+  hipLaunchKernelGGL(gemm_combine_kernel, dim3(static_cast<uint32_t>((n / 4u + 255u) / 256u)), dim3(256), 0, s, jobs,
+                     terms, plan.planes, plan.rows_pad, tokens);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, hipStream_t s) {
+size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens) {
+  if (tokens == 0 || (type_id != 12u && type_id != 14u)) return 0;
+  const SplitPlan p = plan_split(jobs, tokens);
+  return p.segs > 1 ? static_cast<size_t>(p.planes) * p.rows_pad * tokens * sizeof(float) : 0;
+}
+
+hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
+                       hipStream_t s) {
   if (tokens == 0) return hipSuccess;
-  // RUSTICIDE_HIP_GEMM_BN=64|128 forces the token tile, for tuning
-  int bn = tokens >= 512 ? 128 : 64;
-  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMM_BN")) bn = v[0] == '1' ? 128 : 64;
-  if (type_id == 12u) return bn == 128 ? launch_bn<12, 128>(jobs, q, tokens, s) : launch_bn<12, 64>(jobs, q, tokens, s);
-  if (type_id == 14u) return bn == 128 ? launch_bn<14, 128>(jobs, q, tokens, s) : launch_bn<14, 64>(jobs, q, tokens, s);
+  const SplitPlan plan = plan_split(jobs, tokens);
+  const int bn = token_tile(tokens);
+  if (type_id == 12u)
+    return bn == 128 ? launch_bn<12, 128>(jobs, q, tokens, plan, terms, s)
+                     : launch_bn<12, 64>(jobs, q, tokens, plan, terms, s);
+  if (type_id == 14u)
+    return bn == 128 ? launch_bn<14, 128>(jobs, q, tokens, plan, terms, s)
+                     : launch_bn<14, 64>(jobs, q, tokens, plan, terms, s);
   return hipErrorInvalidValue;
 }
 

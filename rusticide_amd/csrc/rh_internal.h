@@ -102,7 +102,12 @@ hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q
 // Prefill GEMM on MFMA for the k-quants (Q4_K, Q6_K): every row of every job
 // against all `tokens` tokens of the quantized activation q, bit-identical to
 // the GEMV kernels (and so to the CPU path).
-hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, hipStream_t s);
+// The float scratch a k-quant GEMM launch over `jobs` needs when it splits K
+// across workgroups (0: it does not split). launch_gemm splits only when
+// `terms` holds that many bytes; without it the launch runs unsplit.
+size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens);
+hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
+                       hipStream_t s);
 // Prefill GEMM on int8 MFMA for I2_S against the I8_S activation q; with
 // `raw` the i32 dots go there instead of the scaled outputs.
 hipError_t launch_gemm_i2s(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, int32_t* raw, hipStream_t s);

@@ -182,6 +182,7 @@ GEMM_SHAPES = [
     (14, 2048, 5632, [64]),               # Q6_K ffn_down: 22 blocks, 4620-byte rows
     (14, 32000, 2048, [64]),              # Q6_K lm_head over a 64-token prefill chunk
     (12, 130, 25600, [16]),               # 100 blocks per row
+    (12, 6400, 2304, [64]),               # K split into segments of 2 blocks, the last one short
 ]
 
 
@@ -198,6 +199,25 @@ def test_prefill_gemm_is_bit_identical_to_the_cpu_path(ctx, type_id, rows, cols,
         out = np.full(rows * tokens, np.nan, np.float32)
         R.matmul_batch(ctx, x, tokens, [(m, out)])
         assert_same_bits(out, want, f"type={type_id} {rows}x{cols} tokens={tokens}")
+
+
+@pytest.mark.parametrize("type_id,rows,cols,tokens", [(12, 2048, 2048, 64), (14, 2048, 5632, 64),
+                                                       (12, 2560, 2048, 64), (12, 6400, 2304, 64),
+                                                       (14, 45, 768, 9), (12, 300, 25600, 33)])
+def test_split_k_gives_the_unsplit_bits(ctx, monkeypatch, type_id, rows, cols, tokens):
+    # a launch with too few row and token tiles to fill the chip splits K
+    # across workgroups and adds the later blocks' terms in block order
+    # afterwards; RUSTICIDE_HIP_GEMM_SPLIT=0 keeps every block in one workgroup
+    data = synth.matrix(type_id, rows, cols, seed=rows + cols)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    x = synth.normal_f32(tokens * cols, seed=7 + tokens)
+    split = np.full(rows * tokens, np.nan, np.float32)
+    R.matmul_batch(ctx, x, tokens, [(m, split)])
+    monkeypatch.setenv("RUSTICIDE_HIP_GEMM_SPLIT", "0")
+    whole = np.full(rows * tokens, np.nan, np.float32)
+    R.matmul_batch(ctx, x, tokens, [(m, whole)])
+    assert_same_bits(split, whole, f"type={type_id} {rows}x{cols} tokens={tokens}")
+    assert_same_bits(split, oracle_matmul(type_id, data, rows, cols, x, tokens, threads=16))
 
 
 def test_prefill_gemm_batch_of_projections_and_hostile_bytes(ctx):
