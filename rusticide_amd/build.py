@@ -32,9 +32,19 @@ FLAGS = [
 ]
 
 
+# The MFMA GEMMs keep their accumulators in ordinary VGPRs (gfx950 allows
+# either file): their accumulators are shifted and read by vector code every
+# K block, which the accumulation registers would force through copies, and
+# the 128-token tiles fit in 256 registers, two waves per SIMD.
+SOURCE_FLAGS = {
+    "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "gemm_i2s.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *FLAGS, *SOURCE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stdout}\n{r.stderr}")
