@@ -180,6 +180,8 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (g.n == 0) return RH_OK;
       const Q8Dev& q = kind == RH_TYPE_I2_S ? row_q : super_q;
       if (is_kquant(kind) && tokens >= g_gemm_min_tokens) {
+        if (!gemm_fits(tokens, q.qstride))
+          return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a batch's quantized activation exceeds 4 GiB");
         float* terms = nullptr;
         if (const size_t tb = gemm_split_bytes(kind, g, tokens)) {
           rh_status es = ensure(ctx, kTerms, tb);

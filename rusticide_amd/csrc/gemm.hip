@@ -102,9 +102,10 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& hd, uint32_t j, uint3
 
 // Four unsigned nibble bytes q (0..15) times sc (0..63) as the hi/lo planes:
 // the products are formed two at a time in 16-bit lanes (< 2^16, no carry).
+// Both factors are below 2^24, so the full-rate 24-bit multiply is exact.
 __device__ __forceinline__ void split4_u(uint32_t q, uint32_t sc, uint32_t& hi, uint32_t& lo) {
-  const uint32_t pe = (q & 0x00FF00FFu) * sc;
-  const uint32_t po = ((q >> 8) & 0x00FF00FFu) * sc;
+  const uint32_t pe = __umul24(q & 0x00FF00FFu, sc);
+  const uint32_t po = __umul24((q >> 8) & 0x00FF00FFu, sc);
   lo = (pe & 0x007F007Fu) | ((po & 0x007F007Fu) << 8);
   hi = ((pe >> 7) & 0x00FF00FFu) | (((po >> 7) & 0x00FF00FFu) << 8);
 }
@@ -165,7 +166,11 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
   const uint8_t* wrow = J.w + __umul24(srow, static_cast<uint32_t>(J.stride));
   constexpr int ACH = BN * 16 / 256;  // activation chunks per thread
   const size_t T = tokens;
-  const size_t stok = min(static_cast<size_t>(tok0 + (tid & (BN - 1))), T - 1);
+  // the launch keeps tokens * qstride below 2^32 and both below 2^24: the
+  // activation offsets are exact 32-bit values from 24-bit multiplies
+  const uint32_t last = static_cast<uint32_t>(T - 1);
+  const uint32_t qs32 = static_cast<uint32_t>(q.qstride), bs32 = static_cast<uint32_t>(q.bstride);
+  const uint32_t stok = min(tok0 + (tid & (BN - 1)), last);
 
   WRaw wr;
   u32x4 ar[ACH];
@@ -177,11 +182,11 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
     for (int c = 0; c < ACH; c++) {
       const uint32_t chunk = tid + static_cast<uint32_t>(c) * kThreads;
       const uint32_t n = chunk >> 4, k = (chunk & 15u) * 16u;
-      const size_t tok = min(static_cast<size_t>(tok0 + n), T - 1);
-      ar[c] = load16(reinterpret_cast<const uint8_t*>(q.quants + tok * q.qstride + static_cast<size_t>(b) * 256u + k));
+      const uint32_t tok = min(tok0 + n, last);
+      ar[c] = load16(reinterpret_cast<const uint8_t*>(q.quants + (__umul24(tok, qs32) + b * 256u + k)));
     }
     if (tid < static_cast<uint32_t>(BN)) {
-      const size_t o = stok * q.bstride + static_cast<size_t>(b) * 8u;
+      const uint32_t o = __umul24(stok, bs32) + b * 8u;
       d8r = q.scales[o];
       if (FMT == 12) {
         sr0 = load16(reinterpret_cast<const uint8_t*>(q.sums + o));
@@ -502,6 +507,10 @@ hipError_t launch_bn(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPl
 
 }  // namespace
 
+bool gemm_fits(size_t tokens, size_t qstride) {
+  return tokens < (size_t{1} << 24) && qstride < (size_t{1} << 24) && tokens * qstride <= size_t{0xffffffffu};
+}
+
 size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens) {
   if (tokens == 0 || (type_id != 12u && type_id != 14u)) return 0;
   const SplitPlan p = plan_split(jobs, tokens);
@@ -511,6 +520,7 @@ size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens) {
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
                        hipStream_t s) {
   if (tokens == 0) return hipSuccess;
+  if (!gemm_fits(tokens, q.qstride)) return hipErrorInvalidValue;
   const SplitPlan plan = plan_split(jobs, tokens);
   const int bn = token_tile(tokens);
   if (type_id == 12u)

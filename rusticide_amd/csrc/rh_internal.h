@@ -106,6 +106,9 @@ hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q
 // across workgroups (0: it does not split). launch_gemm splits only when
 // `terms` holds that many bytes; without it the launch runs unsplit.
 size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens);
+// Whether a k-quant GEMM can address a batch: the quantized activation's
+// offsets (tokens x qstride bytes) are 32-bit.
+bool gemm_fits(size_t tokens, size_t qstride);
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
                        hipStream_t s);
 // Prefill GEMM on int8 MFMA for I2_S against the I8_S activation q; with
