@@ -363,6 +363,15 @@ rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn
   return RH_OK;
 }
 
+rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tokens, const rh_job* jobs,
+                           size_t n_jobs, hipStream_t s) {
+  if (!ctx || (!jobs && n_jobs) || tokens == 0) return RH_ERR_INVALID_ARGUMENT;
+  for (size_t i = 0; i < n_jobs; i++)
+    if (!jobs[i].weights || !is_kquant(jobs[i].weights->type_id) || (!jobs[i].out && jobs[i].out_len))
+      return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a pre-quantized job is not a k-quant matrix with an output");
+  return launch_jobs(ctx, nullptr, width, tokens, jobs, n_jobs, q, q, s, nullptr, 0u);
+}
+
 // Calls made without a context keep their message per thread
 // (rh_last_error(NULL)).
 thread_local std::string t_last_error;

@@ -93,12 +93,15 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint
 // load is issued up front.
 constexpr uint32_t kMaxNormPer = 32;  // widths up to 256 * 32 = 8192
 
-template <uint32_t PER>
+// QUANT: the normalized row is not stored as f32 but quantized to Q8_K into
+// q8 (token t - norm_from), as quantize_super_kernel would from the f32 row;
+// width must then be a multiple of 256.
+template <uint32_t PER, bool QUANT = false>
 __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restrict__ hidden,
                                                                 const float* __restrict__ delta, uint32_t n,
                                                                 uint32_t width, const float* __restrict__ weight,
                                                                 float eps, uint32_t norm_from,
-                                                                float* __restrict__ normed) {
+                                                                float* __restrict__ normed, Q8Dev q8) {
   extern __shared__ __align__(16) float sq[];
   __shared__ float s_rms;
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -146,6 +149,24 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
   }
   __syncthreads();
   const float rms = s_rms;
+  if constexpr (QUANT) {
+    // the squares are summed: their LDS takes the normalized row, which each
+    // wave then quantizes a 256-value block at a time
+#pragma unroll
+    for (uint32_t k = 0; k < PER; k++) {
+      const uint32_t e = tid + k * kNormThreads;
+      if (e < width) sq[e] = __fdiv_rn(v[k], rms) * wt[k];
+    }
+    __syncthreads();
+    const uint32_t lane = tid & 63u;
+    for (uint32_t sb = tid >> 6; sb < width / 256u; sb += kNormThreads / 64u) {
+      float f[4];
+#pragma unroll
+      for (int i = 0; i < 4; i++) f[i] = sq[sb * 256u + lane * 4u + static_cast<uint32_t>(i)];
+      quantize_super_block(f, lane, t - norm_from, sb, q8);
+    }
+    return;
+  }
   float* o = normed + static_cast<size_t>(t - norm_from) * width;
 #pragma unroll
   for (uint32_t k = 0; k < PER; k++) {
@@ -157,17 +178,22 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
   }
 }
 
-using AddNormFn = void (*)(float*, const float*, uint32_t, uint32_t, const float*, float, uint32_t, float*);
+using AddNormFn = void (*)(float*, const float*, uint32_t, uint32_t, const float*, float, uint32_t, float*, Q8Dev);
 
-// Dynamic LDS of add_norm_kernel: the squares in the ordered sum's layout.
-size_t add_norm_lds(uint32_t width) { return static_cast<size_t>(wave_sum_floats(width)) * 4u; }
+// Dynamic LDS of add_norm_kernel: the squares in the ordered sum's layout
+// (at least width floats, which the QUANT form reuses for the row).
+size_t add_norm_lds(uint32_t width) {
+  const size_t n = wave_sum_floats(width);
+  return (n > width ? n : width) * 4u;
+}
 
 // The add_norm_kernel instance for a row width (<= 256 * kMaxNormPer).
+template <bool QUANT = false>
 AddNormFn add_norm_for(uint32_t width) {
-  if (width <= 4u * kNormThreads) return add_norm_kernel<4>;
-  if (width <= 8u * kNormThreads) return add_norm_kernel<8>;
-  if (width <= 16u * kNormThreads) return add_norm_kernel<16>;
-  return add_norm_kernel<kMaxNormPer>;
+  if (width <= 4u * kNormThreads) return add_norm_kernel<4, QUANT>;
+  if (width <= 8u * kNormThreads) return add_norm_kernel<8, QUANT>;
+  if (width <= 16u * kNormThreads) return add_norm_kernel<16, QUANT>;
+  return add_norm_kernel<kMaxNormPer, QUANT>;
 }
 
 // q/k/v from the projections (stored by weight row, x[e*n + t]): q rotated
@@ -684,6 +710,8 @@ struct rh_decoder {
   float *hidden = nullptr, *normed = nullptr, *delta = nullptr, *qr = nullptr, *kr = nullptr, *vr = nullptr;
   float* hidden2 = nullptr;  // the residual's other buffer on the norm-fused path
   bool fuse_norm = false;    // one-token forwards fold each RMSNorm into the GEMV after it
+  bool quant_norm = false;   // batches quantize the normed rows in the norm kernel
+  Q8Dev q8;                  // that activation, for up to `cap` tokens
   float *q = nullptr, *mixed = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
   float* logits = nullptr;
   uint32_t* tokens = nullptr;  // the chunk's token ids
@@ -697,6 +725,11 @@ namespace {
 
 constexpr size_t kPrefillChunk = 64;  // model/src/generate.rs:70
 
+bool is_kquant_matrix(const rh_matrix* m) {
+  const uint32_t t = rh_matrix_type(m);
+  return t == RH_TYPE_Q4_K || t == RH_TYPE_Q6_K;
+}
+
 template <typename T>
 hipError_t dmalloc(T** p, size_t n) {
   return hipMalloc(reinterpret_cast<void**>(p), (n ? n : 1) * sizeof(T));
@@ -708,8 +741,11 @@ void free_acts(rh_decoder* d) {
   for (void* p : {static_cast<void*>(d->hidden), static_cast<void*>(d->normed), static_cast<void*>(d->delta),
                   static_cast<void*>(d->qr), static_cast<void*>(d->kr), static_cast<void*>(d->vr),
                   static_cast<void*>(d->q), static_cast<void*>(d->mixed), static_cast<void*>(d->gate),
-                  static_cast<void*>(d->up), static_cast<void*>(d->hf), static_cast<void*>(d->tokens)})
+                  static_cast<void*>(d->up), static_cast<void*>(d->hf), static_cast<void*>(d->tokens),
+                  static_cast<void*>(d->q8.quants), static_cast<void*>(d->q8.scales), static_cast<void*>(d->q8.sums),
+                  static_cast<void*>(d->q8.sums16)})
     if (p) hipFree(p);
+  d->q8 = Q8Dev{};
   d->hidden = d->normed = d->delta = d->qr = d->kr = d->vr = d->q = d->mixed = d->gate = d->up = d->hf = nullptr;
   d->tokens = nullptr;
   d->cap = 0;
@@ -731,6 +767,17 @@ hipError_t ensure_acts(rh_decoder* d, size_t n) {
     free_acts(d);
     return e;
   }
+  // the Q8_K activation of a batch (the layout ensure_q8 gives matmul_batch)
+  const size_t qstride = (w + 255u) / 256u * 256u, bstride = (qstride / 32u + 7u) / 8u * 8u;
+  if ((e = dmalloc(&d->q8.quants, n * qstride)) != hipSuccess ||
+      (e = dmalloc(&d->q8.scales, n * bstride)) != hipSuccess || (e = dmalloc(&d->q8.sums, n * bstride)) != hipSuccess ||
+      (e = dmalloc(&d->q8.sums16, 2 * n * bstride)) != hipSuccess) {
+    free_acts(d);
+    return e;
+  }
+  d->q8.qstride = qstride;
+  d->q8.bstride = bstride;
+  d->q8.n_blocks = w / 256u * 8u;
   d->cap = n;
   return hipSuccess;
 }
@@ -738,6 +785,12 @@ hipError_t ensure_acts(rh_decoder* d, size_t n) {
 rh_status mm(rh_decoder* d, const float* in, size_t n, size_t width, std::initializer_list<rh_job> jobs) {
   std::vector<rh_job> v(jobs);
   return rh_matmul_batch_device(d->ctx, in, n * width, n, v.data(), v.size(), d->stream);
+}
+
+// mm over the decoder's Q8_K activation (d->q8, which a QUANT norm filled).
+rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_job> jobs) {
+  std::vector<rh_job> v(jobs);
+  return matmul_q8_device(d->ctx, d->q8, width, n, v.data(), v.size(), d->stream);
 }
 
 #define RHD(expr)                                   \
@@ -770,13 +823,20 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
   const size_t norm_lds = add_norm_lds(w);
   const AddNormFn norm_fn = add_norm_for(w);
+  // a batch whose normed rows feed only k-quant GEMMs gets them as Q8_K
+  // straight from the norm kernel
+  const bool qn = d->quant_norm && n >= 2;
+  const AddNormFn norm_in = qn ? add_norm_for<true>(w) : norm_fn;
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
     const rh_decoder::Block& b = d->blocks[l];
-    hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
-                       b.attn_norm, c.rms_norm_eps, 0u, d->normed);
+    hipLaunchKernelGGL(norm_in, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+                       b.attn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
     RHD(hipGetLastError());
-    RHS(mm(d, d->normed, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
+    if (qn)
+      RHS(mm_q8(d, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
+    else
+      RHS(mm(d, d->normed, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
     float* kc = d->keys + l * c.context_length * kv;
     float* vc = d->values + l * c.context_length * kv;
     const uint32_t work = w / 2u + kv / 2u + kv;
@@ -790,10 +850,13 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                        static_cast<uint32_t>(start), d->mixed);
     RHD(hipGetLastError());
     RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
-    hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, d->delta, nn, w,
-                       b.ffn_norm, c.rms_norm_eps, 0u, d->normed);
+    hipLaunchKernelGGL(norm_in, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, d->delta, nn, w,
+                       b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
     RHD(hipGetLastError());
-    RHS(mm(d, d->normed, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
+    if (qn)
+      RHS(mm_q8(d, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
+    else
+      RHS(mm(d, d->normed, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
     const size_t total = n * f;
     hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255u) / 256u)), dim3(256), 0, s, d->gate,
                        d->up, nn, f, d->hf);
@@ -803,7 +866,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   }
   // the last residual for every token, then the last token's output norm
   hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
-                     d->output_norm, c.rms_norm_eps, nn - 1u, d->normed);
+                     d->output_norm, c.rms_norm_eps, nn - 1u, d->normed, Q8Dev{});
   RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
   RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
@@ -878,7 +941,7 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start)
   // more workgroups than fit on the chip at once, and each would repeat the
   // ordered sum
   hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), add_norm_lds(w), s, h, pending, 1u,
-                     w, d->output_norm, c.rms_norm_eps, 0u, d->normed);
+                     w, d->output_norm, c.rms_norm_eps, 0u, d->normed, Q8Dev{});
   RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
   RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
@@ -1038,6 +1101,15 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
     fuse = fuse && fusable(b.q) && fusable(b.k) && fusable(b.v) && fusable(b.gate) && fusable(b.up);
   const char* env = std::getenv("RUSTICIDE_HIP_NORM_FUSE");
   d->fuse_norm = fuse && !(env && env[0] == '0');
+  // batches quantize the normed rows in the norm kernel when every matrix
+  // reading them is a k-quant GEMM operand; RUSTICIDE_HIP_NORM_QUANT=0 keeps
+  // the f32 rows and matmul_batch's own quantize (same bits)
+  bool quant = w % 256 == 0;
+  for (const rh_decoder::Block& b : d->blocks)
+    for (const rh_matrix* m : {b.q, b.k, b.v, b.gate, b.up})
+      quant = quant && is_kquant_matrix(m) && rh_matrix_cols(m) == w;
+  const char* qenv = std::getenv("RUSTICIDE_HIP_NORM_QUANT");
+  d->quant_norm = quant && !(qenv && qenv[0] == '0');
   *out = d;
   return RH_OK;
 }

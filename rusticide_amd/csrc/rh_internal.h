@@ -106,6 +106,10 @@ hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q
 // across workgroups (0: it does not split). launch_gemm splits only when
 // `terms` holds that many bytes; without it the launch runs unsplit.
 size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens);
+// rh_matmul_batch_device for k-quant jobs on an activation already quantized
+// to Q8_K in `q` (width / 256 super-blocks for each of `tokens` tokens).
+rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tokens, const rh_job* jobs,
+                           size_t n_jobs, hipStream_t s);
 // Whether a k-quant GEMM can address a batch: the quantized activation's
 // offsets (tokens x qstride bytes) are 32-bit.
 bool gemm_fits(size_t tokens, size_t qstride);

@@ -29,12 +29,15 @@ def ctx():
 @pytest.fixture(params=["fused", "separate"])
 def norm_path(request, monkeypatch):
     # one-token forwards fold each RMSNorm into the GEMV after it unless
-    # RUSTICIDE_HIP_NORM_FUSE=0 (read when a decoder is created); both give
-    # the CPU path's bits
+    # RUSTICIDE_HIP_NORM_FUSE=0, and batches quantize the normed rows in the
+    # norm kernel unless RUSTICIDE_HIP_NORM_QUANT=0 (both read when a decoder
+    # is created); every combination gives the CPU path's bits
     if request.param == "separate":
         monkeypatch.setenv("RUSTICIDE_HIP_NORM_FUSE", "0")
+        monkeypatch.setenv("RUSTICIDE_HIP_NORM_QUANT", "0")
     else:
         monkeypatch.delenv("RUSTICIDE_HIP_NORM_FUSE", raising=False)
+        monkeypatch.delenv("RUSTICIDE_HIP_NORM_QUANT", raising=False)
     return request.param
 
 
