@@ -507,10 +507,13 @@ void image_range(const rh_matrix* m, const uint8_t* src, size_t lo, size_t hi, u
   }
 }
 
-// image_range over up to 8 host threads, each at least kCopySlice bytes.
+// image_range over up to kCopyThreads host threads, each at least
+// kCopySlice bytes.
+constexpr size_t kCopyThreads = 8;
+
 void image_range_parallel(const rh_matrix* m, const uint8_t* src, size_t lo, size_t hi, uint8_t* dst) {
   const size_t n = hi - lo;
-  size_t threads = std::min<size_t>(8, std::max<size_t>(1, std::thread::hardware_concurrency()));
+  size_t threads = std::min<size_t>(kCopyThreads, std::max<size_t>(1, std::thread::hardware_concurrency()));
   threads = std::min(threads, std::max<size_t>(1, n / kCopySlice));
   if (threads <= 1) {
     image_range(m, src, lo, hi, dst);
