@@ -807,10 +807,11 @@ __device__ __forceinline__ void quantize_row_regs(const RowX& r, uint32_t t, uin
 }
 
 // LDS: act [T][nbmax*128] i8 | qs32 [T][nbmax*4] i32 | divisor [T] f32 |
-// reduction scratch. A team of lpr lanes (a power of two) owns a row; lane l
-// holds chunks l, l + lpr, ... (CPL of them) of 16 bytes, loaded before the
-// activation is quantized.
-template <int T, int CPL>
+// reduction scratch. A team of lpr lanes (a power of two) owns a row of each
+// of the workgroup's G row groups; lane l holds chunks l, l + lpr, ... (CPL
+// of them) of 16 bytes of each, all loaded before the activation is
+// quantized, so one quantization serves G groups of rows.
+template <int T, int CPL, int G>
 __global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, const float* __restrict__ x,
                                                              size_t width, uint32_t nq, uint32_t nbmax,
                                                              uint32_t lpr, size_t tokens, size_t t0,
@@ -825,8 +826,7 @@ __global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, cons
   const GemvJob& J = jobs.j[find_job(jobs)];
   const uint32_t R = kThreads / lpr;
   const uint32_t r = threadIdx.x / lpr, cl = threadIdx.x & (lpr - 1u);
-  const uint32_t row = (blockIdx.x - J.wg_begin) * R + r;
-  const bool live = row < J.rows;
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * R * static_cast<uint32_t>(G) + r;
   const uint32_t nchunk = 2u * J.nb;
   // token t0's values first: loads return in issue order (see load_x_round)
   const float* xt = x + t0 * width;
@@ -834,12 +834,17 @@ __global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, cons
   const bool aligned = ((reinterpret_cast<uintptr_t>(xt) | (width * 4u)) & 15u) == 0;
   RowX rx;
   load_row_x(rx, xt, n, aligned);
-  u32x4 w[CPL];
+  u32x4 w[G][CPL];
 #pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    const uint32_t c = cl + static_cast<uint32_t>(i) * lpr;
-    w[i] = (live && c < nchunk) ? load16(J.w + __umul24(row, static_cast<uint32_t>(J.stride)) + 16u * c)
-                                : u32x4{0, 0, 0, 0};
+  for (int gi = 0; gi < G; gi++) {
+    const uint32_t row = row0 + static_cast<uint32_t>(gi) * R;
+#pragma unroll
+    for (int i = 0; i < CPL; i++) {
+      const uint32_t c = cl + static_cast<uint32_t>(i) * lpr;
+      w[gi][i] = (row < J.rows && c < nchunk)
+                     ? load16(J.w + __umul24(row, static_cast<uint32_t>(J.stride)) + 16u * c)
+                     : u32x4{0, 0, 0, 0};
+    }
   }
 
   uint32_t slot = 0;
@@ -850,54 +855,59 @@ __global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, cons
   }
   __syncthreads();
 
-  uint32_t acc[T];
 #pragma unroll
-  for (int t = 0; t < T; t++) acc[t] = 0;
+  for (int gi = 0; gi < G; gi++) {
+    const uint32_t row = row0 + static_cast<uint32_t>(gi) * R;
+    const bool live = row < J.rows;
+    uint32_t acc[T];
 #pragma unroll
-  for (int i = 0; i < CPL; i++) {
-    const uint32_t c = cl + static_cast<uint32_t>(i) * lpr;
-    if (c >= nchunk) break;
-    uint32_t c6[4], c4[4], c2[4], c0[4];
+    for (int t = 0; t < T; t++) acc[t] = 0;
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-      c6[k] = (w[i][k] >> 2) & 0x30303030u;  // code of shift 6, times 16
-      c4[k] = w[i][k] & 0x30303030u;         // shift 4, times 16
-      c2[k] = w[i][k] & 0x0C0C0C0Cu;         // shift 2, times 4
-      c0[k] = w[i][k] & 0x03030303u;         // shift 0
-    }
-#pragma unroll
-    for (int t = 0; t < T; t++) {
-      const int8_t* a = act + t * nkeep + 128u * (c >> 1) + 16u * (c & 1u);
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
-      int32_t P16 = 0, P4 = 0, P1 = 0;
+    for (int i = 0; i < CPL; i++) {
+      const uint32_t c = cl + static_cast<uint32_t>(i) * lpr;
+      if (c >= nchunk) break;
+      uint32_t c6[4], c4[4], c2[4], c0[4];
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        P16 = dot4(c6[k], a0[k], P16);
-        P16 = dot4(c4[k], a1[k], P16);
-        P4 = dot4(c2[k], a2[k], P4);
-        P1 = dot4(c0[k], a3[k], P1);
+        c6[k] = (w[gi][i][k] >> 2) & 0x30303030u;  // code of shift 6, times 16
+        c4[k] = w[gi][i][k] & 0x30303030u;         // shift 4, times 16
+        c2[k] = w[gi][i][k] & 0x0C0C0C0Cu;         // shift 2, times 4
+        c0[k] = w[gi][i][k] & 0x03030303u;         // shift 0
       }
-      acc[t] += static_cast<uint32_t>(P1 + (P4 >> 2) + (P16 >> 4));
+#pragma unroll
+      for (int t = 0; t < T; t++) {
+        const int8_t* a = act + t * nkeep + 128u * (c >> 1) + 16u * (c & 1u);
+        const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
+        const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
+        const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
+        const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+        int32_t P16 = 0, P4 = 0, P1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          P16 = dot4(c6[k], a0[k], P16);
+          P16 = dot4(c4[k], a1[k], P16);
+          P4 = dot4(c2[k], a2[k], P4);
+          P1 = dot4(c0[k], a3[k], P1);
+        }
+        acc[t] += static_cast<uint32_t>(P1 + (P4 >> 2) + (P16 >> 4));
+      }
     }
-  }
-  // ternary.rs:39,41: minus the sum of the quants of the row's blocks (wrapping)
+    // ternary.rs:39,41: minus the sum of the quants of the row's blocks (wrapping)
 #pragma unroll
-  for (int t = 0; t < T; t++)
-    for (uint32_t k = cl; k < 4u * J.nb; k += lpr) acc[t] -= static_cast<uint32_t>(qs32[t * nbmax * 4u + k]);
+    for (int t = 0; t < T; t++)
+      for (uint32_t k = cl; k < 4u * J.nb; k += lpr) acc[t] -= static_cast<uint32_t>(qs32[t * nbmax * 4u + k]);
 #pragma unroll
-  for (int t = 0; t < T; t++) {
-    uint32_t v = acc[t];
-    for (uint32_t off = lpr >> 1; off > 0; off >>= 1)
-      v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), static_cast<int>(off), 64));
-    const size_t idx = static_cast<size_t>(row) * tokens + t0 + t;
-    if (cl == 0 && live && idx < J.out_len) {
-      const int32_t dot = static_cast<int32_t>(v);
-      if (raw) raw[idx] = dot;
-      // ternary.rs:53-57: (dot as f32) / s * scale; 0 without a scale
-      else J.out[idx] = nq ? __fdiv_rn(static_cast<float>(dot), divisor[t]) * J.scale : 0.0f;
+    for (int t = 0; t < T; t++) {
+      uint32_t v = acc[t];
+      for (uint32_t off = lpr >> 1; off > 0; off >>= 1)
+        v += static_cast<uint32_t>(__shfl_xor(static_cast<int>(v), static_cast<int>(off), 64));
+      const size_t idx = static_cast<size_t>(row) * tokens + t0 + t;
+      if (cl == 0 && live && idx < J.out_len) {
+        const int32_t dot = static_cast<int32_t>(v);
+        if (raw) raw[idx] = dot;
+        // ternary.rs:53-57: (dot as f32) / s * scale; 0 without a scale
+        else J.out[idx] = nq ? __fdiv_rn(static_cast<float>(dot), divisor[t]) * J.scale : 0.0f;
+      }
     }
   }
 }
@@ -1235,6 +1245,8 @@ bool gemv_fused_ok(uint32_t type_id, size_t width, size_t tn) {
 
 namespace {
 
+constexpr uint32_t kI2sMinWgs = 256;  // one per CU
+
 template <int T>
 hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t tokens, size_t t0,
                             hipStream_t s, int32_t* raw) {
@@ -1249,20 +1261,36 @@ hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t 
   const uint32_t cpl = (nchunk + lpr - 1u) / lpr;
   if (cpl > 2u) return hipErrorInvalidValue;
   const uint32_t R = kThreads / lpr;
+  // G row groups per workgroup: the most that still leave at least
+  // kI2sMinWgs workgroups (each repeats the activation's quantization);
+  // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 forces it, for tuning
+  auto count = [&](uint32_t g) {
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < jobs.n; i++) n += (jobs.j[i].rows + R * g - 1u) / (R * g);
+    return n;
+  };
+  uint32_t G = 1;
+  while (G < 4u && count(2u * G) >= kI2sMinWgs) G *= 2u;
+  if (const char* v = std::getenv("RUSTICIDE_HIP_I2S_GROUPS")) G = v[0] == '4' ? 4u : v[0] == '2' ? 2u : 1u;
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     jobs.j[i].wg_begin = wgs;
-    wgs += (jobs.j[i].rows + R - 1u) / R;
+    wgs += (jobs.j[i].rows + R * G - 1u) / (R * G);
   }
   if (wgs == 0) return hipSuccess;
   const size_t lds = T * nbl * 128u + T * nbl * 16u + T * 4u + 4u * (kThreads / 64u) * 4u;
+  void* k;
   if (cpl == 1u)
-    hipLaunchKernelGGL((gemv_i2s_fused_kernel<T, 1>), dim3(wgs), dim3(kThreads), lds, s, jobs, x, width, nq, nbl,
-                       lpr, tokens, t0, raw);
+    k = G == 4u ? reinterpret_cast<void*>(gemv_i2s_fused_kernel<T, 1, 4>)
+      : G == 2u ? reinterpret_cast<void*>(gemv_i2s_fused_kernel<T, 1, 2>)
+                : reinterpret_cast<void*>(gemv_i2s_fused_kernel<T, 1, 1>);
   else
-    hipLaunchKernelGGL((gemv_i2s_fused_kernel<T, 2>), dim3(wgs), dim3(kThreads), lds, s, jobs, x, width, nq, nbl,
-                       lpr, tokens, t0, raw);
-  return hipGetLastError();
+    k = G == 4u ? reinterpret_cast<void*>(gemv_i2s_fused_kernel<T, 2, 4>)
+      : G == 2u ? reinterpret_cast<void*>(gemv_i2s_fused_kernel<T, 2, 2>)
+                : reinterpret_cast<void*>(gemv_i2s_fused_kernel<T, 2, 1>);
+  void* args[] = {&jobs, const_cast<float**>(&x), &width, const_cast<uint32_t*>(&nq), const_cast<uint32_t*>(&nbl),
+                  &lpr, &tokens, &t0, &raw};
+  return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
 }
 
 }  // namespace

@@ -314,6 +314,24 @@ def test_i2s_i32_accumulators_are_bit_exact(ctx, variant, rows, cols, token_coun
         assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, tokens, scale=0.02))
 
 
+@pytest.mark.parametrize("groups", ["1", "2", "4"])
+def test_i2s_row_groups_per_workgroup(ctx, monkeypatch, groups):
+    # RUSTICIDE_HIP_I2S_GROUPS: one activation quantization per workgroup
+    # serves 1, 2 or 4 groups of rows; ragged row counts leave groups empty
+    monkeypatch.setenv("RUSTICIDE_HIP_I2S_GROUPS", groups)
+    for rows, cols in ((6912, 2560), (2560, 6912), (37, 384), (300, 1024)):
+        data = synth.i2s_matrix(rows, cols, seed=rows + 1)
+        m = R.Matrix.load(ctx, 36, data, rows, cols)
+        rb = cols // 4
+        for tokens in (1, 2):
+            x = synth.normal_f32(tokens * cols, seed=20 + tokens)
+            raw = ctx.ternary_dot_i32(m, x, tokens)
+            assert np.array_equal(raw, O.ternary_dot_matrix_i32(data[: rows * rb], rb, x, tokens)), (rows, cols)
+            out = np.full(rows * tokens, np.nan, np.float32)
+            R.matmul_batch(ctx, x, tokens, [(m, out)])
+            assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, tokens, scale=0.02), f"{rows}x{cols}")
+
+
 def test_i2s_code_three_and_hostile_bytes(ctx):
     # i2_s.rs:96-104: code 3 decodes to +2; random bytes use every code
     rows, cols = 16, 512
