@@ -533,3 +533,20 @@ def test_decoder_gguf_round_trips_a_synthetic_model():
         assert f.tensor_info("blk.1.ffn_down.weight")[:2] == ([rows, cols], t)
         assert f.tensor_bytes("blk.1.ffn_down.weight") == data.tobytes()
         assert np.array_equal(np.frombuffer(f.tensor_bytes("output_norm.weight"), np.float32), model["output_norm"])
+
+
+def test_tokenizer_sized_metadata_parses():
+    # a llama file's tokenizer arrays: 32000 strings, f32 scores, i32 types
+    # (crates/rusticide-tokenizer reads them; here they are parsed and skipped)
+    rng = np.random.default_rng(2)
+    tokens = [bytes(rng.integers(32, 127, rng.integers(1, 12)).astype(np.uint8)).decode() for _ in range(32000)]
+    w = Writer().kv("general.architecture", STRING, "llama")
+    w.kv("tokenizer.ggml.model", STRING, "llama")
+    w.kv("tokenizer.ggml.tokens", ARRAY, (STRING, tokens))
+    w.raw_kv("tokenizer.ggml.scores", ARRAY, struct.pack("<IQ", FLOAT32, 32000) + rng.random(32000, np.float32).tobytes())
+    w.raw_kv("tokenizer.ggml.token_type", ARRAY, struct.pack("<IQ", INT32, 32000) + np.ones(32000, np.int32).tobytes())
+    w.kv("tokenizer.ggml.bos_token_id", UINT32, 1)
+    f = parse(w.tensor("token_embd.weight", [32000, 4], F32, bytes(32000 * 16)).build())
+    assert f.metadata_count == 6
+    assert f.meta_type("tokenizer.ggml.tokens") == ARRAY and f.meta_uint("tokenizer.ggml.bos_token_id") == 1
+    assert f.meta_string("tokenizer.ggml.model") == "llama"

@@ -174,3 +174,23 @@ def test_tinyllama_shaped_gguf_greedy_decode(ctx):
     want = ref.generate_greedy(prompt, 32)
     ref.free()
     assert len(got) == 32 and np.array_equal(got, want)
+
+
+def test_q4_k_m_mix_with_q6_k_attn_v(ctx):
+    # llama.cpp's Q4_K_M keeps attn_v (and some ffn_down) in Q6_K: the Q/K/V
+    # launches then mix formats, in the fused one-token path and in the
+    # batched one (its Q8_K norm and split GEMMs)
+    model = synth.decoder_model(SMALL, seed=31)
+    for i, b in enumerate(model["blocks"]):
+        if i % 2 == 0:
+            _, _, rows, cols = b["attn_v"]
+            b["attn_v"] = (14, synth.q6k_centered(rows, cols, 900 + i), rows, cols)
+    f, m = load(ctx, G.decoder_gguf(model))
+    assert f.tensor_info("blk.0.attn_v.weight")[1] == 14 and f.tensor_info("blk.1.attn_v.weight")[1] == 12
+    dec, cpu = m.decoder(), O.Decoder(model, threads=8)
+    prompt = np.random.default_rng(9).integers(0, SMALL["vocab_size"], 70).astype(np.uint32)
+    assert same_bits(dec.forward_batch(prompt[:64], 0), cpu.forward_batch(prompt[:64], 0))
+    assert np.array_equal(dec.generate_greedy(prompt, 24), cpu.generate_greedy(prompt, 24))
+    m.free()
+    f.close()
+    cpu.close()
