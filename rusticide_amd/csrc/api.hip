@@ -521,11 +521,19 @@ void image_range_parallel(const rh_matrix* m, const uint8_t* src, size_t lo, siz
   }
   const size_t part = round_up((n + threads - 1) / threads, 4096);
   std::vector<std::thread> pool;
+  size_t done = std::min(hi, lo + part);  // the caller's own part
   for (size_t t = 1; t < threads && lo + t * part < hi; t++) {
     const size_t a = lo + t * part, b = std::min(hi, a + part);
-    pool.emplace_back(image_range, m, src, a, b, dst + (a - lo));
+    try {
+      pool.emplace_back(image_range, m, src, a, b, dst + (a - lo));
+    } catch (...) {  // no thread to spare: this one fills the rest
+      done = a;
+      break;
+    }
+    done = b;
   }
   image_range(m, src, lo, std::min(hi, lo + part), dst);
+  if (done < hi) image_range(m, src, done, hi, dst + (done - lo));
   for (auto& th : pool) th.join();
 }
 

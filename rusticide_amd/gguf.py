@@ -269,7 +269,11 @@ class GgufFile:
             _gguf_lib().rh_gguf_free(self.handle)
             self.handle = None
 
-    __del__ = close
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
     def __enter__(self):
         return self
