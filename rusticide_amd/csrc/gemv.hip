@@ -1118,11 +1118,14 @@ uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_ro
   if (fq) {
     // every workgroup quantizes the whole activation: when four blocks per
     // team would give three or more workgroups per CU (a 32000-row output
-    // matrix), eight halve that repeated work; smaller launches keep four so
-    // the grid still covers the chip
-    if (T == 1 && (total_rows + rows_per_wg(type_id, nb, 4u) - 1u) / rows_per_wg(type_id, nb, 4u) >=
-                      3u * static_cast<uint32_t>(device_cus()))
-      return 8u;
+    // matrix), eight halve that repeated work; when four would leave most
+    // CUs idle (64 workgroups for the 2048x2048 attention output), two
+    // spread the rows over twice the workgroups
+    const uint32_t r4 = rows_per_wg(type_id, nb, 4u);
+    const uint32_t wgs4 = (total_rows + r4 - 1u) / r4;
+    const uint32_t cus = static_cast<uint32_t>(device_cus());
+    if (T == 1 && wgs4 >= 3u * cus) return 8u;
+    if (T == 1 && 2u * wgs4 < cus && floor_ni <= 2u) return 2u;
     return 4u;
   }
   for (uint32_t ni : {1u, 2u, 4u}) {
