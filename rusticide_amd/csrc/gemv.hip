@@ -1037,9 +1037,12 @@ void* kq_kernel() {
                    : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR>);
 }
 
-// The norm-fused decode kernels: one token, four blocks per team, the row
-// preloaded in one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
-void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair) {
+// The norm-fused decode kernels: one token, four blocks per team (two for a
+// single-round launch that would leave most CUs idle), the row preloaded in
+// one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
+void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair, uint32_t ni) {
+  if (!pair && ni == 2u && fq == 1u)
+    return type_id == 12u ? kq_kernel<12, 1, 2, 1, true>() : kq_kernel<14, 1, 2, 1, true>();
   if (pair) {
     if (type_id == 12u) return fq == 1u ? kq_kernel<12, 1, 4, 1, true, true>() : kq_kernel<12, 1, 4, 4, true, true>();
     return fq == 1u ? kq_kernel<14, 1, 4, 1, true, true>() : kq_kernel<14, 1, 4, 4, true, true>();
@@ -1158,7 +1161,16 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     const size_t nq = width / 256u < nbmax ? width / 256u : nbmax;
     fq = static_cast<size_t>(T) * nq <= kThreads / 32u ? 1u : 4u;
   }
-  const uint32_t ni = norm ? 4u : kquant ? choose_blocks_per_team<T>(type_id, nbl, total_rows, fq) : 1u;
+  uint32_t ni = norm ? 4u : kquant ? choose_blocks_per_team<T>(type_id, nbl, total_rows, fq) : 1u;
+  // a norm-fused launch of fewer workgroups than half the CUs (Q/K/V: 80)
+  // takes two blocks per team, as choose_blocks_per_team does for the others
+  const bool pair_job = jobs.n == 1u && jobs.j[0].w2 != nullptr;
+  if (norm && T == 1 && fq == 1u && !pair_job && min_blocks_per_team(nbl) <= 2u) {
+    const uint32_t r4 = rows_per_wg(type_id, nbl, 4u);
+    uint32_t wgs4 = 0;
+    for (uint32_t i = 0; i < jobs.n; i++) wgs4 += (jobs.j[i].rows + r4 - 1u) / r4;
+    if (2u * wgs4 < static_cast<uint32_t>(device_cus())) ni = 2u;
+  }
   const uint32_t R = rows_per_wg(type_id, nbl, ni);
   // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
   const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
@@ -1187,7 +1199,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       nrm = *norm;
       nrm.lds_offset = static_cast<uint32_t>((lds + 15u) / 16u * 16u);
       lds = nrm.lds_offset + static_cast<size_t>(wave_sum_floats(nbl * 256u)) * 4u + 16u;
-      k = kq_norm_kernel(type_id, fq, pair);
+      k = kq_norm_kernel(type_id, fq, pair, ni);
     } else {
       k = kq_kernel_for<T>(type_id, ni, fq);
     }
