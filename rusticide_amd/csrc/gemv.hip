@@ -1041,8 +1041,10 @@ void* kq_kernel() {
 // single-round launch that would leave most CUs idle), the row preloaded in
 // one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
 void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair, uint32_t ni) {
-  if (!pair && ni == 2u && fq == 1u)
+  if (ni == 2u && fq == 1u) {
+    if (pair) return type_id == 12u ? kq_kernel<12, 1, 2, 1, true, true>() : kq_kernel<14, 1, 2, 1, true, true>();
     return type_id == 12u ? kq_kernel<12, 1, 2, 1, true>() : kq_kernel<14, 1, 2, 1, true>();
+  }
   if (pair) {
     if (type_id == 12u) return fq == 1u ? kq_kernel<12, 1, 4, 1, true, true>() : kq_kernel<12, 1, 4, 4, true, true>();
     return fq == 1u ? kq_kernel<14, 1, 4, 1, true, true>() : kq_kernel<14, 1, 4, 4, true, true>();
@@ -1171,6 +1173,9 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     for (uint32_t i = 0; i < jobs.n; i++) wgs4 += (jobs.j[i].rows + r4 - 1u) / r4;
     if (2u * wgs4 < static_cast<uint32_t>(device_cus())) ni = 2u;
   }
+  // RUSTICIDE_HIP_NORM_NI=2|4 forces the norm-fused one-token launches, for tuning
+  if (const char* v = std::getenv("RUSTICIDE_HIP_NORM_NI"))
+    if (norm && T == 1 && fq == 1u && min_blocks_per_team(nbl) <= 2u) ni = v[0] == '2' ? 2u : 4u;
   const uint32_t R = rows_per_wg(type_id, nbl, ni);
   // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
   const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
