@@ -1041,6 +1041,8 @@ void* kq_kernel() {
 // single-round launch that would leave most CUs idle), the row preloaded in
 // one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
 void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair, uint32_t ni) {
+  if (ni == 8u && fq == 1u && !pair)
+    return type_id == 12u ? kq_kernel<12, 1, 8, 1, true>() : kq_kernel<14, 1, 8, 1, true>();
   if (ni == 2u && fq == 1u) {
     if (pair) return type_id == 12u ? kq_kernel<12, 1, 2, 1, true, true>() : kq_kernel<14, 1, 2, 1, true, true>();
     return type_id == 12u ? kq_kernel<12, 1, 2, 1, true>() : kq_kernel<14, 1, 2, 1, true>();
@@ -1172,6 +1174,9 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     uint32_t wgs4 = 0;
     for (uint32_t i = 0; i < jobs.n; i++) wgs4 += (jobs.j[i].rows + r4 - 1u) / r4;
     if (2u * wgs4 < static_cast<uint32_t>(device_cus())) ni = 2u;
+    // an output-sized launch (32000 rows: 1000 workgroups at four) takes
+    // eight, so the grid fits on the chip at once
+    if (wgs4 >= 3u * static_cast<uint32_t>(device_cus())) ni = 8u;
   }
   // RUSTICIDE_HIP_NORM_NI=2|4 forces the norm-fused one-token launches, for tuning
   if (const char* v = std::getenv("RUSTICIDE_HIP_NORM_NI"))

@@ -711,6 +711,7 @@ struct rh_decoder {
   float* hidden2 = nullptr;  // the residual's other buffer on the norm-fused path
   bool fuse_norm = false;    // one-token forwards fold each RMSNorm into the GEMV after it
   bool quant_norm = false;   // batches quantize the normed rows in the norm kernel
+  bool fuse_output_norm = false;  // one-token forwards fold the output norm into the output matrix's launch
   Q8Dev q8;                  // that activation, for up to `cap` tokens
   float *q = nullptr, *mixed = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
   float* logits = nullptr;
@@ -937,14 +938,24 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start)
     RHS(mm(d, d->hf, 1, f, {{b.down, d->delta, w}}));
     pending = d->delta;
   }
-  // the output norm stays a kernel of its own: the output matrix's launch has
-  // more workgroups than fit on the chip at once, and each would repeat the
-  // ordered sum
-  hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), add_norm_lds(w), s, h, pending, 1u,
-                     w, d->output_norm, c.rms_norm_eps, 0u, d->normed, Q8Dev{});
-  RHD(hipGetLastError());
+  // the output norm folds into the output matrix's launch as the layers'
+  // norms do (eight blocks per team keep that grid on the chip at once);
+  // an output matrix the norm-fused kernels cannot take keeps the separate
+  // norm kernel
   const rh_matrix* out = d->output ? d->output : d->token_embd;
-  RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
+  if (d->fuse_output_norm) {
+    NormIn fo{};
+    fo.delta = pending;
+    fo.weight = d->output_norm;
+    fo.eps = c.rms_norm_eps;
+    const rh_job lm{out, d->logits, c.vocab_size};
+    RHS(matmul_norm_device(d->ctx, h, fo, w, &lm, 1, s));
+  } else {
+    hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), add_norm_lds(w), s, h, pending, 1u,
+                       w, d->output_norm, c.rms_norm_eps, 0u, d->normed, Q8Dev{});
+    RHD(hipGetLastError());
+    RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
+  }
   d->cached = start + 1;
   return RH_OK;
 }
@@ -1108,6 +1119,8 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
   for (const rh_decoder::Block& b : d->blocks)
     for (const rh_matrix* m : {b.q, b.k, b.v, b.gate, b.up})
       quant = quant && is_kquant_matrix(m) && rh_matrix_cols(m) == w;
+  const rh_matrix* om = d->output ? d->output : d->token_embd;
+  d->fuse_output_norm = d->fuse_norm && fusable(om);
   const char* qenv = std::getenv("RUSTICIDE_HIP_NORM_QUANT");
   d->quant_norm = quant && !(qenv && qenv[0] == '0');
   *out = d;
