@@ -41,12 +41,9 @@ constexpr uint32_t kNormThreads = 256;
 
 
 // Token rows of token_embd into hidden (Matrix::copy_row, weights.rs:120-150).
-__global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint8_t* data, size_t stride,
-                                                    const uint32_t* tokens, uint32_t width, float* hidden) {
-  const uint32_t t = blockIdx.y;
-  const uint8_t* row = data + static_cast<size_t>(tokens[t]) * stride;
-  float* out = hidden + static_cast<size_t>(t) * width;
-  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < width; e += gridDim.x * 256u) {
+// Element e of a token_embd row (Matrix::copy_row's dequantization).
+__device__ __forceinline__ float embed_value(uint32_t type_id, const uint8_t* row, uint32_t e) {
+  {
     float v;
     if (type_id == 0u) {
       v = reinterpret_cast<const float*>(row)[e];
@@ -82,8 +79,17 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint
       const float ds = d * sc;
       v = ds * static_cast<float>(qv);
     }
-    out[e] = v;
+    return v;
   }
+}
+
+__global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint8_t* data, size_t stride,
+                                                    const uint32_t* tokens, uint32_t width, float* hidden) {
+  const uint32_t t = blockIdx.y;
+  const uint8_t* row = data + static_cast<size_t>(tokens[t]) * stride;
+  float* out = hidden + static_cast<size_t>(t) * width;
+  for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < width; e += gridDim.x * 256u)
+    out[e] = embed_value(type_id, row, e);
 }
 
 // hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t]),
@@ -589,12 +595,17 @@ __device__ __forceinline__ int32_t total_key(float f) {
 // maximum wins; out[0] = token, out[1] = 1 when some logit is finite. When
 // `tokens` is given the token is also appended at tokens[count[0]] (the
 // generation's record), count[0] advanced, and count[1] set for good once a
-// pick finds no finite logit.
+// pick finds no finite logit. When `hidden` is given, the picked token's
+// embedding row (emb_type blocks at emb_data, emb_stride bytes per row) is
+// written there: the next step's input.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint32_t n, uint32_t* out,
-                                                      uint32_t* tokens, uint32_t* count) {
+                                                      uint32_t* tokens, uint32_t* count, uint32_t emb_type,
+                                                      const uint8_t* emb_data, size_t emb_stride, uint32_t width,
+                                                      float* hidden) {
   __shared__ int32_t skey[16];
   __shared__ uint32_t sidx[16];
   __shared__ uint32_t sfin[16];
+  __shared__ uint32_t s_pick;
   int32_t best = INT32_MIN;
   uint32_t bi = 0, fin = 0;
   bool have = false;
@@ -658,7 +669,12 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint3
       count[0] = count[0] + 1u;
       if (!f) count[1] = 1u;
     }
+    s_pick = idx;
   }
+  if (!hidden) return;  // uniform
+  __syncthreads();
+  const uint8_t* row = emb_data + static_cast<size_t>(s_pick) * emb_stride;
+  for (uint32_t e = threadIdx.x; e < width; e += 1024u) hidden[e] = embed_value(emb_type, row, e);
 }
 
 // the float functions of the kernels above, one per element (test hook)
@@ -808,10 +824,12 @@ rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_
 // Decoder::forward_on_pool (decoder.rs:74-107) for n tokens whose ids are
 // in device memory at `tokens`, at positions start..start+n; leaves the last token's
 // logits in d->logits.
-rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start);
+rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start, bool embedded);
 
-rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t start) {
-  if (n == 1 && d->fuse_norm) return forward_one_fused(d, tokens, start);
+// `embedded`: a one-token forward on the norm-fused path whose embedding row
+// the greedy pick already wrote to hidden.
+rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t start, bool embedded = false) {
+  if (n == 1 && d->fuse_norm) return forward_one_fused(d, tokens, start, embedded);
   const rh_decoder_config& c = d->c;
   const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
   const uint32_t f = static_cast<uint32_t>(c.feed_forward_length), hd = static_cast<uint32_t>(c.head_dim);
@@ -879,15 +897,17 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
 // fused GEMV after them (NormIn): the residual h + delta is formed inside the
 // QKV and gate/up launches, the first workgroup of each writing it to the
 // other hidden buffer. Same arithmetic as the add_norm path, value for value.
-rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start) {
+rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start, bool embedded) {
   const rh_decoder_config& c = d->c;
   const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
   const uint32_t f = static_cast<uint32_t>(c.feed_forward_length), hd = static_cast<uint32_t>(c.head_dim);
   hipStream_t s = d->stream;
   const rh_matrix* E = d->token_embd;
-  hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, 1u), dim3(256), 0, s, rh_matrix_type(E),
-                     matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
-  RHD(hipGetLastError());
+  if (!embedded) {
+    hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, 1u), dim3(256), 0, s, rh_matrix_type(E),
+                       matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
+    RHD(hipGetLastError());
+  }
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
   float* h = d->hidden;
   float* h2 = d->hidden2;
@@ -1203,12 +1223,15 @@ rh_status rh_decoder_generate_greedy(rh_decoder* d, const uint32_t* prompt, size
   size_t position = n;
   size_t emitted = 0;
   for (size_t i = 0; i < max_tokens; i++) {
+    // on the norm-fused path the pick also writes the next step's embedding
+    const rh_matrix* E = d->token_embd;
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, d->logits, static_cast<uint32_t>(d->c.vocab_size),
-                       d->pick, d->record, d->count);
+                       d->pick, d->record, d->count, rh_matrix_type(E), matrix_data(E), matrix_stride(E),
+                       static_cast<uint32_t>(d->c.embedding_length), d->fuse_norm ? d->hidden : nullptr);
     RHD(hipGetLastError());
     emitted++;
     if (position == d->c.context_length) break;
-    RHS(forward_device(d, d->pick, 1, position));
+    RHS(forward_device(d, d->pick, 1, position, d->fuse_norm));
     position++;
   }
   uint32_t flag[2] = {0, 0};
