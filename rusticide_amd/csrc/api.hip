@@ -28,6 +28,9 @@ struct rh_ctx {
   void* buf[9] = {};
   size_t cap[9] = {};
   Q8Dev super_q, row_q;
+  // bumped whenever a scratch slot moves: graphs that captured the old
+  // addresses must not be replayed
+  uint64_t scratch_gen = 0;
   // pinned staging for matrix uploads, made on the first one
   uint8_t* stage[2] = {};
   hipEvent_t stage_done[2] = {};
@@ -113,6 +116,7 @@ rh_status ensure(rh_ctx* ctx, int i, size_t bytes) {
     ctx->cap[i] = 0;
   }
   size_t want = round_up(bytes < 4096 ? 4096 : bytes, 4096);
+  ctx->scratch_gen++;
   RH_HIP(ctx, hipMalloc(&ctx->buf[i], want));
   ctx->cap[i] = want;
   return RH_OK;
@@ -307,6 +311,7 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
 
 namespace rh {
 int ctx_device(const rh_ctx* ctx) { return ctx->device; }
+uint64_t ctx_scratch_generation(const rh_ctx* ctx) { return ctx->scratch_gen; }
 
 rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& norm, size_t width, const rh_job* jobs,
                              size_t n_jobs, hipStream_t s) {

@@ -128,6 +128,9 @@ namespace rh {
 
 // Internal views of the ABI's opaque handles (api.hip).
 int ctx_device(const rh_ctx* ctx);
+// Changes whenever the context's scratch buffers move (a graph that captured
+// their addresses is stale from then on).
+uint64_t ctx_scratch_generation(const rh_ctx* ctx);
 // Records `msg` as the context's rh_last_error and returns `st`.
 rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg);
 const uint8_t* matrix_data(const rh_matrix* m);

@@ -94,6 +94,39 @@ def test_small_decoder_greedy_generation_matches(ctx, norm_path):
     cpu.close()
 
 
+def test_batched_forward_graph_replays_match_the_eager_run(ctx, monkeypatch):
+    # with RUSTICIDE_HIP_GRAPHS=1 (read at creation) a decoder replays the
+    # graph it captured for a (tokens, start) batch; every replay, with eager
+    # work and synchronizations between replays, must give the bits of a
+    # decoder that launches one kernel at a time and of the CPU path
+    model = synth.decoder_model(SMALL, seed=15)
+    monkeypatch.setenv("RUSTICIDE_HIP_GRAPHS", "0")
+    eager = R.Decoder(ctx, model)
+    monkeypatch.setenv("RUSTICIDE_HIP_GRAPHS", "1")
+    graphed = R.Decoder(ctx, model)
+    monkeypatch.delenv("RUSTICIDE_HIP_GRAPHS")
+    cpu = O.Decoder(model, threads=8)
+    rng = np.random.default_rng(8)
+    for rep in range(5):
+        prompt = rng.integers(0, SMALL["vocab_size"], 70).astype(np.uint32)
+        graphed.reset()
+        eager.reset()
+        g = graphed.forward_batch(prompt[:64], 0)  # rep 0 captures, later reps replay
+        e = eager.forward_batch(prompt[:64], 0)
+        assert same_bits(g, e), f"replay {rep}: max |diff| {diff(g, e)}"
+        if rep in (0, 4):
+            cpu.reset()
+            assert same_bits(g, cpu.forward_batch(prompt[:64], 0))
+        # eager work between replays: a single token, then a ragged chunk
+        assert same_bits(graphed.forward(int(prompt[64]), 64), eager.forward(int(prompt[64]), 64))
+        assert same_bits(graphed.forward_batch(prompt[65:70], 65), eager.forward_batch(prompt[65:70], 65))
+        # generation replays the (64, 0) and (6, 64) prefill graphs
+        assert np.array_equal(graphed.generate_greedy(prompt, 6), eager.generate_greedy(prompt, 6))
+    graphed.close()
+    eager.close()
+    cpu.close()
+
+
 def test_decoder_errors_mirror_model_error(ctx):
     # decoder.rs:111-136, cache.rs:35-65, generate.rs:45-48
     model = synth.decoder_model(SMALL, seed=14)
