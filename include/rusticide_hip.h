@@ -303,11 +303,14 @@ size_t rh_gguf_metadata_count(const rh_gguf *g);
 size_t rh_gguf_tensor_count(const rh_gguf *g);
 /* tensor_names()[index] (sorted) and its TensorInfo:
  * the shape outermost first ([1] for a scalar; at most 4 dimensions), the
- * GGML type id and the offset in the data section. The name stays valid
- * until rh_gguf_free (gguf/tensor_info.rs:15-62). */
-rh_status rh_gguf_tensor_at(const rh_gguf *g, size_t index, const char **name, uint32_t *type_id,
-                            size_t *n_dims, uint64_t shape[4], uint64_t *offset);
-/* The index of a tensor name; RH_ERR_MISSING_TENSOR when absent. */
+ * GGML type id and the offset in the data section. The name (`*name_len`
+ * bytes, then a NUL) stays valid until rh_gguf_free
+ * (gguf/tensor_info.rs:15-62). Every out-pointer may be NULL. */
+rh_status rh_gguf_tensor_at(const rh_gguf *g, size_t index, const char **name, size_t *name_len,
+                            uint32_t *type_id, size_t *n_dims, uint64_t shape[4], uint64_t *offset);
+/* The index of a tensor name; RH_ERR_MISSING_TENSOR when absent. Names
+ * here and in rh_gguf_tensor_data are NUL-terminated: a tensor whose name
+ * holds a NUL byte is reachable by index only. */
 rh_status rh_gguf_tensor_find(const rh_gguf *g, const char *name, size_t *index);
 /* GgufFile::quantized_tensor / layout (gguf/load.rs:47-79): the tensor's bytes
  * inside the held file (blocks and any trailer; F32/F16 values), valid until

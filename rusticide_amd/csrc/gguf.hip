@@ -643,11 +643,12 @@ void rh_gguf_free(rh_gguf* g) { delete g; }
 size_t rh_gguf_metadata_count(const rh_gguf* g) { return g ? g->meta.size() : 0; }
 size_t rh_gguf_tensor_count(const rh_gguf* g) { return g ? g->tensors.size() : 0; }
 
-rh_status rh_gguf_tensor_at(const rh_gguf* g, size_t index, const char** name, uint32_t* type_id, size_t* n_dims,
-                            uint64_t shape[4], uint64_t* offset) {
+rh_status rh_gguf_tensor_at(const rh_gguf* g, size_t index, const char** name, size_t* name_len, uint32_t* type_id,
+                            size_t* n_dims, uint64_t shape[4], uint64_t* offset) {
   if (!g || index >= g->tensors.size()) return RH_ERR_INVALID_ARGUMENT;
   const TensorInfo& t = g->tensors[index];
   if (name) *name = t.name.c_str();
+  if (name_len) *name_len = t.name.size();
   if (type_id) *type_id = t.type_id;
   if (n_dims) *n_dims = t.shape.size();
   if (shape)

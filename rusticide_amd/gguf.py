@@ -197,7 +197,7 @@ def _gguf_lib() -> ctypes.CDLL:
         for n in ("rh_gguf_metadata_count", "rh_gguf_tensor_count"):
             getattr(L, n).argtypes = [P]
             getattr(L, n).restype = S
-        L.rh_gguf_tensor_at.argtypes = [P, S, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(U32),
+        L.rh_gguf_tensor_at.argtypes = [P, S, ctypes.POINTER(P), ctypes.POINTER(S), ctypes.POINTER(U32),
                                         ctypes.POINTER(S), ctypes.POINTER(U64), ctypes.POINTER(U64)]
         L.rh_gguf_tensor_at.restype = St
         L.rh_gguf_tensor_find.argtypes = [P, ctypes.c_char_p, ctypes.POINTER(S)]
@@ -290,13 +290,17 @@ class GgufFile:
         return _gguf_lib().rh_gguf_tensor_count(self._h())
 
     def _at(self, index: int):
-        name, t, n, off = ctypes.c_char_p(), ctypes.c_uint32(), ctypes.c_size_t(), ctypes.c_uint64()
+        name, nlen, t, n, off = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_uint32(), ctypes.c_size_t(), ctypes.c_uint64()
         shape = (ctypes.c_uint64 * 4)()
-        st = _gguf_lib().rh_gguf_tensor_at(self._h(), index, ctypes.byref(name), ctypes.byref(t), ctypes.byref(n),
-                                           shape, ctypes.byref(off))
+        st = _gguf_lib().rh_gguf_tensor_at(self._h(), index, ctypes.byref(name), ctypes.byref(nlen), ctypes.byref(t),
+                                           ctypes.byref(n), shape, ctypes.byref(off))
         if st != 0:
             raise IndexError(index)
-        return name.value.decode(), list(shape[: n.value]), t.value, off.value
+        return ctypes.string_at(name, nlen.value).decode(), list(shape[: n.value]), t.value, off.value
+
+    def tensor_info_at(self, index: int):
+        """(name, shape outermost first, type id, offset) of tensor_names()[index]."""
+        return self._at(index)
 
     def tensor_names(self) -> list:
         return [self._at(i)[0] for i in range(self.tensor_count)]
