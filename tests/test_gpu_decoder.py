@@ -1,7 +1,7 @@
 """The device decoder against the CPU restatement of rusticide's decoder.
 
-Bar: end-to-end greedy tokens from random-init models
-identical to the CPU path. The products are bit-identical by construction;
+Bar: end-to-end greedy tokens from random-init models identical to the CPU
+path. The products are bit-identical by construction;
 the f32 glue follows the reference's operation order, so logits are compared
 bit for bit as well, with the largest difference reported if they ever part.
 """

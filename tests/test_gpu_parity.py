@@ -1,9 +1,8 @@
 """GPU parity: the HIP path against the CPU oracle, through the C ABI.
 
-The bar: I2_S int32 accumulators bit-exact; k-quant f32
-outputs bit-identical to the CPU integer path (which is stricter than the
-stated 1e-4 relative tolerance); every token of a batch identical to a
-single-token call. Shapes include the benchmark workloads at full size.
+The bar: I2_S int32 accumulators bit-exact; k-quant f32 outputs
+bit-identical to the CPU integer path (stricter than a 1e-4 relative
+tolerance); every token of a batch identical to a single-token call. Shapes include the benchmark workloads at full size.
 """
 
 import os
