@@ -127,6 +127,22 @@ def test_batched_forward_graph_replays_match_the_eager_run(ctx, monkeypatch):
     cpu.close()
 
 
+@pytest.mark.parametrize("head_dim,heads,kv_heads,width", [(32, 8, 2, 256), (48, 16, 4, 768)])
+def test_head_dims_other_than_64_take_the_generic_attention(ctx, norm_path, head_dim, heads, kv_heads, width):
+    # attention_kernel<0> (any even head_dim up to 64) in the batched and the
+    # one-token forwards, against the CPU path
+    cfg = dict(SMALL, embedding_length=width, head_count=heads, head_count_kv=kv_heads, head_dim=head_dim)
+    model = synth.decoder_model(cfg, seed=head_dim)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
+    tokens = np.random.default_rng(head_dim).integers(0, cfg["vocab_size"], 70).astype(np.uint32)
+    for start, chunk in ((0, tokens[:64]), (64, tokens[64:69]), (69, tokens[69:70])):
+        g, c = gpu.forward_batch(chunk, start), cpu.forward_batch(chunk, start)
+        assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
+    assert np.array_equal(gpu.generate_greedy(tokens, 12), cpu.generate_greedy(tokens, 12))
+    gpu.close()
+    cpu.close()
+
+
 def test_decoder_errors_mirror_model_error(ctx):
     # decoder.rs:111-136, cache.rs:35-65, generate.rs:45-48
     model = synth.decoder_model(SMALL, seed=14)
