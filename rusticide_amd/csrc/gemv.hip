@@ -288,21 +288,36 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
 // once its CU's memory queue is full, which holds back the prologue (the
 // quantize, and the norm in the norm-fused kernels) and every dot behind it.
 template <int NI, bool NORM>
-constexpr int issue_ahead() { return NI < 2 ? NI : 2; }
+#ifndef RH_AHEAD_WIDE
+#define RH_AHEAD_WIDE 2
+#endif
+constexpr int issue_ahead() { return NI < 2 ? NI : (NI >= 8 && !NORM) ? RH_AHEAD_WIDE : 2; }
 
 // The rows of a k-quant workgroup. PAIR (a gate/up launch): the workgroup
 // takes nh rows of the job's w from row0 on as its rows 0..nh-1, and the
 // same rows of w2 as its rows nh..2nh-1.
 struct WgRows {
   uint32_t row0, nrows, nh;
+  uint32_t w, nwg, il;  // the workgroup, the job's workgroups, GemvJob::il
 };
 
 template <bool PAIR>
 __device__ __forceinline__ WgRows wg_rows(const GemvJob& J, uint32_t R) {
   const uint32_t per = PAIR ? R / 2u : R;
-  const uint32_t row0 = (blockIdx.x - J.wg_begin) * per;
+  const uint32_t w = blockIdx.x - J.wg_begin;
+  if (!PAIR && J.il) return WgRows{0u, per, per, w, J.rows / per, J.il};
+  const uint32_t row0 = w * per;
   const uint32_t nh = min(per, J.rows - row0);
-  return WgRows{row0, PAIR ? 2u * nh : nh, nh};
+  return WgRows{row0, PAIR ? 2u * nh : nh, nh, w, 0u, 0u};
+}
+
+// The matrix row of workgroup row r (not of a pair's second half).
+__device__ __forceinline__ uint32_t row_of(const WgRows& g, uint32_t r) {
+  if (g.il) {
+    const uint32_t s = g.il - 1u;
+    return ((__umul24(r >> s, g.nwg) + g.w) << s) | (r & ((1u << s) - 1u));
+  }
+  return g.row0 + r;
 }
 
 // Block b of workgroup row r (matrices stay below 4 GiB and 2^24 rows:
@@ -311,7 +326,7 @@ template <bool PAIR>
 __device__ __forceinline__ const uint8_t* block_at(const GemvJob& J, const WgRows& g, uint32_t r, uint32_t boff) {
   const bool second = PAIR && r >= g.nh;
   const uint8_t* m = second ? J.w2 : J.w;
-  const uint32_t row = g.row0 + (second ? r - g.nh : r);
+  const uint32_t row = PAIR ? g.row0 + (second ? r - g.nh : r) : row_of(g, r);
   return m + (__umul24(row, static_cast<uint32_t>(J.stride)) + boff);
 }
 
@@ -337,7 +352,7 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
       const uint32_t r = i / T, t = i - r * T;
       float s = -0.0f;
       for (uint32_t b = 0; b < nb; b++) s += terms[(__umul24(r, nbmax) + b) * T + t];
-      const size_t idx = static_cast<size_t>(g.row0 + r) * tokens + t0 + t;
+      const size_t idx = static_cast<size_t>(row_of(g, r)) * tokens + t0 + t;
       if (idx < J.out_len) J.out[idx] = s;
     }
   }
@@ -490,28 +505,29 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
   const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
   const uint32_t h = p >> 1, gq = p & 1u;
 
-  // Rows start 16-byte aligned, so block b sits (210*b) mod 4 = 2*(b & 1)
-  // bytes past a dword boundary: load aligned dwords, realign in registers.
-  // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; W: scales at
-  // 192; E: the fifth dwords of A, B, C and the dword holding d (q6_k.rs:13-43).
+  // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; S: the
+  // eight scales of half h at 192+8h; D: d at 208 (q6_k.rs:13-43). Blocks are
+  // 210 bytes, so every load but D's is only 2-byte aligned; each stays
+  // inside its block.
   const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
   if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
   NormRound<FQ ? FQ : 1> nr;
   if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
-  u32x4 A[NI], B[NI], C[NI], W[NI], E[NI];
+  u32x4 A[NI], B[NI], C[NI];
+  uint2 S[NI];
+  uint32_t D[NI];
   auto issue = [&](int i) {
     const uint32_t g = team + static_cast<uint32_t>(i) * (kThreads / 4u);
     const uint32_t gg = g < total ? g : 0u;
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
-    const uint8_t* base = block_at<PAIR>(J, wr, r, b * 210u - 2u * (b & 1u));
-    A[i] = load16_a4(base + 64u * h + 16u * gq);
-    B[i] = load16_a4(base + 64u * h + 32u + 16u * gq);
-    C[i] = load16_a4(base + 128u + 32u * h + 16u * gq);
-    W[i] = load16_a4(base + 192u);
-    E[i] = u32x4{load4(base + 64u * h + 16u * gq + 16u), load4(base + 64u * h + 48u + 16u * gq),
-                 load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
+    const uint8_t* base = block_at<PAIR>(J, wr, r, __umul24(b, 210u));
+    A[i] = load16_any(base + 64u * h + 16u * gq);
+    B[i] = load16_any(base + 64u * h + 32u + 16u * gq);
+    C[i] = load16_any(base + 128u + 32u * h + 16u * gq);
+    S[i] = load8_any(base + 192u + 8u * h);
+    D[i] = *reinterpret_cast<const uint16_t*>(base + 208u);
   };
   constexpr int ahead = issue_ahead<NI, NORM>();
 #pragma unroll
@@ -538,24 +554,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
     const uint32_t g = team + it * (kThreads / 4u);
     if (g >= total) break;  // uniform over the team
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
-    const uint32_t sh = 2u * (b & 1u);
-    const u32x4 a{__builtin_amdgcn_alignbyte(A[it].y, A[it].x, sh), __builtin_amdgcn_alignbyte(A[it].z, A[it].y, sh),
-                  __builtin_amdgcn_alignbyte(A[it].w, A[it].z, sh), __builtin_amdgcn_alignbyte(E[it].x, A[it].w, sh)};
-    const u32x4 bq{__builtin_amdgcn_alignbyte(B[it].y, B[it].x, sh), __builtin_amdgcn_alignbyte(B[it].z, B[it].y, sh),
-                   __builtin_amdgcn_alignbyte(B[it].w, B[it].z, sh), __builtin_amdgcn_alignbyte(E[it].y, B[it].w, sh)};
-    const u32x4 c{__builtin_amdgcn_alignbyte(C[it].y, C[it].x, sh), __builtin_amdgcn_alignbyte(C[it].z, C[it].y, sh),
-                  __builtin_amdgcn_alignbyte(C[it].w, C[it].z, sh), __builtin_amdgcn_alignbyte(E[it].z, C[it].w, sh)};
-    const uint32_t X0 = __builtin_amdgcn_alignbyte(W[it].y, W[it].x, sh);
-    const uint32_t X1 = __builtin_amdgcn_alignbyte(W[it].z, W[it].y, sh);
-    const uint32_t X2 = __builtin_amdgcn_alignbyte(W[it].w, W[it].z, sh);
-    const uint32_t X3 = __builtin_amdgcn_alignbyte(E[it].w, W[it].w, sh);
-    const uint32_t slo = h ? X2 : X0, shi = h ? X3 : X1;
+    const u32x4 a = A[it], bq = B[it], c = C[it];
+    const uint32_t slo = S[it].x, shi = S[it].y;
     // scale of run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
     const int32_t sc0 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq, 8);
     const int32_t sc1 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq + 16u, 8);
     const int32_t sc2 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq, 8);
     const int32_t sc3 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq + 16u, 8);
-    const float d = f16_lo(E[it].w >> (8u * sh));  // bytes 208..209
+    const float d = f16_lo(D[it]);  // bytes 208..209
     uint32_t q0[4], q1[4], q2[4], q3[4];
 #pragma unroll
     for (int k = 0; k < 4; k++) {
@@ -1013,6 +1019,12 @@ size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
 // launch: the smallest that lets every workgroup of the grid be resident at
 // once, so no rows wait for a second generation of workgroups.
 // RUSTICIDE_HIP_GEMV_NI=1|2|4|8 forces it, for tuning.
+// RUSTICIDE_HIP_GEMV_IL=0 keeps every workgroup's rows contiguous, for tuning.
+bool interleave_rows() {
+  const char* v = std::getenv("RUSTICIDE_HIP_GEMV_IL");
+  return !(v && v[0] == '0');
+}
+
 uint32_t forced_blocks_per_team() {
   if (const char* v = std::getenv("RUSTICIDE_HIP_GEMV_NI")) {
     if (v[0] == '1') return 1u;
@@ -1193,6 +1205,15 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     wgs += (jobs.j[i].rows + per - 1u) / per;
   }
   if (wgs == 0) return hipSuccess;
+  // one k-quant matrix whose rows tile a grid of at least one workgroup per
+  // CU exactly: interleave its workgroups over chunks of one iteration's rows
+  // (64 teams / nb blocks). Smaller grids measured no gain.
+  jobs.j[0].il = 0u;
+  if (kquant && jobs.n == 1u && !pair && nbl <= 64u && 64u % nbl == 0u && jobs.j[0].rows == wgs * per &&
+      wgs >= static_cast<uint32_t>(device_cus()) && interleave_rows()) {
+    const uint32_t c = 64u / nbl;
+    if (per % c == 0u) jobs.j[0].il = static_cast<uint32_t>(__builtin_ctz(c)) + 1u;
+  }
   if (type_id == 0u) {
     hipLaunchKernelGGL(gemv_dense_kernel<T>, dim3(wgs), dim3(kThreads), 0, s, jobs, x, width, R,
                        tokens, t0);

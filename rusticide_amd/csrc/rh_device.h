@@ -35,6 +35,20 @@ __device__ __forceinline__ uint32_t load4(const uint8_t* p) {
   return *reinterpret_cast<const uint32_t*>(p);
 }
 
+// 16 and 8 bytes at any byte address: the HSA ABI runs global memory in
+// unaligned-access mode, and LLVM lowers these to one global_load_dwordx4 /
+// global_load_dwordx2 each.
+__device__ __forceinline__ u32x4 load16_any(const uint8_t* p) {
+  u32x4 v;
+  __builtin_memcpy(&v, p, 16);
+  return v;
+}
+__device__ __forceinline__ uint2 load8_any(const uint8_t* p) {
+  uint2 v;
+  __builtin_memcpy(&v, p, 8);
+  return v;
+}
+
 // The 16 bytes at p, where p is only 2-byte aligned: five aligned dwords
 // funnel-shifted by (p & 3) bytes. Reads up to 4 bytes past p + 16.
 __device__ __forceinline__ u32x4 load16_unaligned(const uint8_t* p) {

@@ -46,6 +46,11 @@ struct GemvJob {
   // gate one): the norm-fused k-quant launch then writes silu(w x) * (w2 x)
   // to out instead of w x.
   const uint8_t* w2;
+  // 0: a workgroup's rows are contiguous. c > 0: iteration k of workgroup w
+  // takes the 2^(c-1)-row chunk k * nwg + w, so at any moment the grid reads
+  // one window of the matrix (the launcher sets it only when the rows tile
+  // the grid exactly).
+  uint32_t il = 0;
 };
 
 struct GemvJobs {

@@ -126,7 +126,26 @@ KQ_SHAPES = [
     (14, 45, 768, [1, 2, 9]),
     (12, 40, 25600, [1, 2]),    # 100 blocks per row: two blocks per team
     (14, 24, 38400, [1, 2]),    # 150 blocks per row: four blocks per team
+    (12, 16384, 2048, [1]),     # 512 workgroups of 32 rows: interleaved 8-row chunks
+    (14, 12800, 2048, [1]),     # 400 workgroups of 32 rows: interleaved 8-row chunks
 ]
+
+
+@pytest.mark.parametrize("type_id,rows,cols", [(12, 16384, 2048), (14, 32000, 2048)])
+def test_interleaved_rows_give_the_contiguous_bits(ctx, monkeypatch, type_id, rows, cols):
+    # a workgroup's rows as interleaved chunks (grids of a workgroup per CU
+    # or more) or as one contiguous run: the same outputs in the same rows
+    data = synth.matrix(type_id, rows, cols, seed=7 * rows + cols)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    x = synth.normal_f32(cols, seed=3)
+    outs = []
+    for il in ("1", "0"):
+        monkeypatch.setenv("RUSTICIDE_HIP_GEMV_IL", il)
+        out = np.full(rows, np.nan, np.float32)
+        R.matmul_batch(ctx, x, 1, [(m, out)])
+        outs.append(out)
+    assert_same_bits(outs[0], outs[1], f"type={type_id} {rows}x{cols}")
+    assert_same_bits(outs[0], oracle_matmul(type_id, data, rows, cols, x, 1), "oracle")
 
 
 @pytest.mark.parametrize("type_id,rows,cols,token_counts", KQ_SHAPES)
