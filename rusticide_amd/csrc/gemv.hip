@@ -288,10 +288,7 @@ __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int
 // once its CU's memory queue is full, which holds back the prologue (the
 // quantize, and the norm in the norm-fused kernels) and every dot behind it.
 template <int NI, bool NORM>
-#ifndef RH_AHEAD_WIDE
-#define RH_AHEAD_WIDE 2
-#endif
-constexpr int issue_ahead() { return NI < 2 ? NI : (NI >= 8 && !NORM) ? RH_AHEAD_WIDE : 2; }
+constexpr int issue_ahead() { return NI < 2 ? NI : 2; }
 
 // The rows of a k-quant workgroup. PAIR (a gate/up launch): the workgroup
 // takes nh rows of the job's w from row0 on as its rows 0..nh-1, and the
