@@ -256,7 +256,7 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (kind != RH_TYPE_F32 && m->nblocks < nb) nb = m->nblocks;
       GemvJob& j = g.j[g.n++];
       j.w = m->data;
-      j.stride = m->stride;
+      j.stride = static_cast<uint32_t>(m->stride);
       j.rows = static_cast<uint32_t>(rows);
       j.nb = static_cast<uint32_t>(nb);
       j.out = jobs[i].out;
@@ -330,7 +330,7 @@ rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& nor
       const size_t cover = width / 256;
       GemvJob& j = g.j[g.n++];
       j.w = m->data;
-      j.stride = m->stride;
+      j.stride = static_cast<uint32_t>(m->stride);
       j.rows = static_cast<uint32_t>(rows);
       j.nb = static_cast<uint32_t>(m->nblocks < cover ? m->nblocks : cover);
       j.out = jobs[i].out;
@@ -358,7 +358,7 @@ rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn
   GemvJob& j = g.j[g.n++];
   j.w = gate->data;
   j.w2 = up->data;
-  j.stride = gate->stride;
+  j.stride = static_cast<uint32_t>(gate->stride);
   j.rows = static_cast<uint32_t>(rows);
   j.nb = static_cast<uint32_t>(gate->nblocks);
   j.out = out;

@@ -295,26 +295,29 @@ constexpr int issue_ahead() { return NI < 2 ? NI : 2; }
 // same rows of w2 as its rows nh..2nh-1.
 struct WgRows {
   uint32_t row0, nrows, nh;
-  uint32_t w, nwg, il;  // the workgroup, the job's workgroups, GemvJob::il
+  // row_of's chunk map: row = ((r >> cs) * nwg + w) << cs | (r & mask).
+  // Contiguous rows are the case cs = 0, nwg = 1, w = row0, so the map has
+  // no branch (a branch between two blocks' loads makes the compiler wait
+  // for the first block's loads at the join).
+  uint32_t cs, nwg, w, mask;
 };
 
 template <bool PAIR>
 __device__ __forceinline__ WgRows wg_rows(const GemvJob& J, uint32_t R) {
   const uint32_t per = PAIR ? R / 2u : R;
   const uint32_t w = blockIdx.x - J.wg_begin;
-  if (!PAIR && J.il) return WgRows{0u, per, per, w, J.rows / per, J.il};
+  if (!PAIR && J.il) {
+    const uint32_t cs = J.il - 1u;
+    return WgRows{0u, per, per, cs, J.rows / per, w, (1u << cs) - 1u};
+  }
   const uint32_t row0 = w * per;
   const uint32_t nh = min(per, J.rows - row0);
-  return WgRows{row0, PAIR ? 2u * nh : nh, nh, w, 0u, 0u};
+  return WgRows{row0, PAIR ? 2u * nh : nh, nh, 0u, 1u, row0, 0u};
 }
 
 // The matrix row of workgroup row r (not of a pair's second half).
 __device__ __forceinline__ uint32_t row_of(const WgRows& g, uint32_t r) {
-  if (g.il) {
-    const uint32_t s = g.il - 1u;
-    return ((__umul24(r >> s, g.nwg) + g.w) << s) | (r & ((1u << s) - 1u));
-  }
-  return g.row0 + r;
+  return ((__umul24(r >> g.cs, g.nwg) + g.w) << g.cs) | (r & g.mask);
 }
 
 // Block b of workgroup row r (matrices stay below 4 GiB and 2^24 rows:

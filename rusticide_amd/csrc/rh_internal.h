@@ -35,23 +35,25 @@ struct Q8Dev {
 // One matrix of a grouped launch.
 struct GemvJob {
   const uint8_t* w;     // row-major native blocks (or f32 rows)
-  size_t stride;        // bytes between rows
-  uint32_t rows;        // rows to compute (already bounded by out_len)
-  uint32_t nb;          // blocks per row both operands cover
-  float* out;           // out[row * tokens + token]
-  size_t out_len;
-  float scale;          // I2_S tensor scale
-  uint32_t wg_begin;    // first workgroup of this job in the grid
   // A second matrix of w's shape and stride (the up projection beside the
   // gate one): the norm-fused k-quant launch then writes silu(w x) * (w2 x)
   // to out instead of w x.
   const uint8_t* w2;
+  float* out;           // out[row * tokens + token]
+  size_t out_len;
+  uint32_t stride;      // bytes between rows (a matrix stays below 4 GiB)
+  uint32_t rows;        // rows to compute (already bounded by out_len)
+  uint32_t nb;          // blocks per row both operands cover
+  float scale;          // I2_S tensor scale
+  uint32_t wg_begin;    // first workgroup of this job in the grid
   // 0: a workgroup's rows are contiguous. c > 0: iteration k of workgroup w
   // takes the 2^(c-1)-row chunk k * nwg + w, so at any moment the grid reads
   // one window of the matrix (the launcher sets it only when the rows tile
   // the grid exactly).
   uint32_t il = 0;
 };
+// 56 bytes: every launch's kernel arguments hold kMaxJobs of these
+static_assert(sizeof(GemvJob) == 56, "GemvJob packs into 56 bytes");
 
 struct GemvJobs {
   GemvJob j[kMaxJobs];
