@@ -183,6 +183,17 @@ rh_status rh_math_device(rh_ctx *ctx, uint32_t op, const float *a, const float *
 enum { RH_STREAM_READ_SINK_WORDS = 2048 };
 rh_status rh_stream_read_device(rh_ctx *ctx, const void *const *buffers, size_t n_buffers, size_t bytes,
                                 size_t launches, uint32_t *sink);
+/* Bench hook with no reference counterpart: `launches` calls of
+ * rh_matmul_batch_device(ctx, inputs, inputs_len, tokens, {matrices[i %
+ * n_matrices], out, out_len}, 1, stream), queued from C so that the host's
+ * per-call cost does not pace launches shorter than it. */
+rh_status rh_matmul_batch_device_repeat(rh_ctx *ctx, const float *inputs, size_t inputs_len, size_t tokens,
+                                        const rh_matrix *const *matrices, size_t n_matrices, float *out,
+                                        size_t out_len, size_t launches, void *stream);
+/* Tuning hook with no reference counterpart: re-reads the RUSTICIDE_HIP_*
+ * kernel switches from the environment (rh_init reads them once). Every
+ * switch gives the same bits; they select among equivalent kernels. */
+void rh_reload_tuning(void);
 /* Test hook with no reference counterpart: the ordered float sum the decoder
  * kernels form for RMSNorm, ((init + values[0]) + values[1]) + ... one IEEE
  * add at a time (the f32 `Sum` fold of

@@ -103,6 +103,10 @@ def lib() -> ctypes.CDLL:
         L.rh_dot_matrix_device.restype = St
         L.rh_gemm_min_tokens.restype = S
         L.rh_set_gemm_min_tokens.argtypes = [S]
+        L.rh_matmul_batch_device_repeat.argtypes = [P, P, S, S, P, S, P, S, S, P]
+        L.rh_matmul_batch_device_repeat.restype = St
+        L.rh_reload_tuning.argtypes = []
+        L.rh_reload_tuning.restype = None
         _lib = L
     return _lib
 
@@ -286,6 +290,21 @@ def matmul_batch_device(ctx: Context, inputs, tokens: int, jobs, stream: int = 0
     """Device-resident form: `inputs` and outputs are torch device tensors."""
     ctx.check(lib().rh_matmul_batch_device(ctx.handle, _ptr(inputs), inputs.numel(), tokens, _jobs(jobs),
                                            len(jobs), stream or None))
+
+
+def matmul_batch_device_repeat(ctx: Context, inputs, tokens: int, matrices, out, launches: int,
+                               stream: int = 0) -> None:
+    """`launches` rh_matmul_batch_device calls queued from C, call i on
+    matrices[i % len(matrices)] (a bench hook)."""
+    arr = (ctypes.c_void_p * len(matrices))(*[ctypes.cast(m.handle, ctypes.c_void_p).value for m in matrices])
+    ctx.check(lib().rh_matmul_batch_device_repeat(ctx.handle, _ptr(inputs), inputs.numel(), tokens, arr,
+                                                  len(matrices), _ptr(out), out.numel(), launches,
+                                                  stream or None))
+
+
+def reload_tuning() -> None:
+    """Re-read the RUSTICIDE_HIP_* kernel switches (rh_init reads them once)."""
+    lib().rh_reload_tuning()
 
 
 # ------------------------------------------------------------------ decoder

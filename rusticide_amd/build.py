@@ -16,7 +16,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "librusticide_hip.so")
-SOURCES = ["api.hip", "quantize.hip", "gemv.hip", "gemv_stream.hip", "gemv_kq.hip", "gemm.hip", "gemm_i2s.hip", "model.hip", "stream_read.hip", "gguf.hip"]
+SOURCES = ["api.hip", "quantize.hip", "gemv.hip", "gemm.hip", "gemm_i2s.hip", "model.hip", "stream_read.hip", "gguf.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -85,21 +85,13 @@ rh_status hip_fail(rh_ctx* ctx, hipError_t e, const char* what) {
 
 size_t round_up(size_t v, size_t m) { return (v + m - 1) / m * m; }
 
-// Which GEMV kernel family serves a format. The default, kFused, is one
-// launch per format in which every workgroup quantizes the activation itself
-// (decode-sized batches; larger ones fall back to a quantize launch plus the
-// LDS-staged kernels). RUSTICIDE_HIP_GEMV=kq|stream|lds forces a family that
-// reads a separately quantized activation. All give the same bits; the switch
-// exists to test and time one against another.
-enum class Family { kFused, kPersistent, kStream, kLds };
+// Which GEMV kernel family serves a format (Tuning::gemv). The default is
+// one launch per format in which the kernels quantize the activation
+// themselves (decode-sized batches; larger ones fall back to a quantize
+// launch plus kernels that read its result, the kLds family).
+enum class Family { kFused, kLds };
 
-Family family(uint32_t type_id) {
-  const char* v = std::getenv("RUSTICIDE_HIP_GEMV");
-  if (v && std::strcmp(v, "lds") == 0) return Family::kLds;
-  if (v && std::strcmp(v, "stream") == 0) return Family::kStream;
-  if (v && std::strcmp(v, "kq") == 0 && type_id != RH_TYPE_I2_S) return Family::kPersistent;
-  return Family::kFused;
-}
+Family family() { return tuning().gemv == 1 ? Family::kLds : Family::kFused; }
 
 unsigned format_bit(uint32_t type_id) {
   return type_id == RH_TYPE_Q4_K ? 1u : type_id == RH_TYPE_Q6_K ? 2u : type_id == RH_TYPE_I2_S ? 4u : 0u;
@@ -212,29 +204,6 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
         nbmax = 0;
         return RH_OK;
       }
-      const Family fam = kind == RH_TYPE_F32 ? Family::kLds : family(kind);
-      if (fam == Family::kStream && tokens <= 2) {
-        hipError_t e = hipSuccess;
-        if (launch_gemv_stream(kind, g, q, tokens, 0, tokens, s, raw, &e)) {
-          RH_HIP(ctx, e);
-          g = GemvJobs{};
-          nbmax = 0;
-          return RH_OK;
-        }
-      }
-      if (fam == Family::kPersistent) {
-        const uint32_t nbl = nbmax ? nbmax : 1u;
-        const size_t tk = gemv_kq_max_tokens(nbl);
-        if (tk) {
-          for (size_t t0 = 0; t0 < tokens; t0 += tk) {
-            const size_t tn = tokens - t0 < tk ? tokens - t0 : tk;
-            RH_HIP(ctx, launch_gemv_kq(kind, g, q, nbl, tokens, t0, tn, s));
-          }
-          g = GemvJobs{};
-          nbmax = 0;
-          return RH_OK;
-        }
-      }
       for (size_t t0 = 0; t0 < tokens; t0 += tmax) {
         size_t tn = tokens - t0 < tmax ? tokens - t0 : tmax;
         RH_HIP(ctx, launch_gemv(kind, g, q, d_in, width, tokens, t0, tn, s, raw));
@@ -293,7 +262,7 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
   for (int k = 0; k < 3; k++) {
     const uint32_t kind = kinds[k];
     const unsigned bit = format_bit(kind);
-    if (!(present & bit) || family(kind) != Family::kFused || !gemv_fused_ok(kind, width, tokens)) continue;
+    if (!(present & bit) || family() != Family::kFused || !gemv_fused_ok(kind, width, tokens)) continue;
     if (kind != RH_TYPE_I2_S && tokens >= g_gemm_min_tokens) continue;
     if (tokens > gemv_max_tokens(kind, nbmax[bit >> 1])) continue;
     fused |= bit;
@@ -310,6 +279,36 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
 }  // namespace
 
 namespace rh {
+
+namespace {
+Tuning g_tuning;
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+}  // namespace
+
+const Tuning& tuning() { return g_tuning; }
+
+void load_tuning() {
+  Tuning t;
+  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMV")) {
+    if (std::strcmp(v, "lds") == 0) t.gemv = 1;
+  }
+  const int ni = env_int("RUSTICIDE_HIP_GEMV_NI", 0);
+  t.gemv_ni = ni == 1 || ni == 2 || ni == 4 || ni == 8 ? ni : 0;
+  t.interleave = env_int("RUSTICIDE_HIP_GEMV_IL", 1) != 0;
+  const int nni = env_int("RUSTICIDE_HIP_NORM_NI", 0);
+  t.norm_ni = nni == 2 || nni == 4 ? nni : 0;
+  const int gr = env_int("RUSTICIDE_HIP_I2S_GROUPS", 0);
+  t.i2s_groups = gr == 1 || gr == 2 || gr == 4 ? gr : 0;
+  const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
+  t.gemm_bn = bn == 64 || bn == 128 ? bn : 0;
+  t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;
+  g_tuning = t;
+}
+
 int ctx_device(const rh_ctx* ctx) { return ctx->device; }
 uint64_t ctx_scratch_generation(const rh_ctx* ctx) { return ctx->scratch_gen; }
 
@@ -429,6 +428,11 @@ rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
     m->row_bytes = cols * 4;
     m->stride = m->row_bytes;
     m->nblocks = cols;
+    // the GEMV jobs carry a row count and a row stride in 32 bits
+    if (rows > size_t{0xffffffffu} || m->stride > size_t{0xffffffffu}) {
+      delete m;
+      return fail(ctx, RH_ERR_SHAPE_MISMATCH, "dense matrix exceeds 2^32 rows or 4 GiB per row");
+    }
   } else if (geometry(type_id, &bs, &bb)) {
     if (cols % bs != 0) {
       delete m;
@@ -606,6 +610,8 @@ extern "C" {
 
 const char* rh_adapter_name(void) { return "hip-gfx950"; }
 
+void rh_reload_tuning(void) { load_tuning(); }
+
 rh_status rh_init(int device, rh_ctx** out) {
   if (!out) return RH_ERR_INVALID_ARGUMENT;
   *out = nullptr;
@@ -616,6 +622,7 @@ rh_status rh_init(int device, rh_ctx** out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RH_ERR_NO_DEVICE;
   rh_ctx* ctx = new (std::nothrow) rh_ctx();
   if (!ctx) return RH_ERR_OUT_OF_MEMORY;
+  load_tuning();
   ctx->device = device;
   if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
     delete ctx;
@@ -723,6 +730,18 @@ rh_status rh_matmul_batch_device(rh_ctx* ctx, const float* inputs, size_t inputs
   RH_HIP(ctx, hipSetDevice(ctx->device));
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
   return run_batch(ctx, inputs, inputs_len, tokens, jobs, n_jobs, s, nullptr);
+}
+
+rh_status rh_matmul_batch_device_repeat(rh_ctx* ctx, const float* inputs, size_t inputs_len, size_t tokens,
+                                        const rh_matrix* const* matrices, size_t n_matrices, float* out,
+                                        size_t out_len, size_t launches, void* stream) {
+  if (!ctx || (!matrices && launches) || (n_matrices == 0 && launches)) return RH_ERR_INVALID_ARGUMENT;
+  for (size_t i = 0; i < launches; i++) {
+    const rh_job job{matrices[i % n_matrices], out, out_len};
+    const rh_status st = rh_matmul_batch_device(ctx, inputs, inputs_len, tokens, &job, 1, stream);
+    if (st != RH_OK) return st;
+  }
+  return RH_OK;
 }
 
 rh_status rh_matmul_batch(rh_ctx* ctx, const float* inputs, size_t inputs_len, size_t tokens,

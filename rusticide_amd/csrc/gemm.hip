@@ -435,10 +435,9 @@ __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const 
 }
 
 int token_tile(size_t tokens) {
-  // RUSTICIDE_HIP_GEMM_BN=64|128 forces the token tile, for tuning
-  int bn = tokens >= 512 ? 128 : 64;
-  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMM_BN")) bn = v[0] == '1' ? 128 : 64;
-  return bn;
+  // Tuning::gemm_bn forces the token tile, for tuning
+  if (const int bn = tuning().gemm_bn) return bn;
+  return tokens >= 512 ? 128 : 64;
 }
 
 // Workgroups along rows, with each job's first one recorded in wg_begin.
@@ -457,7 +456,7 @@ struct SplitPlan {
 
 // Splits K when the launch has fewer than kSplitBelow workgroups, aiming at
 // kSplitTarget; every job must have the same block count. Below 2 blocks, or
-// with RUSTICIDE_HIP_GEMM_SPLIT=0, nothing is split.
+// with Tuning::gemm_split off, nothing is split.
 constexpr uint32_t kSplitBelow = 128, kSplitTarget = 512;
 
 SplitPlan plan_split(GemvJobs jobs, size_t tokens) {
@@ -467,8 +466,7 @@ SplitPlan plan_split(GemvJobs jobs, size_t tokens) {
   const uint32_t nb = jobs.j[0].nb;
   for (uint32_t i = 1; i < jobs.n; i++)
     if (jobs.j[i].nb != nb) return p;
-  const char* env = std::getenv("RUSTICIDE_HIP_GEMM_SPLIT");
-  if (env && env[0] == '0') return p;
+  if (!tuning().gemm_split) return p;
   const size_t tiles = (tokens + token_tile(tokens) - 1) / token_tile(tokens);
   const size_t base = static_cast<size_t>(wgs) * tiles;
   if (nb < 2 || base >= kSplitBelow) return p;

@@ -15,8 +15,6 @@
 //
 // I2_S: a team of 8 lanes walks a row 16 bytes at a time; the i32 dot is
 // order-free (wrapping) and is scaled once per row, as portable/ternary.rs:48-58.
-#include <cstdlib>
-
 #include "rh_device.h"
 #include "rh_internal.h"
 #include "rh_math.h"
@@ -1018,22 +1016,11 @@ size_t lds_bytes(uint32_t type_id, uint32_t nbmax, uint32_t R) {
 // Blocks per 4-lane team in the k-quant kernels (1, 2 or 4), chosen per
 // launch: the smallest that lets every workgroup of the grid be resident at
 // once, so no rows wait for a second generation of workgroups.
-// RUSTICIDE_HIP_GEMV_NI=1|2|4|8 forces it, for tuning.
-// RUSTICIDE_HIP_GEMV_IL=0 keeps every workgroup's rows contiguous, for tuning.
-bool interleave_rows() {
-  const char* v = std::getenv("RUSTICIDE_HIP_GEMV_IL");
-  return !(v && v[0] == '0');
-}
+// Tuning::gemv_ni forces it and Tuning::interleave = false keeps every
+// workgroup's rows contiguous, for tuning.
+bool interleave_rows() { return tuning().interleave; }
 
-uint32_t forced_blocks_per_team() {
-  if (const char* v = std::getenv("RUSTICIDE_HIP_GEMV_NI")) {
-    if (v[0] == '1') return 1u;
-    if (v[0] == '2') return 2u;
-    if (v[0] == '4') return 4u;
-    if (v[0] == '8') return 8u;
-  }
-  return 0u;
-}
+uint32_t forced_blocks_per_team() { return static_cast<uint32_t>(tuning().gemv_ni); }
 
 // Rows per workgroup: one per 8-lane team for I2_S and dense rows; for the
 // k-quants, whole rows of nb blocks over 64 teams of ni blocks each.
@@ -1190,9 +1177,9 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // eight, so the grid fits on the chip at once
     if (wgs4 >= 3u * static_cast<uint32_t>(device_cus())) ni = 8u;
   }
-  // RUSTICIDE_HIP_NORM_NI=2|4 forces the norm-fused one-token launches, for tuning
-  if (const char* v = std::getenv("RUSTICIDE_HIP_NORM_NI"))
-    if (norm && T == 1 && fq == 1u && min_blocks_per_team(nbl) <= 2u) ni = v[0] == '2' ? 2u : 4u;
+  // Tuning::norm_ni forces the norm-fused one-token launches, for tuning
+  if (const int v = tuning().norm_ni)
+    if (norm && T == 1 && fq == 1u && min_blocks_per_team(nbl) <= 2u) ni = static_cast<uint32_t>(v);
   const uint32_t R = rows_per_wg(type_id, nbl, ni);
   // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
   const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
@@ -1309,7 +1296,7 @@ hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t 
   const uint32_t R = kThreads / lpr;
   // G row groups per workgroup: the most that still leave at least
   // kI2sMinWgs workgroups (each repeats the activation's quantization);
-  // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 forces it, for tuning
+  // Tuning::i2s_groups forces it, for tuning
   auto count = [&](uint32_t g) {
     uint32_t n = 0;
     for (uint32_t i = 0; i < jobs.n; i++) n += (jobs.j[i].rows + R * g - 1u) / (R * g);
@@ -1317,7 +1304,7 @@ hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t 
   };
   uint32_t G = 1;
   while (G < 4u && count(2u * G) >= kI2sMinWgs) G *= 2u;
-  if (const char* v = std::getenv("RUSTICIDE_HIP_I2S_GROUPS")) G = v[0] == '4' ? 4u : v[0] == '2' ? 2u : 1u;
+  if (const int v = tuning().i2s_groups) G = static_cast<uint32_t>(v);
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     jobs.j[i].wg_begin = wgs;

@@ -762,8 +762,16 @@ hipError_t dmalloc(T** p, size_t n) {
   return hipMalloc(reinterpret_cast<void**>(p), (n ? n : 1) * sizeof(T));
 }
 
+// Destroys a graph exec once no replay of it can still be queued: work on
+// the decoder's stream (a replay launched earlier in the same call) drains
+// first.
+void destroy_exec(rh_decoder* d, hipGraphExec_t exec) {
+  hipStreamSynchronize(d->stream);
+  hipGraphExecDestroy(exec);
+}
+
 void drop_graphs(rh_decoder* d) {
-  for (rh_decoder::Graph& g : d->graphs) hipGraphExecDestroy(g.exec);
+  for (rh_decoder::Graph& g : d->graphs) destroy_exec(d, g.exec);
   d->graphs.clear();
 }
 
@@ -1216,7 +1224,7 @@ rh_status forward_cached(rh_decoder* d, size_t n, size_t start) {
       d->cached = start + n;
       return RH_OK;
     }
-    hipGraphExecDestroy(g.exec);
+    destroy_exec(d, g.exec);
     d->graphs.erase(d->graphs.begin() + static_cast<std::ptrdiff_t>(i));
     break;
   }
@@ -1244,7 +1252,7 @@ rh_status forward_cached(rh_decoder* d, size_t n, size_t start) {
     size_t lru = 0;
     for (size_t i = 1; i < d->graphs.size(); i++)
       if (d->graphs[i].used < d->graphs[lru].used) lru = i;
-    hipGraphExecDestroy(d->graphs[lru].exec);
+    destroy_exec(d, d->graphs[lru].exec);
     d->graphs.erase(d->graphs.begin() + static_cast<std::ptrdiff_t>(lru));
   }
   d->graphs.push_back(rh_decoder::Graph{n, start, cg2, ag, ++d->graph_clock, exec});

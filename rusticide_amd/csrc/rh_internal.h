@@ -73,6 +73,24 @@ struct NormIn {
   uint32_t lds_offset = 0;  // filled by the launcher
 };
 
+// Kernel choices, read from the environment by rh_init (and
+// rh_reload_tuning) instead of on every launch. Every choice gives the same
+// bits; the switches exist to test and time one kernel against another.
+struct Tuning {
+  // RUSTICIDE_HIP_GEMV: 0 the quantize-fused decode kernels (decode-sized
+  // batches), 1 "lds" (a quantize launch, then kernels that read the
+  // quantized activation)
+  int gemv = 0;
+  int gemv_ni = 0;         // RUSTICIDE_HIP_GEMV_NI=1|2|4|8: blocks per team
+  bool interleave = true;  // RUSTICIDE_HIP_GEMV_IL=0: contiguous rows
+  int norm_ni = 0;         // RUSTICIDE_HIP_NORM_NI=2|4
+  int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4
+  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=64|128
+  bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
+};
+const Tuning& tuning();
+void load_tuning();
+
 // Launchers (stream-ordered; they return the launch status).
 hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, const Q8Dev& q,
                                  hipStream_t s);
@@ -95,17 +113,6 @@ hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float
                              size_t tokens, size_t t0, size_t tn, hipStream_t s, int32_t* raw,
                              const NormIn* norm = nullptr);
 bool norm_fusable(uint32_t type_id, size_t width, uint32_t nbmax);
-// Streaming decode GEMV for one or two tokens; false when the launch's shape
-// is outside what it handles (the caller then uses launch_gemv).
-bool launch_gemv_stream(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0,
-                        size_t tn, hipStream_t s, int32_t* raw, hipError_t* err);
-
-// Persistent k-quant GEMV (Q4_K, Q6_K) for up to gemv_kq_max_tokens tokens
-// per launch (0: the rows are too wide for it).
-size_t gemv_kq_max_tokens(uint32_t nb);
-hipError_t launch_gemv_kq(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, uint32_t nbmax, size_t tokens,
-                          size_t t0, size_t tn, hipStream_t s);
-
 // Prefill GEMM on MFMA for the k-quants (Q4_K, Q6_K): every row of every job
 // against all `tokens` tokens of the quantized activation q, bit-identical to
 // the GEMV kernels (and so to the CPU path).

@@ -127,6 +127,28 @@ def test_batched_forward_graph_replays_match_the_eager_run(ctx, monkeypatch):
     cpu.close()
 
 
+def test_graph_cache_evicts_within_one_generate_call(ctx, monkeypatch):
+    # the decoder keeps 8 graphs. A first call caches the 8 prefill chunks of
+    # a 512-token prompt; a second call on a 583-token prompt replays those 8
+    # (queued on the stream) and then captures two more chunks, evicting
+    # graphs it replayed earlier in the same call. Every pick must equal the
+    # eager decoder's.
+    cfg = dict(SMALL, context_length=640)
+    model = synth.decoder_model(cfg, seed=21)
+    monkeypatch.setenv("RUSTICIDE_HIP_GRAPHS", "0")
+    eager = R.Decoder(ctx, model)
+    monkeypatch.setenv("RUSTICIDE_HIP_GRAPHS", "1")
+    graphed = R.Decoder(ctx, model)
+    monkeypatch.delenv("RUSTICIDE_HIP_GRAPHS")
+    rng = np.random.default_rng(21)
+    prompt = rng.integers(0, cfg["vocab_size"], 64 * 9 + 7).astype(np.uint32)
+    for n in (512, 64 * 9 + 7, 512, 64 * 9 + 7):
+        want = eager.generate_greedy(prompt[:n], 8)
+        assert np.array_equal(graphed.generate_greedy(prompt[:n], 8), want), f"prompt of {n}"
+    graphed.close()
+    eager.close()
+
+
 @pytest.mark.parametrize("head_dim,heads,kv_heads,width", [(32, 8, 2, 256), (48, 16, 4, 768)])
 def test_head_dims_other_than_64_take_the_generic_attention(ctx, norm_path, head_dim, heads, kv_heads, width):
     # attention_kernel<0> (any even head_dim up to 64) in the batched and the

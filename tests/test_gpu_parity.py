@@ -24,22 +24,45 @@ def ctx():
     c.close()
 
 
-@pytest.fixture(params=["auto", "kq", "stream", "lds-1", "lds-2", "lds-4"])
+VARIANTS = {
+    # the default: the quantize-fused kernels for decode-sized batches
+    "auto": {},
+    # a quantize launch, then the kernels reading its result, at 1, 2 and 4
+    # blocks per team
+    "lds-1": {"RUSTICIDE_HIP_GEMV": "lds", "RUSTICIDE_HIP_GEMV_NI": "1"},
+    "lds-2": {"RUSTICIDE_HIP_GEMV": "lds", "RUSTICIDE_HIP_GEMV_NI": "2"},
+    "lds-4": {"RUSTICIDE_HIP_GEMV": "lds", "RUSTICIDE_HIP_GEMV_NI": "4"},
+}
+SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI")
+
+
+@pytest.fixture(params=list(VARIANTS))
 def variant(request):
     """Every decode GEMV kernel variant must give the CPU path's bits."""
-    family, _, ni = request.param.partition("-")
-    saved = {k: os.environ.get(k) for k in ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI")}
-    os.environ["RUSTICIDE_HIP_GEMV"] = family
-    if ni:
-        os.environ["RUSTICIDE_HIP_GEMV_NI"] = ni
-    else:
-        os.environ.pop("RUSTICIDE_HIP_GEMV_NI", None)
+    saved = {k: os.environ.get(k) for k in SWITCHES}
+    for k in SWITCHES:
+        os.environ.pop(k, None)
+    os.environ.update(VARIANTS[request.param])
+    R.reload_tuning()
     yield request.param
     for k, v in saved.items():
         if v is None:
             os.environ.pop(k, None)
         else:
             os.environ[k] = v
+    R.reload_tuning()
+
+
+@pytest.fixture
+def tuning(monkeypatch):
+    """monkeypatch.setenv for the kernel switches, re-read by the library."""
+    class Env:
+        def set(self, name, value):
+            monkeypatch.setenv(name, value)
+            R.reload_tuning()
+    yield Env()
+    monkeypatch.undo()
+    R.reload_tuning()
 
 
 def bits(a):
@@ -132,7 +155,7 @@ KQ_SHAPES = [
 
 
 @pytest.mark.parametrize("type_id,rows,cols", [(12, 16384, 2048), (14, 32000, 2048)])
-def test_interleaved_rows_give_the_contiguous_bits(ctx, monkeypatch, type_id, rows, cols):
+def test_interleaved_rows_give_the_contiguous_bits(ctx, tuning, type_id, rows, cols):
     # a workgroup's rows as interleaved chunks (grids of a workgroup per CU
     # or more) or as one contiguous run: the same outputs in the same rows
     data = synth.matrix(type_id, rows, cols, seed=7 * rows + cols)
@@ -140,7 +163,7 @@ def test_interleaved_rows_give_the_contiguous_bits(ctx, monkeypatch, type_id, ro
     x = synth.normal_f32(cols, seed=3)
     outs = []
     for il in ("1", "0"):
-        monkeypatch.setenv("RUSTICIDE_HIP_GEMV_IL", il)
+        tuning.set("RUSTICIDE_HIP_GEMV_IL", il)
         out = np.full(rows, np.nan, np.float32)
         R.matmul_batch(ctx, x, 1, [(m, out)])
         outs.append(out)
@@ -222,7 +245,7 @@ def test_prefill_gemm_is_bit_identical_to_the_cpu_path(ctx, type_id, rows, cols,
 @pytest.mark.parametrize("type_id,rows,cols,tokens", [(12, 2048, 2048, 64), (14, 2048, 5632, 64),
                                                        (12, 2560, 2048, 64), (12, 6400, 2304, 64),
                                                        (14, 45, 768, 9), (12, 300, 25600, 33)])
-def test_split_k_gives_the_unsplit_bits(ctx, monkeypatch, type_id, rows, cols, tokens):
+def test_split_k_gives_the_unsplit_bits(ctx, tuning, type_id, rows, cols, tokens):
     # a launch with too few row and token tiles to fill the chip splits K
     # across workgroups and adds the later blocks' terms in block order
     # afterwards; RUSTICIDE_HIP_GEMM_SPLIT=0 keeps every block in one workgroup
@@ -231,7 +254,7 @@ def test_split_k_gives_the_unsplit_bits(ctx, monkeypatch, type_id, rows, cols, t
     x = synth.normal_f32(tokens * cols, seed=7 + tokens)
     split = np.full(rows * tokens, np.nan, np.float32)
     R.matmul_batch(ctx, x, tokens, [(m, split)])
-    monkeypatch.setenv("RUSTICIDE_HIP_GEMM_SPLIT", "0")
+    tuning.set("RUSTICIDE_HIP_GEMM_SPLIT", "0")
     whole = np.full(rows * tokens, np.nan, np.float32)
     R.matmul_batch(ctx, x, tokens, [(m, whole)])
     assert_same_bits(split, whole, f"type={type_id} {rows}x{cols} tokens={tokens}")
@@ -333,10 +356,10 @@ def test_i2s_i32_accumulators_are_bit_exact(ctx, variant, rows, cols, token_coun
 
 
 @pytest.mark.parametrize("groups", ["1", "2", "4"])
-def test_i2s_row_groups_per_workgroup(ctx, monkeypatch, groups):
+def test_i2s_row_groups_per_workgroup(ctx, tuning, groups):
     # RUSTICIDE_HIP_I2S_GROUPS: one activation quantization per workgroup
     # serves 1, 2 or 4 groups of rows; ragged row counts leave groups empty
-    monkeypatch.setenv("RUSTICIDE_HIP_I2S_GROUPS", groups)
+    tuning.set("RUSTICIDE_HIP_I2S_GROUPS", groups)
     for rows, cols in ((6912, 2560), (2560, 6912), (37, 384), (300, 1024)):
         data = synth.i2s_matrix(rows, cols, seed=rows + 1)
         m = R.Matrix.load(ctx, 36, data, rows, cols)
