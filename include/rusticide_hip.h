@@ -119,6 +119,20 @@ rh_status rh_matvec_batch(rh_ctx *ctx, const float *input, size_t len, const rh_
  * context's stream) and the call returns without waiting. */
 rh_status rh_matmul_batch_device(rh_ctx *ctx, const float *inputs, size_t inputs_len,
                                  size_t tokens, const rh_job *jobs, size_t n_jobs, void *stream);
+/* No counterpart in the reference: rh_matmul_batch_device for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). It computes the same outputs,
+ * bit for bit, and allocates nothing: the batch's quantized activations go
+ * to a file-scope array of RH_NOALLOC_SCRATCH_BYTES on each GPU, whose
+ * address rh_init looks up once per device, and K-split GEMMs run unsplit.
+ * A batch whose quantized activations would not fit, about
+ * 2 * tokens * width bytes plus a fifth of that, is refused with
+ * RH_ERR_INVALID_ARGUMENT. Every call on a GPU shares that GPU's array:
+ * calls that overlap on one GPU (other streams, other contexts, other
+ * threads) race, and must be ordered by the caller. */
+enum { RH_NOALLOC_SCRATCH_BYTES = 4 << 20 };
+rh_status rh_matmul_batch_device_noalloc(rh_ctx *ctx, const float *inputs, size_t inputs_len, size_t tokens,
+                                         const rh_job *jobs, size_t n_jobs, void *stream);
 
 /* A quantized activation batch on the device: Q8Input
  * (crates/rusticide-kernels/src/q8_input.rs:66-73), one per token. */

@@ -103,6 +103,8 @@ def lib() -> ctypes.CDLL:
         L.rh_dot_matrix_device.restype = St
         L.rh_gemm_min_tokens.restype = S
         L.rh_set_gemm_min_tokens.argtypes = [S]
+        L.rh_matmul_batch_device_noalloc.argtypes = [P, P, S, S, P, S, P]
+        L.rh_matmul_batch_device_noalloc.restype = St
         L.rh_matmul_batch_device_repeat.argtypes = [P, P, S, S, P, S, P, S, S, P]
         L.rh_matmul_batch_device_repeat.restype = St
         L.rh_reload_tuning.argtypes = []
@@ -290,6 +292,12 @@ def matmul_batch_device(ctx: Context, inputs, tokens: int, jobs, stream: int = 0
     """Device-resident form: `inputs` and outputs are torch device tensors."""
     ctx.check(lib().rh_matmul_batch_device(ctx.handle, _ptr(inputs), inputs.numel(), tokens, _jobs(jobs),
                                            len(jobs), stream or None))
+
+
+def matmul_batch_device_noalloc(ctx: Context, inputs, tokens: int, jobs, stream: int = 0) -> None:
+    """rh_matmul_batch_device_noalloc: the device-resident form that allocates nothing."""
+    ctx.check(lib().rh_matmul_batch_device_noalloc(ctx.handle, _ptr(inputs), inputs.numel(), tokens, _jobs(jobs),
+                                                   len(jobs), stream or None))
 
 
 def matmul_batch_device_repeat(ctx: Context, inputs, tokens: int, matrices, out, launches: int,

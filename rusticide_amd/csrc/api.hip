@@ -12,6 +12,7 @@
 #include <cstring>
 #include <new>
 #include <string>
+#include <mutex>
 #include <thread>
 #include <vector>
 
@@ -166,7 +167,7 @@ size_t rows_for(const rh_matrix* m, size_t out_len, size_t tokens) {
 // launches quantize d_in themselves.
 rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t tokens, const rh_job* jobs,
                       size_t n_jobs, const Q8Dev& super_q, const Q8Dev& row_q, hipStream_t s,
-                      int32_t* raw, unsigned fused) {
+                      int32_t* raw, unsigned fused, bool allow_split = true) {
   rh_status st = RH_OK;
   const uint32_t kinds[4] = {RH_TYPE_Q4_K, RH_TYPE_Q6_K, RH_TYPE_I2_S, RH_TYPE_F32};
   for (uint32_t kind : kinds) {
@@ -178,8 +179,8 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (is_kquant(kind) && tokens >= g_gemm_min_tokens) {
         if (!gemm_fits(tokens, q.qstride))
           return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a batch's quantized activation exceeds 4 GiB");
-        float* terms = nullptr;
-        if (const size_t tb = gemm_split_bytes(kind, g, tokens)) {
+        float* terms = nullptr;  // without it the GEMM runs unsplit (the same bits)
+        if (const size_t tb = allow_split ? gemm_split_bytes(kind, g, tokens) : 0) {
           rh_status es = ensure(ctx, kTerms, tb);
           if (es != RH_OK) return es;
           terms = static_cast<float*>(ctx->buf[kTerms]);
@@ -239,8 +240,12 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
   return RH_OK;
 }
 
+// With `fixed`, the quantized activations go to the two Q8Dev of `fixed`
+// (super-block, row kind) and nothing is allocated: the context's scratch is
+// not grown and the GEMMs do not split K.
 rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t tokens,
-                    const rh_job* jobs, size_t n_jobs, hipStream_t s, int32_t* raw) {
+                    const rh_job* jobs, size_t n_jobs, hipStream_t s, int32_t* raw,
+                    const Q8Dev* fixed = nullptr) {
   const size_t width = inputs_len / tokens;
   uint32_t nbmax[3] = {0, 0, 0};  // Q4_K, Q6_K, I2_S
   for (size_t i = 0; i < n_jobs; i++) {
@@ -269,11 +274,72 @@ rh_status run_batch(rh_ctx* ctx, const float* d_in, size_t inputs_len, size_t to
   }
   const bool need_super = (present & ~fused & 3u) != 0;
   const bool need_row = (present & ~fused & 4u) != 0;
-  rh_status st = ensure_q8(ctx, width, tokens);
-  if (st != RH_OK) return st;
-  if (need_super) RH_HIP(ctx, launch_quantize_super(d_in, width, tokens, ctx->super_q, s));
-  if (need_row) RH_HIP(ctx, launch_quantize_row(d_in, width, tokens, ctx->row_q, s));
-  return launch_jobs(ctx, d_in, width, tokens, jobs, n_jobs, ctx->super_q, ctx->row_q, s, raw, fused);
+  if (!fixed) {
+    rh_status st = ensure_q8(ctx, width, tokens);
+    if (st != RH_OK) return st;
+  }
+  const Q8Dev& sq = fixed ? fixed[0] : ctx->super_q;
+  const Q8Dev& rq = fixed ? fixed[1] : ctx->row_q;
+  if (need_super) RH_HIP(ctx, launch_quantize_super(d_in, width, tokens, sq, s));
+  if (need_row) RH_HIP(ctx, launch_quantize_row(d_in, width, tokens, rq, s));
+  return launch_jobs(ctx, d_in, width, tokens, jobs, n_jobs, sq, rq, s, raw, fused, fixed == nullptr);
+}
+
+// The allocation-free entry point's device memory: the quantized
+// activations of one batch, both kinds, in a file-scope array of every GPU
+// the library runs on. Host code reaches it only through the address
+// hipGetSymbolAddress gives on each device (scratch_setup), never by name.
+constexpr size_t kScratchBytes = RH_NOALLOC_SCRATCH_BYTES;
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};
+
+// The bytes of the activation layout q8_layout builds for `tokens` rows of
+// `width` values (each part 256-byte aligned).
+size_t q8_layout_bytes(size_t width, size_t tokens) {
+  const size_t qstride = round_up(width < 256 ? 256 : width, 256);
+  const size_t bstride = round_up(qstride / 32, 8);
+  return 2 * round_up(tokens * qstride, 256) + 6 * round_up(tokens * bstride * 4, 256);
+}
+
+// Both activation kinds of a batch laid out from `base`: quants, scales,
+// per-32 sums and (super-block kind) per-16 sums, as ensure_q8 lays them out
+// in the context's buffers.
+void q8_layout(uint8_t* base, size_t width, size_t tokens, Q8Dev out[2]) {
+  const size_t qstride = round_up(width < 256 ? 256 : width, 256);
+  const size_t bstride = round_up(qstride / 32, 8);
+  const size_t qb = round_up(tokens * qstride, 256), fb = round_up(tokens * bstride * 4, 256);
+  for (int k = 0; k < 2; k++) {
+    Q8Dev& q = out[k];
+    q.qstride = qstride;
+    q.bstride = bstride;
+    q.quants = reinterpret_cast<int8_t*>(base + k * qb);
+    q.scales = reinterpret_cast<float*>(base + 2 * qb + k * fb);
+    q.sums = reinterpret_cast<int32_t*>(base + 2 * qb + (2 + k) * fb);
+    q.sums16 = reinterpret_cast<int32_t*>(base + 2 * qb + 4 * fb);  // two per 32-block, super-block kind
+    q.n_blocks = k == 0 ? width / 256 * 8 : width / 32;
+  }
+}
+}  // namespace
+
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+// Finds the array's address on `device` (current) once per process.
+hipError_t scratch_setup(int device) {
+  if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return hipSuccess;
+  void* ptr = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (e == hipSuccess) g_scratch_ptr[device] = ptr;
+  return e;
+}
+
+void* scratch_ptr(int device) {
+  if (device < 0 || device >= kScratchDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_ptr[device];
 }
 
 }  // namespace
@@ -628,6 +694,13 @@ rh_status rh_init(int device, rh_ctx** out) {
     delete ctx;
     return RH_ERR_DEVICE;
   }
+  // the allocation-free entry point's array on this device; a failure only
+  // disables that entry point (it reports the error)
+  const hipError_t se = scratch_setup(device);
+  if (se != hipSuccess) {
+    (void)hipGetLastError();
+    ctx->last_error = std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(se);
+  }
   *out = ctx;
   return RH_OK;
 }
@@ -730,6 +803,26 @@ rh_status rh_matmul_batch_device(rh_ctx* ctx, const float* inputs, size_t inputs
   RH_HIP(ctx, hipSetDevice(ctx->device));
   hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
   return run_batch(ctx, inputs, inputs_len, tokens, jobs, n_jobs, s, nullptr);
+}
+
+rh_status rh_matmul_batch_device_noalloc(rh_ctx* ctx, const float* inputs, size_t inputs_len, size_t tokens,
+                                         const rh_job* jobs, size_t n_jobs, void* stream) {
+  if (!ctx || (!jobs && n_jobs)) return RH_ERR_INVALID_ARGUMENT;
+  if (tokens == 0 || tokens > inputs_len) return RH_OK;  // matmul.rs:230-232
+  if (!inputs) return fail(ctx, RH_ERR_INVALID_ARGUMENT, "no inputs");
+  const size_t width = inputs_len / tokens;
+  const size_t need = q8_layout_bytes(width, tokens);
+  if (need > kScratchBytes)
+    return fail(ctx, RH_ERR_INVALID_ARGUMENT,
+                "the batch's quantized activations need " + std::to_string(need) +
+                    " bytes; rh_matmul_batch_device_noalloc holds " + std::to_string(kScratchBytes));
+  uint8_t* base = static_cast<uint8_t*>(scratch_ptr(ctx->device));
+  if (!base) return fail(ctx, RH_ERR_DEVICE, "the allocation-free scratch has no address on this device");
+  RH_HIP(ctx, hipSetDevice(ctx->device));
+  hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+  Q8Dev q[2];
+  q8_layout(base, width, tokens, q);
+  return run_batch(ctx, inputs, inputs_len, tokens, jobs, n_jobs, s, nullptr, q);
 }
 
 rh_status rh_matmul_batch_device_repeat(rh_ctx* ctx, const float* inputs, size_t inputs_len, size_t tokens,
