@@ -514,3 +514,87 @@ def test_copy_row_dequantizes_like_the_cpu_path(ctx, type_id):
             want = (want * np.float32(0.02)).astype(np.float32)
         assert_same_bits(out, want)
     assert not m.copy_row(rows, np.zeros(cols, np.float32))
+
+
+# ------------------------------------------- Q8Input::quantize + dot_matrix
+
+
+@pytest.mark.parametrize("type_id,rows,cols", [(12, 300, 2048), (14, 257, 1536), (36, 333, 2560)])
+@pytest.mark.parametrize("tokens", [1, 2, 9, 33])
+def test_dot_matrix_device_matches_the_oracle(ctx, type_id, rows, cols, tokens):
+    # QuantKernel::dot_matrix (quant_kernel.rs:112-119, tested at
+    # quant_kernel_tests.rs:202-230): every row against each pre-quantized
+    # input, out[row * tokens + token], here with the activation quantized on
+    # the device (rh_q8_quantize_device) and 9+ tokens taking the MFMA GEMM
+    from rusticide_amd import hip as H
+    data = synth.i2s_matrix(rows, cols, seed=rows) if type_id == 36 else synth.matrix(type_id, rows, cols, seed=rows)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    x = synth.normal_f32(tokens * cols, seed=tokens + cols)
+    want = oracle_matmul(type_id, data, rows, cols, x, tokens, scale=0.02, threads=16)
+    d_x = H.DeviceArray.from_numpy(x)
+    q8 = R.Q8(ctx).quantize(d_x, tokens, R.ROW if type_id == 36 else R.SUPER_BLOCK)
+    out = H.DeviceArray(rows * tokens)
+    out.fill_bytes(0xFF)
+    R.dot_matrix_device(m, q8, out)
+    H.synchronize()
+    assert_same_bits(out.numpy(), want, f"type={type_id} {rows}x{cols} tokens={tokens}")
+    # out.len() bounds the rows computed: nothing past it is written
+    short = H.DeviceArray(rows * tokens)
+    short.fill_bytes(0xFF)
+    n = 5 * tokens + 1
+    lib_out = R.lib().rh_dot_matrix_device(ctx.handle, m.handle, q8.handle, short.data_ptr(), n, None)
+    ctx.check(lib_out)
+    H.synchronize()
+    got = short.numpy()
+    assert_same_bits(got[:n], want[:n], "short output")
+    assert np.all(got[n:].view(np.uint32) == 0xFFFFFFFF), "wrote past out_len"
+    for a in (d_x, out, short):
+        a.free()
+    q8.free()
+    m.free()
+
+
+def test_device_block_terms_round_like_the_reference(ctx):
+    # the rounding pins of test_oracle_rounding.py, on the device path: a
+    # Q4_K and a Q6_K matrix whose rows separate the reference's combine
+    # (d8 * d.mul_add(isum, -(dmin*msum)); (d*d8)*isum; the fold from -0.0
+    # in block order) from its plausible slips, with the expected bits from
+    # exact rationals on the activation the quantizer produced
+    from fractions import Fraction
+    import test_oracle_rounding as T
+    rng = np.random.default_rng(4)
+    cols, rows = 2048, 24
+    x = rng.standard_normal(cols).astype(np.float32)
+    q = O.quantize(x, O.SUPER_BLOCK)
+    steps = [Fraction(float(q.scales[8 * b])) for b in range(cols // 256)]  # one step per super-block
+    quants = q.quants.astype(np.int64)
+    for type_id in (12, 14):
+        data, want = b"", []
+        for r in range(rows):
+            blocks, seq = [], Fraction(0)
+            for b in range(cols // 256):
+                qb = quants[256 * b:256 * (b + 1)]
+                if type_id == 12:
+                    d, dmin, sc, mn, nib, _ = T.q4k_parts(rng)
+                    isum, msum = T.q4k_sums(sc, mn, nib, qb)
+                    blocks.append(T.q4k_block(d, dmin, sc, mn, nib))
+                    term = T.q4k_term(T.f16_value(d), T.f16_value(dmin), steps[b], isum, msum)
+                else:
+                    qq = [int(v) for v in rng.integers(0, 64, 256)]
+                    scales = rng.integers(-32, 32, 16)
+                    d = T.f16_bits(float(rng.uniform(-0.01, 0.01)))
+                    blocks.append(T.q6k_block(qq, scales, d))
+                    term = T.f32(T.f32(T.f16_value(d) * steps[b]) * T.q6k_isum(qq, scales, qb))
+                seq = T.f32(seq + term)  # from -0.0: the first term unchanged
+            data += b"".join(blocks)
+            assert seq != 0  # a zero sum's sign is not a rational's to tell
+            want.append(float(seq))
+        m = R.Matrix.load(ctx, type_id, np.frombuffer(data, np.uint8), rows, cols)
+        for tokens in (1, 9):  # the decode GEMV and the MFMA GEMM
+            xt = np.tile(x, tokens)
+            out = np.full(rows * tokens, np.nan, np.float32)
+            R.matmul_batch(ctx, xt, tokens, [(m, out)])
+            got = out.reshape(rows, tokens)
+            for t in range(tokens):
+                assert [T.bits32(v) for v in got[:, t]] == [T.bits32(v) for v in want], (type_id, tokens, t)
+        m.free()
