@@ -52,7 +52,7 @@ enum {
     RH_TYPE_I2_S = 36
 };
 
-/* Q8Kind (crates/rusticide-kernels/src/q8_input.rs:86-100). */
+/* Q8Kind (crates/rusticide-kernels/src/q8_input.rs:33-50). */
 enum { RH_Q8_SUPER_BLOCK = 1, RH_Q8_ROW = 2 };
 
 typedef struct rh_ctx rh_ctx;
@@ -135,16 +135,16 @@ rh_status rh_matmul_batch_device_noalloc(rh_ctx *ctx, const float *inputs, size_
                                          const rh_job *jobs, size_t n_jobs, void *stream);
 
 /* A quantized activation batch on the device: Q8Input
- * (crates/rusticide-kernels/src/q8_input.rs:66-73), one per token. */
+ * (crates/rusticide-kernels/src/q8_input.rs:13-23), one per token. */
 typedef struct rh_q8 rh_q8;
 rh_status rh_q8_new(rh_ctx *ctx, rh_q8 **out);
 void rh_q8_free(rh_q8 *q);
-/* Q8Input::quantize (q8_input.rs:105-108) of every token of `inputs`, a
+/* Q8Input::quantize (q8_input.rs:52-58) of every token of `inputs`, a
  * device pointer holding `tokens` rows of inputs_len / tokens values. Queued
  * on `stream` (NULL = the context's stream). */
 rh_status rh_q8_quantize_device(rh_ctx *ctx, rh_q8 *q, int kind, const float *inputs,
                                 size_t inputs_len, size_t tokens, void *stream);
-/* QuantKernel::dot_matrix (crates/rusticide-kernels/src/quant_kernel.rs:372-379)
+/* QuantKernel::dot_matrix (crates/rusticide-kernels/src/quant_kernel.rs:106-119)
  * and dot_ternary_matrix (portable/ternary.rs:66-82): every row of `m`
  * against every token of `q` into the device buffer out[row * tokens + token].
  * `q` must hold the kind the matrix pairs with (SUPER_BLOCK for Q4_K/Q6_K,
@@ -152,7 +152,7 @@ rh_status rh_q8_quantize_device(rh_ctx *ctx, rh_q8 *q, int kind, const float *in
 rh_status rh_dot_matrix_device(rh_ctx *ctx, const rh_matrix *m, const rh_q8 *q, float *out,
                                size_t out_len, void *stream);
 
-/* Test hook: Q8Input::quantize (q8_input.rs:105-108, portable/q8.rs:64-106)
+/* Test hook: Q8Input::quantize (q8_input.rs:52-58, portable/q8.rs:64-106)
  * on the device, for one row of `len` host values. Writes n_blocks =
  * whole 32-blocks (whole 256-blocks for SUPER_BLOCK) quants, scales, sums. */
 rh_status rh_quantize(rh_ctx *ctx, int kind, const float *x, size_t len, int8_t *quants,
@@ -356,7 +356,7 @@ rh_status rh_gguf_meta_float(const rh_gguf *g, const char *key, float *out);
  * hold NULs) followed by a NUL, valid until rh_gguf_free. */
 rh_status rh_gguf_meta_string(const rh_gguf *g, const char *key, const char **out, size_t *len);
 
-/* DecoderConfig::from_source (crates/rusticide-transformer/src/hyperparameters.rs:80-135) for the llama
+/* DecoderConfig::from_source (crates/rusticide-transformer/src/hyperparameters.rs:80-120) for the llama
  * family (crates/rusticide-llama/src/variant.rs:41-49): the llama.* keys,
  * head_count_kv defaulting to head_count, rope.freq_base to 10000 and the
  * RMS epsilon to 1e-5, vocab_size from token_embd.weight. Errors:
@@ -368,7 +368,7 @@ rh_status rh_gguf_meta_string(const rh_gguf *g, const char *key, const char **ou
 rh_status rh_gguf_decoder_config(rh_ctx *ctx, const rh_gguf *g, rh_decoder_config *out);
 
 /* A decoder's weights uploaded from a GGUF file: DecoderWeights::from_source
- * (crates/rusticide-transformer/src/loader.rs:19-93) for the llama family.
+ * (crates/rusticide-transformer/src/loader.rs:19-92) for the llama family.
  * Every matrix is checked against its expected shape and format as
  * rh_matrix_load checks it, in the reference's order, before any byte moves;
  * then all go up in one pass through two pinned staging buffers of the

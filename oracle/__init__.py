@@ -167,7 +167,7 @@ def bench_activations(n: int, seed: int) -> np.ndarray:
 # ------------------------------------------------------------- quantizers
 
 class Q8Input:
-    """Mirror of Q8Input (crates/rusticide-kernels/src/q8_input.rs:66-73)."""
+    """Mirror of Q8Input (crates/rusticide-kernels/src/q8_input.rs:13-23)."""
 
     def __init__(self, kind, quants, scales, sums):
         self.kind, self.quants, self.scales, self.sums = kind, quants, scales, sums

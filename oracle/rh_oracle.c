@@ -354,7 +354,7 @@ size_t orc_quantize(int kind, const float *x, size_t len, int8_t *quants,
     return 0;
 }
 
-/* q8_input.rs:125-142: scale * q, or q / scale for Row. */
+/* q8_input.rs:72-93: scale * q, or q / scale for Row. */
 void orc_q8_dequantize(int kind, const int8_t *quants, const float *scales,
                        size_t n_blocks, float *out)
 {

@@ -17,7 +17,7 @@
 extern "C" {
 #endif
 
-/* Q8Kind (crates/rusticide-kernels/src/q8_input.rs:86-100). Block (ggml Q8_0)
+/* Q8Kind (crates/rusticide-kernels/src/q8_input.rs:33-50). Block (ggml Q8_0)
  * is out of scope: no format on this path pairs with it. */
 enum { ORC_Q8_SUPER_BLOCK = 1, ORC_Q8_ROW = 2 };
 
@@ -47,7 +47,7 @@ float orc_f16_to_f32(uint16_t bits);
 /* half 2.7.1 f16::from_f32 (format.rs:210): round to nearest even. */
 uint16_t orc_f32_to_f16(float value);
 
-/* format.rs:219-226 with q4_k.rs:38-66, q6_k.rs:205-216, i2_s.rs:15-21. */
+/* format.rs:219-226 with q4_k.rs:38-66, q6_k.rs:13-43, i2_s.rs:15-21. */
 void orc_dequantize_row(uint32_t type_id, const uint8_t *row, size_t row_len,
                         float *out, size_t out_len);
 /* i2_s.rs:26-30: little-endian f32 opening the trailer; 0 if too short. */
@@ -63,7 +63,7 @@ void orc_bench_activations(float *out, size_t len, uint32_t seed);
 /* portable/q8.rs:64-106: returns the number of 32-element blocks written. */
 size_t orc_quantize(int kind, const float *x, size_t len, int8_t *quants,
                     float *scales, int32_t *sums);
-/* q8_input.rs:125-142. */
+/* q8_input.rs:72-93. */
 void orc_q8_dequantize(int kind, const int8_t *quants, const float *scales,
                        size_t n_blocks, float *out);
 

@@ -7,7 +7,7 @@ A thin Python mirror of rusticide's kernel facade over the C ABI of
 * ``Matrix.load``   -- ``Matrix::load_on`` (crates/rusticide-model/src/weights.rs:53-98):
   native GGUF blocks uploaded to HBM once;
 * ``matmul_batch`` / ``matvec_batch`` -- crates/rusticide-kernels/src/matmul.rs:218-248;
-* ``quantize``      -- ``Q8Input::quantize`` (q8_input.rs:105-108) on the device.
+* ``quantize``      -- ``Q8Input::quantize`` (q8_input.rs:52-58) on the device.
 
 There is no CPU fallback: if the library is missing, or no gfx950 device is
 present, calls raise ``RusticideError``.
@@ -233,7 +233,7 @@ class Matrix:
 
 
 class Q8:
-    """Device-quantized activations (Q8Input, q8_input.rs:66-73) of a batch."""
+    """Device-quantized activations (Q8Input, q8_input.rs:13-23) of a batch."""
 
     def __init__(self, ctx: Context):
         h = ctypes.c_void_p()
@@ -260,7 +260,7 @@ class Q8:
 
 
 def dot_matrix_device(m: Matrix, q: Q8, out, stream: int = 0) -> None:
-    """QuantKernel::dot_matrix (quant_kernel.rs:372-379) into a device tensor."""
+    """QuantKernel::dot_matrix (quant_kernel.rs:106-119) into a device tensor."""
     m.ctx.check(lib().rh_dot_matrix_device(m.ctx.handle, m.handle, q.handle, _ptr(out), out.numel(),
                                            stream or None))
 

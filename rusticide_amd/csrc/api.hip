@@ -155,7 +155,7 @@ rh_status ensure_q8(rh_ctx* ctx, size_t width, size_t tokens) {
   return RH_OK;
 }
 
-// Rows worth computing: out_len bounds them (quant_kernel.rs:416-419).
+// Rows worth computing: out_len bounds them (quant_kernel.rs:106-111).
 size_t rows_for(const rh_matrix* m, size_t out_len, size_t tokens) {
   size_t by_out = (out_len + tokens - 1) / tokens;
   return m->rows < by_out ? m->rows : by_out;

@@ -721,7 +721,7 @@ rh_status rh_gguf_decoder_config(rh_ctx* ctx, const rh_gguf* g, rh_decoder_confi
     return model_fail(ctx, RH_ERR_MISSING_METADATA, "missing metadata general.architecture");
   if (arch->s != "llama")
     return model_fail(ctx, RH_ERR_UNKNOWN_ARCHITECTURE, "unknown architecture " + arch->s + "; supported: llama");
-  // DecoderConfig::read (hyperparameters.rs:99-135)
+  // DecoderConfig::read (hyperparameters.rs:96-120)
   auto required = [&](const char* suffix, size_t* v) -> rh_status {
     const std::string key = std::string("llama.") + suffix;
     const Value* x = meta(g, key.c_str());
@@ -801,7 +801,7 @@ rh_status rh_gguf_model_load(rh_ctx* ctx, const rh_gguf* g, rh_gguf_model** out)
       m->blocks.resize(c.block_count);
     }
     const size_t e = c.embedding_length, f = c.feed_forward_length, kv = c.head_count_kv * c.head_dim;
-    // load_block (loader.rs:49-93), in its order
+    // load_block (loader.rs:49-92), in its order
     for (size_t l = 0; st == RH_OK && l < c.block_count; l++) {
       rh_decoder_block& b = m->blocks[l];
       auto name = [&](const char* part) { return "blk." + std::to_string(l) + "." + part + ".weight"; };

@@ -11,7 +11,7 @@ section, every tensor starting on the alignment (``general.alignment``,
 ``GgufFile`` parses bytes with ``rh_gguf_parse`` (GgufFile::from_bytes,
 gguf/file.rs:39-62) and raises ``GgufError`` with the reference's error kind;
 ``GgufModel`` uploads a llama-family decoder's tensors to HBM
-(DecoderWeights::from_source, crates/rusticide-transformer/src/loader.rs:19-93).
+(DecoderWeights::from_source, crates/rusticide-transformer/src/loader.rs:19-92).
 """
 
 from __future__ import annotations
@@ -124,7 +124,7 @@ def decoder_gguf(model: dict, alignment: int = 32, tied_output: bool = False) ->
     """A llama-family GGUF of a decoder model dict (the layout of
     rusticide_amd.synth.decoder_model): the llama.* hyperparameters, norms
     as F32, matrices in their block formats under GGUF tensor names
-    (crates/rusticide-transformer/src/loader.rs:49-93). `tied_output` leaves
+    (crates/rusticide-transformer/src/loader.rs:49-92). `tied_output` leaves
     output.weight out, so the output shares token_embd."""
     c = model["config"]
     w = Writer()

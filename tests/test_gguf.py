@@ -121,7 +121,7 @@ def test_data_start_follows_the_alignment():
 
 
 def test_invalid_alignment_rejects_the_file():
-    # file_tests.rs:163-176, metadata_tests.rs:115-140
+    # file_tests.rs:163-176, metadata_tests.rs:115-139
     for tag, value in ((UINT32, 0), (UINT32, 48), (STRING, "32"), (UINT64, 32)):
         e = error(Writer().kv("general.alignment", tag, value).build())
         assert e.gguf_kind == "InvalidAlignment", (tag, value)

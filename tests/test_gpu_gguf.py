@@ -1,6 +1,6 @@
 """Decoders uploaded from GGUF files (rh_gguf_model_load) against the CPU
 restatement of rusticide's decoder, and the loader's errors
-(DecoderWeights::from_source, crates/rusticide-transformer/src/loader.rs:19-93;
+(DecoderWeights::from_source, crates/rusticide-transformer/src/loader.rs:19-92;
 Matrix::load, crates/rusticide-model/src/weights.rs:48-98).
 
 The files come from rusticide_amd.gguf.decoder_gguf over the seeded

@@ -408,7 +408,7 @@ def test_one_batch_mixes_formats_and_matches_per_token_calls(ctx, variant):
 
 
 def test_no_ops_and_output_bounds(ctx):
-    # matmul_tests.rs:188-235; quant_kernel.rs:416-419
+    # matmul_tests.rs:188-235; quant_kernel.rs:106-111
     rows, cols = 20, 512
     data = synth.matrix(12, rows, cols, seed=5)
     m = R.Matrix.load(ctx, 12, data, rows, cols)

@@ -532,7 +532,7 @@ def test_matmul_batch_no_ops():
 
 
 def test_short_output_bounds_the_rows():
-    # matmul.rs:239-244 + quant_kernel.rs:416-419: out.len() bounds the rows
+    # matmul.rs:239-244 + quant_kernel.rs:106-111: out.len() bounds the rows
     data = O.synthetic_blocks(12, 4, 2)
     x = O.pseudo_random_values(256, 3)
     full = np.zeros(4, np.float32)
