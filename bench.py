@@ -114,8 +114,10 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
     B = algorithmic_bytes(type_id, rows, cols)
 
     def run(copies: int, n: int, first: int = 0) -> None:
-        for i in range(first, first + n):
-            R.matmul_batch_device(ctx, x, 1, [(mats[i % copies], out)])
+        # the launches are queued from C (one rh_matmul_batch_device each):
+        # a Python call per launch can take as long as the kernel itself
+        order = [mats[(first + i) % copies] for i in range(copies)]
+        R.matmul_batch_device_repeat(ctx, x, 1, order, out, n)
 
     # the timed region: `steps` steps bracketed by device synchronization,
     # with events on the stream the step's one kernel runs on
@@ -196,8 +198,27 @@ def measure_stream_read(ctx, nbytes: int, copies: int, steps: int, warmup: int) 
     return n / (us * 1e-6) / 1e9
 
 
+# The reference's own published single-thread kernel rates for these formats
+# (weights per second, 1 token), with the GB/s they imply at
+# the format's bytes per weight.
+REFERENCE_CPU_PUBLISHED = {
+    14: {"format": "Q6_K", "bytes_per_weight": 210 / 256,
+         "avx2_xeon_w2150b_gw_s": 16.39, "neon_m1_pro_gw_s": 28.82,
+         "source": "crates/rusticide-bench/baselines/intel-r-xeon-r-w-2150b-cpu-3-00ghz-20.json:61-64, "
+                   "apple-m1-pro-8.json:61-64"},
+    12: {"format": "Q4_K", "bytes_per_weight": 144 / 256,
+         "avx2_xeon_w2150b_gw_s": 37.92, "neon_m1_pro_gw_s": 47.32,
+         "source": "intel-r-xeon-r-w-2150b-cpu-3-00ghz-20.json:45-48, apple-m1-pro-8.json:45-48"},
+    36: {"format": "I2_S", "bytes_per_weight": 32 / 128,
+         "avx2_xeon_w2150b_gw_s": 7.99, "neon_m1_pro_gw_s": 3.73,
+         "source": "intel-r-xeon-r-w-2150b-cpu-3-00ghz-20.json:29-32, apple-m1-pro-8.json:29-32"},
+}
+
+
 def measure_cpu(res: dict, seconds: float):
-    """The oracle (a C restatement of the reference CPU path) on this host's cores."""
+    """The oracle -- a portable scalar C restatement of the reference's CPU
+    path, not its hand-vectorized avx2/neon adapters -- on this job's share
+    of the host's cores."""
     import oracle as O
     from rusticide_amd import synth
 
@@ -219,6 +240,13 @@ def measure_cpu(res: dict, seconds: float):
         if el >= seconds:
             break
     per = el / n
+    pub = REFERENCE_CPU_PUBLISHED[type_id]
+    published = {
+        "reference_adapter": "avx2 (Xeon W-2150B) and neon (Apple M1 Pro), one thread each, published",
+        "avx2_gbs_per_thread": round(pub["avx2_xeon_w2150b_gw_s"] * pub["bytes_per_weight"], 2),
+        "neon_gbs_per_thread": round(pub["neon_m1_pro_gw_s"] * pub["bytes_per_weight"], 2),
+        "source": pub["source"],
+    }
     cpu = platform.processor() or platform.machine()
     try:
         with open("/proc/cpuinfo") as f:
@@ -230,9 +258,12 @@ def measure_cpu(res: dict, seconds: float):
         pass
     return {
         "value": round(res["bytes"] / per / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-        "sample": (f"{n} full {rows}x{cols} GEMVs incl. activation quantization, "
-                   f"{threads} threads ({os.cpu_count()} visible), {el:.2f} s wall on {cpu}; "
+        "sample": (f"the oracle (portable scalar C restatement of the reference CPU path, not its avx2 "
+                   f"adapter): {n} full {rows}x{cols} GEMVs incl. activation quantization on {threads} threads, "
+                   f"this job's CPU share of the GPU box ({os.cpu_count()} visible), {el:.2f} s wall on {cpu}; "
                    f"bit-identical to the GPU: {same}"),
+        "per_thread_gbs": round(res["bytes"] / per / 1e9 / threads, 3),
+        "reference_published_per_thread": published,
     }
 
 
@@ -241,13 +272,15 @@ INT8_PEAK_TOPS = 5000.0
 
 GEMM_WORKLOADS = (
     (12, 5632, 2048, "Q4_K 5632x2048 (TinyLlama ffn_gate)"),
+    (14, 2048, 5632, "Q6_K 2048x5632 (TinyLlama ffn_down)"),
     (36, 6912, 2560, "I2_S 6912x2560 (BitNet 2B4T up/gate)"),
 )
 
 
 def measure_gemm(ctx, token_counts=(128, 512, 2048), reps: int = 20):
     """Prefill GEMMs (int8 MFMA): the k-quant path on the ffn_gate shape in
-    Q4_K and the ternary path on the BitNet up/gate shape."""
+    Q4_K and the ffn_down shape in Q6_K, and the ternary path on the BitNet
+    up/gate shape."""
     import rusticide_amd as R
     from rusticide_amd import hip as H
     from rusticide_amd import synth
@@ -428,21 +461,21 @@ def traffic_for(name: str):
 
 
 def pmc_probe(steps: int) -> int:
-    """A short, fixed sequence for `rocprofv3 --pmc` runs: the headline step on
-    rotating copies, the prefill GEMM at 2048 tokens, then device-to-device
-    copies of a known size (the calibration for the counters)."""
+    """A short, fixed sequence for `rocprofv3 --pmc` runs: each GEMV workload's
+    step on rotating copies, the prefill GEMM at 2048 tokens, then
+    device-to-device copies of a known size (the calibration for the
+    counters)."""
     import rusticide_amd as R
     from rusticide_amd import hip as H
     from rusticide_amd import synth
 
     ctx = R.Context(0)
-    for name in (HEADLINE, "q4k_ffn_gate", "i2s_up"):
+    for name in (HEADLINE, "q6k_ffn_down", "q4k_ffn_gate", "i2s_up", "i2s_down"):
         type_id, rows, cols = WORKLOADS[name][:3]
         _, mats = load_rotation(ctx, name)
         x = H.DeviceArray.from_numpy(synth.normal_f32(cols, seed=2))
         out = H.DeviceArray(rows)
-        for i in range(steps):
-            R.matmul_batch_device(ctx, x, 1, [(mats[i % len(mats)], out)])
+        R.matmul_batch_device_repeat(ctx, x, 1, mats, out, steps)
         H.synchronize()
         for m in mats:
             m.free()
