@@ -369,6 +369,9 @@ void load_tuning() {
   t.norm_ni = nni == 2 || nni == 4 ? nni : 0;
   const int gr = env_int("RUSTICIDE_HIP_I2S_GROUPS", 0);
   t.i2s_groups = gr == 1 || gr == 2 || gr == 4 ? gr : 0;
+  const int lpr = env_int("RUSTICIDE_HIP_I2S_LPR", 0);
+  t.i2s_lpr = lpr == 8 || lpr == 16 || lpr == 32 || lpr == 64 ? lpr : 0;
+  t.i2s_one = env_int("RUSTICIDE_HIP_I2S_ONE", 1) != 0;
   const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
   t.gemm_bn = bn == 64 || bn == 128 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;

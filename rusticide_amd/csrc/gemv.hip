@@ -916,6 +916,207 @@ __global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, cons
   }
 }
 
+// I2_S x I8_S, one token ----------------------------------------------------
+// The decode case of the kernel above, arranged so that each step waits for
+// its own inputs only. Every global load is unconditional (addresses clamped,
+// surplus values masked in registers), so the number of loads in flight is
+// known where each is used: the activation's loads go out first and the
+// weights' after them, and since loads complete in issue order the
+// activation's quantization waits for its own loads while the weights are
+// still arriving. The sum of the quants that ternary.rs:39,41 subtracts is the
+// same for every row of a job: it is reduced once, beside the quantization,
+// rather than per row. A team of LPR lanes owns a row; lane l of the team
+// holds chunks l, l + LPR, ... (CPL of them) of 16 bytes. Job fields are read
+// into registers once.
+// LDS: act [nkeep] i8 | red [2 slots][2][waves] i32 | qsw [waves] i32
+template <int LPR, int CPL, bool ONE_JOB>
+__global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const float* __restrict__ x, uint32_t n,
+                                                           uint32_t nkeep, size_t tokens, size_t t0, int32_t* raw) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr uint32_t kWaves = kThreads / 64u;
+  constexpr uint32_t R = kThreads / static_cast<uint32_t>(LPR);
+  int8_t* act = reinterpret_cast<int8_t*>(lds);
+  int32_t* red = reinterpret_cast<int32_t*>(lds + nkeep);  // nkeep is a multiple of 128
+  int32_t* qsw = red + 4u * kWaves;
+
+  // a launch of one job reads it at a fixed offset, without find_job's
+  // dependent round trip
+  const GemvJob& J = jobs.j[ONE_JOB ? 0u : find_job(jobs)];
+  const uint8_t* const wbase = J.w;
+  const uint32_t stride = J.stride, rows = J.rows, nb = J.nb;
+  float* const out = J.out;
+  const size_t out_len = J.out_len;
+  const float scale = J.scale;
+  const uint32_t cl = threadIdx.x & static_cast<uint32_t>(LPR - 1);
+  const uint32_t row = (blockIdx.x - J.wg_begin) * R + threadIdx.x / static_cast<uint32_t>(LPR);
+  const uint32_t nchunk = 2u * nb;
+
+  // the activation (x: token t0's n values): 4 consecutive values of every
+  // 1024 per lane; positions past n read the last 4 values and are zeroed below
+  f32x4 xv[kFusedRowPasses];
+#pragma unroll
+  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+    const uint32_t e = min(4u * threadIdx.x + 4u * kThreads * k, n - 4u);
+    const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(x + e));
+    xv[k] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+  }
+  // then the weights (rows past the job's last read its last row)
+  // (a matrix stays below 4 GiB, rows below 2^24: the 24-bit product is exact)
+  const uint8_t* wrow = wbase + __umul24(min(row, rows - 1u), stride);
+  u32x4 w[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = min(cl + static_cast<uint32_t>(i * LPR), nchunk - 1u);
+    w[i] = load16(wrow + 16u * c);
+  }
+  // the scalars the stores need, loaded now rather than after the dot (the
+  // compiler otherwise reloads them there, one dependent round trip each)
+  __asm__ volatile("" ::"s"(out), "s"(out_len), "s"(scale), "s"(tokens), "s"(t0), "s"(raw));
+  // keep the weights' loads ahead of the quantization (the scheduler would
+  // otherwise sink them below the activation's first use)
+  __builtin_amdgcn_sched_barrier(0);
+
+  // C's MAX over |x| from 1e-5 in f64 (portable/q8.rs:38-49). Without a NaN
+  // or an infinity in the row (the usual case) that is its largest magnitude,
+  // floored at 1e-5, and the quants need no NaN rule; a row with either takes
+  // the exact path below. Only the passes that hold values are computed.
+  const uint32_t npass = (n + 4u * kThreads - 1u) / (4u * kThreads);
+  float all_max = 0.0f;
+  bool has_nan = false;
+#pragma unroll
+  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+    if (k < npass) {
+      if (4u * kThreads * (k + 1u) > n) {  // the last pass may run past n
+        const bool in = 4u * threadIdx.x + 4u * kThreads * k < n;
+#pragma unroll
+        for (int i = 0; i < 4; i++) xv[k][i] = in ? xv[k][i] : 0.0f;
+      }
+      // maxNum: a NaN never enters the maximum
+      all_max = __builtin_fmaxf(all_max, __builtin_fmaxf(__builtin_fabsf(xv[k][0]), __builtin_fabsf(xv[k][1])));
+      all_max = __builtin_fmaxf(all_max, __builtin_fmaxf(__builtin_fabsf(xv[k][2]), __builtin_fabsf(xv[k][3])));
+      has_nan |= __builtin_isunordered(xv[k][0], xv[k][1]) | __builtin_isunordered(xv[k][2], xv[k][3]);
+    }
+  }
+  int32_t p = has_nan ? 0 : -1;
+  uint32_t mb = __float_as_uint(all_max);
+  wg_max_pair(p, mb, red, 0u);
+  const bool exact = p >= 0 || mb == 0x7f800000u;  // a NaN, or an infinity
+  double mx;
+  if (p < 0) {
+    mx = static_cast<double>(__uint_as_float(mb));
+    mx = 1e-5 > mx ? 1e-5 : mx;
+  } else {
+    // a NaN restarts the maximum at the next value (without the floor); a
+    // trailing NaN leaves it NaN
+    int32_t last_nan = -1;
+#pragma unroll
+    for (uint32_t k = 0; k < kFusedRowPasses; k++)
+      if (k < npass)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++)
+          if (xv[k][i] != xv[k][i]) last_nan = static_cast<int32_t>(4u * threadIdx.x + 4u * kThreads * k + i);
+    uint32_t unused = 0;
+    wg_max_pair(last_nan, unused, red, 1u);
+    float after = 0.0f;
+#pragma unroll
+    for (uint32_t k = 0; k < kFusedRowPasses; k++)
+      if (k < npass)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; i++) {
+          const int32_t e = static_cast<int32_t>(4u * threadIdx.x + 4u * kThreads * k + i);
+          const float m = __builtin_fabsf(xv[k][i]);
+          if (e > last_nan) after = m > after ? m : after;
+        }
+    int32_t none = -1;
+    uint32_t ab = __float_as_uint(after);
+    wg_max_pair(none, ab, red, 0u);  // slot 0 is free again after slot 1's barrier
+    mx = last_nan == static_cast<int32_t>(n) - 1 ? __builtin_nan("") : static_cast<double>(__uint_as_float(ab));
+  }
+  const float div = static_cast<float>(127.0 / mx);
+
+  // the quants into LDS (round_row_to_i8; on the usual path every product is
+  // finite and within +-127.5, so a clamp replaces the NaN rule); the sum of
+  // those of the job's blocks, per wave
+  const uint32_t ncover = 128u * nb;
+  int32_t qsum = 0;
+#pragma unroll
+  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+    if (k < npass) {
+      const uint32_t base = 4u * threadIdx.x + 4u * kThreads * k;
+      int32_t qv[4];
+      if (!exact) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          qv[i] = static_cast<int32_t>(__builtin_amdgcn_fmed3f(__builtin_rintf(xv[k][i] * div), -128.0f, 127.0f));
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) qv[i] = round_row_to_i8(xv[k][i] * div);
+      }
+      // bytes q0 q1 q2 q3, low first
+      const uint32_t lo = __builtin_amdgcn_perm(static_cast<uint32_t>(qv[1]), static_cast<uint32_t>(qv[0]), 0x0c0c0400u);
+      const uint32_t hi = __builtin_amdgcn_perm(static_cast<uint32_t>(qv[3]), static_cast<uint32_t>(qv[2]), 0x04000c0cu);
+      const uint32_t packed = lo | hi;
+      if (base < nkeep) *reinterpret_cast<uint32_t*>(act + base) = packed;
+      if (base < ncover) qsum = dot4(packed, 0x01010101u, qsum);
+    }
+  }
+  uint32_t ws = static_cast<uint32_t>(qsum);
+  ws += dpp<0xB1>(ws);
+  ws += dpp<0x4E>(ws);
+  ws += dpp<0x141>(ws);
+  ws += dpp<0x140>(ws);
+  ws += static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(ws), 0x401F));
+  ws = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ws), 0)) +
+       static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ws), 32));
+  if ((threadIdx.x & 63u) == 0) qsw[threadIdx.x >> 6] = static_cast<int32_t>(ws);
+  __syncthreads();
+  uint32_t qtotal = 0;
+#pragma unroll
+  for (uint32_t v = 0; v < kWaves; v++) qtotal += static_cast<uint32_t>(qsw[v]);
+
+  uint32_t acc = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t craw = cl + static_cast<uint32_t>(i * LPR);
+    const uint32_t c = min(craw, nchunk - 1u);
+    const uint32_t live = craw < nchunk ? 0xffffffffu : 0u;
+    const int8_t* a = act + 128u * (c >> 1) + 16u * (c & 1u);
+    const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
+    const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
+    const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
+    const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+    int32_t P16 = 0, P4 = 0, P1 = 0;
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t wk = w[i][k] & live;
+      P16 = dot4((wk >> 2) & 0x30303030u, a0[k], P16);  // code of shift 6, times 16
+      P16 = dot4(wk & 0x30303030u, a1[k], P16);         // shift 4, times 16
+      P4 = dot4(wk & 0x0C0C0C0Cu, a2[k], P4);           // shift 2, times 4
+      P1 = dot4(wk & 0x03030303u, a3[k], P1);           // shift 0
+    }
+    acc += static_cast<uint32_t>(P1 + (P4 >> 2) + (P16 >> 4));
+  }
+  // the team's sum, left in every lane of it (wrapping)
+  acc += dpp<0xB1>(acc);
+  acc += dpp<0x4E>(acc);
+  if constexpr (LPR >= 8) acc += dpp<0x141>(acc);
+  if constexpr (LPR >= 16) acc += dpp<0x140>(acc);
+  if constexpr (LPR >= 32) acc += static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(acc), 0x401F));
+  if constexpr (LPR == 64)
+    acc = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(acc), 0)) +
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(acc), 32));
+  if (cl == 0 && row < rows) {
+    const size_t idx = static_cast<size_t>(row) * tokens + t0;
+    if (idx < out_len) {
+      // ternary.rs:39,41: sum(code*q) - sum(q), wrapping
+      const int32_t dot = static_cast<int32_t>(acc - qtotal);
+      if (raw) raw[idx] = dot;
+      // ternary.rs:53-57: (dot as f32) / s * scale
+      else out[idx] = __fdiv_rn(static_cast<float>(dot), div) * scale;
+    }
+  }
+}
+
 // Dense f32 ---------------------------------------------------------------
 // rusticide-simd/src/float.rs:23-36: eight fused lanes over the whole chunks,
 // the lanes added in order from -0.0, then the unfused tail (from -0.0).
@@ -1326,6 +1527,66 @@ hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t 
   return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
 }
 
+template <int LPR, int CPL>
+void* i2s_one_kernel(bool one_job) {
+  return one_job ? reinterpret_cast<void*>(gemv_i2s_one_kernel<LPR, CPL, true>)
+                 : reinterpret_cast<void*>(gemv_i2s_one_kernel<LPR, CPL, false>);
+}
+
+template <int LPR>
+void* i2s_one_pick(uint32_t cpl, bool one_job) {
+  switch (cpl) {
+    case 1: return i2s_one_kernel<LPR, 1>(one_job);
+    case 2: return i2s_one_kernel<LPR, 2>(one_job);
+    case 3: return i2s_one_kernel<LPR, 3>(one_job);
+    case 4: return i2s_one_kernel<LPR, 4>(one_job);
+    case 5: return i2s_one_kernel<LPR, 5>(one_job);
+    case 6: return i2s_one_kernel<LPR, 6>(one_job);
+    case 7: return i2s_one_kernel<LPR, 7>(one_job);
+    case 8: return i2s_one_kernel<LPR, 8>(one_job);
+    default: return nullptr;
+  }
+}
+
+// One token of I2_S on gemv_i2s_one_kernel; hipErrorNotSupported for shapes
+// it does not take (the two-token kernel serves those).
+hipError_t launch_i2s_one(GemvJobs jobs, const float* x, size_t width, size_t tokens, size_t t0, hipStream_t s,
+                          int32_t* raw) {
+  uint32_t nbmax = 0, nbmin = ~0u;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    nbmax = jobs.j[i].nb > nbmax ? jobs.j[i].nb : nbmax;
+    nbmin = jobs.j[i].nb < nbmin ? jobs.j[i].nb : nbmin;
+  }
+  const uint32_t n = static_cast<uint32_t>(width / 32u) * 32u;
+  if (jobs.n == 0 || nbmin == 0 || n < 32u || n > 4u * kThreads * kFusedRowPasses) return hipErrorNotSupported;
+  const uint32_t nchunk = 2u * nbmax;
+  // lanes per row: the fewest that hold a row in at most 8 chunks each. Each
+  // workgroup repeats the activation's quantization, so fewer and fuller
+  // workgroups win even below one per CU (6912x2560: 216 workgroups of 32
+  // rows beat 432 of 16; 2560x6912: 160 of 16 beat 320 of 8).
+  // tuning().i2s_lpr forces it.
+  uint32_t lpr = 8;
+  while (lpr < 64u && (nchunk + lpr - 1u) / lpr > 8u) lpr *= 2u;
+  if (const int v = tuning().i2s_lpr) lpr = static_cast<uint32_t>(v);
+  const uint32_t cpl = (nchunk + lpr - 1u) / lpr;
+  const bool one = jobs.n == 1u;
+  void* k = lpr == 8u ? i2s_one_pick<8>(cpl, one) : lpr == 16u ? i2s_one_pick<16>(cpl, one)
+          : lpr == 32u ? i2s_one_pick<32>(cpl, one) : i2s_one_pick<64>(cpl, one);
+  if (!k) return hipErrorNotSupported;
+  const uint32_t R = kThreads / lpr;
+  uint32_t wgs = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    jobs.j[i].wg_begin = wgs;
+    wgs += (jobs.j[i].rows + R - 1u) / R;
+  }
+  if (wgs == 0) return hipSuccess;
+  uint32_t nkeep = nbmax * 128u;
+  const size_t lds = nkeep + 4u * (4u + 1u) * (kThreads / 64u);
+  const float* xt = x + t0 * width;
+  void* args[] = {&jobs, const_cast<float**>(&xt), const_cast<uint32_t*>(&n), &nkeep, &tokens, &t0, &raw};
+  return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
+}
+
 }  // namespace
 
 bool norm_fusable(uint32_t type_id, size_t width, uint32_t nbmax) {
@@ -1345,9 +1606,14 @@ hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float
     const Q8Dev none{};
     return launch_t<1, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr, norm);
   }
-  if (type_id == 36u)
+  if (type_id == 36u) {
+    if (tn == 1 && tuning().i2s_one) {
+      const hipError_t e = launch_i2s_one(jobs, x, width, tokens, t0, s, raw);
+      if (e != hipErrorNotSupported) return e;
+    }
     return tn == 1 ? launch_i2s_fused<1>(jobs, x, width, tokens, t0, s, raw)
                    : launch_i2s_fused<2>(jobs, x, width, tokens, t0, s, raw);
+  }
   const Q8Dev none{};
   switch (tn) {
     case 1: return launch_t<1, true>(type_id, jobs, none, x, width, tokens, t0, s, nullptr);

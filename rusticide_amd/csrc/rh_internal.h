@@ -84,7 +84,9 @@ struct Tuning {
   int gemv_ni = 0;         // RUSTICIDE_HIP_GEMV_NI=1|2|4|8: blocks per team
   bool interleave = true;  // RUSTICIDE_HIP_GEMV_IL=0: contiguous rows
   int norm_ni = 0;         // RUSTICIDE_HIP_NORM_NI=2|4
-  int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4
+  int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 (two-token kernel)
+  int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
+  bool i2s_one = true;     // RUSTICIDE_HIP_I2S_ONE=0: one token on the two-token kernel
   int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=64|128
   bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
 };

@@ -384,6 +384,61 @@ def test_i2s_code_three_and_hostile_bytes(ctx):
     assert np.array_equal(raw, O.ternary_dot_matrix_i32(body, cols // 4, x, 1))
 
 
+def hostile_rows(cols):
+    # q8.rs:38-49: a NaN restarts the running maximum, a trailing NaN leaves
+    # it NaN, an infinity makes the divisor 0, all zeros floor it at 1e-5
+    rows = []
+    for case in range(5):
+        x = synth.normal_f32(cols, seed=40 + case)
+        if case == 0:
+            x[cols // 3] = np.nan
+            x[cols // 3 + 7] = 9.0
+            x[cols // 5] = -50.0  # larger, but before the NaN
+        elif case == 1:
+            x[-1] = np.nan
+        elif case == 2:
+            x[cols // 2] = np.inf
+        elif case == 3:
+            x[:] = 0.0
+        else:
+            x[3] = -np.inf
+            x[cols - 40] = np.nan
+        rows.append(x)
+    return rows
+
+
+@pytest.mark.parametrize("lanes", ["8", "16", "32", "64", "two-token"])
+def test_i2s_one_token_kernel_at_every_team_width(ctx, tuning, lanes):
+    # the one-token kernel with 8..64 lanes per row (and the two-token kernel
+    # it replaces): ragged row counts, 128 to 8192 values, hostile
+    # activations, and one launch over matrices that cover different numbers
+    # of blocks of the activation (ternary.rs:21-26)
+    if lanes == "two-token":
+        tuning.set("RUSTICIDE_HIP_I2S_ONE", "0")
+    else:
+        tuning.set("RUSTICIDE_HIP_I2S_LPR", lanes)
+    for rows, cols in ((6912, 2560), (2560, 6912), (37, 384), (300, 1024), (17, 8192), (5, 128)):
+        data = synth.i2s_matrix(rows, cols, seed=rows + 3)
+        m = R.Matrix.load(ctx, 36, data, rows, cols)
+        rb = cols // 4
+        xs = [synth.normal_f32(cols, seed=cols)] + (hostile_rows(cols) if rows == 300 else [])
+        for i, x in enumerate(xs):
+            raw = ctx.ternary_dot_i32(m, x, 1)
+            assert np.array_equal(raw, O.ternary_dot_matrix_i32(data[: rows * rb], rb, x, 1)), (rows, cols, i)
+            out = np.full(rows, 7.0, np.float32)
+            R.matmul_batch(ctx, x, 1, [(m, out)])
+            assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, 1, scale=0.02), f"{rows}x{cols} x{i}")
+    specs = [(70, 1024), (33, 512), (129, 384), (8, 1280)]
+    datas = [synth.i2s_matrix(r, c, seed=r) for r, c in specs]
+    mats = [R.Matrix.load(ctx, 36, d, r, c) for d, (r, c) in zip(datas, specs)]
+    for width in (1024, 1000):
+        x = synth.normal_f32(width, seed=width)
+        outs = [np.full(r, 7.0, np.float32) for r, _ in specs]
+        R.matmul_batch(ctx, x, 1, list(zip(mats, outs)))
+        for (r, c), d, out in zip(specs, datas, outs):
+            assert_same_bits(out, oracle_matmul(36, d, r, c, x, 1, scale=0.02), f"{r}x{c} width {width}")
+
+
 # ------------------------------------------------------------ batch rules
 
 
