@@ -375,6 +375,7 @@ void load_tuning() {
   const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
   t.gemm_bn = bn == 64 || bn == 128 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;
+  t.attn_lds = env_int("RUSTICIDE_HIP_ATTN_LDS", 1) != 0;
   g_tuning = t;
 }
 

@@ -572,6 +572,178 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_kernel(
   if (wave == 0) mixed[static_cast<size_t>(h) * hd + lane] = acc;
 }
 
+// mix_rows (float.rs:52-62) for output lane `lane` over value rows 0..rows
+// held in LDS at 64 floats a row, with the weights w: one fused add per row
+// in order from 0.0. Batches of 16 rows (values and weights) are read while
+// the previous batch is added; the scheduling barriers keep the compiler from
+// sinking the reads below the adds.
+struct MixBatch {
+  float v[16];
+  f32x4 w[4];
+};
+
+__device__ __forceinline__ void mix_load(MixBatch& b, const float* col, const float* w) {
+#pragma unroll
+  for (int k = 0; k < 16; k++) b.v[k] = col[k * 64];
+#pragma unroll
+  for (int k = 0; k < 4; k++) b.w[k] = reinterpret_cast<const f32x4*>(w)[k];
+}
+
+__device__ __forceinline__ float mix_add(float acc, const MixBatch& b) {
+#pragma unroll
+  for (int k = 0; k < 16; k++) acc = __builtin_fmaf(b.v[k], b.w[k >> 2][k & 3], acc);
+  return acc;
+}
+
+__device__ __forceinline__ float mix_lds(const float* va, const float* w, uint32_t rows, uint32_t lane) {
+  const float* col = va + lane;
+  float acc = 0.0f;
+  uint32_t r = 0;
+  if (rows >= 16u) {
+    MixBatch a, b;
+    mix_load(a, col, w);
+    for (r = 16u; r + 32u <= rows; r += 32u) {
+      mix_load(b, col + r * 64u, w + r);
+      __builtin_amdgcn_sched_barrier(0);
+      acc = mix_add(acc, a);
+      mix_load(a, col + (r + 16u) * 64u, w + r + 16u);
+      __builtin_amdgcn_sched_barrier(0);
+      acc = mix_add(acc, b);
+    }
+    if (r + 16u <= rows) {
+      mix_load(b, col + r * 64u, w + r);
+      __builtin_amdgcn_sched_barrier(0);
+      acc = mix_add(acc, a);
+      acc = mix_add(acc, b);
+      r += 16u;
+    } else {
+      acc = mix_add(acc, a);
+    }
+  }
+  for (; r < rows; r++) acc = __builtin_fmaf(col[r * 64u], w[r], acc);
+  return acc;
+}
+
+// attention_step_kernel's arithmetic for up to kStepLdsRows rows (the new
+// one included), with its memory traffic rearranged. The key rows arrive by
+// coalesced loads (16 lanes per 256-byte row) and pass through LDS, padded to
+// kKeyStride floats a row so that one row per thread reads back without bank
+// conflicts; the value rows, loaded in the same first burst, wait in
+// registers and take the keys' place once every score is computed. The
+// softmax denominator is ordered_sum_wave's (the sequential sum's bits), and
+// wave 0 divides and mixes from LDS. Three barriers in all.
+constexpr uint32_t kStepLdsRows = 224;
+constexpr uint32_t kKeyStride = 68;
+
+inline size_t attention_step_lds_bytes(uint32_t nk) {
+  const uint32_t cap = 16u * nk;
+  return 4u * (cap * kKeyStride + cap + wave_sum_floats(cap) + 64u + 8u);
+}
+
+template <uint32_t NK>  // rows <= 16 * NK
+__global__ __launch_bounds__(kAttnThreads) void attention_step_lds_kernel(
+    const float* qr, const float* kr, const float* vr, const float* rcos, const float* rsin, float* kcache,
+    float* vcache, uint32_t kv, uint32_t group, float scale, uint32_t start, float* mixed) {
+  constexpr uint32_t hd = 64u, cap = 16u * NK;
+  extern __shared__ __align__(16) float sh[];
+  float* ka = sh;                         // [cap][kKeyStride] keys, then [cap][64] values
+  float* w = ka + cap * kKeyStride;       // [cap] softmax weights
+  float* ws = w + cap;                    // the exps, in ordered_sum_wave's layout
+  float* qh = ws + wave_sum_floats(cap);  // [64] the rotated query
+  float* red = qh + 64;                   // [8]
+  const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t rows = start + 1u;
+  const uint32_t off = (h / group) * hd;
+  const bool appends = h % group == 0u;
+  const float* vnew = vr + off;
+
+  // RoPE inputs first (threads 0..31 the query's pairs, 32..63 the new
+  // key's): loads return in issue order and the rotation needs only these
+  float lo = 0.0f, hi = 0.0f, cs = 0.0f, sn = 0.0f;
+  const uint32_t pair = tid & 31u;
+  if (tid < 64u) {
+    const float* src = tid < 32u ? qr + static_cast<size_t>(h) * hd : kr + off;
+    lo = src[2u * pair];
+    hi = src[2u * pair + 1u];
+    cs = rcos[static_cast<size_t>(start) * (hd / 2u) + pair];
+    sn = rsin[static_cast<size_t>(start) * (hd / 2u) + pair];
+  }
+  // chunk k of this thread: row (tid / 16) + 16k, floats 4 (tid % 16) ..;
+  // rows from `start` on read row 0 (keys, not stored) or the new value row
+  const uint32_t col = tid & 15u;
+  f32x4 kc[NK], vc[NK];
+#pragma unroll
+  for (uint32_t k = 0; k < NK; k++) {
+    const uint32_t row = (tid >> 4) + 16u * k;
+    kc[k] = reinterpret_cast<const f32x4*>(kcache + static_cast<size_t>(row < start ? row : 0u) * kv + off)[col];
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < NK; k++) {
+    const uint32_t row = (tid >> 4) + 16u * k;
+    const float* src = row < start ? vcache + static_cast<size_t>(row) * kv + off : vnew;
+    vc[k] = reinterpret_cast<const f32x4*>(src)[col];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // qkv_post_kernel's rotation: the query to qh, the new key to key row start
+  if (tid < 64u) {
+    const float hs = hi * sn, ls = lo * sn;
+    const float nlo = __builtin_fmaf(lo, cs, -hs), nhi = __builtin_fmaf(hi, cs, ls);
+    float* dst = tid < 32u ? qh : ka + start * kKeyStride;
+    dst[2u * pair] = nlo;
+    dst[2u * pair + 1u] = nhi;
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < NK; k++) {
+    const uint32_t row = (tid >> 4) + 16u * k;
+    if (row < start) reinterpret_cast<f32x4*>(ka + row * kKeyStride)[col] = kc[k];
+  }
+  __syncthreads();
+  if (appends) {
+    if (tid < 16u)
+      reinterpret_cast<f32x4*>(kcache + static_cast<size_t>(start) * kv + off)[tid] =
+          reinterpret_cast<const f32x4*>(ka + start * kKeyStride)[tid];
+    else if (tid >= 64u && tid < 80u)
+      reinterpret_cast<f32x4*>(vcache + static_cast<size_t>(start) * kv + off)[tid - 64u] =
+          reinterpret_cast<const f32x4*>(vnew)[tid - 64u];
+  }
+
+  // thread i scores row i (rows <= cap <= the workgroup's threads)
+  float sc = 0.0f, mx = -INFINITY;
+  if (tid < rows) {
+    f32x4 kk[16];
+#pragma unroll
+    for (int c = 0; c < 16; c++) kk[c] = reinterpret_cast<const f32x4*>(ka + tid * kKeyStride)[c];
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    lanes64(qh, kk, acc);
+    sc = score_from_lanes(acc, -0.0f, scale);
+    mx = fmaxf(mx, sc);
+  }
+  // softmax_rows' maximum
+  mx = max_key_float(half_max_u32(max_key(mx)));
+  mx = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
+             __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)));
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();  // and every key has been read
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+#pragma unroll
+  for (uint32_t k = 0; k < NK; k++) {
+    const uint32_t row = (tid >> 4) + 16u * k;
+    reinterpret_cast<f32x4*>(ka + row * 64u)[col] = vc[k];
+  }
+  // the exps, -0.0 (the sum's identity) up to a multiple of 32
+  if (tid < rows)
+    ws[wave_sum_index(tid)] = expf_ref(sc - mx);
+  else if (tid < ((rows + 31u) & ~31u))
+    ws[wave_sum_index(tid)] = -0.0f;
+  __syncthreads();
+  if (wave != 0) return;
+  // portable/norm.rs: the sum from 0.0 in order, then each exp over it
+  const float sum = ordered_sum_wave(ws, rows, 0.0f);
+  for (uint32_t i = lane; i < rows; i += 64u) w[i] = __fdiv_rn(ws[wave_sum_index(i)], sum);
+  mixed[static_cast<size_t>(h) * hd + lane] = mix_lds(ka, w, rows, lane);
+}
+
 // hf[t][e] = silu(gate) * up, both stored by weight row (x[e*n + t])
 // (feed_forward.rs:51-66, portable/elementwise.rs:6-9).
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const float* up, uint32_t n, uint32_t len,
@@ -951,7 +1123,29 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start,
     float* vc = d->values + l * c.context_length * kv;
     const size_t att_lds = attention_lds_floats(start + 1) * 4u;
     const uint32_t group = static_cast<uint32_t>(c.head_count / c.head_count_kv);
-    if (hd == 64u) {
+    if (hd == 64u && start + 1u <= kStepLdsRows && tuning().attn_lds) {
+      // 16-row groups, rounded up to an even count: 7 kernels cover every row count
+      const uint32_t nk = ((static_cast<uint32_t>(start) + 1u + 31u) / 32u) * 2u;
+      void* k = nk == 2u ? reinterpret_cast<void*>(attention_step_lds_kernel<2>)
+              : nk == 4u ? reinterpret_cast<void*>(attention_step_lds_kernel<4>)
+              : nk == 6u ? reinterpret_cast<void*>(attention_step_lds_kernel<6>)
+              : nk == 8u ? reinterpret_cast<void*>(attention_step_lds_kernel<8>)
+              : nk == 10u ? reinterpret_cast<void*>(attention_step_lds_kernel<10>)
+              : nk == 12u ? reinterpret_cast<void*>(attention_step_lds_kernel<12>)
+                          : reinterpret_cast<void*>(attention_step_lds_kernel<14>);
+      const float* qr = d->qr;
+      const float* kr = d->kr;
+      const float* vr = d->vr;
+      const float* rc = d->rope_cos;
+      const float* rs = d->rope_sin;
+      uint32_t kv32 = static_cast<uint32_t>(kv), st = static_cast<uint32_t>(start);
+      float sc = scale;
+      uint32_t gr = group;
+      float* mixed = d->mixed;
+      void* args[] = {&qr, &kr, &vr, &rc, &rs, &kc, &vc, &kv32, &gr, &sc, &st, &mixed};
+      RHD(hipLaunchKernel(k, dim3(static_cast<uint32_t>(c.head_count)), dim3(kAttnThreads), args,
+                          attention_step_lds_bytes(nk), s));
+    } else if (hd == 64u) {
       hipLaunchKernelGGL(attention_step_kernel, dim3(static_cast<uint32_t>(c.head_count)), dim3(kAttnThreads),
                          att_lds, s, d->qr, d->kr, d->vr, d->rope_cos, d->rope_sin, kc, vc, kv, group, scale,
                          static_cast<uint32_t>(start), d->mixed);

@@ -89,6 +89,7 @@ struct Tuning {
   bool i2s_one = true;     // RUSTICIDE_HIP_I2S_ONE=0: one token on the two-token kernel
   int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=64|128
   bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
+  bool attn_lds = true;    // RUSTICIDE_HIP_ATTN_LDS=0: the tiled attention step only
 };
 const Tuning& tuning();
 void load_tuning();

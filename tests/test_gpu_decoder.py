@@ -127,6 +127,33 @@ def test_batched_forward_graph_replays_match_the_eager_run(ctx, monkeypatch):
     cpu.close()
 
 
+def test_one_token_attention_kernels_agree_at_every_length(ctx, monkeypatch):
+    # a one-token step up to 224 cached rows runs the LDS-staged attention
+    # kernel (RUSTICIDE_HIP_ATTN_LDS=0 keeps the tiled one); every length from
+    # 1 to 241 rows, across all seven of its row-count variants and past its
+    # limit, gives the tiled kernel's bits and the CPU path's
+    model = synth.decoder_model(dict(SMALL, context_length=256), seed=16)
+    lds, tiled = R.Decoder(ctx, model), R.Decoder(ctx, model)
+    cpu = O.Decoder(model, threads=8)
+    tokens = np.random.default_rng(9).integers(0, SMALL["vocab_size"], 241).astype(np.uint32)
+    for pos, tok in enumerate(tokens):
+        monkeypatch.setenv("RUSTICIDE_HIP_ATTN_LDS", "1")
+        R.reload_tuning()
+        a = lds.forward(int(tok), pos)
+        monkeypatch.setenv("RUSTICIDE_HIP_ATTN_LDS", "0")
+        R.reload_tuning()
+        b = tiled.forward(int(tok), pos)
+        assert same_bits(a, b), f"rows {pos + 1}: max |diff| {diff(a, b)}"
+        c = cpu.forward(int(tok), pos)
+        if pos in (0, 1, 31, 32, 100, 191, 223, 224, 240):
+            assert same_bits(a, c), f"rows {pos + 1}: max |diff| {diff(a, c)}"
+    monkeypatch.delenv("RUSTICIDE_HIP_ATTN_LDS")
+    R.reload_tuning()
+    lds.close()
+    tiled.close()
+    cpu.close()
+
+
 def test_graph_cache_evicts_within_one_generate_call(ctx, monkeypatch):
     # the decoder keeps 8 graphs. A first call caches the 8 prefill chunks of
     # a 512-token prompt; a second call on a 583-token prompt replays those 8
