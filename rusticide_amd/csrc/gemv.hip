@@ -1117,6 +1117,156 @@ __global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const 
   }
 }
 
+// The team sum of gemv_i2s_one_kernel's row accumulators, left in every lane
+// of the team (wrapping).
+template <int LPR>
+__device__ __forceinline__ uint32_t i2s_team_sum(uint32_t acc) {
+  acc += dpp<0xB1>(acc);
+  acc += dpp<0x4E>(acc);
+  if constexpr (LPR >= 8) acc += dpp<0x141>(acc);
+  if constexpr (LPR >= 16) acc += dpp<0x140>(acc);
+  if constexpr (LPR >= 32) acc += static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(acc), 0x401F));
+  if constexpr (LPR == 64)
+    acc = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(acc), 0)) +
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(acc), 32));
+  return acc;
+}
+
+// The sum of v over the wave, in every lane (wrapping).
+__device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  v += static_cast<uint32_t>(__builtin_amdgcn_ds_swizzle(static_cast<int>(v), 0x401F));
+  return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 0)) +
+         static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 32));
+}
+
+// I2_S x a pre-quantized I8_S activation (Q8Kind::Row), T tokens: the layout
+// of gemv_i2s_one_kernel with the quantization replaced by a copy. Every load
+// is unconditional: the tokens' quants (nkeep bytes each, at most 8192) and
+// the 32-block sums of the job's blocks go out first, the weights after
+// them; the quants go to LDS and each token's sum of quants (ternary.rs:39,41
+// subtracts it) is reduced once per workgroup.
+// LDS: act [T][nkeep] i8 | qsw [T][waves] i32
+template <int T, int LPR, int CPL>
+__global__ __launch_bounds__(256) void gemv_i2s_q8_kernel(GemvJobs jobs, Q8Dev q, uint32_t nkeep, size_t tokens,
+                                                          size_t t0, int32_t* raw) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  constexpr uint32_t kWaves = kThreads / 64u;
+  constexpr uint32_t R = kThreads / static_cast<uint32_t>(LPR);
+  constexpr uint32_t ACH = 2u * static_cast<uint32_t>(T);  // 16-byte chunks a thread: nkeep <= 8192
+  int8_t* act = reinterpret_cast<int8_t*>(lds);
+  int32_t* qsw = reinterpret_cast<int32_t*>(lds + T * nkeep);
+
+  const GemvJob& J = jobs.j[find_job(jobs)];
+  const uint8_t* const wbase = J.w;
+  const uint32_t stride = J.stride, rows = J.rows, nb = J.nb;
+  float* const out = J.out;
+  const size_t out_len = J.out_len;
+  const float scale = J.scale;
+  const uint32_t cl = threadIdx.x & static_cast<uint32_t>(LPR - 1);
+  const uint32_t row = (blockIdx.x - J.wg_begin) * R + threadIdx.x / static_cast<uint32_t>(LPR);
+  const uint32_t nchunk = 2u * nb;
+  const uint32_t qs32 = static_cast<uint32_t>(q.qstride), bs32 = static_cast<uint32_t>(q.bstride);
+
+  // the tokens' quants: chunk c of token t is c + t * cpt (past the last,
+  // the last chunk again, not stored)
+  const uint32_t cpt = nkeep / 16u, nch = static_cast<uint32_t>(T) * cpt;
+  u32x4 ar[ACH];
+#pragma unroll
+  for (uint32_t i = 0; i < ACH; i++) {
+    const uint32_t c = min(threadIdx.x + i * kThreads, nch - 1u);
+    const uint32_t t = T == 1 ? 0u : c / cpt, k = c - t * cpt;
+    ar[i] = load16(reinterpret_cast<const uint8_t*>(q.quants) + (t0 + t) * qs32 + 16u * k);
+  }
+  // the job's 32-block sums, one a thread and token (4 nb <= 256)
+  int32_t sv[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) sv[t] = q.sums[(t0 + t) * bs32 + min(threadIdx.x, 4u * nb - 1u)];
+  // the weights (rows past the job's last read its last row)
+  const uint8_t* wrow = wbase + __umul24(min(row, rows - 1u), stride);
+  u32x4 w[CPL];
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t c = min(cl + static_cast<uint32_t>(i * LPR), nchunk - 1u);
+    w[i] = load16(wrow + 16u * c);
+  }
+  __asm__ volatile("" ::"s"(out), "s"(out_len), "s"(scale), "s"(tokens), "s"(t0), "s"(raw));
+  __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+  for (uint32_t i = 0; i < ACH; i++) {
+    const uint32_t c = threadIdx.x + i * kThreads;
+    if (c < nch) {
+      const uint32_t t = T == 1 ? 0u : c / cpt, k = c - t * cpt;
+      *reinterpret_cast<u32x4*>(act + t * nkeep + 16u * k) = ar[i];
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const uint32_t ws = wave_sum_u32(threadIdx.x < 4u * nb ? static_cast<uint32_t>(sv[t]) : 0u);
+    if ((threadIdx.x & 63u) == 0) qsw[t * kWaves + (threadIdx.x >> 6)] = static_cast<int32_t>(ws);
+  }
+  __syncthreads();
+
+  uint32_t acc[T];
+#pragma unroll
+  for (int t = 0; t < T; t++) acc[t] = 0;
+#pragma unroll
+  for (int i = 0; i < CPL; i++) {
+    const uint32_t craw = cl + static_cast<uint32_t>(i * LPR);
+    const uint32_t c = min(craw, nchunk - 1u);
+    const uint32_t live = craw < nchunk ? 0xffffffffu : 0u;
+    uint32_t c6[4], c4[4], c2[4], c0[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const uint32_t wk = w[i][k] & live;
+      c6[k] = (wk >> 2) & 0x30303030u;  // code of shift 6, times 16
+      c4[k] = wk & 0x30303030u;         // shift 4, times 16
+      c2[k] = wk & 0x0C0C0C0Cu;         // shift 2, times 4
+      c0[k] = wk & 0x03030303u;         // shift 0
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+      const int8_t* a = act + t * nkeep + 128u * (c >> 1) + 16u * (c & 1u);
+      const u32x4 a0 = *reinterpret_cast<const u32x4*>(a);
+      const u32x4 a1 = *reinterpret_cast<const u32x4*>(a + 32u);
+      const u32x4 a2 = *reinterpret_cast<const u32x4*>(a + 64u);
+      const u32x4 a3 = *reinterpret_cast<const u32x4*>(a + 96u);
+      int32_t P16 = 0, P4 = 0, P1 = 0;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        P16 = dot4(c6[k], a0[k], P16);
+        P16 = dot4(c4[k], a1[k], P16);
+        P4 = dot4(c2[k], a2[k], P4);
+        P1 = dot4(c0[k], a3[k], P1);
+      }
+      acc[t] += static_cast<uint32_t>(P1 + (P4 >> 2) + (P16 >> 4));
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < T; t++) {
+    const uint32_t v = i2s_team_sum<LPR>(acc[t]);
+    uint32_t qtotal = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < kWaves; u++) qtotal += static_cast<uint32_t>(qsw[t * kWaves + u]);
+    const size_t idx = static_cast<size_t>(row) * tokens + t0 + t;
+    if (cl == 0 && row < rows && idx < out_len) {
+      // ternary.rs:39,41: sum(code*q) - sum(q), wrapping
+      const int32_t dot = static_cast<int32_t>(v - qtotal);
+      if (raw) {
+        raw[idx] = dot;
+      } else {
+        // ternary.rs:53-57: (dot as f32) / s * scale; 0 without a scale
+        const float s = q.n_blocks ? q.scales[(t0 + t) * bs32] : 0.0f;
+        out[idx] = q.n_blocks ? __fdiv_rn(static_cast<float>(dot), s) * scale : 0.0f;
+      }
+    }
+  }
+}
+
 // Dense f32 ---------------------------------------------------------------
 // rusticide-simd/src/float.rs:23-36: eight fused lanes over the whole chunks,
 // the lanes added in order from -0.0, then the unfused tail (from -0.0).
@@ -1347,6 +1497,9 @@ uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_ro
 
 // One grouped launch. FUSED: the k-quant kernels quantize x themselves
 // (T <= kMaxFusedTokens); otherwise they read the activation q holds.
+template <int T>
+hipError_t launch_i2s_q8(GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0, hipStream_t s, int32_t* raw);
+
 template <int T, bool FUSED>
 hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float* x, size_t width,
                     size_t tokens, size_t t0, hipStream_t s, int32_t* raw, const NormIn* norm = nullptr) {
@@ -1425,6 +1578,10 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
                     const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};
     return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
+  }
+  if (tuning().i2s_one) {
+    const hipError_t e = launch_i2s_q8<T>(jobs, q, tokens, t0, s, raw);
+    if (e != hipErrorNotSupported) return e;
   }
   hipLaunchKernelGGL(gemv_i2s_kernel<T>, dim3(wgs), dim3(kThreads), lds, s, jobs, q, R, nbl, tokens, t0, raw);
   return hipGetLastError();
@@ -1584,6 +1741,60 @@ hipError_t launch_i2s_one(GemvJobs jobs, const float* x, size_t width, size_t to
   const size_t lds = nkeep + 4u * (4u + 1u) * (kThreads / 64u);
   const float* xt = x + t0 * width;
   void* args[] = {&jobs, const_cast<float**>(&xt), const_cast<uint32_t*>(&n), &nkeep, &tokens, &t0, &raw};
+  return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
+}
+
+template <int T, int LPR>
+void* i2s_q8_pick(uint32_t cpl) {
+  if constexpr (T == 1) {
+    switch (cpl) {
+      case 1: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 1>);
+      case 2: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 2>);
+      case 3: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 3>);
+      case 4: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 4>);
+      case 5: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 5>);
+      case 6: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 6>);
+      case 7: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 7>);
+      case 8: return reinterpret_cast<void*>(gemv_i2s_q8_kernel<1, LPR, 8>);
+      default: return nullptr;
+    }
+  } else {
+    return cpl <= 4u ? reinterpret_cast<void*>(gemv_i2s_q8_kernel<T, LPR, 4>)
+         : cpl <= 8u ? reinterpret_cast<void*>(gemv_i2s_q8_kernel<T, LPR, 8>)
+                     : nullptr;
+  }
+}
+
+// T tokens of I2_S against a pre-quantized activation on gemv_i2s_q8_kernel;
+// hipErrorNotSupported for shapes it does not take.
+template <int T>
+hipError_t launch_i2s_q8(GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0, hipStream_t s, int32_t* raw) {
+  uint32_t nbmax = 0, nbmin = ~0u;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    nbmax = jobs.j[i].nb > nbmax ? jobs.j[i].nb : nbmax;
+    nbmin = jobs.j[i].nb < nbmin ? jobs.j[i].nb : nbmin;
+  }
+  if (jobs.n == 0 || nbmin == 0 || nbmax > 64u) return hipErrorNotSupported;
+  // 32-bit activation offsets (the launchers keep tokens * qstride below 2^32)
+  if ((t0 + T) * q.qstride > 0xffffffffu || (t0 + T) * q.bstride > 0xffffffffu) return hipErrorNotSupported;
+  const uint32_t nchunk = 2u * nbmax;
+  uint32_t lpr = 8;
+  while (lpr < 64u && (nchunk + lpr - 1u) / lpr > 8u) lpr *= 2u;
+  if (const int v = tuning().i2s_lpr) lpr = static_cast<uint32_t>(v);
+  const uint32_t cpl = (nchunk + lpr - 1u) / lpr;
+  void* k = lpr == 8u ? i2s_q8_pick<T, 8>(cpl) : lpr == 16u ? i2s_q8_pick<T, 16>(cpl)
+          : lpr == 32u ? i2s_q8_pick<T, 32>(cpl) : i2s_q8_pick<T, 64>(cpl);
+  if (!k) return hipErrorNotSupported;
+  const uint32_t R = kThreads / lpr;
+  uint32_t wgs = 0;
+  for (uint32_t i = 0; i < jobs.n; i++) {
+    jobs.j[i].wg_begin = wgs;
+    wgs += (jobs.j[i].rows + R - 1u) / R;
+  }
+  if (wgs == 0) return hipSuccess;
+  uint32_t nkeep = nbmax * 128u;
+  const size_t lds = static_cast<size_t>(T) * nkeep + static_cast<size_t>(T) * 4u * (kThreads / 64u);
+  void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &nkeep, &tokens, &t0, &raw};
   return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
 }
 

@@ -407,12 +407,16 @@ def hostile_rows(cols):
     return rows
 
 
+@pytest.mark.parametrize("family", ["fused", "lds"])
 @pytest.mark.parametrize("lanes", ["8", "16", "32", "64", "two-token"])
-def test_i2s_one_token_kernel_at_every_team_width(ctx, tuning, lanes):
+def test_i2s_one_token_kernel_at_every_team_width(ctx, tuning, lanes, family):
     # the one-token kernel with 8..64 lanes per row (and the two-token kernel
-    # it replaces): ragged row counts, 128 to 8192 values, hostile
-    # activations, and one launch over matrices that cover different numbers
-    # of blocks of the activation (ternary.rs:21-26)
+    # it replaces), fused or on a separately quantized activation: ragged row
+    # counts, 128 to 8192 values, hostile activations, and one launch over
+    # matrices that cover different numbers of blocks of the activation
+    # (ternary.rs:21-26); on the pre-quantized path also 3 to 8 tokens at once
+    if family == "lds":
+        tuning.set("RUSTICIDE_HIP_GEMV", "lds")
     if lanes == "two-token":
         tuning.set("RUSTICIDE_HIP_I2S_ONE", "0")
     else:
@@ -437,6 +441,17 @@ def test_i2s_one_token_kernel_at_every_team_width(ctx, tuning, lanes):
         R.matmul_batch(ctx, x, 1, list(zip(mats, outs)))
         for (r, c), d, out in zip(specs, datas, outs):
             assert_same_bits(out, oracle_matmul(36, d, r, c, x, 1, scale=0.02), f"{r}x{c} width {width}")
+    if family == "lds":
+        rows, cols = 300, 2560
+        data = synth.i2s_matrix(rows, cols, seed=5)
+        m = R.Matrix.load(ctx, 36, data, rows, cols)
+        for tokens in (3, 5, 8):
+            x = np.concatenate([synth.normal_f32(cols * (tokens - 1), seed=tokens), hostile_rows(cols)[0]])
+            raw = ctx.ternary_dot_i32(m, x, tokens)
+            assert np.array_equal(raw, O.ternary_dot_matrix_i32(data[: rows * cols // 4], cols // 4, x, tokens))
+            out = np.full(rows * tokens, 7.0, np.float32)
+            R.matmul_batch(ctx, x, tokens, [(m, out)])
+            assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, tokens, scale=0.02), f"tokens {tokens}")
 
 
 # ------------------------------------------------------------ batch rules
