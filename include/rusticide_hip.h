@@ -255,8 +255,9 @@ typedef struct rh_decoder_weights {
 typedef struct rh_decoder rh_decoder;
 
 /* Decoder::new (decoder.rs:28-46): validates the config (config.rs:55-80;
- * this build also needs head_dim <= 64, embedding_length <= 8192 and
- * context_length <= 8064), copies
+ * this build also needs head_dim <= 128, embedding_length <= 8192 and the
+ * attention weights of the whole context in one workgroup's LDS:
+ * context_length <= 32,576 with gfx950's 160 KiB), copies
  * the norms, computes the RoPE
  * angle table and allocates the f32 KV cache for context_length positions. */
 rh_status rh_decoder_new(rh_ctx *ctx, const rh_decoder_config *config, const rh_decoder_weights *weights,

@@ -234,11 +234,18 @@ __global__ __launch_bounds__(256) void qkv_post_kernel(const float* qr, const fl
 
 constexpr uint32_t kAttnThreads = 256;
 constexpr uint32_t kVTile = 64;  // value rows per LDS tile
-constexpr size_t kMaxAttentionLds = 65536;  // bytes of dynamic LDS per workgroup
 
-// LDS floats attention_kernel needs for `rows` cached rows: the query head,
-// a reduction area, the weights, and two value tiles.
-inline size_t attention_lds_floats(size_t rows) { return 128u + ((rows + 3u) & ~size_t{3}) + 2u * kVTile * 64u; }
+constexpr uint32_t kMaxHeadDim = 128;
+
+// LDS floats attention_kernel needs for `rows` cached rows: the query head
+// (up to kMaxHeadDim), a reduction area, the weights, and two value tiles of
+// kVTile * 64 floats (kVTile rows up to head_dim 64, half as many above).
+inline size_t attention_lds_floats(size_t rows) {
+  return kMaxHeadDim + 64u + ((rows + 3u) & ~size_t{3}) + 2u * kVTile * 64u;
+}
+
+// Value rows per tile of attention_kernel.
+__host__ __device__ constexpr uint32_t tile_rows(uint32_t hd) { return hd <= 64u ? kVTile : kVTile / 2u; }
 
 // Value rows r0..r0+count of one kv head into registers, one tile's share
 // per thread (HD = 64: 16 f32x4 per row, 16 threads a row).
@@ -357,7 +364,8 @@ __device__ __forceinline__ float mix_tile(const float* cur, const float* wr, uin
 // One workgroup per (query head, token): scores over cached rows
 // 0..=start+t, softmax, then the weighted sum of value rows
 // (attention.rs:41-57,189-207). HD = 64 specializes head_dim; HD = 0 reads
-// it at run time (any even head_dim <= 64).
+// it at run time (any even head_dim <= kMaxHeadDim; above 64 the value tiles
+// hold 32 rows and the row chains of output lanes 64.. run on wave 1).
 template <uint32_t HD>
 __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q, const float* kcache,
                                                                  const float* vcache, uint32_t width, uint32_t kv,
@@ -365,11 +373,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
                                                                  uint32_t start, float* mixed) {
   extern __shared__ __align__(16) float sh[];
   const uint32_t hd = HD ? HD : head_dim;
-  const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+  const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const uint32_t rows = start + t + 1u;
-  float* qh = sh;          // [64]
-  float* red = sh + 64;    // [64]
-  float* w = sh + 128;     // [rows rounded up to 4]
+  const uint32_t tr = tile_rows(hd);
+  float* qh = sh;                      // [kMaxHeadDim]
+  float* red = sh + kMaxHeadDim;       // [64]
+  float* w = red + 64;                 // [rows rounded up to 4]
   float* vt = w + ((rows + 3u) & ~3u);  // [2][kVTile * 64]
   const uint32_t off = (h / group) * hd;
   if (tid < hd) qh[tid] = q[static_cast<size_t>(t) * width + h * hd + tid];
@@ -405,23 +414,23 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
   // mix_rows (float.rs:52-62): out starts at 0.0, each row fused in order.
   // Value tiles are staged through LDS by every thread, a tile ahead of
   // the first wave's chain of fused adds.
-  const uint32_t tiles = (rows + kVTile - 1u) / kVTile;
+  const uint32_t tiles = (rows + tr - 1u) / tr;
   VTileRegs<HD> regs;
-  regs.load(vcache, kv, off, hd, 0u, rows < kVTile ? rows : kVTile);
-  regs.store(vt, hd, rows < kVTile ? rows : kVTile);
+  regs.load(vcache, kv, off, hd, 0u, rows < tr ? rows : tr);
+  regs.store(vt, hd, rows < tr ? rows : tr);
   __syncthreads();
   float acc = 0.0f;
   for (uint32_t tile = 0; tile < tiles; tile++) {
-    const uint32_t r0 = tile * kVTile;
-    const uint32_t count = rows - r0 < kVTile ? rows - r0 : kVTile;
+    const uint32_t r0 = tile * tr;
+    const uint32_t count = rows - r0 < tr ? rows - r0 : tr;
     const bool more = tile + 1u < tiles;
-    const uint32_t nr0 = r0 + kVTile, ncount = more ? (rows - nr0 < kVTile ? rows - nr0 : kVTile) : 0u;
+    const uint32_t nr0 = r0 + tr, ncount = more ? (rows - nr0 < tr ? rows - nr0 : tr) : 0u;
     if (more) regs.load(vcache, kv, off, hd, nr0, ncount);
-    if (wave == 0 && lane < hd) acc = mix_tile(vt + (tile & 1u) * kVTile * 64u, w + r0, count, hd, lane, acc);
+    if (tid < hd) acc = mix_tile(vt + (tile & 1u) * kVTile * 64u, w + r0, count, hd, tid, acc);
     if (more) regs.store(vt + ((tile + 1u) & 1u) * kVTile * 64u, hd, ncount);
     __syncthreads();
   }
-  if (wave == 0 && lane < hd) mixed[static_cast<size_t>(t) * width + h * hd + lane] = acc;
+  if (tid < hd) mixed[static_cast<size_t>(t) * width + h * hd + tid] = acc;
 }
 
 // Value tile rows r0.. (below `rows`) of one kv head for head_dim 64, a
@@ -1287,14 +1296,18 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
   *out = nullptr;
   const rh_decoder_config& c = *config;
   // DecoderConfig::validate (transformer/src/config.rs:55-80), plus this
-  // kernel set's limits: head_dim <= 64, embedding_length <= 8192, attention
-  // weights for the whole context in LDS (context_length <= 8064),
-  // f32/Q4_K/Q6_K embedding rows
+  // kernel set's limits: head_dim <= 128, embedding_length <= 8192, attention
+  // weights for the whole context in one workgroup's LDS (160 KiB on gfx950:
+  // context_length <= 32,576), f32/Q4_K/Q6_K embedding rows
+  int lds_max = 0;
+  if (hipSetDevice(ctx_device(ctx)) != hipSuccess ||
+      hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, ctx_device(ctx)) != hipSuccess)
+    return RH_ERR_DEVICE;
   if (c.head_count == 0 || c.head_count_kv == 0 || c.head_count % c.head_count_kv != 0 || c.head_dim == 0 ||
       c.head_dim % 2 != 0 || c.head_count * c.head_dim != c.embedding_length || c.block_count == 0 ||
-      c.feed_forward_length == 0 || c.context_length == 0 || c.vocab_size == 0 || c.head_dim > 64 ||
+      c.feed_forward_length == 0 || c.context_length == 0 || c.vocab_size == 0 || c.head_dim > kMaxHeadDim ||
       c.embedding_length > kMaxNormPer * kNormThreads ||
-      attention_lds_floats(c.context_length) * 4u > kMaxAttentionLds)
+      attention_lds_floats(c.context_length) * 4u > static_cast<size_t>(lds_max))
     return RH_ERR_INVALID_CONFIG;
   const uint32_t et = rh_matrix_type(weights->token_embd);
   if ((et != RH_TYPE_F32 && et != RH_TYPE_Q4_K && et != RH_TYPE_Q6_K) ||

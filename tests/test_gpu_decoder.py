@@ -176,9 +176,11 @@ def test_graph_cache_evicts_within_one_generate_call(ctx, monkeypatch):
     eager.close()
 
 
-@pytest.mark.parametrize("head_dim,heads,kv_heads,width", [(32, 8, 2, 256), (48, 16, 4, 768)])
+@pytest.mark.parametrize("head_dim,heads,kv_heads,width",
+                         [(32, 8, 2, 256), (48, 16, 4, 768), (80, 16, 4, 1280), (128, 4, 2, 512)])
 def test_head_dims_other_than_64_take_the_generic_attention(ctx, norm_path, head_dim, heads, kv_heads, width):
-    # attention_kernel<0> (any even head_dim up to 64) in the batched and the
+    # attention_kernel<0> (any even head_dim up to 128; above 64, 32-row value
+    # tiles and a second wave of output lanes) in the batched and the
     # one-token forwards, against the CPU path
     cfg = dict(SMALL, embedding_length=width, head_count=heads, head_count_kv=kv_heads, head_dim=head_dim)
     model = synth.decoder_model(cfg, seed=head_dim)
@@ -190,6 +192,26 @@ def test_head_dims_other_than_64_take_the_generic_attention(ctx, norm_path, head
     assert np.array_equal(gpu.generate_greedy(tokens, 12), cpu.generate_greedy(tokens, 12))
     gpu.close()
     cpu.close()
+
+
+def test_contexts_past_64_kib_of_attention_lds(ctx):
+    # the attention kernels keep a context's weights in one workgroup's LDS:
+    # at 9,000 rows that is more than 64 KiB (gfx950 gives a workgroup
+    # 160 KiB). A batch's last logits equal those of the same tokens fed one
+    # at a time (decoder_batch_tests.rs:50-66), here deep in the context
+    model = synth.decoder_model(dict(SMALL, context_length=9100), seed=17)
+    batched, single = R.Decoder(ctx, model), R.Decoder(ctx, model)
+    tokens = np.random.default_rng(10).integers(0, SMALL["vocab_size"], 8969).astype(np.uint32)
+    for d in (batched, single):
+        for start in range(0, 8960, 64):
+            d.forward_batch(tokens[start:start + 64], start)
+    b = batched.forward_batch(tokens[8960:], 8960)
+    for pos in range(8960, 8969):
+        s_ = single.forward(int(tokens[pos]), pos)
+    assert same_bits(b, s_), diff(b, s_)
+    assert np.all(np.isfinite(b))
+    batched.close()
+    single.close()
 
 
 def test_decoder_errors_mirror_model_error(ctx):
