@@ -435,8 +435,8 @@ __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const 
 }
 
 int token_tile(size_t tokens) {
-  // Tuning::gemm_bn forces the token tile, for tuning
-  if (const int bn = tuning().gemm_bn) return bn;
+  // Tuning::gemm_bn forces the token tile (64 or 128 here), for tuning
+  if (const int bn = tuning().gemm_bn) return bn == 256 ? 128 : bn;
   return tokens >= 512 ? 128 : 64;
 }
 

@@ -39,10 +39,10 @@ __device__ __forceinline__ uint32_t job_index(const GemvJobs& jobs, uint32_t wg)
   return j;
 }
 
-// Four 2-bit codes (one per byte, 0..3) minus one, bytewise without borrows:
-// each byte of (x | 0x80) is at least 0x80, so subtracting 1 stays in it.
+// Four 2-bit codes (one per byte, 0..3) minus one: a byte table lookup
+// (v_perm_b32 picks byte c of 0x020100FF: -1, 0, 1, 2 for codes 0..3).
 __device__ __forceinline__ uint32_t codes_minus_one(uint32_t x) {
-  return ((x | 0x80808080u) - 0x01010101u) ^ 0x80808080u;
+  return __builtin_amdgcn_perm(0u, 0x020100FFu, x);
 }
 
 template <int BN>
@@ -198,7 +198,13 @@ hipError_t launch_bn(GemvJobs jobs, const Q8Dev& q, size_t tokens, int32_t* raw,
 
 hipError_t launch_gemm_i2s(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, int32_t* raw, hipStream_t s) {
   if (tokens == 0 || jobs.n == 0) return hipSuccess;
-  return tokens >= 256 ? launch_bn<128>(jobs, q, tokens, raw, s) : launch_bn<64>(jobs, q, tokens, raw, s);
+  // 64 tokens a workgroup up to 1023 tokens (512: 26.4 against 31.8 us at
+  // 128), 128 from 1024 (2048: 77-79 against 88 us at 64; 256 is slower at
+  // every size: one workgroup per CU); tuning().gemm_bn forces it
+  const int bn = tuning().gemm_bn ? tuning().gemm_bn : tokens >= 1024 ? 128 : 64;
+  return bn == 256 ? launch_bn<256>(jobs, q, tokens, raw, s)
+       : bn == 128 ? launch_bn<128>(jobs, q, tokens, raw, s)
+                   : launch_bn<64>(jobs, q, tokens, raw, s);
 }
 
 }  // namespace rh

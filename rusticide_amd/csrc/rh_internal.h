@@ -87,7 +87,7 @@ struct Tuning {
   int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 (two-token kernel)
   int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
   bool i2s_one = true;     // RUSTICIDE_HIP_I2S_ONE=0: one token on the two-token kernel
-  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=64|128
+  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=64|128 (k-quants), 64|128|256 (I2_S)
   bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
   bool attn_lds = true;    // RUSTICIDE_HIP_ATTN_LDS=0: the tiled attention step only
 };
