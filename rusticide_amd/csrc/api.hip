@@ -372,6 +372,8 @@ void load_tuning() {
   const int lpr = env_int("RUSTICIDE_HIP_I2S_LPR", 0);
   t.i2s_lpr = lpr == 8 || lpr == 16 || lpr == 32 || lpr == 64 ? lpr : 0;
   t.i2s_one = env_int("RUSTICIDE_HIP_I2S_ONE", 1) != 0;
+  const int nt = env_int("RUSTICIDE_HIP_I2S_NT", 0);
+  t.i2s_nt = nt == 256 || nt == 512 || nt == 1024 ? nt : 0;
   const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
   t.gemm_bn = bn == 64 || bn == 128 || bn == 256 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;

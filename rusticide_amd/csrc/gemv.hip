@@ -701,23 +701,25 @@ constexpr uint32_t kFusedRowPasses = 8;  // rows of up to 8192 values
 
 // Workgroup maxima of (p, m) over its 4 waves; `slot` alternates between
 // calls so that one barrier per reduction suffices.
+template <uint32_t NW = kThreads / 64u>  // waves in the workgroup
 __device__ __forceinline__ void wg_max_pair(int32_t& p, uint32_t& m, int32_t* red, uint32_t slot) {
   p = half_max_i32(p);
   m = half_max_u32(m);
   p = max(__builtin_amdgcn_readlane(p, 0), __builtin_amdgcn_readlane(p, 32));
   m = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 0)),
           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 32)));
-  int32_t* r = red + slot * 2u * (kThreads / 64u);
+  int32_t* r = red + slot * 2u * NW;
   if ((threadIdx.x & 63u) == 0) {
     r[threadIdx.x >> 6] = p;
-    r[(kThreads / 64u) + (threadIdx.x >> 6)] = static_cast<int32_t>(m);
+    r[NW + (threadIdx.x >> 6)] = static_cast<int32_t>(m);
   }
   __syncthreads();
   p = r[0];
-  m = static_cast<uint32_t>(r[kThreads / 64u]);
-  for (uint32_t w = 1; w < kThreads / 64u; w++) {
+  m = static_cast<uint32_t>(r[NW]);
+#pragma unroll
+  for (uint32_t w = 1; w < NW; w++) {
     p = max(p, r[w]);
-    m = max(m, static_cast<uint32_t>(r[(kThreads / 64u) + w]));
+    m = max(m, static_cast<uint32_t>(r[NW + w]));
   }
 }
 
@@ -929,12 +931,13 @@ __global__ __launch_bounds__(256) void gemv_i2s_fused_kernel(GemvJobs jobs, cons
 // holds chunks l, l + LPR, ... (CPL of them) of 16 bytes. Job fields are read
 // into registers once.
 // LDS: act [nkeep] i8 | red [2 slots][2][waves] i32 | qsw [waves] i32
-template <int LPR, int CPL, bool ONE_JOB>
-__global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const float* __restrict__ x, uint32_t n,
+template <uint32_t NT, int LPR, int CPL, bool ONE_JOB>
+__global__ __launch_bounds__(NT) void gemv_i2s_one_kernel(GemvJobs jobs, const float* __restrict__ x, uint32_t n,
                                                            uint32_t nkeep, size_t tokens, size_t t0, int32_t* raw) {
   extern __shared__ __align__(16) uint8_t lds[];
-  constexpr uint32_t kWaves = kThreads / 64u;
-  constexpr uint32_t R = kThreads / static_cast<uint32_t>(LPR);
+  constexpr uint32_t kWaves = NT / 64u;
+  constexpr uint32_t R = NT / static_cast<uint32_t>(LPR);
+  constexpr uint32_t kPasses = 4u * kThreads * kFusedRowPasses / (4u * NT);  // rows of up to 8192 values
   int8_t* act = reinterpret_cast<int8_t*>(lds);
   int32_t* red = reinterpret_cast<int32_t*>(lds + nkeep);  // nkeep is a multiple of 128
   int32_t* qsw = red + 4u * kWaves;
@@ -953,10 +956,10 @@ __global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const 
 
   // the activation (x: token t0's n values): 4 consecutive values of every
   // 1024 per lane; positions past n read the last 4 values and are zeroed below
-  f32x4 xv[kFusedRowPasses];
+  f32x4 xv[kPasses];
 #pragma unroll
-  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
-    const uint32_t e = min(4u * threadIdx.x + 4u * kThreads * k, n - 4u);
+  for (uint32_t k = 0; k < kPasses; k++) {
+    const uint32_t e = min(4u * threadIdx.x + 4u * NT * k, n - 4u);
     const u32x4 v = load16_a4(reinterpret_cast<const uint8_t*>(x + e));
     xv[k] = f32x4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
   }
@@ -980,14 +983,14 @@ __global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const 
   // or an infinity in the row (the usual case) that is its largest magnitude,
   // floored at 1e-5, and the quants need no NaN rule; a row with either takes
   // the exact path below. Only the passes that hold values are computed.
-  const uint32_t npass = (n + 4u * kThreads - 1u) / (4u * kThreads);
+  const uint32_t npass = (n + 4u * NT - 1u) / (4u * NT);
   float all_max = 0.0f;
   bool has_nan = false;
 #pragma unroll
-  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+  for (uint32_t k = 0; k < kPasses; k++) {
     if (k < npass) {
-      if (4u * kThreads * (k + 1u) > n) {  // the last pass may run past n
-        const bool in = 4u * threadIdx.x + 4u * kThreads * k < n;
+      if (4u * NT * (k + 1u) > n) {  // the last pass may run past n
+        const bool in = 4u * threadIdx.x + 4u * NT * k < n;
 #pragma unroll
         for (int i = 0; i < 4; i++) xv[k][i] = in ? xv[k][i] : 0.0f;
       }
@@ -999,7 +1002,7 @@ __global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const 
   }
   int32_t p = has_nan ? 0 : -1;
   uint32_t mb = __float_as_uint(all_max);
-  wg_max_pair(p, mb, red, 0u);
+  wg_max_pair<kWaves>(p, mb, red, 0u);
   const bool exact = p >= 0 || mb == 0x7f800000u;  // a NaN, or an infinity
   double mx;
   if (p < 0) {
@@ -1010,26 +1013,26 @@ __global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const 
     // trailing NaN leaves it NaN
     int32_t last_nan = -1;
 #pragma unroll
-    for (uint32_t k = 0; k < kFusedRowPasses; k++)
+    for (uint32_t k = 0; k < kPasses; k++)
       if (k < npass)
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++)
-          if (xv[k][i] != xv[k][i]) last_nan = static_cast<int32_t>(4u * threadIdx.x + 4u * kThreads * k + i);
+          if (xv[k][i] != xv[k][i]) last_nan = static_cast<int32_t>(4u * threadIdx.x + 4u * NT * k + i);
     uint32_t unused = 0;
-    wg_max_pair(last_nan, unused, red, 1u);
+    wg_max_pair<kWaves>(last_nan, unused, red, 1u);
     float after = 0.0f;
 #pragma unroll
-    for (uint32_t k = 0; k < kFusedRowPasses; k++)
+    for (uint32_t k = 0; k < kPasses; k++)
       if (k < npass)
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) {
-          const int32_t e = static_cast<int32_t>(4u * threadIdx.x + 4u * kThreads * k + i);
+          const int32_t e = static_cast<int32_t>(4u * threadIdx.x + 4u * NT * k + i);
           const float m = __builtin_fabsf(xv[k][i]);
           if (e > last_nan) after = m > after ? m : after;
         }
     int32_t none = -1;
     uint32_t ab = __float_as_uint(after);
-    wg_max_pair(none, ab, red, 0u);  // slot 0 is free again after slot 1's barrier
+    wg_max_pair<kWaves>(none, ab, red, 0u);  // slot 0 is free again after slot 1's barrier
     mx = last_nan == static_cast<int32_t>(n) - 1 ? __builtin_nan("") : static_cast<double>(__uint_as_float(ab));
   }
   const float div = static_cast<float>(127.0 / mx);
@@ -1040,9 +1043,9 @@ __global__ __launch_bounds__(256) void gemv_i2s_one_kernel(GemvJobs jobs, const 
   const uint32_t ncover = 128u * nb;
   int32_t qsum = 0;
 #pragma unroll
-  for (uint32_t k = 0; k < kFusedRowPasses; k++) {
+  for (uint32_t k = 0; k < kPasses; k++) {
     if (k < npass) {
-      const uint32_t base = 4u * threadIdx.x + 4u * kThreads * k;
+      const uint32_t base = 4u * threadIdx.x + 4u * NT * k;
       int32_t qv[4];
       if (!exact) {
 #pragma unroll
@@ -1684,25 +1687,53 @@ hipError_t launch_i2s_fused(GemvJobs jobs, const float* x, size_t width, size_t 
   return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
 }
 
-template <int LPR, int CPL>
+template <uint32_t NT, int LPR, int CPL>
 void* i2s_one_kernel(bool one_job) {
-  return one_job ? reinterpret_cast<void*>(gemv_i2s_one_kernel<LPR, CPL, true>)
-                 : reinterpret_cast<void*>(gemv_i2s_one_kernel<LPR, CPL, false>);
+  return one_job ? reinterpret_cast<void*>(gemv_i2s_one_kernel<NT, LPR, CPL, true>)
+                 : reinterpret_cast<void*>(gemv_i2s_one_kernel<NT, LPR, CPL, false>);
 }
 
-template <int LPR>
+// The kernels built: 256 threads at every team width with 1-8 chunks a lane;
+// 512 threads at 16-64 lanes with 1-4 chunks; 1024 at 32-64 lanes with 1-2
+// (a row of at most 128 chunks never needs more at those widths).
+template <uint32_t NT, int LPR>
 void* i2s_one_pick(uint32_t cpl, bool one_job) {
-  switch (cpl) {
-    case 1: return i2s_one_kernel<LPR, 1>(one_job);
-    case 2: return i2s_one_kernel<LPR, 2>(one_job);
-    case 3: return i2s_one_kernel<LPR, 3>(one_job);
-    case 4: return i2s_one_kernel<LPR, 4>(one_job);
-    case 5: return i2s_one_kernel<LPR, 5>(one_job);
-    case 6: return i2s_one_kernel<LPR, 6>(one_job);
-    case 7: return i2s_one_kernel<LPR, 7>(one_job);
-    case 8: return i2s_one_kernel<LPR, 8>(one_job);
-    default: return nullptr;
+  constexpr uint32_t kMaxCpl = NT == 256u ? 8u : NT == 512u ? 4u : 2u;
+  if (cpl == 0u || cpl > kMaxCpl) return nullptr;
+  if constexpr (NT == 256u) {
+    switch (cpl) {
+      case 1: return i2s_one_kernel<NT, LPR, 1>(one_job);
+      case 2: return i2s_one_kernel<NT, LPR, 2>(one_job);
+      case 3: return i2s_one_kernel<NT, LPR, 3>(one_job);
+      case 4: return i2s_one_kernel<NT, LPR, 4>(one_job);
+      case 5: return i2s_one_kernel<NT, LPR, 5>(one_job);
+      case 6: return i2s_one_kernel<NT, LPR, 6>(one_job);
+      case 7: return i2s_one_kernel<NT, LPR, 7>(one_job);
+      default: return i2s_one_kernel<NT, LPR, 8>(one_job);
+    }
+  } else if constexpr (NT == 512u) {
+    switch (cpl) {
+      case 1: return i2s_one_kernel<NT, LPR, 1>(one_job);
+      case 2: return i2s_one_kernel<NT, LPR, 2>(one_job);
+      case 3: return i2s_one_kernel<NT, LPR, 3>(one_job);
+      default: return i2s_one_kernel<NT, LPR, 4>(one_job);
+    }
+  } else {
+    return cpl == 1u ? i2s_one_kernel<NT, LPR, 1>(one_job) : i2s_one_kernel<NT, LPR, 2>(one_job);
   }
+}
+
+void* i2s_one_for(uint32_t nt, uint32_t lpr, uint32_t cpl, bool one_job) {
+  if (nt == 256u)
+    return lpr == 8u ? i2s_one_pick<256, 8>(cpl, one_job) : lpr == 16u ? i2s_one_pick<256, 16>(cpl, one_job)
+         : lpr == 32u ? i2s_one_pick<256, 32>(cpl, one_job) : i2s_one_pick<256, 64>(cpl, one_job);
+  if (nt == 512u)
+    return lpr == 16u ? i2s_one_pick<512, 16>(cpl, one_job) : lpr == 32u ? i2s_one_pick<512, 32>(cpl, one_job)
+         : lpr == 64u ? i2s_one_pick<512, 64>(cpl, one_job) : nullptr;
+  if (nt == 1024u)
+    return lpr == 32u ? i2s_one_pick<1024, 32>(cpl, one_job) : lpr == 64u ? i2s_one_pick<1024, 64>(cpl, one_job)
+                      : nullptr;
+  return nullptr;
 }
 
 // One token of I2_S on gemv_i2s_one_kernel; hipErrorNotSupported for shapes
@@ -1717,20 +1748,24 @@ hipError_t launch_i2s_one(GemvJobs jobs, const float* x, size_t width, size_t to
   const uint32_t n = static_cast<uint32_t>(width / 32u) * 32u;
   if (jobs.n == 0 || nbmin == 0 || n < 32u || n > 4u * kThreads * kFusedRowPasses) return hipErrorNotSupported;
   const uint32_t nchunk = 2u * nbmax;
-  // lanes per row: the fewest that hold a row in at most 8 chunks each. Each
-  // workgroup repeats the activation's quantization, so fewer and fuller
-  // workgroups win even below one per CU (6912x2560: 216 workgroups of 32
-  // rows beat 432 of 16; 2560x6912: 160 of 16 beat 320 of 8).
-  // tuning().i2s_lpr forces it.
+  // lanes per row at 256 threads: the fewest that hold a row in at most 8
+  // chunks each. Each workgroup repeats the activation's quantization, so
+  // fewer and fuller workgroups win even below one per CU (6912x2560: 216
+  // workgroups of 32 rows beat 432 of 16; 2560x6912: 160 of 16 beat 320 of
+  // 8). Wider workgroups keep the rows a workgroup takes and give each lane
+  // a smaller share of the quantization and of the row.
+  // tuning().i2s_nt and tuning().i2s_lpr force them.
   uint32_t lpr = 8;
   while (lpr < 64u && (nchunk + lpr - 1u) / lpr > 8u) lpr *= 2u;
+  // 512 threads for rows of more than 4096 values (2560x6912: 5.8 against
+  // 6.2-6.4 us; 6912x2560 keeps 256: 4.3-4.9 against 5.1)
+  uint32_t nt = tuning().i2s_nt ? static_cast<uint32_t>(tuning().i2s_nt) : n > 4096u ? 512u : 256u;
+  lpr = lpr * (nt / 256u) > 64u ? 64u : lpr * (nt / 256u);
   if (const int v = tuning().i2s_lpr) lpr = static_cast<uint32_t>(v);
   const uint32_t cpl = (nchunk + lpr - 1u) / lpr;
-  const bool one = jobs.n == 1u;
-  void* k = lpr == 8u ? i2s_one_pick<8>(cpl, one) : lpr == 16u ? i2s_one_pick<16>(cpl, one)
-          : lpr == 32u ? i2s_one_pick<32>(cpl, one) : i2s_one_pick<64>(cpl, one);
+  void* k = i2s_one_for(nt, lpr, cpl, jobs.n == 1u);
   if (!k) return hipErrorNotSupported;
-  const uint32_t R = kThreads / lpr;
+  const uint32_t R = nt / lpr;
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     jobs.j[i].wg_begin = wgs;
@@ -1738,10 +1773,10 @@ hipError_t launch_i2s_one(GemvJobs jobs, const float* x, size_t width, size_t to
   }
   if (wgs == 0) return hipSuccess;
   uint32_t nkeep = nbmax * 128u;
-  const size_t lds = nkeep + 4u * (4u + 1u) * (kThreads / 64u);
+  const size_t lds = nkeep + 4u * (4u + 1u) * (nt / 64u);
   const float* xt = x + t0 * width;
   void* args[] = {&jobs, const_cast<float**>(&xt), const_cast<uint32_t*>(&n), &nkeep, &tokens, &t0, &raw};
-  return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
+  return hipLaunchKernel(k, dim3(wgs), dim3(nt), args, lds, s);
 }
 
 template <int T, int LPR>

@@ -384,6 +384,24 @@ def test_i2s_code_three_and_hostile_bytes(ctx):
     assert np.array_equal(raw, O.ternary_dot_matrix_i32(body, cols // 4, x, 1))
 
 
+@pytest.mark.parametrize("threads", ["256", "512", "1024"])
+def test_i2s_one_token_kernel_at_every_workgroup_size(ctx, tuning, threads):
+    # 256, 512 or 1024 threads a workgroup (lanes per row scaled with them):
+    # ragged rows, 128 to 8192 values, hostile activations
+    tuning.set("RUSTICIDE_HIP_I2S_NT", threads)
+    for rows, cols in ((6912, 2560), (2560, 6912), (37, 384), (300, 1024), (17, 8192), (5, 128)):
+        data = synth.i2s_matrix(rows, cols, seed=rows + 5)
+        m = R.Matrix.load(ctx, 36, data, rows, cols)
+        rb = cols // 4
+        xs = [synth.normal_f32(cols, seed=cols + 1)] + (hostile_rows(cols) if rows == 300 else [])
+        for i, x in enumerate(xs):
+            raw = ctx.ternary_dot_i32(m, x, 1)
+            assert np.array_equal(raw, O.ternary_dot_matrix_i32(data[: rows * rb], rb, x, 1)), (rows, cols, i)
+            out = np.full(rows, 7.0, np.float32)
+            R.matmul_batch(ctx, x, 1, [(m, out)])
+            assert_same_bits(out, oracle_matmul(36, data, rows, cols, x, 1, scale=0.02), f"{rows}x{cols} x{i}")
+
+
 def hostile_rows(cols):
     # q8.rs:38-49: a NaN restarts the running maximum, a trailing NaN leaves
     # it NaN, an infinity makes the divisor 0, all zeros floor it at 1e-5
