@@ -51,11 +51,11 @@ __device__ __forceinline__ void stage_quants(int8_t* act, uint32_t bytes, const 
 // stored at chunk c ^ (b & 15). The teams of a wave read the same chunk
 // offsets of different blocks at once; unswizzled those all land in the same
 // few LDS banks (a 256-byte block stride is a whole number of bank rows).
-template <int T>
+template <int T, uint32_t NT = kThreads>
 __device__ __forceinline__ void stage_quants_swizzled(int8_t* act, uint32_t bytes, const Q8Dev& q, size_t t0) {
   for (uint32_t t = 0; t < static_cast<uint32_t>(T); t++) {
     const int8_t* src = q.quants + (t0 + t) * q.qstride;
-    for (uint32_t i = threadIdx.x * 16u; i < bytes; i += kThreads * 16u) {
+    for (uint32_t i = threadIdx.x * 16u; i < bytes; i += NT * 16u) {
       const uint32_t b = i >> 8, c = (i >> 4) & 15u;
       *reinterpret_cast<u32x4*>(act + t * bytes + (b << 8) + ((c ^ (b & 15u)) << 4)) =
           *reinterpret_cast<const u32x4*>(src + i);
@@ -107,12 +107,12 @@ __device__ __forceinline__ XGeom x_geom(const float* x, size_t width, uint32_t n
   return g;
 }
 
-template <int K>
+template <int K, uint32_t NT = kThreads>
 __device__ __forceinline__ void load_x_round(XRound<K>& xr, const XGeom& g, uint32_t u0) {
   const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
 #pragma unroll
   for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
-    const uint32_t u = u0 + hw + k * (kThreads / 32u);
+    const uint32_t u = u0 + hw + k * (NT / 32u);
     if (u >= g.total) {
 #pragma unroll
       for (int i = 0; i < 8; i++) xr.f[k][i] = 0.0f;
@@ -135,14 +135,14 @@ __device__ __forceinline__ void load_x_round(XRound<K>& xr, const XGeom& g, uint
   }
 }
 
-template <int FMT, int K>
+template <int FMT, int K, uint32_t NT = kThreads>
 __device__ __forceinline__ void quantize_x_round(const XRound<K>& xr, const XGeom& g, uint32_t u0, uint32_t nb,
                                                  int8_t* act, float* d8, int32_t* side) {
   const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
   const uint32_t abytes = nb * 256u;
 #pragma unroll
   for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
-    const uint32_t u = u0 + hw + k * (kThreads / 32u);
+    const uint32_t u = u0 + hw + k * (NT / 32u);
     if (u >= g.total) break;  // uniform over the half-wave
     const uint32_t t = u / g.nq, b = u - t * g.nq;
     const float* f = xr.f[k];
@@ -199,12 +199,12 @@ struct NormRound {
   float w[K][8];
 };
 
-template <int K>
+template <int K, uint32_t NT = kThreads>
 __device__ __forceinline__ void norm_load(NormRound<K>& nr, const XGeom& g, const NormIn& nrm) {
   const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
 #pragma unroll
   for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
-    const uint32_t u = hw + k * (kThreads / 32u);
+    const uint32_t u = hw + k * (NT / 32u);
     const size_t e0 = static_cast<size_t>(u < g.total ? u : 0u) * 256u + 8u * hl;
     const u32x4 w0 = load16(reinterpret_cast<const uint8_t*>(nrm.weight + e0));
     const u32x4 w1 = load16(reinterpret_cast<const uint8_t*>(nrm.weight + e0 + 4));
@@ -223,13 +223,13 @@ __device__ __forceinline__ void norm_load(NormRound<K>& nr, const XGeom& g, cons
   }
 }
 
-template <int K>
+template <int K, uint32_t NT = kThreads>
 __device__ __forceinline__ void norm_apply(XRound<K>& xr, const NormRound<K>& nr, const XGeom& g, const NormIn& nrm,
                                            float* sq, float* s_rms) {
   const uint32_t hl = threadIdx.x & 31u, hw = threadIdx.x >> 5;
 #pragma unroll
   for (uint32_t k = 0; k < static_cast<uint32_t>(K); k++) {
-    const uint32_t u = hw + k * (kThreads / 32u);
+    const uint32_t u = hw + k * (NT / 32u);
     if (u >= g.total) continue;
     const uint32_t e0 = u * 256u + 8u * hl;
     float s2[8];
@@ -269,14 +269,14 @@ __device__ __forceinline__ void norm_apply(XRound<K>& xr, const NormRound<K>& nr
 }
 
 // The rounds after the first (which the kernel quantizes from its preload).
-template <int FMT, int K>
+template <int FMT, int K, uint32_t NT = kThreads>
 __device__ __forceinline__ void quantize_x_rest(const XGeom& g, uint32_t nb, int8_t* act, float* d8,
                                                 int32_t* side) {
-  for (uint32_t u0 = static_cast<uint32_t>(K) * (kThreads / 32u); u0 < g.total;
-       u0 += static_cast<uint32_t>(K) * (kThreads / 32u)) {
+  for (uint32_t u0 = static_cast<uint32_t>(K) * (NT / 32u); u0 < g.total;
+       u0 += static_cast<uint32_t>(K) * (NT / 32u)) {
     XRound<K> xr;
-    load_x_round<K>(xr, g, u0);
-    quantize_x_round<FMT, K>(xr, g, u0, nb, act, d8, side);
+    load_x_round<K, NT>(xr, g, u0);
+    quantize_x_round<FMT, K, NT>(xr, g, u0, nb, act, d8, side);
   }
 }
 
@@ -331,12 +331,12 @@ __device__ __forceinline__ const uint8_t* block_at(const GemvJob& J, const WgRow
 // Each row's block terms summed in block order from -0.0
 // (portable/int_dot/rows.rs:9-12,59) and written; PAIR writes
 // silu(gate) * up with silu_mul's expressions (portable/elementwise.rs:6-9).
-template <int T, bool PAIR>
+template <int T, bool PAIR, uint32_t NT = kThreads>
 __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, const float* terms, uint32_t nb,
                                            uint32_t nbmax, size_t tokens, size_t t0) {
   if constexpr (PAIR) {
     static_assert(T == 1, "a gate/up pair serves one token");
-    for (uint32_t r = threadIdx.x; r < g.nh; r += kThreads) {
+    for (uint32_t r = threadIdx.x; r < g.nh; r += NT) {
       float gs = -0.0f, us = -0.0f;
       for (uint32_t b = 0; b < nb; b++) gs += terms[__umul24(r, nbmax) + b];
       for (uint32_t b = 0; b < nb; b++) us += terms[__umul24(r + g.nh, nbmax) + b];
@@ -346,7 +346,7 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
       if (idx < J.out_len) J.out[idx] = sg * us;
     }
   } else {
-    for (uint32_t i = threadIdx.x; i < g.nrows * T; i += kThreads) {
+    for (uint32_t i = threadIdx.x; i < g.nrows * T; i += NT) {
       const uint32_t r = i / T, t = i - r * T;
       float s = -0.0f;
       for (uint32_t b = 0; b < nb; b++) s += terms[(__umul24(r, nbmax) + b) * T + t];
@@ -363,8 +363,8 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
 // preloading FQ blocks per half-wave before the weights.
 // NORM (T = 1, the whole row in the preload): x is the hidden state and the
 // kernel applies the NormIn residual add and RMSNorm before quantizing.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false>
-__global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads>
+__global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -384,12 +384,12 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
   const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
-  if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
+  if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
   NormRound<FQ ? FQ : 1> nr;
-  if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
+  if constexpr (NORM) norm_load<FQ ? FQ : 1, NT>(nr, xg, nrm);
   u32x4 hd[NI], c0[NI], c1[NI];
   auto issue = [&](int i) {
-    const uint32_t g = team + static_cast<uint32_t>(i) * (kThreads / 4u);
+    const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
     const uint32_t gg = g < total ? g : 0u;  // a spare team re-reads block 0
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
     const uint8_t* blk = block_at<PAIR>(J, wr, r, b * 144u);
@@ -401,14 +401,14 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
 #pragma unroll
   for (int i = 0; i < ahead; i++) issue(i);
 
-  if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
+  if constexpr (NORM) norm_apply<FQ ? FQ : 1, NT>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
                                     reinterpret_cast<float*>(lds + nrm.lds_offset) + wave_sum_floats(xg.total * 256u));
   if (FQ) {
-    quantize_x_round<12, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, sums);
-    quantize_x_rest<12, FQ ? FQ : 1>(xg, nbmax, act, d8, sums);
+    quantize_x_round<12, FQ ? FQ : 1, NT>(xr, xg, 0u, nbmax, act, d8, sums);
+    quantize_x_rest<12, FQ ? FQ : 1, NT>(xg, nbmax, act, d8, sums);
   } else {
-    stage_quants_swizzled<T>(act, abytes, q, t0);
-    for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += kThreads) {
+    stage_quants_swizzled<T, NT>(act, abytes, q, t0);
+    for (uint32_t i = threadIdx.x; i < T * nbmax * 8u; i += NT) {
       const uint32_t t = i / (nbmax * 8u), k = i - t * nbmax * 8u;
       const size_t src = (t0 + t) * q.bstride + k;
       sums[i] = q.sums[src];
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
 #pragma unroll
   for (int it = 0; it < NI; it++) {
     if (it + ahead < NI) issue(it + ahead);
-    const uint32_t g = team + it * (kThreads / 4u);
+    const uint32_t g = team + it * (NT / 4u);
     if (g >= total) break;  // uniform over the team
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
     const u32x4 h = hd[it];
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
     }
   }
   __syncthreads();
-  write_rows<T, PAIR>(J, wr, terms, nb, nbmax, tokens, t0);
+  write_rows<T, PAIR, NT>(J, wr, terms, nb, nbmax, tokens, t0);
 }
 
 // Q6_K x Q8_K --------------------------------------------------------------
@@ -485,8 +485,8 @@ __global__ __launch_bounds__(256) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, c
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false>
-__global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads>
+__global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
@@ -510,14 +510,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
   const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
-  if (FQ) load_x_round<FQ ? FQ : 1>(xr, xg, 0u);
+  if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
   NormRound<FQ ? FQ : 1> nr;
-  if constexpr (NORM) norm_load<FQ ? FQ : 1>(nr, xg, nrm);
+  if constexpr (NORM) norm_load<FQ ? FQ : 1, NT>(nr, xg, nrm);
   u32x4 A[NI], B[NI], C[NI];
   uint2 S[NI];
   uint32_t D[NI];
   auto issue = [&](int i) {
-    const uint32_t g = team + static_cast<uint32_t>(i) * (kThreads / 4u);
+    const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
     const uint32_t gg = g < total ? g : 0u;
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
     const uint8_t* base = block_at<PAIR>(J, wr, r, __umul24(b, 210u));
@@ -531,14 +531,14 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
 #pragma unroll
   for (int i = 0; i < ahead; i++) issue(i);
 
-  if constexpr (NORM) norm_apply<FQ ? FQ : 1>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
+  if constexpr (NORM) norm_apply<FQ ? FQ : 1, NT>(xr, nr, xg, nrm, reinterpret_cast<float*>(lds + nrm.lds_offset),
                                     reinterpret_cast<float*>(lds + nrm.lds_offset) + wave_sum_floats(xg.total * 256u));
   if (FQ) {
-    quantize_x_round<14, FQ ? FQ : 1>(xr, xg, 0u, nbmax, act, d8, bias);
-    quantize_x_rest<14, FQ ? FQ : 1>(xg, nbmax, act, d8, bias);
+    quantize_x_round<14, FQ ? FQ : 1, NT>(xr, xg, 0u, nbmax, act, d8, bias);
+    quantize_x_rest<14, FQ ? FQ : 1, NT>(xg, nbmax, act, d8, bias);
   } else {
-    stage_quants_swizzled<T>(act, abytes, q, t0);
-    for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += kThreads) {
+    stage_quants_swizzled<T, NT>(act, abytes, q, t0);
+    for (uint32_t i = threadIdx.x; i < T * nbmax * 16u; i += NT) {
       const uint32_t t = i / (nbmax * 16u), k = i - t * nbmax * 16u;
       bias[i] = -32 * q.sums16[2u * (t0 + t) * q.bstride + k];
       if ((k & 15u) == 0) d8[t * nbmax + k / 16u] = q.scales[(t0 + t) * q.bstride + k / 2u];
@@ -549,7 +549,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
 #pragma unroll
   for (int it = 0; it < NI; it++) {
     if (it + ahead < NI) issue(it + ahead);
-    const uint32_t g = team + it * (kThreads / 4u);
+    const uint32_t g = team + it * (NT / 4u);
     if (g >= total) break;  // uniform over the team
     const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
     const u32x4 a = A[it], bq = B[it], c = C[it];
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(256) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, c
     }
   }
   __syncthreads();
-  write_rows<T, PAIR>(J, wr, terms, nb, nbmax, tokens, t0);
+  write_rows<T, PAIR, NT>(J, wr, terms, nb, nbmax, tokens, t0);
 }
 
 // I2_S x I8_S --------------------------------------------------------------
@@ -1384,10 +1384,42 @@ uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
   return R < 1u ? 1u : R;
 }
 
-template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false>
+template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false, uint32_t NT = kThreads>
 void* kq_kernel() {
-  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR>)
-                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR>);
+  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT>)
+                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT>);
+}
+
+// The 512-lane one-token kernels: 128 teams of ni blocks each take the rows
+// that 64 teams of 2*ni take at 256 lanes (nullptr where none is built).
+template <int FMT>
+void* kq_wide_kernel_fmt(uint32_t fq, uint32_t ni, bool norm, bool pair) {
+  constexpr uint32_t W = 2u * kThreads;
+  if (norm) {
+    if (fq != 1u) return nullptr;
+    if (pair) {
+      return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, true, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, true, W>()
+             : ni == 4u                                            ? kq_kernel<FMT, 1, 4, 1, true, true, W>()
+                                                                   : nullptr;
+    }
+    return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, false, W>()
+           : ni == 4u                                             ? kq_kernel<FMT, 1, 4, 1, true, false, W>()
+                                                                  : nullptr;
+  }
+  if (pair) return nullptr;
+  if (fq == 1u)
+    return ni == 1u ? kq_kernel<FMT, 1, 1, 1, false, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, false, false, W>()
+           : ni == 4u                                              ? kq_kernel<FMT, 1, 4, 1, false, false, W>()
+                                                                   : nullptr;
+  if (fq == 4u)
+    return ni == 1u ? kq_kernel<FMT, 1, 1, 4, false, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 4, false, false, W>()
+           : ni == 4u                                              ? kq_kernel<FMT, 1, 4, 4, false, false, W>()
+                                                                   : nullptr;
+  return nullptr;
+}
+
+void* kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool pair) {
+  return type_id == 12u ? kq_wide_kernel_fmt<12>(fq, ni, norm, pair) : kq_wide_kernel_fmt<14>(fq, ni, norm, pair);
 }
 
 // The norm-fused decode kernels: one token, four blocks per team (two for a
@@ -1578,9 +1610,25 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     } else {
       k = kq_kernel_for<T>(type_id, ni, fq);
     }
+    // A one-token grid of fewer workgroups than CUs takes 512 lanes and half
+    // the blocks per team: the same rows and the same one quantization per
+    // workgroup, twice the waves to cover the weight loads' latency (Q6_K
+    // 2048x5632: 6.6-6.75 against 7.45 us; Q4_K 5632x2048: 4.9 against 5.1).
+    // The 500-workgroup 32000x2048 output launch keeps 256 (12.3 against
+    // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
+    uint32_t nt = kThreads;
+    if (T == 1 && FUSED && ni >= 2u) {
+      const int forced = norm ? tuning().norm_nt : tuning().kq_nt;
+      const bool wide = forced ? forced == 512 : wgs < static_cast<uint32_t>(device_cus());
+      void* kw = wide ? kq_wide_kernel(type_id, fq, ni / 2u, norm != nullptr, pair) : nullptr;
+      if (kw) {
+        k = kw;
+        nt = 2u * kThreads;
+      }
+    }
     void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
                     const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};
-    return hipLaunchKernel(k, dim3(wgs), dim3(kThreads), args, lds, s);
+    return hipLaunchKernel(k, dim3(wgs), dim3(nt), args, lds, s);
   }
   if (tuning().i2s_one) {
     const hipError_t e = launch_i2s_q8<T>(jobs, q, tokens, t0, s, raw);

@@ -252,6 +252,38 @@ def test_tinyllama_shaped_greedy_decode_matches_the_cpu_path(ctx, norm_path):
     cpu.close()
 
 
+def test_one_token_launches_at_both_workgroup_sizes(ctx, monkeypatch):
+    # RUSTICIDE_HIP_KQ_NT / RUSTICIDE_HIP_NORM_NT: the one-token k-quant
+    # launches (norm-fused Q/K/V, attention output, gate/up, output; the
+    # down projection) on 256-lane workgroups, or on 512-lane ones with half
+    # the blocks per team wherever a launch has two or more: the CPU path's
+    # logits either way
+    model = synth.decoder_model(synth.TINYLLAMA, seed=2027)
+    prompt = np.random.default_rng(8).integers(0, 32000, 9).astype(np.uint32)
+    follow = [311, 7, 29999, 0, 1234]
+    cpu = O.Decoder(model, threads=16)
+    want = [cpu.forward_batch(prompt, 0)]
+    for i, t in enumerate(follow):
+        want.append(cpu.forward(t, len(prompt) + i))
+    cpu.close()
+    try:
+        for nt in ("256", "512"):
+            monkeypatch.setenv("RUSTICIDE_HIP_KQ_NT", nt)
+            monkeypatch.setenv("RUSTICIDE_HIP_NORM_NT", nt)
+            R.reload_tuning()
+            gpu = R.Decoder(ctx, model)
+            got = [gpu.forward_batch(prompt, 0)]
+            for i, t in enumerate(follow):
+                got.append(gpu.forward(t, len(prompt) + i))
+            gpu.close()
+            for k, (g, c) in enumerate(zip(got, want)):
+                assert same_bits(g, c), f"{nt} lanes, step {k}: max |diff| {diff(g, c)}"
+    finally:
+        monkeypatch.delenv("RUSTICIDE_HIP_KQ_NT")
+        monkeypatch.delenv("RUSTICIDE_HIP_NORM_NT")
+        R.reload_tuning()
+
+
 def _device_math(ctx, op, a, b=None):
     import ctypes
     L = R.lib()

@@ -32,8 +32,12 @@ VARIANTS = {
     "lds-1": {"RUSTICIDE_HIP_GEMV": "lds", "RUSTICIDE_HIP_GEMV_NI": "1"},
     "lds-2": {"RUSTICIDE_HIP_GEMV": "lds", "RUSTICIDE_HIP_GEMV_NI": "2"},
     "lds-4": {"RUSTICIDE_HIP_GEMV": "lds", "RUSTICIDE_HIP_GEMV_NI": "4"},
+    # one-token k-quant launches on 256-lane workgroups only, and on 512-lane
+    # ones (half the blocks per team) wherever a launch has two or more
+    "nt-256": {"RUSTICIDE_HIP_KQ_NT": "256"},
+    "nt-512": {"RUSTICIDE_HIP_KQ_NT": "512"},
 }
-SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI")
+SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT")
 
 
 @pytest.fixture(params=list(VARIANTS))
