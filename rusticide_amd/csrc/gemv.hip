@@ -93,7 +93,6 @@ struct XGeom {
   size_t width;
   uint32_t nq;     // blocks quantized per token: min(nb, width / 256)
   uint32_t total;  // T * nq
-  bool aligned;    // 16-byte loads are legal
 };
 
 template <int T>
@@ -103,7 +102,6 @@ __device__ __forceinline__ XGeom x_geom(const float* x, size_t width, uint32_t n
   g.width = width;
   g.nq = width / 256u < nb ? static_cast<uint32_t>(width / 256u) : nb;
   g.total = static_cast<uint32_t>(T) * g.nq;
-  g.aligned = ((reinterpret_cast<uintptr_t>(x) | (width * 4u)) & 15u) == 0;
   return g;
 }
 
@@ -120,17 +118,15 @@ __device__ __forceinline__ void load_x_round(XRound<K>& xr, const XGeom& g, uint
     }
     const uint32_t t = u / g.nq, b = u - t * g.nq;
     const float* v = g.x + t * g.width + static_cast<size_t>(b) * 256u + 8u * hl;
-    if (g.aligned) {
-      const u32x4 lo = load16(reinterpret_cast<const uint8_t*>(v));
-      const u32x4 hi = load16(reinterpret_cast<const uint8_t*>(v + 4));
+    // dword-aligned 16-byte loads, whatever x's and the width's alignment: no
+    // branch for the compiler to join (a join between these loads and the
+    // weight loads after them makes it wait for x before issuing the weights)
+    const u32x4 lo = load16_a4(reinterpret_cast<const uint8_t*>(v));
+    const u32x4 hi = load16_a4(reinterpret_cast<const uint8_t*>(v + 4));
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        xr.f[k][i] = __uint_as_float(lo[i]);
-        xr.f[k][4 + i] = __uint_as_float(hi[i]);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; i++) xr.f[k][i] = v[i];
+    for (int i = 0; i < 4; i++) {
+      xr.f[k][i] = __uint_as_float(lo[i]);
+      xr.f[k][4 + i] = __uint_as_float(hi[i]);
     }
   }
 }
@@ -356,6 +352,71 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
   }
 }
 
+// Where a team finds its blocks. A workgroup's teams take team blocks
+// g = team + i * NT/4, i = 0..NI-1, of its rows x nb blocks in row-major
+// order. The general walk divides each g into (row g / nb, block g % nb).
+// FIX (nb a power of two up to NT/4: rows of 256, 512, ... values): g % nb
+// is the same for every i, so the team keeps one
+// block column fb, its row advances by step = NT/4/nb an iteration, and the
+// block's address by a constant stride (row_of is affine in i: step is a
+// whole number of interleaved chunks). The activation a team reads is then
+// the same for all of its blocks and leaves the loop.
+template <bool PAIR, uint32_t NT, bool FIX>
+struct BlockWalk {
+  const GemvJob& J;
+  const WgRows& wr;
+  uint32_t nb, total, team, bbytes;
+  float inv_nb;
+  uint32_t r0, fb, step, delta;  // FIX
+  const uint8_t* p0;             // FIX: the team's first block (block 0 of row 0 for a spare team)
+
+  __device__ __forceinline__ BlockWalk(const GemvJob& j, const WgRows& w, uint32_t block_bytes)
+      : J(j), wr(w), nb(j.nb), total(w.nrows * j.nb), team(threadIdx.x >> 2), bbytes(block_bytes) {
+    inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
+    r0 = fb = step = delta = 0u;
+    p0 = nullptr;
+    if constexpr (FIX) {
+      const uint32_t sh = static_cast<uint32_t>(__builtin_ctz(nb));
+      r0 = team >> sh;
+      fb = team & (nb - 1u);
+      step = (NT / 4u) >> sh;
+      delta = (((step >> wr.cs) * wr.nwg) << wr.cs) * J.stride;
+      const bool in = r0 < wr.nrows;
+      p0 = block_at<PAIR>(J, wr, in ? r0 : 0u, in ? fb * bbytes : 0u);
+    }
+  }
+  // whether team block i lies in the workgroup's rows (uniform over a team)
+  __device__ __forceinline__ bool live(int i) const {
+    if constexpr (FIX) return r0 + static_cast<uint32_t>(i) * step < wr.nrows;
+    return team + static_cast<uint32_t>(i) * (NT / 4u) < total;
+  }
+  // the workgroup row and block of team block i
+  __device__ __forceinline__ void rb(int i, uint32_t& r, uint32_t& b) const {
+    if constexpr (FIX) {
+      r = r0 + static_cast<uint32_t>(i) * step;
+      b = fb;
+    } else {
+      const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
+      r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb);
+      b = g - __umul24(r, nb);
+    }
+  }
+  // the address of team block i; a spare team re-reads a block of its own
+  __device__ __forceinline__ const uint8_t* addr(int i) const {
+    if constexpr (FIX) {
+      const uint32_t r = r0 + static_cast<uint32_t>(i) * step;
+      if constexpr (PAIR) return r < wr.nrows ? block_at<true>(J, wr, r, fb * bbytes) : p0;
+      return r < wr.nrows ? p0 + static_cast<uint32_t>(i) * delta : p0;
+    } else {
+      // g = r*nb + b with g < 8*128: a float reciprocal divides exactly here
+      const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
+      const uint32_t gg = g < total ? g : 0u;
+      const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
+      return block_at<PAIR>(J, wr, r, __umul24(b, bbytes));
+    }
+  }
+};
+
 // Q4_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
 //      terms [R][nbmax][T] f32
@@ -363,25 +424,21 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
 // preloading FQ blocks per half-wave before the weights.
 // NORM (T = 1, the whole row in the preload): x is the hidden state and the
 // kernel applies the NormIn residual add and RMSNorm before quantizing.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads>
-__global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
-                                                       size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
-                                                       size_t t0, NormIn nrm) {
-  extern __shared__ __align__(16) uint8_t lds[];
+// FIX: see BlockWalk (one token).
+template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX>
+__device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const float* __restrict__ x, size_t width,
+                                         uint32_t R, uint32_t nbmax, size_t tokens, size_t t0, const NormIn& nrm,
+                                         uint8_t* lds) {
   const uint32_t abytes = nbmax * 256u;
   int8_t* act = reinterpret_cast<int8_t*>(lds);
   float* d8 = reinterpret_cast<float*>(lds + T * abytes);
   int32_t* sums = reinterpret_cast<int32_t*>(d8 + T * nbmax);
   float* terms = reinterpret_cast<float*>(sums + T * nbmax * 8u);
 
-  const GemvJob& J = jobs.j[find_job(jobs)];
   const WgRows wr = wg_rows<PAIR>(J, R);
-  const uint32_t nb = J.nb;
-  const uint32_t total = wr.nrows * nb;
-  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
+  const BlockWalk<PAIR, NT, FIX> walk(J, wr, 144u);
+  const uint32_t p = threadIdx.x & 3u;
 
-  // g = r*nb + b with g < 4*64: a float reciprocal divides exactly here
-  const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
   if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
@@ -389,10 +446,7 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
   if constexpr (NORM) norm_load<FQ ? FQ : 1, NT>(nr, xg, nrm);
   u32x4 hd[NI], c0[NI], c1[NI];
   auto issue = [&](int i) {
-    const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
-    const uint32_t gg = g < total ? g : 0u;  // a spare team re-reads block 0
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
-    const uint8_t* blk = block_at<PAIR>(J, wr, r, b * 144u);
+    const uint8_t* blk = walk.addr(i);
     hd[i] = load16(blk);
     c0[i] = load16(blk + 16u + 16u * p);
     c1[i] = load16(blk + 80u + 16u * p);
@@ -418,13 +472,30 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
   __syncthreads();
 
   const uint32_t j0 = 2u * (p >> 1), e0 = 16u * (p & 1u);
+  const uint32_t k0 = e0 + 32u * j0;
   const bool min_lane = (p & 1u) == 0;
+  // FIX: the team's activation quants, 32-block sums and d8, read once
+  u32x4 fa[4] = {};
+  int32_t fs[4] = {};
+  float fd8 = 0.0f;
+  if constexpr (FIX) {
+    fa[0] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0));
+    fa[1] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0 + 32u));
+    fa[2] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0 + 128u));
+    fa[3] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0 + 160u));
+    const int32_t* S = sums + walk.fb * 8u + j0;
+    fs[0] = S[0];
+    fs[1] = S[1];
+    fs[2] = S[4];
+    fs[3] = S[5];
+    fd8 = d8[walk.fb];
+  }
 #pragma unroll
   for (int it = 0; it < NI; it++) {
     if (it + ahead < NI) issue(it + ahead);
-    const uint32_t g = team + it * (NT / 4u);
-    if (g >= total) break;  // uniform over the team
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
+    if (!walk.live(it)) break;  // uniform over the team
+    uint32_t r, b;
+    walk.rb(it, r, b);
     const u32x4 h = hd[it];
     // 6-bit scales/mins of sub-blocks j0, j0+1, j0+4, j0+5 (ggml get_scale_min_k4,
     // quantize/src/q4_k.rs:17-25)
@@ -447,12 +518,22 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const int8_t* at = act + t * abytes;
-      const uint32_t k0 = e0 + 32u * j0;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(swz(at, b, k0));
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 32u));
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 128u));
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 160u));
+      u32x4 a0 = fa[0], a1 = fa[1], a2 = fa[2], a3 = fa[3];
+      int32_t s0 = fs[0], s1 = fs[1], s2 = fs[2], s3 = fs[3];
+      float dd8 = fd8;
+      if constexpr (!FIX) {
+        const int8_t* at = act + t * abytes;
+        a0 = *reinterpret_cast<const u32x4*>(swz(at, b, k0));
+        a1 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 32u));
+        a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 128u));
+        a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 160u));
+        const int32_t* S = sums + t * nbmax * 8u + b * 8u + j0;
+        s0 = S[0];
+        s1 = S[1];
+        s2 = S[4];
+        s3 = S[5];
+        dd8 = d8[t * nbmax + b];
+      }
       int32_t D0 = 0, D1 = 0, D2 = 0, D3 = 0;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
@@ -464,20 +545,31 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
       // 24-bit multiplies are exact here: |D| < 2^17, sums of 32 quants < 2^12,
       // scales and mins below 64
       int32_t isum = __mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3);
-      const int32_t* S = sums + t * nbmax * 8u + b * 8u + j0;
-      int32_t msum =
-          min_lane ? (__mul24(m0, S[0]) + __mul24(m1, S[1]) + __mul24(m2, S[4]) + __mul24(m3, S[5])) : 0;
+      int32_t msum = min_lane ? (__mul24(m0, s0) + __mul24(m1, s1) + __mul24(m2, s2) + __mul24(m3, s3)) : 0;
       isum = quad_sum(isum);
       msum = quad_sum(msum);
       if (p == 0) {
         // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
         const float neg = -(dmin * static_cast<float>(msum));
-        terms[(__umul24(r, nbmax) + b) * T + t] = d8[t * nbmax + b] * __builtin_fmaf(d, static_cast<float>(isum), neg);
+        terms[(__umul24(r, nbmax) + b) * T + t] = dd8 * __builtin_fmaf(d, static_cast<float>(isum), neg);
       }
     }
   }
   __syncthreads();
-  write_rows<T, PAIR, NT>(J, wr, terms, nb, nbmax, tokens, t0);
+  write_rows<T, PAIR, NT>(J, wr, terms, J.nb, nbmax, tokens, t0);
+}
+
+// FIX: every job's nb is a power of two up to NT/4 (the launch checks). It is
+// a kernel of its own rather than a branch in one: at the join of two walks
+// the compiler merges their pending loads and then waits for the activation
+// before issuing the first weights.
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
+__global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
+                                                       size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
+                                                       size_t t0, NormIn nrm) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  static_assert(!FIX || T == 1, "fixed columns: one token");
+  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // Q6_K x Q8_K --------------------------------------------------------------
@@ -485,29 +577,25 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads>
-__global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
-                                                       size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
-                                                       size_t t0, NormIn nrm) {
-  extern __shared__ __align__(16) uint8_t lds[];
+template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX>
+__device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const float* __restrict__ x, size_t width,
+                                         uint32_t R, uint32_t nbmax, size_t tokens, size_t t0, const NormIn& nrm,
+                                         uint8_t* lds) {
   const uint32_t abytes = nbmax * 256u;
   int8_t* act = reinterpret_cast<int8_t*>(lds);
   float* d8 = reinterpret_cast<float*>(lds + T * abytes);
   int32_t* bias = reinterpret_cast<int32_t*>(d8 + T * nbmax);
   float* terms = reinterpret_cast<float*>(bias + T * nbmax * 16u);
 
-  const GemvJob& J = jobs.j[find_job(jobs)];
   const WgRows wr = wg_rows<PAIR>(J, R);
-  const uint32_t nb = J.nb;
-  const uint32_t total = wr.nrows * nb;
-  const uint32_t team = threadIdx.x >> 2, p = threadIdx.x & 3u;
+  const BlockWalk<PAIR, NT, FIX> walk(J, wr, 210u);
+  const uint32_t p = threadIdx.x & 3u;
   const uint32_t h = p >> 1, gq = p & 1u;
 
   // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; S: the
   // eight scales of half h at 192+8h; D: d at 208 (q6_k.rs:13-43). Blocks are
   // 210 bytes, so every load but D's is only 2-byte aligned; each stays
   // inside its block.
-  const float inv_nb = nb ? 1.0f / static_cast<float>(nb) : 0.0f;
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
   if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
@@ -517,10 +605,7 @@ __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, co
   uint2 S[NI];
   uint32_t D[NI];
   auto issue = [&](int i) {
-    const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
-    const uint32_t gg = g < total ? g : 0u;
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
-    const uint8_t* base = block_at<PAIR>(J, wr, r, __umul24(b, 210u));
+    const uint8_t* base = walk.addr(i);
     A[i] = load16_any(base + 64u * h + 16u * gq);
     B[i] = load16_any(base + 64u * h + 32u + 16u * gq);
     C[i] = load16_any(base + 128u + 32u * h + 16u * gq);
@@ -546,12 +631,29 @@ __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, co
   }
   __syncthreads();
 
+  const uint32_t k0 = 128u * h + 16u * gq;
+  // FIX: the team's activation quants, 16-run biases and d8, read once
+  u32x4 fa[4] = {};
+  int32_t fb4[4] = {};
+  float fd8 = 0.0f;
+  if constexpr (FIX) {
+    fa[0] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0));
+    fa[1] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0 + 32u));
+    fa[2] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0 + 64u));
+    fa[3] = *reinterpret_cast<const u32x4*>(swz(act, walk.fb, k0 + 96u));
+    const int32_t* bb = bias + walk.fb * 16u + 8u * h + gq;
+    fb4[0] = bb[0];
+    fb4[1] = bb[2];
+    fb4[2] = bb[4];
+    fb4[3] = bb[6];
+    fd8 = d8[walk.fb];
+  }
 #pragma unroll
   for (int it = 0; it < NI; it++) {
     if (it + ahead < NI) issue(it + ahead);
-    const uint32_t g = team + it * (NT / 4u);
-    if (g >= total) break;  // uniform over the team
-    const uint32_t r = static_cast<uint32_t>((static_cast<float>(g) + 0.5f) * inv_nb), b = g - __umul24(r, nb);
+    if (!walk.live(it)) break;  // uniform over the team
+    uint32_t r, b;
+    walk.rb(it, r, b);
     const u32x4 a = A[it], bq = B[it], c = C[it];
     const uint32_t slo = S[it].x, shi = S[it].y;
     // scale of run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
@@ -570,14 +672,22 @@ __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, co
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-      const int8_t* at = act + t * abytes;
-      const uint32_t k0 = 128u * h + 16u * gq;
-      const u32x4 a0 = *reinterpret_cast<const u32x4*>(swz(at, b, k0));
-      const u32x4 a1 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 32u));
-      const u32x4 a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 64u));
-      const u32x4 a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 96u));
-      const int32_t* bb = bias + t * nbmax * 16u + b * 16u + 8u * h + gq;
-      int32_t D0 = bb[0], D1 = bb[2], D2 = bb[4], D3 = bb[6];
+      u32x4 a0 = fa[0], a1 = fa[1], a2 = fa[2], a3 = fa[3];
+      int32_t D0 = fb4[0], D1 = fb4[1], D2 = fb4[2], D3 = fb4[3];
+      float dd8 = fd8;
+      if constexpr (!FIX) {
+        const int8_t* at = act + t * abytes;
+        a0 = *reinterpret_cast<const u32x4*>(swz(at, b, k0));
+        a1 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 32u));
+        a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 64u));
+        a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 96u));
+        const int32_t* bb = bias + t * nbmax * 16u + b * 16u + 8u * h + gq;
+        D0 = bb[0];
+        D1 = bb[2];
+        D2 = bb[4];
+        D3 = bb[6];
+        dd8 = d8[t * nbmax + b];
+      }
 #pragma unroll
       for (int k = 0; k < 4; k++) {
         D0 = dot4(q0[k], a0[k], D0);
@@ -589,13 +699,26 @@ __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, co
       int32_t isum = quad_sum(__mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3));
       if (p == 0) {
         // int_dot.rs:203: read_f16_le(block, 208) * span.scales[0] * lossy(sum)
-        const float dd = d * d8[t * nbmax + b];
+        const float dd = d * dd8;
         terms[(__umul24(r, nbmax) + b) * T + t] = dd * static_cast<float>(isum);
       }
     }
   }
   __syncthreads();
-  write_rows<T, PAIR, NT>(J, wr, terms, nb, nbmax, tokens, t0);
+  write_rows<T, PAIR, NT>(J, wr, terms, J.nb, nbmax, tokens, t0);
+}
+
+// FIX: every job's nb is a power of two up to NT/4 (the launch checks). It is
+// a kernel of its own rather than a branch in one: at the join of two walks
+// the compiler merges their pending loads and then waits for the activation
+// before issuing the first weights.
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
+__global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
+                                                       size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
+                                                       size_t t0, NormIn nrm) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  static_assert(!FIX || T == 1, "fixed columns: one token");
+  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // I2_S x I8_S --------------------------------------------------------------
@@ -1384,10 +1507,45 @@ uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
   return R < 1u ? 1u : R;
 }
 
-template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false, uint32_t NT = kThreads>
+template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false, uint32_t NT = kThreads,
+          bool FIX = false>
 void* kq_kernel() {
-  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT>)
-                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT>);
+  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX>)
+                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX>);
+}
+
+// The fixed-column kernels of the one-token, one-round launches (nullptr
+// where none is built): NT = 256 at 1, 2, 4 or 8 blocks per team, 512 at 1,
+// 2 or 4; norm-fused (pair or not) and plain.
+template <int FMT, uint32_t NT>
+void* kq_fix_kernel_nt(uint32_t ni, bool norm, bool pair) {
+  if (norm && pair) {
+    return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, true, NT, true>()
+           : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, true, NT, true>()
+           : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, true, NT, true>()
+                      : nullptr;
+  }
+  if (pair) return nullptr;
+  if (norm) {
+    return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, false, NT, true>()
+           : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, false, NT, true>()
+           : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, false, NT, true>()
+           : (ni == 8u && NT == kThreads) ? kq_kernel<FMT, 1, 8, 1, true, false, NT, true>()
+                                          : nullptr;
+  }
+  return ni == 1u ? kq_kernel<FMT, 1, 1, 1, false, false, NT, true>()
+         : ni == 2u ? kq_kernel<FMT, 1, 2, 1, false, false, NT, true>()
+         : ni == 4u ? kq_kernel<FMT, 1, 4, 1, false, false, NT, true>()
+         : (ni == 8u && NT == kThreads) ? kq_kernel<FMT, 1, 8, 1, false, false, NT, true>()
+                                        : nullptr;
+}
+
+void* kq_fix_kernel(uint32_t type_id, uint32_t ni, bool norm, bool pair, uint32_t nt) {
+  if (nt == kThreads)
+    return type_id == 12u ? kq_fix_kernel_nt<12, kThreads>(ni, norm, pair)
+                          : kq_fix_kernel_nt<14, kThreads>(ni, norm, pair);
+  return type_id == 12u ? kq_fix_kernel_nt<12, 2u * kThreads>(ni, norm, pair)
+                        : kq_fix_kernel_nt<14, 2u * kThreads>(ni, norm, pair);
 }
 
 // The 512-lane one-token kernels: 128 teams of ni blocks each take the rows
@@ -1616,7 +1774,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // 2048x5632: 6.6-6.75 against 7.45 us; Q4_K 5632x2048: 4.9 against 5.1).
     // The 500-workgroup 32000x2048 output launch keeps 256 (12.3 against
     // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
-    uint32_t nt = kThreads;
+    uint32_t nt = kThreads, nit = ni;
     if (T == 1 && FUSED && ni >= 2u) {
       const int forced = norm ? tuning().norm_nt : tuning().kq_nt;
       const bool wide = forced ? forced == 512 : wgs < static_cast<uint32_t>(device_cus());
@@ -1624,7 +1782,19 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       if (kw) {
         k = kw;
         nt = 2u * kThreads;
+        nit = ni / 2u;
       }
+    }
+    // One token, one preload round, and every job's blocks a power of two
+    // no larger than the teams: the fixed-column walk (BlockWalk).
+    // Tuning::kq_fix = false keeps the general walk.
+    if (T == 1 && FUSED && fq == 1u && tuning().kq_fix) {
+      bool fix = true;
+      for (uint32_t i = 0; i < jobs.n; i++) {
+        const uint32_t b = jobs.j[i].nb;
+        fix = fix && b != 0u && (b & (b - 1u)) == 0u && b <= nt / 4u;
+      }
+      if (void* kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : nullptr) k = kf;
     }
     void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
                     const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};

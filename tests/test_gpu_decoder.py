@@ -256,8 +256,9 @@ def test_one_token_launches_at_both_workgroup_sizes(ctx, monkeypatch):
     # RUSTICIDE_HIP_KQ_NT / RUSTICIDE_HIP_NORM_NT: the one-token k-quant
     # launches (norm-fused Q/K/V, attention output, gate/up, output; the
     # down projection) on 256-lane workgroups, or on 512-lane ones with half
-    # the blocks per team wherever a launch has two or more: the CPU path's
-    # logits either way
+    # the blocks per team wherever a launch has two or more; with the
+    # fixed-column block walk and (RUSTICIDE_HIP_KQ_FIX=0) without: the CPU
+    # path's logits every way
     model = synth.decoder_model(synth.TINYLLAMA, seed=2027)
     prompt = np.random.default_rng(8).integers(0, 32000, 9).astype(np.uint32)
     follow = [311, 7, 29999, 0, 1234]
@@ -267,9 +268,10 @@ def test_one_token_launches_at_both_workgroup_sizes(ctx, monkeypatch):
         want.append(cpu.forward(t, len(prompt) + i))
     cpu.close()
     try:
-        for nt in ("256", "512"):
+        for nt, fix in (("256", "1"), ("512", "1"), ("256", "0"), ("512", "0")):
             monkeypatch.setenv("RUSTICIDE_HIP_KQ_NT", nt)
             monkeypatch.setenv("RUSTICIDE_HIP_NORM_NT", nt)
+            monkeypatch.setenv("RUSTICIDE_HIP_KQ_FIX", fix)
             R.reload_tuning()
             gpu = R.Decoder(ctx, model)
             got = [gpu.forward_batch(prompt, 0)]
@@ -277,10 +279,10 @@ def test_one_token_launches_at_both_workgroup_sizes(ctx, monkeypatch):
                 got.append(gpu.forward(t, len(prompt) + i))
             gpu.close()
             for k, (g, c) in enumerate(zip(got, want)):
-                assert same_bits(g, c), f"{nt} lanes, step {k}: max |diff| {diff(g, c)}"
+                assert same_bits(g, c), f"{nt} lanes, fixed walk {fix}, step {k}: max |diff| {diff(g, c)}"
     finally:
-        monkeypatch.delenv("RUSTICIDE_HIP_KQ_NT")
-        monkeypatch.delenv("RUSTICIDE_HIP_NORM_NT")
+        for name in ("RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_NORM_NT", "RUSTICIDE_HIP_KQ_FIX"):
+            monkeypatch.delenv(name, raising=False)
         R.reload_tuning()
 
 

@@ -12,6 +12,7 @@ import pytest
 
 import oracle as O
 import rusticide_amd as R
+from rusticide_amd import hip as H
 from rusticide_amd import synth
 
 pytestmark = pytest.mark.gpu
@@ -36,8 +37,10 @@ VARIANTS = {
     # ones (half the blocks per team) wherever a launch has two or more
     "nt-256": {"RUSTICIDE_HIP_KQ_NT": "256"},
     "nt-512": {"RUSTICIDE_HIP_KQ_NT": "512"},
+    # the general block walk where the fixed-column one would run
+    "walk": {"RUSTICIDE_HIP_KQ_FIX": "0"},
 }
-SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT")
+SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_KQ_FIX")
 
 
 @pytest.fixture(params=list(VARIANTS))
@@ -185,6 +188,38 @@ def test_kquant_gemv_is_bit_identical_to_the_cpu_path(ctx, variant, type_id, row
         out = np.full(rows * tokens, np.nan, np.float32)
         R.matmul_batch(ctx, x, tokens, [(m, out)])
         assert_same_bits(out, want, f"type={type_id} {rows}x{cols} tokens={tokens}")
+
+
+@pytest.mark.parametrize("type_id", [12, 14])
+def test_activations_at_any_dword_offset(ctx, variant, type_id):
+    # device inputs 4, 8 or 12 bytes past a 16-byte boundary, and token rows
+    # of 2049 or 2051 values (later tokens start off one too): the fused
+    # kernels' 16-byte activation loads need only dword alignment
+    class At:  # the device values from float `off` of `buf` on
+        def __init__(self, buf, off, n):
+            self.buf, self.off, self.n = buf, off, n
+
+        def data_ptr(self):
+            return self.buf.data_ptr() + 4 * self.off
+
+        def numel(self):
+            return self.n
+
+    rows, cols = 64, 2048
+    data = synth.matrix(type_id, rows, cols, seed=31)
+    m = R.Matrix.load(ctx, type_id, data, rows, cols)
+    for tokens, width in ((1, 2048), (2, 2049), (3, 2051)):
+        x = synth.normal_f32(tokens * width, seed=width)
+        want = oracle_matmul(type_id, data, rows, cols, x, tokens)
+        for off in (1, 2, 3):
+            buf = H.DeviceArray.from_numpy(np.concatenate([np.zeros(off, np.float32), x, np.zeros(4, np.float32)]))
+            out = H.DeviceArray(rows * tokens)
+            out.fill_bytes(0xFF)
+            R.matmul_batch_device(ctx, At(buf, off, tokens * width), tokens, [(m, out)])
+            H.synchronize()
+            assert_same_bits(out.numpy(), want, f"tokens {tokens} width {width} offset {off}")
+            buf.free()
+            out.free()
 
 
 @pytest.mark.parametrize("type_id", [12, 14])
