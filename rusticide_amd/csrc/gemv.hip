@@ -204,11 +204,12 @@ __device__ __forceinline__ void norm_load(NormRound<K>& nr, const XGeom& g, cons
     const size_t e0 = static_cast<size_t>(u < g.total ? u : 0u) * 256u + 8u * hl;
     const u32x4 w0 = load16(reinterpret_cast<const uint8_t*>(nrm.weight + e0));
     const u32x4 w1 = load16(reinterpret_cast<const uint8_t*>(nrm.weight + e0 + 4));
-    u32x4 d0{}, d1{};
-    if (nrm.delta) {
-      d0 = load16(reinterpret_cast<const uint8_t*>(nrm.delta + e0));
-      d1 = load16(reinterpret_cast<const uint8_t*>(nrm.delta + e0 + 4));
-    }
+    // without a delta the weights are read twice and the copy discarded: a
+    // branch around these loads would make the compiler wait for them at
+    // its join, before the weight loads behind it
+    const float* dsrc = nrm.delta ? nrm.delta : nrm.weight;
+    const u32x4 d0 = load16(reinterpret_cast<const uint8_t*>(dsrc + e0));
+    const u32x4 d1 = load16(reinterpret_cast<const uint8_t*>(dsrc + e0 + 4));
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       nr.w[k][i] = __uint_as_float(w0[i]);
@@ -288,6 +289,14 @@ constexpr int issue_ahead() { return NI < 2 ? NI : 2; }
 // takes nh rows of the job's w from row0 on as its rows 0..nh-1, and the
 // same rows of w2 as its rows nh..2nh-1.
 struct WgRows {
+  // The job's first matrix and the byte offset of its second (a pair's up
+  // rows), the offset pinned in SGPRs: a per-lane select between J.w and
+  // J.w2 otherwise becomes a per-lane load of the pointer itself, whose wait
+  // (loads return in issue order) holds every weight load behind the
+  // activation loads issued before it. A pointer passed through the pin
+  // would lose its global address space (flat loads).
+  const uint8_t* w1;
+  uint64_t d2;
   uint32_t row0, nrows, nh;
   // row_of's chunk map: row = ((r >> cs) * nwg + w) << cs | (r & mask).
   // Contiguous rows are the case cs = 0, nwg = 1, w = row0, so the map has
@@ -300,13 +309,15 @@ template <bool PAIR>
 __device__ __forceinline__ WgRows wg_rows(const GemvJob& J, uint32_t R) {
   const uint32_t per = PAIR ? R / 2u : R;
   const uint32_t w = blockIdx.x - J.wg_begin;
+  uint64_t d2 = PAIR ? reinterpret_cast<uintptr_t>(J.w2) - reinterpret_cast<uintptr_t>(J.w) : 0u;
+  asm volatile("" : "+s"(d2));
   if (!PAIR && J.il) {
     const uint32_t cs = J.il - 1u;
-    return WgRows{0u, per, per, cs, J.rows / per, w, (1u << cs) - 1u};
+    return WgRows{J.w, d2, 0u, per, per, cs, J.rows / per, w, (1u << cs) - 1u};
   }
   const uint32_t row0 = w * per;
   const uint32_t nh = min(per, J.rows - row0);
-  return WgRows{row0, PAIR ? 2u * nh : nh, nh, 0u, 1u, row0, 0u};
+  return WgRows{J.w, d2, row0, PAIR ? 2u * nh : nh, nh, 0u, 1u, row0, 0u};
 }
 
 // The matrix row of workgroup row r (not of a pair's second half).
@@ -319,7 +330,7 @@ __device__ __forceinline__ uint32_t row_of(const WgRows& g, uint32_t r) {
 template <bool PAIR>
 __device__ __forceinline__ const uint8_t* block_at(const GemvJob& J, const WgRows& g, uint32_t r, uint32_t boff) {
   const bool second = PAIR && r >= g.nh;
-  const uint8_t* m = second ? J.w2 : J.w;
+  const uint8_t* m = g.w1 + (second ? g.d2 : 0u);
   const uint32_t row = PAIR ? g.row0 + (second ? r - g.nh : r) : row_of(g, r);
   return m + (__umul24(row, static_cast<uint32_t>(J.stride)) + boff);
 }
@@ -444,6 +455,9 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
   NormRound<FQ ? FQ : 1> nr;
   if constexpr (NORM) norm_load<FQ ? FQ : 1, NT>(nr, xg, nrm);
+  // the activation's loads go out before any weight load (loads return in
+  // issue order: the prologue waits only for these)
+  __builtin_amdgcn_sched_barrier(0);
   u32x4 hd[NI], c0[NI], c1[NI];
   auto issue = [&](int i) {
     const uint8_t* blk = walk.addr(i);
@@ -601,6 +615,9 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
   NormRound<FQ ? FQ : 1> nr;
   if constexpr (NORM) norm_load<FQ ? FQ : 1, NT>(nr, xg, nrm);
+  // the activation's loads go out before any weight load (loads return in
+  // issue order: the prologue waits only for these)
+  __builtin_amdgcn_sched_barrier(0);
   u32x4 A[NI], B[NI], C[NI];
   uint2 S[NI];
   uint32_t D[NI];
