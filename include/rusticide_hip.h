@@ -216,6 +216,11 @@ void rh_reload_tuning(void);
  * the guessing rounds it took; 7 means it finished with the sequential chain. */
 rh_status rh_ordered_sum_device(rh_ctx *ctx, const float *values, size_t n, float init, float *sum,
                                 uint32_t *rounds);
+/* Test hook with no reference counterpart: the same sum by the short form
+ * the one-token attention step uses for its softmax denominator (four values
+ * a lane); n <= 256. */
+rh_status rh_ordered_sum4_device(rh_ctx *ctx, const float *values, size_t n, float init, float *sum,
+                                 uint32_t *rounds);
 /* Test hook: the RoPE angle table rh_decoder_new builds on the host,
  * cos/sin of position * theta^(-2p/columns) per (position, pair)
  * (crates/rusticide-kernels/src/portable/rope.rs:7-23). */

@@ -642,6 +642,7 @@ __device__ __forceinline__ float mix_lds(const float* va, const float* w, uint32
 // softmax denominator is ordered_sum_wave's (the sequential sum's bits), and
 // wave 0 divides and mixes from LDS. Three barriers in all.
 constexpr uint32_t kStepLdsRows = 224;
+static_assert(kStepLdsRows <= 256u, "ordered_sum_wave4 sums at most 256 values");
 constexpr uint32_t kKeyStride = 68;
 
 inline size_t attention_step_lds_bytes(uint32_t nk) {
@@ -657,7 +658,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_lds_kernel(
   extern __shared__ __align__(16) float sh[];
   float* ka = sh;                         // [cap][kKeyStride] keys, then [cap][64] values
   float* w = ka + cap * kKeyStride;       // [cap] softmax weights
-  float* ws = w + cap;                    // the exps, in ordered_sum_wave's layout
+  float* ws = w + cap;                    // the exps, in order
   float* qh = ws + wave_sum_floats(cap);  // [64] the rotated query
   float* red = qh + 64;                   // [8]
   const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
@@ -740,16 +741,17 @@ __global__ __launch_bounds__(kAttnThreads) void attention_step_lds_kernel(
     const uint32_t row = (tid >> 4) + 16u * k;
     reinterpret_cast<f32x4*>(ka + row * 64u)[col] = vc[k];
   }
-  // the exps, -0.0 (the sum's identity) up to a multiple of 32
+  // the exps in order, -0.0 (the sum's identity) up to a multiple of 4
   if (tid < rows)
-    ws[wave_sum_index(tid)] = expf_ref(sc - mx);
-  else if (tid < ((rows + 31u) & ~31u))
-    ws[wave_sum_index(tid)] = -0.0f;
+    ws[tid] = expf_ref(sc - mx);
+  else if (tid < ((rows + 3u) & ~3u))
+    ws[tid] = -0.0f;
   __syncthreads();
   if (wave != 0) return;
-  // portable/norm.rs: the sum from 0.0 in order, then each exp over it
-  const float sum = ordered_sum_wave(ws, rows, 0.0f);
-  for (uint32_t i = lane; i < rows; i += 64u) w[i] = __fdiv_rn(ws[wave_sum_index(i)], sum);
+  // portable/norm.rs: the sum from 0.0 in order (runs of 4 a lane: rows <=
+  // 256), then each exp over it
+  const float sum = ordered_sum_wave4(ws, rows, 0.0f);
+  for (uint32_t i = lane; i < rows; i += 64u) w[i] = __fdiv_rn(ws[i], sum);
   mixed[static_cast<size_t>(h) * hd + lane] = mix_lds(ka, w, rows, lane);
 }
 
@@ -879,6 +881,16 @@ __global__ __launch_bounds__(64) void ordered_sum_kernel(const float* values, ui
 }
 
 constexpr size_t kMaxOrderedSumTest = 8192;
+
+// ordered_sum_wave4 over values[0..n), n <= 256, in its plain layout.
+__global__ __launch_bounds__(64) void ordered_sum4_kernel(const float* values, uint32_t n, float init, float* out,
+                                                          uint32_t* rounds) {
+  __shared__ __align__(16) float buf[256];
+  for (uint32_t i = threadIdx.x; i < 256u; i += 64u) buf[i] = i < n ? values[i] : -0.0f;
+  __syncthreads();
+  const float s = ordered_sum_wave4(buf, n, init, rounds);
+  if (threadIdx.x == 0) *out = s;
+}
 
 }  // namespace
 }  // namespace rh
@@ -1276,6 +1288,36 @@ rh_status rh_ordered_sum_device(rh_ctx* ctx, const float* values, size_t n, floa
   if (e == hipSuccess) {
     hipLaunchKernelGGL(ordered_sum_kernel, dim3(1), dim3(64), wave_sum_floats(static_cast<uint32_t>(n)) * 4u + 16u,
                        s, dv, static_cast<uint32_t>(n), init, dout, dr);
+    e = hipGetLastError();
+  }
+  uint32_t r = 0;
+  if (e == hipSuccess) e = hipMemcpyAsync(sum, dout, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipMemcpyAsync(&r, dr, 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (rounds) *rounds = r;
+  hipFree(dv);
+  hipFree(dout);
+  hipFree(dr);
+  return e == hipSuccess ? RH_OK : RH_ERR_DEVICE;
+}
+
+rh_status rh_ordered_sum4_device(rh_ctx* ctx, const float* values, size_t n, float init, float* sum,
+                                 uint32_t* rounds) {
+  if (!ctx || !sum || n > 256u || (n && !values)) return RH_ERR_INVALID_ARGUMENT;
+  if (hipSetDevice(ctx_device(ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  hipStream_t s = static_cast<hipStream_t>(rh_stream(ctx));
+  float *dv = nullptr, *dout = nullptr;
+  uint32_t* dr = nullptr;
+  if (dmalloc(&dv, n + 1) != hipSuccess || dmalloc(&dout, 1) != hipSuccess ||
+      hipMalloc(reinterpret_cast<void**>(&dr), 4) != hipSuccess) {
+    hipFree(dv);
+    hipFree(dout);
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  hipError_t e = n ? hipMemcpyAsync(dv, values, n * 4, hipMemcpyHostToDevice, s) : hipSuccess;
+  if (e == hipSuccess) e = hipMemsetAsync(dr, 0, 4, s);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(ordered_sum4_kernel, dim3(1), dim3(64), 0, s, dv, static_cast<uint32_t>(n), init, dout, dr);
     e = hipGetLastError();
   }
   uint32_t r = 0;

@@ -393,8 +393,9 @@ __device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, fl
       }
     }
     // which candidate of the next lane each end is: bits equal, one below,
-    // one above
-    const uint32_t next = dpp_fill<kDppWaveShl1>(gb, 0u);
+    // one above (the move kept out of DPP combining, as in ordered_sum_wave4)
+    uint32_t next = dpp_fill<kDppWaveShl1>(gb, 0u);
+    asm volatile("" : "+v"(next));
     uint32_t map = 0x03000000u;
 #pragma unroll
     for (int i = 0; i < 3; i++) {
@@ -427,6 +428,89 @@ __device__ __forceinline__ float ordered_sum_wave(const float* p, uint32_t n, fl
       load_chunk(p + c * 36u, w);
       end = chain1(end, w);
     }
+    r++;
+  }
+  if (rounds && lane == 0) *rounds = r;
+  return end;
+}
+
+// ordered_sum_wave for at most 256 values in plain order: p 16-byte aligned,
+// -0.0 from n up to the next multiple of 4. Lane l holds values 4l..4l+3,
+// so every chain is 4 additions long where ordered_sum_wave's are 32 (a
+// softmax over a few hundred rows spread 1-7 lanes of 32). Same contract
+// and the same rounds.
+__device__ __forceinline__ float ordered_sum_wave4(const float* p, uint32_t n, float init,
+                                                   uint32_t* rounds = nullptr) {
+  const uint32_t lane = __lane_id();
+  const uint32_t lanes = (n + 3u) >> 2;  // lanes holding values
+  if (lanes == 0) return init;
+  const bool mine = lane < lanes;
+  float v[4] = {-0.0f, -0.0f, -0.0f, -0.0f};
+  if (mine) {
+    const f32x4 t = reinterpret_cast<const f32x4*>(p)[lane];
+    v[0] = t[0];
+    v[1] = t[1];
+    v[2] = t[2];
+    v[3] = t[3];
+  }
+  double d = mine ? static_cast<double>((v[0] + v[1]) + (v[2] + v[3])) : 0.0;
+  {
+    // one chain from the approximate start refines the increment
+    const float g = guess_starts(d, init);
+    float e = g;
+#pragma unroll
+    for (int i = 0; i < 4; i++) e += v[i];
+    d = mine ? static_cast<double>(e) - static_cast<double>(g) : 0.0;
+  }
+  uint32_t r = 0, first_bad = 0;
+  float end = init;
+  bool done = false;
+  while (true) {
+    r++;
+    const float g = guess_starts(d, init);
+    const uint32_t gb = __float_as_uint(g);
+    const float cand[3] = {g, __uint_as_float(gb - 1u), __uint_as_float(gb + 1u)};
+    float s[3] = {cand[0], cand[1], cand[2]};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      s[0] += v[i];
+      s[1] += v[i];
+      s[2] += v[i];
+    }
+    uint32_t next = dpp_fill<kDppWaveShl1>(gb, 0u);
+    // kept out of the compiler's DPP combining: folded into the subtraction
+    // below as v_subrev_u32_dpp wave_shl:1 it read wrong lanes on gfx950
+    asm volatile("" : "+v"(next));
+    // the next lane's candidate each end is: ulp distance 0, -1, +1 are 0,
+    // 1, 2 (2|delta| - (delta < 0)), any other none; in arithmetic, so that
+    // no lane-dependent branch appears
+    uint32_t map = 0x03000000u;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const uint32_t delta = __float_as_uint(s[i]) - next;
+      const uint32_t neg = delta >> 31;
+      const uint32_t mag = min(neg ? 0u - delta : delta, 2u);
+      map |= min(2u * mag - neg, 3u) << (8 * i);
+    }
+    if (lane + 1u >= lanes) map = kMapIdentity;
+    const uint32_t state = wave_prefix_maps_excl(map) & 0xFFu;
+    const float mine_end = state == 1u ? s[1] : state == 2u ? s[2] : s[0];
+    const uint64_t bad = __ballot(mine && state == 3u);
+    if (bad == 0) {
+      end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine_end), static_cast<int>(lanes - 1u)));
+      done = true;
+      break;
+    }
+    first_bad = static_cast<uint32_t>(__builtin_ctzll(bad));  // >= 1: lane 0 is always resolved
+    end = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine_end), static_cast<int>(first_bad - 1u)));
+    if (r == kWaveSumRounds) break;
+    const float start = state == 1u ? cand[1] : state == 2u ? cand[2] : cand[0];
+    d = lane < first_bad ? static_cast<double>(mine_end) - static_cast<double>(start)
+                         : static_cast<double>(s[0]) - static_cast<double>(cand[0]);
+  }
+  if (!done) {
+    // `end` is the exact sum of the runs before lane first_bad
+    for (uint32_t i = 4u * first_bad; i < 4u * lanes; i++) end += p[i];
     r++;
   }
   if (rounds && lane == 0) *rounds = r;

@@ -391,6 +391,37 @@ def test_device_ordered_sum_is_the_sequential_fold(ctx):
         assert got.view(np.uint32) == want.view(np.uint32), (name, values.size, got, want, rounds)
 
 
+def _device_ordered_sum4(ctx, values, init):
+    import ctypes
+    L = R.lib()
+    L.rh_ordered_sum4_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_float,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    v = np.ascontiguousarray(values, np.float32)
+    out = np.zeros(1, np.float32)
+    rounds = np.zeros(1, np.uint32)
+    ctx.check(L.rh_ordered_sum4_device(ctx.handle, v.ctypes.data if v.size else None, v.size, float(init),
+                                       out.ctypes.data, rounds.ctypes.data))
+    return out[0], int(rounds[0])
+
+
+def test_device_short_ordered_sum_is_the_sequential_fold(ctx):
+    # the four-values-a-lane form (softmax denominators of up to 256 rows):
+    # every length to 256, and the hostile cases cut to 256 values
+    rng = np.random.default_rng(17)
+    cases = [("exps", rng.exponential(1.0, n).astype(np.float32), 0.0) for n in range(0, 257)]
+    cases += [(name, v[:256], init) for name, v, init in _ordered_sum_cases()]
+    for _ in range(64):
+        n = int(rng.integers(1, 257))
+        cases.append(("softmax", np.exp(rng.standard_normal(n) * 4).astype(np.float32), 0.0))
+    for name, values, init in cases:
+        got, rounds = _device_ordered_sum4(ctx, values, init)
+        want = _fold(values, init)
+        if np.isnan(want):
+            assert np.isnan(got), name
+            continue
+        assert got.view(np.uint32) == want.view(np.uint32), (name, values.size, got, want, rounds)
+
+
 def test_device_ordered_sum_settles_in_few_rounds(ctx):
     # the speculative rounds, not the closing sequential chain, finish the
     # RMSNorm-shaped sums (squares of hidden states, 2048 and 4096 wide)
