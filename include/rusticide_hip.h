@@ -216,6 +216,12 @@ void rh_reload_tuning(void);
  * the guessing rounds it took; 7 means it finished with the sequential chain. */
 rh_status rh_ordered_sum_device(rh_ctx *ctx, const float *values, size_t n, float init, float *sum,
                                 uint32_t *rounds);
+/* Test hook: the decoder's greedy pick over n logits on the device
+ * (Sampler::greedy_logits, crates/rusticide-sampling/src/sampler.rs:75-87 with
+ * filters.rs:37-43: NaN as -inf, f32::total_cmp, the last maximum wins);
+ * `finite` receives whether any logit is finite (when none is, the decoder
+ * reports RH_ERR_NO_VALID_TOKENS). */
+rh_status rh_greedy_pick_device(rh_ctx *ctx, const float *logits, size_t n, uint32_t *token, uint32_t *finite);
 /* Test hook with no reference counterpart: the same sum by the short form
  * the one-token attention step uses for its softmax denominator (four values
  * a lane); n <= 256. */

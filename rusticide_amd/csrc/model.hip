@@ -781,75 +781,88 @@ __device__ __forceinline__ int32_t total_key(float f) {
 // pick finds no finite logit. When `hidden` is given, the picked token's
 // embedding row (emb_type blocks at emb_data, emb_stride bytes per row) is
 // written there: the next step's input.
+// (key, index) as one unsigned 64-bit value in the pick's order: the
+// total-order key (made unsigned) above the index (a larger index wins a
+// tie: the last maximum). Keys of real logits are above INT32_MIN (a NaN
+// enters as -inf), so 0 stands for "no logit".
+__device__ __forceinline__ uint64_t pick_code(int32_t key, uint32_t idx) {
+  return (static_cast<uint64_t>(static_cast<uint32_t>(key) ^ 0x80000000u) << 32) | idx;
+}
+
+// The maximum code over the wave, in every lane: the keys first, then the
+// indices among the lanes holding the largest key.
+__device__ __forceinline__ uint64_t wave_max_code(uint64_t c) {
+  uint32_t hi = static_cast<uint32_t>(c >> 32);
+  uint32_t m = half_max_u32(hi);
+  m = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 0)),
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 32)));
+  uint32_t lo = hi == m ? static_cast<uint32_t>(c) : 0u;
+  lo = half_max_u32(lo);
+  lo = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), 0)),
+           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), 32)));
+  return (static_cast<uint64_t>(m) << 32) | lo;
+}
+
+// Greedy pick over the logits: NaN as -inf, max by total order, the last
+// maximum wins; out[0] = token, out[1] = 1 when some logit is finite. When
+// `tokens` is given the token is also appended at tokens[count[0]] (the
+// generation's record), count[0] advanced, and count[1] set for good once a
+// pick finds no finite logit. When `hidden` is given, the picked token's
+// embedding row (emb_type blocks at emb_data, emb_stride bytes per row) is
+// written there: the next step's input.
+// Each thread issues all of its loads (32 a pass, clamped into range) before
+// it looks at any, and the record's count is read first of all: the pick
+// waits on one memory round trip, not one per eight loads.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint32_t n, uint32_t* out,
                                                       uint32_t* tokens, uint32_t* count, uint32_t emb_type,
                                                       const uint8_t* emb_data, size_t emb_stride, uint32_t width,
                                                       float* hidden) {
-  __shared__ int32_t skey[16];
-  __shared__ uint32_t sidx[16];
-  __shared__ uint32_t sfin[16];
+  constexpr uint32_t kPer = 32;
+  __shared__ uint32_t shi[16], slo[16], sfin[16];
   __shared__ uint32_t s_pick;
-  int32_t best = INT32_MIN;
-  uint32_t bi = 0, fin = 0;
-  bool have = false;
-  // each thread visits its indices in increasing order, eight loads at once
-  for (uint32_t base = threadIdx.x; base < n; base += 8u * 1024u) {
-    float v[8];
+  uint32_t cnt = 0;
+  if (tokens && threadIdx.x == 0) cnt = count[0];
+  uint64_t best = 0;
+  uint32_t fin = 0;
+  for (uint32_t base = 0; base < n; base += kPer * 1024u) {  // uniform
+    float v[kPer];
 #pragma unroll
-    for (uint32_t j = 0; j < 8u; j++) {
-      const uint32_t i = base + j * 1024u;
-      if (i < n) v[j] = logits[i];
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t i = base + threadIdx.x + j * 1024u;
+      v[j] = logits[i < n ? i : n - 1u];
     }
 #pragma unroll
-    for (uint32_t j = 0; j < 8u; j++) {
-      const uint32_t i = base + j * 1024u;
-      if (i >= n) break;
-      fin |= __builtin_isfinite(v[j]) ? 1u : 0u;
-      const int32_t k = total_key(v[j] != v[j] ? -INFINITY : v[j]);
-      if (!have || k >= best) {
-        best = k;
-        bi = i;
-        have = true;
-      }
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t i = base + threadIdx.x + j * 1024u;
+      const bool in = i < n;
+      fin |= in && __builtin_isfinite(v[j]) ? 1u : 0u;
+      const uint64_t c = pick_code(total_key(v[j] != v[j] ? -INFINITY : v[j]), i);
+      best = in && c > best ? c : best;
     }
   }
-  // (key, index) maximum: a larger key, or an equal key at a larger index
-  for (int o = 32; o > 0; o >>= 1) {
-    const int32_t ok = __shfl_xor(best, o, 64);
-    const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(bi), o, 64));
-    const bool oh = __shfl_xor(have ? 1 : 0, o, 64) != 0;
-    fin |= static_cast<uint32_t>(__shfl_xor(static_cast<int>(fin), o, 64));
-    if (oh && (!have || ok > best || (ok == best && oi > bi))) {
-      best = ok;
-      bi = oi;
-      have = true;
-    }
-  }
+  best = wave_max_code(best);
+  fin = __ballot(fin != 0u) ? 1u : 0u;
   const uint32_t wv = threadIdx.x >> 6;
   if ((threadIdx.x & 63u) == 0) {
-    skey[wv] = have ? best : INT32_MIN;
-    sidx[wv] = have ? bi : 0u;
-    sfin[wv] = fin | (have ? 2u : 0u);
+    shi[wv] = static_cast<uint32_t>(best >> 32);
+    slo[wv] = static_cast<uint32_t>(best);
+    sfin[wv] = fin;
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    int32_t b = INT32_MIN;
-    uint32_t idx = 0, f = 0;
-    bool any = false;
+    uint64_t b = 0;
+    uint32_t f = 0;
     for (uint32_t w = 0; w < 16u; w++) {
-      f |= sfin[w] & 1u;
-      if (!(sfin[w] & 2u)) continue;
-      if (!any || skey[w] > b || (skey[w] == b && sidx[w] > idx)) {
-        b = skey[w];
-        idx = sidx[w];
-        any = true;
-      }
+      const uint64_t c = (static_cast<uint64_t>(shi[w]) << 32) | slo[w];
+      b = c > b ? c : b;
+      f |= sfin[w];
     }
+    const uint32_t idx = static_cast<uint32_t>(b);
     out[0] = idx;
     out[1] = f;
     if (tokens) {
-      tokens[count[0]] = idx;
-      count[0] = count[0] + 1u;
+      tokens[cnt] = idx;
+      count[0] = cnt + 1u;
       if (!f) count[1] = 1u;
     }
     s_pick = idx;
@@ -1298,6 +1311,32 @@ rh_status rh_ordered_sum_device(rh_ctx* ctx, const float* values, size_t n, floa
   hipFree(dv);
   hipFree(dout);
   hipFree(dr);
+  return e == hipSuccess ? RH_OK : RH_ERR_DEVICE;
+}
+
+rh_status rh_greedy_pick_device(rh_ctx* ctx, const float* logits, size_t n, uint32_t* token, uint32_t* finite) {
+  if (!ctx || !token || !finite || n == 0 || n > 0xFFFFFFFFu || !logits) return RH_ERR_INVALID_ARGUMENT;
+  if (hipSetDevice(ctx_device(ctx)) != hipSuccess) return RH_ERR_DEVICE;
+  hipStream_t s = static_cast<hipStream_t>(rh_stream(ctx));
+  float* dl = nullptr;
+  uint32_t* dout = nullptr;
+  if (dmalloc(&dl, n) != hipSuccess || hipMalloc(reinterpret_cast<void**>(&dout), 8) != hipSuccess) {
+    hipFree(dl);
+    return RH_ERR_OUT_OF_MEMORY;
+  }
+  hipError_t e = hipMemcpyAsync(dl, logits, n * 4, hipMemcpyHostToDevice, s);
+  if (e == hipSuccess) {
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, dl, static_cast<uint32_t>(n), dout, nullptr, nullptr,
+                       0u, nullptr, size_t{0}, 0u, nullptr);
+    e = hipGetLastError();
+  }
+  uint32_t o[2] = {0, 0};
+  if (e == hipSuccess) e = hipMemcpyAsync(o, dout, 8, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  *token = o[0];
+  *finite = o[1];
+  hipFree(dl);
+  hipFree(dout);
   return e == hipSuccess ? RH_OK : RH_ERR_DEVICE;
 }
 

@@ -435,6 +435,55 @@ def test_device_ordered_sum_settles_in_few_rounds(ctx):
     assert max(rounds) <= 6 and np.mean(rounds) <= 3.5, rounds
 
 
+def test_greedy_pick_matches_the_cpu_rule(ctx):
+    # filters.rs:37-43 / sampler.rs:75-87 on the device: NaN as -inf,
+    # total_cmp order (-0.0 below +0.0), the last maximum wins; vocabularies
+    # past one pass of loads (32768) included
+    import ctypes
+    L = R.lib()
+    L.rh_greedy_pick_device.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p,
+                                        ctypes.c_void_p]
+    rng = np.random.default_rng(21)
+
+    def pick(x):
+        x = np.ascontiguousarray(x, np.float32)
+        tok, fin = ctypes.c_uint32(), ctypes.c_uint32()
+        ctx.check(L.rh_greedy_pick_device(ctx.handle, x.ctypes.data, x.size, ctypes.byref(tok), ctypes.byref(fin)))
+        return tok.value, fin.value
+
+    cases = []
+    for n in (1, 2, 63, 1000, 32000, 32768, 32769, 50000, 128256):
+        cases.append(rng.standard_normal(n).astype(np.float32))
+    ties = np.zeros(32000, np.float32)
+    ties[[5, 700, 31999]] = 3.0
+    cases.append(ties)
+    ties2 = np.full(32000, -1.0, np.float32)
+    ties2[[10, 20000]] = 2.0
+    cases.append(ties2)
+    zeros = np.zeros(5000, np.float32)
+    zeros[[100, 4000]] = -0.0
+    cases.append(zeros)
+    signed_zeros = np.full(4096, -0.0, np.float32)
+    signed_zeros[17] = 0.0
+    cases.append(signed_zeros)
+    nan = rng.standard_normal(32000).astype(np.float32)
+    nan[[3, 77, 31000]] = np.nan
+    cases.append(nan)
+    inf = rng.standard_normal(32000).astype(np.float32)
+    inf[[9, 30000]] = np.inf
+    cases.append(inf)
+    for x in cases:
+        tok, fin = pick(x)
+        assert fin == 1
+        assert tok == O.greedy(x), (x.size, tok, O.greedy(x))
+    # no finite logit: the CPU path reports NoValidTokens
+    for x in (np.full(100, np.nan, np.float32), np.float32([np.inf, -np.inf, np.nan])):
+        tok, fin = pick(x)
+        assert fin == 0
+        with pytest.raises(O.DecoderError):
+            O.greedy(x)
+
+
 def test_device_division_is_rounded_to_nearest(ctx):
     rng = np.random.default_rng(5)
     a = rng.integers(0, 0x7F800000, 1 << 22, dtype=np.uint32).view(np.float32)
