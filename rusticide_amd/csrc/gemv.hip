@@ -1532,8 +1532,8 @@ void* kq_kernel() {
 }
 
 // The fixed-column kernels of the one-token, one-round launches (nullptr
-// where none is built): NT = 256 at 1, 2, 4 or 8 blocks per team, 512 at 1,
-// 2 or 4; norm-fused (pair or not) and plain.
+// where none is built): 1, 2, 4 or 8 blocks per team (8: not for a pair);
+// norm-fused (pair or not) and plain.
 template <int FMT, uint32_t NT>
 void* kq_fix_kernel_nt(uint32_t ni, bool norm, bool pair) {
   if (norm && pair) {
@@ -1547,14 +1547,14 @@ void* kq_fix_kernel_nt(uint32_t ni, bool norm, bool pair) {
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, false, NT, true>()
            : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, false, NT, true>()
            : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, false, NT, true>()
-           : (ni == 8u && NT == kThreads) ? kq_kernel<FMT, 1, 8, 1, true, false, NT, true>()
-                                          : nullptr;
+           : ni == 8u ? kq_kernel<FMT, 1, 8, 1, true, false, NT, true>()
+                      : nullptr;
   }
   return ni == 1u ? kq_kernel<FMT, 1, 1, 1, false, false, NT, true>()
          : ni == 2u ? kq_kernel<FMT, 1, 2, 1, false, false, NT, true>()
          : ni == 4u ? kq_kernel<FMT, 1, 4, 1, false, false, NT, true>()
-         : (ni == 8u && NT == kThreads) ? kq_kernel<FMT, 1, 8, 1, false, false, NT, true>()
-                                        : nullptr;
+         : ni == 8u ? kq_kernel<FMT, 1, 8, 1, false, false, NT, true>()
+                    : nullptr;
 }
 
 void* kq_fix_kernel(uint32_t type_id, uint32_t ni, bool norm, bool pair, uint32_t nt) {
@@ -1578,14 +1578,16 @@ void* kq_wide_kernel_fmt(uint32_t fq, uint32_t ni, bool norm, bool pair) {
                                                                    : nullptr;
     }
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, false, W>()
-           : ni == 4u                                             ? kq_kernel<FMT, 1, 4, 1, true, false, W>()
-                                                                  : nullptr;
+           : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, false, W>()
+           : ni == 8u ? kq_kernel<FMT, 1, 8, 1, true, false, W>()
+                      : nullptr;
   }
   if (pair) return nullptr;
   if (fq == 1u)
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, false, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, false, false, W>()
-           : ni == 4u                                              ? kq_kernel<FMT, 1, 4, 1, false, false, W>()
-                                                                   : nullptr;
+           : ni == 4u ? kq_kernel<FMT, 1, 4, 1, false, false, W>()
+           : ni == 8u ? kq_kernel<FMT, 1, 8, 1, false, false, W>()
+                      : nullptr;
   if (fq == 4u)
     return ni == 1u ? kq_kernel<FMT, 1, 1, 4, false, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 4, false, false, W>()
            : ni == 4u                                              ? kq_kernel<FMT, 1, 4, 4, false, false, W>()
@@ -1744,7 +1746,22 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
   // Tuning::norm_ni forces the norm-fused one-token launches, for tuning
   if (const int v = tuning().norm_ni)
     if (norm && T == 1 && fq == 1u && min_blocks_per_team(nbl) <= 2u) ni = static_cast<uint32_t>(v);
-  const uint32_t R = rows_per_wg(type_id, nbl, ni);
+  // A one-round launch of eight blocks per team (an output-sized matrix)
+  // takes 512 lanes and twice the rows per workgroup when that still gives
+  // 15/16 of the CUs a workgroup: half the activation quantizations (32000x2048
+  // Q6_K: 250 workgroups, 12.03-12.22 against 12.33-12.58 us). The
+  // norm-fused output launch of the decoder keeps 256 (1-2 us a token
+  // slower at 512). Tuning::kq_nt and Tuning::norm_nt force it (512) or keep
+  // 256.
+  bool wide8 = false;
+  if (T == 1 && FUSED && fq == 1u && ni == 8u && !pair_job) {
+    const uint32_t r8 = rows_per_wg(type_id, nbl, 16u);
+    uint32_t w8 = 0;
+    for (uint32_t i = 0; i < jobs.n; i++) w8 += (jobs.j[i].rows + r8 - 1u) / r8;
+    const int forced = norm ? tuning().norm_nt : tuning().kq_nt;
+    wide8 = forced ? forced == 512 : !norm && 16u * w8 >= 15u * static_cast<uint32_t>(device_cus());
+  }
+  const uint32_t R = rows_per_wg(type_id, nbl, wide8 ? 16u : ni);
   // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
   const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
   if (pair && (!norm || !kquant || R < 2u)) return hipErrorInvalidValue;
@@ -1761,7 +1778,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
   // (64 teams / nb blocks). Smaller grids measured no gain.
   jobs.j[0].il = 0u;
   if (kquant && jobs.n == 1u && !pair && nbl <= 64u && 64u % nbl == 0u && jobs.j[0].rows == wgs * per &&
-      wgs >= static_cast<uint32_t>(device_cus()) && interleave_rows()) {
+      (wgs >= static_cast<uint32_t>(device_cus()) || wide8) && interleave_rows()) {
     const uint32_t c = 64u / nbl;
     if (per % c == 0u) jobs.j[0].il = static_cast<uint32_t>(__builtin_ctz(c)) + 1u;
   }
@@ -1792,7 +1809,14 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // The 500-workgroup 32000x2048 output launch keeps 256 (12.3 against
     // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
     uint32_t nt = kThreads, nit = ni;
-    if (T == 1 && FUSED && ni >= 2u) {
+    if (wide8) {
+      if (void* kw = kq_wide_kernel(type_id, fq, 8u, norm != nullptr, pair)) {
+        k = kw;
+        nt = 2u * kThreads;
+      } else {
+        return hipErrorNotSupported;  // every one-round eight-block form is built
+      }
+    } else if (T == 1 && FUSED && ni >= 2u) {
       const int forced = norm ? tuning().norm_nt : tuning().kq_nt;
       const bool wide = forced ? forced == 512 : wgs < static_cast<uint32_t>(device_cus());
       void* kw = wide ? kq_wide_kernel(type_id, fq, ni / 2u, norm != nullptr, pair) : nullptr;
