@@ -2053,9 +2053,18 @@ void* i2s_q8_pick(uint32_t cpl) {
       default: return nullptr;
     }
   } else {
-    return cpl <= 4u ? reinterpret_cast<void*>(gemv_i2s_q8_kernel<T, LPR, 4>)
-         : cpl <= 8u ? reinterpret_cast<void*>(gemv_i2s_q8_kernel<T, LPR, 8>)
-                     : nullptr;
+    // only the forms whose registers hold their chunks (no scratch): four
+    // chunks a lane up to seven tokens, eight up to three; gemv_i2s_kernel
+    // takes the rest
+    if (cpl <= 4u) {
+      if constexpr (T <= 7) return reinterpret_cast<void*>(gemv_i2s_q8_kernel<T, LPR, 4>);
+      return nullptr;
+    }
+    if (cpl <= 8u) {
+      if constexpr (T <= 3) return reinterpret_cast<void*>(gemv_i2s_q8_kernel<T, LPR, 8>);
+      return nullptr;
+    }
+    return nullptr;
   }
 }
 
