@@ -372,6 +372,7 @@ void load_tuning() {
   const int nnt = env_int("RUSTICIDE_HIP_NORM_NT", 0);
   t.norm_nt = nnt == 256 || nnt == 512 ? nnt : 0;
   t.kq_fix = env_int("RUSTICIDE_HIP_KQ_FIX", 1) != 0;
+  t.kq_balance = env_int("RUSTICIDE_HIP_KQ_BALANCE", 1) != 0;
   const int gr = env_int("RUSTICIDE_HIP_I2S_GROUPS", 0);
   t.i2s_groups = gr == 1 || gr == 2 || gr == 4 ? gr : 0;
   const int lpr = env_int("RUSTICIDE_HIP_I2S_LPR", 0);

@@ -1761,7 +1761,36 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     const int forced = norm ? tuning().norm_nt : tuning().kq_nt;
     wide8 = forced ? forced == 512 : !norm && 16u * w8 >= 15u * static_cast<uint32_t>(device_cus());
   }
-  const uint32_t R = rows_per_wg(type_id, nbl, wide8 ? 16u : ni);
+  uint32_t R = rows_per_wg(type_id, nbl, wide8 ? 16u : ni);
+  // A one-token grid of between one and two workgroups per CU leaves some
+  // CUs twice the rows of others and repeats the activation prologue once
+  // per workgroup: it takes one workgroup per CU instead, 512 lanes and the
+  // blocks per team that hold its rows (the gate/up pair: 256 workgroups of
+  // 22 + 22 rows at four blocks a team, 8.36 against 9.57 us). Grids below
+  // one workgroup per CU keep their shape (more workgroups measured slower:
+  // Q/K/V 7.52 against 6.57 us), and so do the eight-block output launches
+  // (the rule above). Tuning::kq_balance = false keeps every grid, and so
+  // does a forced 256-lane shape (Tuning::kq_nt, Tuning::norm_nt).
+  bool balanced = false;
+  if (T == 1 && FUSED && kquant && !wide8 && ni < 8u && tuning().kq_balance &&
+      (norm ? tuning().norm_nt : tuning().kq_nt) != 256) {
+    const uint32_t cus = static_cast<uint32_t>(device_cus());
+    const uint32_t per0 = pair_job ? R / 2u : R;
+    uint32_t wcur = 0;
+    for (uint32_t i = 0; i < jobs.n; i++) wcur += (jobs.j[i].rows + per0 - 1u) / per0;
+    if (per0 > 0u && wcur > cus && wcur < 2u * cus) {
+      const uint32_t rows_main = pair_job ? jobs.j[0].rows : total_rows;
+      const uint32_t per = (rows_main + cus - 1u) / cus;
+      const uint32_t R2 = pair_job ? 2u * per : per;
+      const uint32_t need = (R2 * nbl + 2u * kThreads / 4u - 1u) / (2u * kThreads / 4u);
+      const uint32_t nib = need <= 1u ? 1u : need <= 2u ? 2u : need <= 4u ? 4u : need <= 8u ? 8u : 0u;
+      if (nib && (!pair_job || R2 >= 2u) && kq_wide_kernel(type_id, fq, nib, norm != nullptr, pair_job)) {
+        R = R2;
+        ni = nib;
+        balanced = true;
+      }
+    }
+  }
   // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
   const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
   if (pair && (!norm || !kquant || R < 2u)) return hipErrorInvalidValue;
@@ -1809,7 +1838,10 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // The 500-workgroup 32000x2048 output launch keeps 256 (12.3 against
     // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
     uint32_t nt = kThreads, nit = ni;
-    if (wide8) {
+    if (balanced) {
+      k = kq_wide_kernel(type_id, fq, ni, norm != nullptr, pair);
+      nt = 2u * kThreads;
+    } else if (wide8) {
       if (void* kw = kq_wide_kernel(type_id, fq, 8u, norm != nullptr, pair)) {
         k = kw;
         nt = 2u * kThreads;

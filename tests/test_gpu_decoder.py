@@ -268,10 +268,15 @@ def test_one_token_launches_at_both_workgroup_sizes(ctx, monkeypatch):
         want.append(cpu.forward(t, len(prompt) + i))
     cpu.close()
     try:
-        for nt, fix in (("256", "1"), ("512", "1"), ("256", "0"), ("512", "0")):
-            monkeypatch.setenv("RUSTICIDE_HIP_KQ_NT", nt)
-            monkeypatch.setenv("RUSTICIDE_HIP_NORM_NT", nt)
+        for nt, fix, bal in (("256", "1", "1"), ("512", "1", "1"), ("256", "0", "1"), ("512", "0", "1"),
+                             ("0", "1", "0")):
+            for name, v in (("RUSTICIDE_HIP_KQ_NT", nt), ("RUSTICIDE_HIP_NORM_NT", nt)):
+                if v == "0":
+                    monkeypatch.delenv(name, raising=False)
+                else:
+                    monkeypatch.setenv(name, v)
             monkeypatch.setenv("RUSTICIDE_HIP_KQ_FIX", fix)
+            monkeypatch.setenv("RUSTICIDE_HIP_KQ_BALANCE", bal)
             R.reload_tuning()
             gpu = R.Decoder(ctx, model)
             got = [gpu.forward_batch(prompt, 0)]
@@ -279,9 +284,9 @@ def test_one_token_launches_at_both_workgroup_sizes(ctx, monkeypatch):
                 got.append(gpu.forward(t, len(prompt) + i))
             gpu.close()
             for k, (g, c) in enumerate(zip(got, want)):
-                assert same_bits(g, c), f"{nt} lanes, fixed walk {fix}, step {k}: max |diff| {diff(g, c)}"
+                assert same_bits(g, c), f"{nt} lanes, fixed walk {fix}, balance {bal}, step {k}: {diff(g, c)}"
     finally:
-        for name in ("RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_NORM_NT", "RUSTICIDE_HIP_KQ_FIX"):
+        for name in ("RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_NORM_NT", "RUSTICIDE_HIP_KQ_FIX", "RUSTICIDE_HIP_KQ_BALANCE"):
             monkeypatch.delenv(name, raising=False)
         R.reload_tuning()
 

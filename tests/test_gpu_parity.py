@@ -39,8 +39,11 @@ VARIANTS = {
     "nt-512": {"RUSTICIDE_HIP_KQ_NT": "512"},
     # the general block walk where the fixed-column one would run
     "walk": {"RUSTICIDE_HIP_KQ_FIX": "0"},
+    # grids of one to two workgroups per CU kept as they are
+    "no-balance": {"RUSTICIDE_HIP_KQ_BALANCE": "0"},
 }
-SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_KQ_FIX")
+SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_KQ_FIX",
+            "RUSTICIDE_HIP_KQ_BALANCE")
 
 
 @pytest.fixture(params=list(VARIANTS))
