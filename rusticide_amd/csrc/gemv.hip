@@ -428,6 +428,114 @@ struct BlockWalk {
   }
 };
 
+// One 4-lane team's share of a k-quant block: decoded once per block (the
+// scales and the lane's 16 bytes of each run), then against each token's
+// activation. The term is valid in lane p == 0 of the team after the quad
+// sums, which every lane runs.
+
+// Q4_K: lane p takes sub-blocks j0, j0+1, j0+4, j0+5 (j0 = 2(p >> 1)),
+// bytes 16(p & 1).. of each (quantize/src/q4_k.rs:17-25, ggml
+// get_scale_min_k4 for the 6-bit scales and mins).
+struct Q4Dec {
+  int32_t sc[4], m[4];
+  float d, dmin;
+  uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
+};
+
+__device__ __forceinline__ Q4Dec q4k_decode(const u32x4& h, const u32x4& c0, const u32x4& c1, uint32_t j0) {
+  Q4Dec q;
+  q.sc[0] = static_cast<int32_t>(bfe(h.y, 8u * j0, 6));
+  q.sc[1] = static_cast<int32_t>(bfe(h.y, 8u * j0 + 8u, 6));
+  q.sc[2] = static_cast<int32_t>(bfe(h.w, 8u * j0, 4) | (bfe(h.y, 8u * j0 + 6u, 2) << 4));
+  q.sc[3] = static_cast<int32_t>(bfe(h.w, 8u * j0 + 8u, 4) | (bfe(h.y, 8u * j0 + 14u, 2) << 4));
+  q.m[0] = static_cast<int32_t>(bfe(h.z, 8u * j0, 6));
+  q.m[1] = static_cast<int32_t>(bfe(h.z, 8u * j0 + 8u, 6));
+  q.m[2] = static_cast<int32_t>(bfe(h.w, 8u * j0 + 4u, 4) | (bfe(h.z, 8u * j0 + 6u, 2) << 4));
+  q.m[3] = static_cast<int32_t>(bfe(h.w, 8u * j0 + 12u, 4) | (bfe(h.z, 8u * j0 + 14u, 2) << 4));
+  q.d = f16_lo(h.x);
+  q.dmin = f16_hi(h.x);
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    q.lo0[k] = c0[k] & 0x0F0F0F0Fu;
+    q.hi0[k] = (c0[k] >> 4) & 0x0F0F0F0Fu;
+    q.lo1[k] = c1[k] & 0x0F0F0F0Fu;
+    q.hi1[k] = (c1[k] >> 4) & 0x0F0F0F0Fu;
+  }
+  return q;
+}
+
+// a: the activation quants of the lane's four runs; s: their 32-block sums
+// (S[0], S[1], S[4], S[5] of the block, read by the min lanes); dd8: d8.
+__device__ __forceinline__ float q4k_term(const Q4Dec& q, const u32x4& a0, const u32x4& a1, const u32x4& a2,
+                                          const u32x4& a3, const int32_t (&s)[4], float dd8, bool min_lane) {
+  int32_t D0 = 0, D1 = 0, D2 = 0, D3 = 0;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    D0 = dot4(q.lo0[k], a0[k], D0);
+    D1 = dot4(q.hi0[k], a1[k], D1);
+    D2 = dot4(q.lo1[k], a2[k], D2);
+    D3 = dot4(q.hi1[k], a3[k], D3);
+  }
+  // 24-bit multiplies are exact here: |D| < 2^17, sums of 32 quants < 2^12,
+  // scales and mins below 64
+  int32_t isum = __mul24(q.sc[0], D0) + __mul24(q.sc[1], D1) + __mul24(q.sc[2], D2) + __mul24(q.sc[3], D3);
+  int32_t msum =
+      min_lane ? (__mul24(q.m[0], s[0]) + __mul24(q.m[1], s[1]) + __mul24(q.m[2], s[2]) + __mul24(q.m[3], s[3])) : 0;
+  isum = quad_sum(isum);
+  msum = quad_sum(msum);
+  // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
+  const float neg = -(q.dmin * static_cast<float>(msum));
+  return dd8 * __builtin_fmaf(q.d, static_cast<float>(isum), neg);
+}
+
+// Q6_K: lane p (h = p >> 1, gq = p & 1) takes runs of ql[64h+16gq..],
+// ql[64h+32+16gq..] and qh[32h+16gq..] (q6_k.rs:13-43), four 16-groups of
+// half h.
+struct Q6Dec {
+  int32_t sc[4];
+  float d;
+  uint32_t q0[4], q1[4], q2[4], q3[4];
+};
+
+__device__ __forceinline__ Q6Dec q6k_decode(const u32x4& a, const u32x4& bq, const u32x4& c, uint2 S, uint32_t D,
+                                            uint32_t gq) {
+  Q6Dec q;
+  // scale of run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
+  q.sc[0] = __builtin_amdgcn_sbfe(static_cast<int32_t>(S.x), 8u * gq, 8);
+  q.sc[1] = __builtin_amdgcn_sbfe(static_cast<int32_t>(S.x), 8u * gq + 16u, 8);
+  q.sc[2] = __builtin_amdgcn_sbfe(static_cast<int32_t>(S.y), 8u * gq, 8);
+  q.sc[3] = __builtin_amdgcn_sbfe(static_cast<int32_t>(S.y), 8u * gq + 16u, 8);
+  q.d = f16_lo(D);  // bytes 208..209
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    q.q0[k] = (a[k] & 0x0F0F0F0Fu) | ((c[k] << 4) & 0x30303030u);
+    q.q1[k] = (bq[k] & 0x0F0F0F0Fu) | ((c[k] << 2) & 0x30303030u);
+    q.q2[k] = ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0x30303030u);
+    q.q3[k] = ((bq[k] >> 4) & 0x0F0F0F0Fu) | ((c[k] >> 2) & 0x30303030u);
+  }
+  return q;
+}
+
+// a: the activation quants of the lane's four runs; bias: -32 x their
+// 16-run quant sums; dd8: d8.
+__device__ __forceinline__ float q6k_term(const Q6Dec& q, const u32x4& a0, const u32x4& a1, const u32x4& a2,
+                                          const u32x4& a3, const int32_t (&bias)[4], float dd8) {
+  int32_t D0 = bias[0], D1 = bias[1], D2 = bias[2], D3 = bias[3];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    D0 = dot4(q.q0[k], a0[k], D0);
+    D1 = dot4(q.q1[k], a1[k], D1);
+    D2 = dot4(q.q2[k], a2[k], D2);
+    D3 = dot4(q.q3[k], a3[k], D3);
+  }
+  // |D| < 2^20 and |scale| <= 128: the 24-bit multiplies are exact
+  const int32_t isum =
+      quad_sum(__mul24(q.sc[0], D0) + __mul24(q.sc[1], D1) + __mul24(q.sc[2], D2) + __mul24(q.sc[3], D3));
+  // int_dot.rs:203: read_f16_le(block, 208) * span.scales[0] * lossy(sum)
+  const float dd = q.d * dd8;
+  return dd * static_cast<float>(isum);
+}
+
 // Q4_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | sums [T][nbmax*8] i32 |
 //      terms [R][nbmax][T] f32
@@ -510,30 +618,11 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
     if (!walk.live(it)) break;  // uniform over the team
     uint32_t r, b;
     walk.rb(it, r, b);
-    const u32x4 h = hd[it];
-    // 6-bit scales/mins of sub-blocks j0, j0+1, j0+4, j0+5 (ggml get_scale_min_k4,
-    // quantize/src/q4_k.rs:17-25)
-    const int32_t sc0 = static_cast<int32_t>(bfe(h.y, 8u * j0, 6));
-    const int32_t sc1 = static_cast<int32_t>(bfe(h.y, 8u * j0 + 8u, 6));
-    const int32_t sc2 = static_cast<int32_t>(bfe(h.w, 8u * j0, 4) | (bfe(h.y, 8u * j0 + 6u, 2) << 4));
-    const int32_t sc3 = static_cast<int32_t>(bfe(h.w, 8u * j0 + 8u, 4) | (bfe(h.y, 8u * j0 + 14u, 2) << 4));
-    const int32_t m0 = static_cast<int32_t>(bfe(h.z, 8u * j0, 6));
-    const int32_t m1 = static_cast<int32_t>(bfe(h.z, 8u * j0 + 8u, 6));
-    const int32_t m2 = static_cast<int32_t>(bfe(h.w, 8u * j0 + 4u, 4) | (bfe(h.z, 8u * j0 + 6u, 2) << 4));
-    const int32_t m3 = static_cast<int32_t>(bfe(h.w, 8u * j0 + 12u, 4) | (bfe(h.z, 8u * j0 + 14u, 2) << 4));
-    const float d = f16_lo(h.x), dmin = f16_hi(h.x);
-    uint32_t lo0[4], hi0[4], lo1[4], hi1[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      lo0[k] = c0[it][k] & 0x0F0F0F0Fu;
-      hi0[k] = (c0[it][k] >> 4) & 0x0F0F0F0Fu;
-      lo1[k] = c1[it][k] & 0x0F0F0F0Fu;
-      hi1[k] = (c1[it][k] >> 4) & 0x0F0F0F0Fu;
-    }
+    const Q4Dec q = q4k_decode(hd[it], c0[it], c1[it], j0);
 #pragma unroll
     for (int t = 0; t < T; t++) {
       u32x4 a0 = fa[0], a1 = fa[1], a2 = fa[2], a3 = fa[3];
-      int32_t s0 = fs[0], s1 = fs[1], s2 = fs[2], s3 = fs[3];
+      int32_t sv[4] = {fs[0], fs[1], fs[2], fs[3]};
       float dd8 = fd8;
       if constexpr (!FIX) {
         const int8_t* at = act + t * abytes;
@@ -542,31 +631,14 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
         a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 128u));
         a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 160u));
         const int32_t* S = sums + t * nbmax * 8u + b * 8u + j0;
-        s0 = S[0];
-        s1 = S[1];
-        s2 = S[4];
-        s3 = S[5];
+        sv[0] = S[0];
+        sv[1] = S[1];
+        sv[2] = S[4];
+        sv[3] = S[5];
         dd8 = d8[t * nbmax + b];
       }
-      int32_t D0 = 0, D1 = 0, D2 = 0, D3 = 0;
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        D0 = dot4(lo0[k], a0[k], D0);
-        D1 = dot4(hi0[k], a1[k], D1);
-        D2 = dot4(lo1[k], a2[k], D2);
-        D3 = dot4(hi1[k], a3[k], D3);
-      }
-      // 24-bit multiplies are exact here: |D| < 2^17, sums of 32 quants < 2^12,
-      // scales and mins below 64
-      int32_t isum = __mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3);
-      int32_t msum = min_lane ? (__mul24(m0, s0) + __mul24(m1, s1) + __mul24(m2, s2) + __mul24(m3, s3)) : 0;
-      isum = quad_sum(isum);
-      msum = quad_sum(msum);
-      if (p == 0) {
-        // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
-        const float neg = -(dmin * static_cast<float>(msum));
-        terms[(__umul24(r, nbmax) + b) * T + t] = dd8 * __builtin_fmaf(d, static_cast<float>(isum), neg);
-      }
+      const float term = q4k_term(q, a0, a1, a2, a3, sv, dd8, min_lane);
+      if (p == 0) terms[(__umul24(r, nbmax) + b) * T + t] = term;
     }
   }
   __syncthreads();
@@ -671,26 +743,11 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
     if (!walk.live(it)) break;  // uniform over the team
     uint32_t r, b;
     walk.rb(it, r, b);
-    const u32x4 a = A[it], bq = B[it], c = C[it];
-    const uint32_t slo = S[it].x, shi = S[it].y;
-    // scale of run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
-    const int32_t sc0 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq, 8);
-    const int32_t sc1 = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq + 16u, 8);
-    const int32_t sc2 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq, 8);
-    const int32_t sc3 = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq + 16u, 8);
-    const float d = f16_lo(D[it]);  // bytes 208..209
-    uint32_t q0[4], q1[4], q2[4], q3[4];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      q0[k] = (a[k] & 0x0F0F0F0Fu) | ((c[k] << 4) & 0x30303030u);
-      q1[k] = (bq[k] & 0x0F0F0F0Fu) | ((c[k] << 2) & 0x30303030u);
-      q2[k] = ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0x30303030u);
-      q3[k] = ((bq[k] >> 4) & 0x0F0F0F0Fu) | ((c[k] >> 2) & 0x30303030u);
-    }
+    const Q6Dec q = q6k_decode(A[it], B[it], C[it], S[it], D[it], gq);
 #pragma unroll
     for (int t = 0; t < T; t++) {
       u32x4 a0 = fa[0], a1 = fa[1], a2 = fa[2], a3 = fa[3];
-      int32_t D0 = fb4[0], D1 = fb4[1], D2 = fb4[2], D3 = fb4[3];
+      int32_t bv[4] = {fb4[0], fb4[1], fb4[2], fb4[3]};
       float dd8 = fd8;
       if constexpr (!FIX) {
         const int8_t* at = act + t * abytes;
@@ -699,26 +756,14 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
         a2 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 64u));
         a3 = *reinterpret_cast<const u32x4*>(swz(at, b, k0 + 96u));
         const int32_t* bb = bias + t * nbmax * 16u + b * 16u + 8u * h + gq;
-        D0 = bb[0];
-        D1 = bb[2];
-        D2 = bb[4];
-        D3 = bb[6];
+        bv[0] = bb[0];
+        bv[1] = bb[2];
+        bv[2] = bb[4];
+        bv[3] = bb[6];
         dd8 = d8[t * nbmax + b];
       }
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        D0 = dot4(q0[k], a0[k], D0);
-        D1 = dot4(q1[k], a1[k], D1);
-        D2 = dot4(q2[k], a2[k], D2);
-        D3 = dot4(q3[k], a3[k], D3);
-      }
-      // |D| < 2^20 and |scale| <= 128: the 24-bit multiplies are exact
-      int32_t isum = quad_sum(__mul24(sc0, D0) + __mul24(sc1, D1) + __mul24(sc2, D2) + __mul24(sc3, D3));
-      if (p == 0) {
-        // int_dot.rs:203: read_f16_le(block, 208) * span.scales[0] * lossy(sum)
-        const float dd = d * dd8;
-        terms[(__umul24(r, nbmax) + b) * T + t] = dd * static_cast<float>(isum);
-      }
+      const float term = q6k_term(q, a0, a1, a2, a3, bv, dd8);
+      if (p == 0) terms[(__umul24(r, nbmax) + b) * T + t] = term;
     }
   }
   __syncthreads();
