@@ -1644,6 +1644,14 @@ void* kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool
   return type_id == 12u ? kq_wide_kernel_fmt<12>(fq, ni, norm, pair) : kq_wide_kernel_fmt<14>(fq, ni, norm, pair);
 }
 
+// The one-token kernels with a half-wave for every block of a 17- to
+// 32-block activation (768 or 1024 lanes, one block per team).
+void* kq_onepass_kernel(uint32_t type_id, uint32_t nt) {
+  if (nt == 768u)
+    return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, 768u>() : kq_kernel<14, 1, 1, 4, false, false, 768u>();
+  return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, 1024u>() : kq_kernel<14, 1, 1, 4, false, false, 1024u>();
+}
+
 // The norm-fused decode kernels: one token, four blocks per team (two for a
 // single-round launch that would leave most CUs idle), the row preloaded in
 // one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
@@ -1836,6 +1844,28 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       }
     }
   }
+  // A one-token row of 17 to 32 blocks (5632 or 8192 values) leaves a
+  // 512-lane workgroup's 16 half-waves a second round of quantization, which
+  // every wave then waits for at the barrier: 768 lanes (up to 24 blocks)
+  // or 1024 (up to 32) quantize it in one round, with one block a team, when
+  // that grid still fits one workgroup per CU (2048x5632: Q6_K 5.45 against
+  // 6.37 us, Q4_K 4.85 against 5.32; Q4_K 2048x8192 at 1024 lanes: 5.95
+  // against 7.1). Larger grids measured slower (4096x5632: 6.7 against 6.1
+  // us) and keep their shape. Tuning::kq_onepass = false keeps every grid.
+  uint32_t onepass_nt = 0u;
+  if (T == 1 && FUSED && kquant && !norm && !pair_job && fq == 4u && nbl > 16u && nbl <= 32u &&
+      tuning().kq_onepass) {
+    const uint32_t nt1 = nbl <= 24u ? 768u : 1024u;
+    const uint32_t r1 = (nt1 / 4u) / nbl;
+    uint32_t w1 = 0;
+    for (uint32_t i = 0; i < jobs.n; i++) w1 += (jobs.j[i].rows + r1 - 1u) / r1;
+    if (w1 <= static_cast<uint32_t>(device_cus())) {
+      onepass_nt = nt1;
+      R = r1;
+      ni = 1u;
+      balanced = false;
+    }
+  }
   // a gate/up pair: one norm-fused job, R/2 rows of each matrix per workgroup
   const bool pair = jobs.n == 1u && jobs.j[0].w2 != nullptr;
   if (pair && (!norm || !kquant || R < 2u)) return hipErrorInvalidValue;
@@ -1883,7 +1913,10 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // The 500-workgroup 32000x2048 output launch keeps 256 (12.3 against
     // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
     uint32_t nt = kThreads, nit = ni;
-    if (balanced) {
+    if (onepass_nt) {
+      k = kq_onepass_kernel(type_id, onepass_nt);
+      nt = onepass_nt;
+    } else if (balanced) {
       k = kq_wide_kernel(type_id, fq, ni, norm != nullptr, pair);
       nt = 2u * kThreads;
     } else if (wide8) {
@@ -1906,7 +1939,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // One token, one preload round, and every job's blocks a power of two
     // no larger than the teams: the fixed-column walk (BlockWalk).
     // Tuning::kq_fix = false keeps the general walk.
-    if (T == 1 && FUSED && fq == 1u && tuning().kq_fix) {
+    if (!onepass_nt && T == 1 && FUSED && fq == 1u && tuning().kq_fix) {
       bool fix = true;
       for (uint32_t i = 0; i < jobs.n; i++) {
         const uint32_t b = jobs.j[i].nb;

@@ -88,6 +88,7 @@ struct Tuning {
   int norm_nt = 0;         // RUSTICIDE_HIP_NORM_NT=256|512: the same, norm-fused launches
   bool kq_fix = true;      // RUSTICIDE_HIP_KQ_FIX=0: the general block walk only
   bool kq_balance = true;  // RUSTICIDE_HIP_KQ_BALANCE=0: no one-workgroup-per-CU reshaping
+  bool kq_onepass = true;  // RUSTICIDE_HIP_KQ_ONEPASS=0: no 768/1024-lane one-round quantization
   int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 (two-token kernel)
   int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
   int i2s_nt = 0;          // RUSTICIDE_HIP_I2S_NT=256|512|1024: threads per workgroup, one token

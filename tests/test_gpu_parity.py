@@ -41,9 +41,12 @@ VARIANTS = {
     "walk": {"RUSTICIDE_HIP_KQ_FIX": "0"},
     # grids of one to two workgroups per CU kept as they are
     "no-balance": {"RUSTICIDE_HIP_KQ_BALANCE": "0"},
+    # 17- to 32-block rows on 512 lanes (two rounds of quantization) instead
+    # of 768 or 1024
+    "no-onepass": {"RUSTICIDE_HIP_KQ_ONEPASS": "0"},
 }
 SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_KQ_FIX",
-            "RUSTICIDE_HIP_KQ_BALANCE")
+            "RUSTICIDE_HIP_KQ_BALANCE", "RUSTICIDE_HIP_KQ_ONEPASS")
 
 
 @pytest.fixture(params=list(VARIANTS))
@@ -153,7 +156,9 @@ KQ_SHAPES = [
     (12, 37, 512, [1, 3, 8, 11]),
     (14, 32000, 2048, [1, 2]),  # Q6_K lm_head (benchmark workload)
     (12, 64, 4096, [1, 2]),     # 16 blocks: one full pass
-    (14, 19, 8192, [1, 2]),     # 32 blocks: two passes
+    (14, 19, 8192, [1, 2]),     # 32 blocks: two passes (one token: 1024 lanes)
+    (12, 1000, 8192, [1]),      # 32 blocks, 125 workgroups of 1024 lanes
+    (14, 333, 4608, [1, 2]),    # 18 blocks, 34 workgroups of 768 lanes
     (12, 11, 256, [1, 2]),      # one block per row: 16 rows per wave
     (14, 2048, 5632, [1, 3]),   # Q6_K ffn_down: 4620-byte rows, padded stride
     (14, 45, 768, [1, 2, 9]),
