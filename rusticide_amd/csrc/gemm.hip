@@ -10,9 +10,9 @@
 // from int8 MFMA (v_mfma_i32_32x32x32_i8), exact in i32:
 //   * the sub-block scale is folded into the weight, w = sc*q (Q4_K: 0..945;
 //     Q6_K: sc*(q-32), -4096..4064), split into two int8 planes w = 128*hi +
-//     lo (lo in 0..127). One accumulator takes the hi plane over the block's
-//     eight 32-deep steps, is shifted left by 7, then takes the lo plane:
-//     it ends holding isum;
+//     lo (lo in 0..127). Two accumulators take the hi and the lo plane side
+//     by side over the block's eight 32-deep steps (each activation fragment
+//     read from LDS once for both); isum = 128*hi + lo;
 //   * the Q4_K min term needs only the block sums: with bsum = 128*bh + bl
 //     (bl in 0..127), msum = 128 * sum_j m_j*bh_j + sum_j m_j*bl_j, two MFMAs
 //     whose 32-deep operands carry the eight (m_j, bl_j) / (m_j, bh_j) pairs
@@ -299,15 +299,21 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
     for (int t = 0; t < NT; t++) bcol[t] = static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
 #pragma unroll
     for (int t = 0; t < NT; t++) acc_i[t] = v16i{};
-    // hi plane over the block, then x128, then the lo plane
+    v16i acc_l[NT];
+#pragma unroll
+    for (int t = 0; t < NT; t++) acc_l[t] = v16i{};
+    // hi and lo planes side by side per 32-deep step: each activation
+    // fragment is read from LDS once
 #pragma unroll
     for (uint32_t kk = 0; kk < 8u; kk++) {
       const uint32_t ko = 32u * kk + 16u * g;
       const v4i Ah = *reinterpret_cast<const v4i*>(hiT + arow * kStride + ko);
+      const v4i Al = *reinterpret_cast<const v4i*>(loT + arow * kStride + ko);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         const v4i Bv = *reinterpret_cast<const v4i*>(actT + bcol[t] * kStride + ko);
         acc_i[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah, Bv, acc_i[t], 0, 0, 0);
+        acc_l[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al, Bv, acc_l[t], 0, 0, 0);
       }
     }
     if (FMT == 12) {
@@ -320,35 +326,16 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
         const u32x4 bs = *reinterpret_cast<const u32x4*>(bsT + bcol[t] * 16u);
         const v4i Bh{g == 0 ? static_cast<int32_t>(bs.z) : 0, g == 0 ? static_cast<int32_t>(bs.w) : 0, 0, 0};
         acc_m[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bh, v16i{}, 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) acc_i[t][i] <<= 7;
-    if (FMT == 12) {
-      const uint32_t mw0 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u) : 0u;
-      const uint32_t mw1 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u + 4u) : 0u;
-      const v4i Am{static_cast<int32_t>(mw0), static_cast<int32_t>(mw1), 0, 0};
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
 #pragma unroll
         for (int i = 0; i < 16; i++) acc_m[t][i] <<= 7;
-        const u32x4 bs = *reinterpret_cast<const u32x4*>(bsT + bcol[t] * 16u);
         const v4i Bl{g == 0 ? static_cast<int32_t>(bs.x) : 0, g == 0 ? static_cast<int32_t>(bs.y) : 0, 0, 0};
         acc_m[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bl, acc_m[t], 0, 0, 0);
       }
     }
 #pragma unroll
-    for (uint32_t kk = 0; kk < 8u; kk++) {
-      const uint32_t ko = 32u * kk + 16u * g;
-      const v4i Al = *reinterpret_cast<const v4i*>(loT + arow * kStride + ko);
+    for (int t = 0; t < NT; t++)
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const v4i Bv = *reinterpret_cast<const v4i*>(actT + bcol[t] * kStride + ko);
-        acc_i[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al, Bv, acc_i[t], 0, 0, 0);
-      }
-    }
+      for (int i = 0; i < 16; i++) acc_i[t][i] = (acc_i[t][i] << 7) + acc_l[t][i];
     // the block's float term per (row, token), added in block order
     // (D layout: lane n + 32*((m/4)%2), register 4*(m/8) + m%4)
     float d8n[NT];
