@@ -96,7 +96,10 @@ def load_rotation(ctx, name: str):
     type_id, rows, cols = WORKLOADS[name][:3]
     data = synth.matrix(type_id, rows, cols, seed=1)
     one = R.Matrix.load(ctx, type_id, data, rows, cols)
-    ncopies = max(2, math.ceil(ROTATE_BYTES / one.device_bytes))
+    # copies enough that the bytes one launch reads, over all of them, pass
+    # ROTATE_BYTES (a k-quant matrix also holds a regrouped copy, which the
+    # one-token kernels read instead of its native rows)
+    ncopies = max(2, math.ceil(ROTATE_BYTES / algorithmic_bytes(type_id, rows, cols)))
     return data, [one] + [R.Matrix.load(ctx, type_id, data, rows, cols) for _ in range(ncopies - 1)]
 
 

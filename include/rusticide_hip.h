@@ -85,7 +85,10 @@ void *rh_stream(rh_ctx *ctx);
  * validates `len` against rows x cols for `type_id`, copies the native
  * blocks to HBM once (rows padded to a 16-byte stride), and for I2_S parses
  * and validates the trailer scale (weights.rs:190-202). F16 is widened to
- * f32 as `widen` does (weights.rs:241-247). */
+ * f32 as `widen` does (weights.rs:241-247). A Q4_K or Q6_K matrix whose rows
+ * hold 1, 2, 4, ... 128 blocks also gets a second copy of its blocks,
+ * regrouped so that one-token GEMVs read them in contiguous runs (the same
+ * bytes again; skipped, with no error, when HBM cannot hold it). */
 rh_status rh_matrix_load(rh_ctx *ctx, uint32_t type_id, const void *data, size_t len,
                          size_t rows, size_t cols, rh_matrix **out);
 /* Frees the matrix; valid before or after its context is destroyed. */
@@ -95,7 +98,7 @@ size_t rh_matrix_cols(const rh_matrix *m);
 uint32_t rh_matrix_type(const rh_matrix *m);
 /* Weights::Ternary::scale (matmul.rs:41-45); 0 for other formats. */
 float rh_matrix_ternary_scale(const rh_matrix *m);
-/* Bytes of HBM the matrix occupies. */
+/* Bytes of HBM the matrix occupies (with the regrouped copy, if any). */
 size_t rh_matrix_device_bytes(const rh_matrix *m);
 
 /* Matrix::copy_row (weights.rs:120-150): dequantizes row `index` into the

@@ -48,6 +48,9 @@ struct rh_matrix {
   float scale = 0.0f;
   uint8_t* data = nullptr;
   size_t bytes = 0;
+  // the same blocks in the unit layout (launch_kq_units) for the one-token
+  // fixed-column GEMVs, or null
+  uint8_t* units = nullptr;
 };
 
 struct rh_q8 {
@@ -226,6 +229,7 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (kind != RH_TYPE_F32 && m->nblocks < nb) nb = m->nblocks;
       GemvJob& j = g.j[g.n++];
       j.w = m->data;
+      j.wu = nb == m->nblocks ? m->units : nullptr;
       j.stride = static_cast<uint32_t>(m->stride);
       j.rows = static_cast<uint32_t>(rows);
       j.nb = static_cast<uint32_t>(nb);
@@ -411,6 +415,7 @@ rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& nor
       j.stride = static_cast<uint32_t>(m->stride);
       j.rows = static_cast<uint32_t>(rows);
       j.nb = static_cast<uint32_t>(m->nblocks < cover ? m->nblocks : cover);
+      j.wu = j.nb == m->nblocks ? m->units : nullptr;
       j.out = jobs[i].out;
       j.out_len = jobs[i].out_len;
       j.scale = m->scale;
@@ -436,6 +441,10 @@ rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn
   GemvJob& j = g.j[g.n++];
   j.w = gate->data;
   j.w2 = up->data;
+  if (gate->units && up->units) {
+    j.wu = gate->units;
+    j.wu2 = up->units;
+  }
   j.stride = static_cast<uint32_t>(gate->stride);
   j.rows = static_cast<uint32_t>(rows);
   j.nb = static_cast<uint32_t>(gate->nblocks);
@@ -680,6 +689,19 @@ rh_status matrix_upload(rh_ctx* ctx, PendingUpload* p, size_t n) {
     rh_status st = flush();
     if (st != RH_OK) return st;
   }
+  // the unit-layout copies, from the uploaded rows (a matrix without one,
+  // for want of memory or an eligible shape, takes the general block walk)
+  for (size_t i = 0; i < n; i++) {
+    rh_matrix* m = p[i].m;
+    if (m->units || !units_eligible(m->type_id, m->rows, m->nblocks)) continue;
+    void* u = nullptr;
+    if (hipMalloc(&u, units_bytes(m->type_id, m->rows, m->nblocks)) != hipSuccess) {
+      (void)hipGetLastError();
+      continue;
+    }
+    m->units = static_cast<uint8_t*>(u);
+    RH_HIP(ctx, launch_kq_units(m->type_id, m->data, m->stride, m->rows, m->nblocks, m->units, ctx->stream));
+  }
   RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return RH_OK;
 }
@@ -762,6 +784,7 @@ void rh_matrix_free(rh_matrix* m) {
   hipSetDevice(m->device);
   hipDeviceSynchronize();
   hipFree(m->data);
+  if (m->units) hipFree(m->units);
   delete m;
 }
 
@@ -769,7 +792,10 @@ size_t rh_matrix_rows(const rh_matrix* m) { return m ? m->rows : 0; }
 size_t rh_matrix_cols(const rh_matrix* m) { return m ? m->cols : 0; }
 uint32_t rh_matrix_type(const rh_matrix* m) { return m ? m->type_id : 0; }
 float rh_matrix_ternary_scale(const rh_matrix* m) { return m ? m->scale : 0.0f; }
-size_t rh_matrix_device_bytes(const rh_matrix* m) { return m ? m->bytes : 0; }
+size_t rh_matrix_device_bytes(const rh_matrix* m) {
+  if (!m) return 0;
+  return m->bytes + (m->units ? units_bytes(m->type_id, m->rows, m->nblocks) : 0);
+}
 
 rh_status rh_matrix_copy_row(rh_ctx* ctx, const rh_matrix* m, size_t index, float* out,
                              size_t out_len, int* found) {

@@ -335,6 +335,17 @@ __device__ __forceinline__ const uint8_t* block_at(const GemvJob& J, const WgRow
   return m + (__umul24(row, static_cast<uint32_t>(J.stride)) + boff);
 }
 
+// The group of 16 blocks (unit layout, launch_kq_units) holding block fb of
+// workgroup row r: a wave's step reads one group, its team tw at position tw.
+template <bool PAIR>
+__device__ __forceinline__ const uint8_t* unit_at(const WgRows& g, uint32_t r, uint32_t fb, uint32_t nb,
+                                                  uint32_t ubytes) {
+  const bool second = PAIR && r >= g.nh;
+  const uint8_t* m = g.w1 + (second ? g.d2 : 0u);
+  const uint32_t row = PAIR ? g.row0 + (second ? r - g.nh : r) : row_of(g, r);
+  return m + ((row * nb + fb) >> 4) * ubytes;
+}
+
 // Each row's block terms summed in block order from -0.0
 // (portable/int_dot/rows.rs:9-12,59) and written; PAIR writes
 // silu(gate) * up with silu_mul's expressions (portable/elementwise.rs:6-9).
@@ -365,13 +376,16 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
 
 // Where a team finds its blocks. A workgroup's teams take team blocks
 // g = team + i * NT/4, i = 0..NI-1, of its rows x nb blocks in row-major
-// order. The general walk divides each g into (row g / nb, block g % nb).
+// order. The general walk divides each g into (row g / nb, block g % nb) and
+// reads the matrix's native rows.
 // FIX (nb a power of two up to NT/4: rows of 256, 512, ... values): g % nb
 // is the same for every i, so the team keeps one
 // block column fb, its row advances by step = NT/4/nb an iteration, and the
-// block's address by a constant stride (row_of is affine in i: step is a
-// whole number of interleaved chunks). The activation a team reads is then
-// the same for all of its blocks and leaves the loop.
+// activation a team reads is the same for all of its blocks and leaves the
+// loop. FIX reads the unit layout (launch_kq_units): a wave's 16 teams take
+// the 16 blocks of one group, and the group's address advances by a constant
+// stride (row_of is affine in i: step is a whole number of interleaved
+// chunks, and the launcher checks that every wave's rows start a group).
 template <bool PAIR, uint32_t NT, bool FIX>
 struct BlockWalk {
   const GemvJob& J;
@@ -391,9 +405,10 @@ struct BlockWalk {
       r0 = team >> sh;
       fb = team & (nb - 1u);
       step = (NT / 4u) >> sh;
-      delta = (((step >> wr.cs) * wr.nwg) << wr.cs) * J.stride;
+      // matrix rows an iteration, times the unit layout's bytes a row
+      delta = (((step >> wr.cs) * wr.nwg) << wr.cs) * nb * bbytes;
       const bool in = r0 < wr.nrows;
-      p0 = block_at<PAIR>(J, wr, in ? r0 : 0u, in ? fb * bbytes : 0u);
+      p0 = unit_at<PAIR>(wr, in ? r0 : 0u, in ? fb : 0u, nb, 16u * bbytes);
     }
   }
   // whether team block i lies in the workgroup's rows (uniform over a team)
@@ -416,7 +431,7 @@ struct BlockWalk {
   __device__ __forceinline__ const uint8_t* addr(int i) const {
     if constexpr (FIX) {
       const uint32_t r = r0 + static_cast<uint32_t>(i) * step;
-      if constexpr (PAIR) return r < wr.nrows ? block_at<true>(J, wr, r, fb * bbytes) : p0;
+      if constexpr (PAIR) return r < wr.nrows ? unit_at<true>(wr, r, fb, nb, 16u * bbytes) : p0;
       return r < wr.nrows ? p0 + static_cast<uint32_t>(i) * delta : p0;
     } else {
       // g = r*nb + b with g < 8*128: a float reciprocal divides exactly here
@@ -567,11 +582,20 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   // issue order: the prologue waits only for these)
   __builtin_amdgcn_sched_barrier(0);
   u32x4 hd[NI], c0[NI], c1[NI];
+  // FIX, unit layout: headers [16 teams][16] | qs[0..64) [64 lanes][16] |
+  // qs[64..128) [64 lanes][16]
+  const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
   auto issue = [&](int i) {
     const uint8_t* blk = walk.addr(i);
-    hd[i] = load16(blk);
-    c0[i] = load16(blk + 16u + 16u * p);
-    c1[i] = load16(blk + 80u + 16u * p);
+    if constexpr (FIX) {
+      hd[i] = load16(blk + 16u * utw);
+      c0[i] = load16(blk + 256u + 16u * ul);
+      c1[i] = load16(blk + 1280u + 16u * ul);
+    } else {
+      hd[i] = load16(blk);
+      c0[i] = load16(blk + 16u + 16u * p);
+      c1[i] = load16(blk + 80u + 16u * p);
+    }
   };
   constexpr int ahead = issue_ahead<NI, NORM>();
 #pragma unroll
@@ -693,13 +717,24 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   u32x4 A[NI], B[NI], C[NI];
   uint2 S[NI];
   uint32_t D[NI];
+  // FIX, unit layout: A [64 lanes][16] | B [64][16] | C [64][16] | the
+  // scales [16 teams][16] | d [16 teams][2]
+  const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
   auto issue = [&](int i) {
     const uint8_t* base = walk.addr(i);
-    A[i] = load16_any(base + 64u * h + 16u * gq);
-    B[i] = load16_any(base + 64u * h + 32u + 16u * gq);
-    C[i] = load16_any(base + 128u + 32u * h + 16u * gq);
-    S[i] = load8_any(base + 192u + 8u * h);
-    D[i] = *reinterpret_cast<const uint16_t*>(base + 208u);
+    if constexpr (FIX) {
+      A[i] = load16(base + 16u * ul);
+      B[i] = load16(base + 1024u + 16u * ul);
+      C[i] = load16(base + 2048u + 16u * ul);
+      S[i] = *reinterpret_cast<const uint2*>(base + 3072u + 16u * utw + 8u * h);
+      D[i] = *reinterpret_cast<const uint16_t*>(base + 3328u + 2u * utw);
+    } else {
+      A[i] = load16_any(base + 64u * h + 16u * gq);
+      B[i] = load16_any(base + 64u * h + 32u + 16u * gq);
+      C[i] = load16_any(base + 128u + 32u * h + 16u * gq);
+      S[i] = load8_any(base + 192u + 8u * h);
+      D[i] = *reinterpret_cast<const uint16_t*>(base + 208u);
+    }
   };
   constexpr int ahead = issue_ahead<NI, NORM>();
 #pragma unroll
@@ -781,6 +816,40 @@ __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, co
   extern __shared__ __align__(16) uint8_t lds[];
   static_assert(!FIX || T == 1, "fixed columns: one token");
   q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+}
+
+// The unit layout (launch_kq_units): one thread per (group of 16 blocks,
+// lane), the lane's pieces of its team's block as the fixed-column kernels'
+// lane l = 4*tw + p loads them (tw the team in the wave, p its lane).
+template <int FMT>
+__global__ __launch_bounds__(256) void kq_units_kernel(const uint8_t* __restrict__ src, uint32_t stride,
+                                                       uint32_t rows, uint32_t nb, uint32_t groups,
+                                                       uint8_t* __restrict__ dst) {
+  constexpr uint32_t bb = FMT == 12 ? 144u : 210u;
+  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
+  const uint32_t grp = gid >> 6, l = gid & 63u;
+  if (grp >= groups) return;
+  const uint32_t tw = l >> 2, p = l & 3u;
+  const uint32_t blk = grp * 16u + tw;
+  uint32_t row = blk / nb;
+  const uint32_t col = blk - row * nb;
+  row = row < rows ? row : rows - 1u;
+  const uint8_t* b = src + static_cast<size_t>(row) * stride + col * bb;
+  uint8_t* u = dst + static_cast<size_t>(grp) * (16u * bb);
+  if (FMT == 12) {
+    if (p == 0) *reinterpret_cast<u32x4*>(u + 16u * tw) = load16(b);
+    *reinterpret_cast<u32x4*>(u + 256u + 16u * l) = load16(b + 16u + 16u * p);
+    *reinterpret_cast<u32x4*>(u + 1280u + 16u * l) = load16(b + 80u + 16u * p);
+  } else {
+    const uint32_t h = p >> 1, gq = p & 1u;
+    *reinterpret_cast<u32x4*>(u + 16u * l) = load16_any(b + 64u * h + 16u * gq);
+    *reinterpret_cast<u32x4*>(u + 1024u + 16u * l) = load16_any(b + 64u * h + 32u + 16u * gq);
+    *reinterpret_cast<u32x4*>(u + 2048u + 16u * l) = load16_any(b + 128u + 32u * h + 16u * gq);
+    if (p == 0) {
+      *reinterpret_cast<u32x4*>(u + 3072u + 16u * tw) = load16_any(b + 192u);
+      *reinterpret_cast<uint16_t*>(u + 3328u + 2u * tw) = *reinterpret_cast<const uint16_t*>(b + 208u);
+    }
+  }
 }
 
 // I2_S x I8_S --------------------------------------------------------------
@@ -1765,6 +1834,35 @@ uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_ro
 template <int T>
 hipError_t launch_i2s_q8(GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0, hipStream_t s, int32_t* raw);
 
+}  // namespace
+
+bool units_eligible(uint32_t type_id, size_t rows, size_t nb) {
+  return (type_id == 12u || type_id == 14u) && rows > 0 && nb > 0 && nb <= 128u && (nb & (nb - 1u)) == 0u;
+}
+
+size_t units_bytes(uint32_t type_id, size_t rows, size_t nb) {
+  const size_t groups = (rows * nb + 15u) / 16u;
+  return groups * 16u * (type_id == 12u ? 144u : 210u);
+}
+
+hipError_t launch_kq_units(uint32_t type_id, const uint8_t* src, size_t stride, size_t rows, size_t nb, uint8_t* dst,
+                           hipStream_t s) {
+  if (!units_eligible(type_id, rows, nb)) return hipErrorInvalidValue;
+  const uint32_t groups = static_cast<uint32_t>((rows * nb + 15u) / 16u);
+  const uint32_t threads = groups * 64u;
+  if (type_id == 12u)
+    hipLaunchKernelGGL(kq_units_kernel<12>, dim3((threads + 255u) / 256u), dim3(256), 0, s, src,
+                       static_cast<uint32_t>(stride), static_cast<uint32_t>(rows), static_cast<uint32_t>(nb), groups,
+                       dst);
+  else
+    hipLaunchKernelGGL(kq_units_kernel<14>, dim3((threads + 255u) / 256u), dim3(256), 0, s, src,
+                       static_cast<uint32_t>(stride), static_cast<uint32_t>(rows), static_cast<uint32_t>(nb), groups,
+                       dst);
+  return hipGetLastError();
+}
+
+namespace {
+
 template <int T, bool FUSED>
 hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float* x, size_t width,
                     size_t tokens, size_t t0, hipStream_t s, int32_t* raw, const NormIn* norm = nullptr) {
@@ -1937,15 +2035,29 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       }
     }
     // One token, one preload round, and every job's blocks a power of two
-    // no larger than the teams: the fixed-column walk (BlockWalk).
-    // Tuning::kq_fix = false keeps the general walk.
+    // no larger than the teams, in a matrix with a unit-layout copy, with
+    // every wave's rows starting a group of 16 blocks: the fixed-column walk
+    // (BlockWalk) on those copies. Tuning::kq_fix = false keeps the general
+    // walk on the native rows.
     if (!onepass_nt && T == 1 && FUSED && fq == 1u && tuning().kq_fix) {
       bool fix = true;
       for (uint32_t i = 0; i < jobs.n; i++) {
-        const uint32_t b = jobs.j[i].nb;
-        fix = fix && b != 0u && (b & (b - 1u)) == 0u && b <= nt / 4u;
+        const GemvJob& j = jobs.j[i];
+        const uint32_t b = j.nb;
+        fix = fix && b != 0u && (b & (b - 1u)) == 0u && b <= nt / 4u && j.wu && (!pair || j.wu2);
+        // rows per group of 16 blocks; a workgroup's first row, and an
+        // interleave chunk, must be whole groups
+        const uint32_t rpu = b != 0u && b < 16u ? 16u / b : 1u;
+        fix = fix && (j.il ? (1u << (j.il - 1u)) % rpu == 0u : per % rpu == 0u);
       }
-      if (void* kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : nullptr) k = kf;
+      void* kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : nullptr;
+      if (kf) {
+        k = kf;
+        for (uint32_t i = 0; i < jobs.n; i++) {
+          jobs.j[i].w = jobs.j[i].wu;
+          if (pair) jobs.j[i].w2 = jobs.j[i].wu2;
+        }
+      }
     }
     void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
                     const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};

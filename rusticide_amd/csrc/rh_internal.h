@@ -51,9 +51,14 @@ struct GemvJob {
   // one window of the matrix (the launcher sets it only when the rows tile
   // the grid exactly).
   uint32_t il = 0;
+  // The matrices' copies in the unit layout (launch_kq_units), or null; set
+  // only when the job covers whole rows (nb = the matrix's blocks per row).
+  // The launcher swaps them into w and w2 when it takes the fixed-column walk.
+  const uint8_t* wu = nullptr;
+  const uint8_t* wu2 = nullptr;
 };
-// 56 bytes: every launch's kernel arguments hold kMaxJobs of these
-static_assert(sizeof(GemvJob) == 56, "GemvJob packs into 56 bytes");
+// 72 bytes: every launch's kernel arguments hold kMaxJobs of these
+static_assert(sizeof(GemvJob) == 72, "GemvJob packs into 72 bytes");
 
 struct GemvJobs {
   GemvJob j[kMaxJobs];
@@ -105,6 +110,18 @@ hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, co
                                  hipStream_t s);
 hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, const Q8Dev& q,
                                hipStream_t s);
+
+// The unit layout of a k-quant matrix whose rows hold nb blocks (a power of
+// two up to 128): the blocks in row-major order, cut into groups of 16, each
+// group stored as the 64 lanes of the wave that reads it in one step of the
+// fixed-column walk take it (the lane's 16-byte pieces side by side, then
+// the per-block scales and d), so each of that wave's loads reads
+// consecutive bytes. A group past the last row repeats the last row. Bytes:
+// units_bytes(); launch_kq_units fills `dst` from the native rows.
+size_t units_bytes(uint32_t type_id, size_t rows, size_t nb);
+bool units_eligible(uint32_t type_id, size_t rows, size_t nb);
+hipError_t launch_kq_units(uint32_t type_id, const uint8_t* src, size_t stride, size_t rows, size_t nb, uint8_t* dst,
+                           hipStream_t s);
 
 // Grouped GEMV for one format: tokens [t0, t0+tn) of `tokens` total.
 hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, const float* x,
