@@ -86,7 +86,8 @@ void *rh_stream(rh_ctx *ctx);
  * blocks to HBM once (rows padded to a 16-byte stride), and for I2_S parses
  * and validates the trailer scale (weights.rs:190-202). F16 is widened to
  * f32 as `widen` does (weights.rs:241-247). A Q4_K or Q6_K matrix whose rows
- * hold 1, 2, 4, ... 128 blocks also gets a second copy of its blocks,
+ * hold 1, 2, 4, ... 128 blocks, or 22, 24 or 30 (5632, 6144 or 7680
+ * values), also gets a second copy of its blocks,
  * regrouped so that one-token GEMVs read them in contiguous runs (the same
  * bytes again; skipped, with no error, when HBM cannot hold it). */
 rh_status rh_matrix_load(rh_ctx *ctx, uint32_t type_id, const void *data, size_t len,

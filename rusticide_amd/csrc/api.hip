@@ -378,6 +378,7 @@ void load_tuning() {
   t.kq_fix = env_int("RUSTICIDE_HIP_KQ_FIX", 1) != 0;
   t.kq_balance = env_int("RUSTICIDE_HIP_KQ_BALANCE", 1) != 0;
   t.kq_onepass = env_int("RUSTICIDE_HIP_KQ_ONEPASS", 1) != 0;
+  t.kq_units = env_int("RUSTICIDE_HIP_KQ_UNITS", 1) != 0;
   const int gr = env_int("RUSTICIDE_HIP_I2S_GROUPS", 0);
   t.i2s_groups = gr == 1 || gr == 2 || gr == 4 ? gr : 0;
   const int lpr = env_int("RUSTICIDE_HIP_I2S_LPR", 0);

@@ -386,7 +386,11 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
 // the 16 blocks of one group, and the group's address advances by a constant
 // stride (row_of is affine in i: step is a whole number of interleaved
 // chunks, and the launcher checks that every wave's rows start a group).
-template <bool PAIR, uint32_t NT, bool FIX>
+// UNITS without FIX: the general walk on the unit layout. A wave's 16 teams
+// take team blocks 16w..16w+15 (+ i * NT/4), one group when the workgroup's
+// first block starts one (the launcher checks: contiguous rows, R * nb a
+// multiple of 16, no pair).
+template <bool PAIR, uint32_t NT, bool FIX, bool UNITS = FIX>
 struct BlockWalk {
   const GemvJob& J;
   const WgRows& wr;
@@ -438,6 +442,7 @@ struct BlockWalk {
       const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
       const uint32_t gg = g < total ? g : 0u;
       const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
+      if constexpr (UNITS) return unit_at<PAIR>(wr, r, b, nb, 16u * bbytes);
       return block_at<PAIR>(J, wr, r, __umul24(b, bbytes));
     }
   }
@@ -559,7 +564,7 @@ __device__ __forceinline__ float q6k_term(const Q6Dec& q, const u32x4& a0, const
 // NORM (T = 1, the whole row in the preload): x is the hidden state and the
 // kernel applies the NormIn residual add and RMSNorm before quantizing.
 // FIX: see BlockWalk (one token).
-template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX>
+template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX, bool UNITS>
 __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const float* __restrict__ x, size_t width,
                                          uint32_t R, uint32_t nbmax, size_t tokens, size_t t0, const NormIn& nrm,
                                          uint8_t* lds) {
@@ -570,7 +575,7 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   float* terms = reinterpret_cast<float*>(sums + T * nbmax * 8u);
 
   const WgRows wr = wg_rows<PAIR>(J, R);
-  const BlockWalk<PAIR, NT, FIX> walk(J, wr, 144u);
+  const BlockWalk<PAIR, NT, FIX, UNITS> walk(J, wr, 144u);
   const uint32_t p = threadIdx.x & 3u;
 
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
@@ -582,12 +587,12 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   // issue order: the prologue waits only for these)
   __builtin_amdgcn_sched_barrier(0);
   u32x4 hd[NI], c0[NI], c1[NI];
-  // FIX, unit layout: headers [16 teams][16] | qs[0..64) [64 lanes][16] |
+  // UNITS, unit layout: headers [16 teams][16] | qs[0..64) [64 lanes][16] |
   // qs[64..128) [64 lanes][16]
   const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
   auto issue = [&](int i) {
     const uint8_t* blk = walk.addr(i);
-    if constexpr (FIX) {
+    if constexpr (UNITS) {
       hd[i] = load16(blk + 16u * utw);
       c0[i] = load16(blk + 256u + 16u * ul);
       c1[i] = load16(blk + 1280u + 16u * ul);
@@ -673,13 +678,16 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
 // a kernel of its own rather than a branch in one: at the join of two walks
 // the compiler merges their pending loads and then waits for the activation
 // before issuing the first weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
+          bool UNITS = FIX>
 __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
   static_assert(!FIX || T == 1, "fixed columns: one token");
-  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+  static_assert(!FIX || UNITS, "fixed columns read the unit layout");
+  static_assert(!UNITS || !PAIR || FIX, "the general walk reads a pair's native rows");
+  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // Q6_K x Q8_K --------------------------------------------------------------
@@ -687,7 +695,7 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX>
+template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX, bool UNITS>
 __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const float* __restrict__ x, size_t width,
                                          uint32_t R, uint32_t nbmax, size_t tokens, size_t t0, const NormIn& nrm,
                                          uint8_t* lds) {
@@ -698,7 +706,7 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   float* terms = reinterpret_cast<float*>(bias + T * nbmax * 16u);
 
   const WgRows wr = wg_rows<PAIR>(J, R);
-  const BlockWalk<PAIR, NT, FIX> walk(J, wr, 210u);
+  const BlockWalk<PAIR, NT, FIX, UNITS> walk(J, wr, 210u);
   const uint32_t p = threadIdx.x & 3u;
   const uint32_t h = p >> 1, gq = p & 1u;
 
@@ -717,12 +725,12 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   u32x4 A[NI], B[NI], C[NI];
   uint2 S[NI];
   uint32_t D[NI];
-  // FIX, unit layout: A [64 lanes][16] | B [64][16] | C [64][16] | the
+  // UNITS, unit layout: A [64 lanes][16] | B [64][16] | C [64][16] | the
   // scales [16 teams][16] | d [16 teams][2]
   const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
   auto issue = [&](int i) {
     const uint8_t* base = walk.addr(i);
-    if constexpr (FIX) {
+    if constexpr (UNITS) {
       A[i] = load16(base + 16u * ul);
       B[i] = load16(base + 1024u + 16u * ul);
       C[i] = load16(base + 2048u + 16u * ul);
@@ -809,13 +817,16 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
 // a kernel of its own rather than a branch in one: at the join of two walks
 // the compiler merges their pending loads and then waits for the activation
 // before issuing the first weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
+          bool UNITS = FIX>
 __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
   static_assert(!FIX || T == 1, "fixed columns: one token");
-  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+  static_assert(!FIX || UNITS, "fixed columns read the unit layout");
+  static_assert(!UNITS || !PAIR || FIX, "the general walk reads a pair's native rows");
+  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // The unit layout (launch_kq_units): one thread per (group of 16 blocks,
@@ -1630,6 +1641,10 @@ bool interleave_rows() { return tuning().interleave; }
 
 uint32_t forced_blocks_per_team() { return static_cast<uint32_t>(tuning().gemv_ni); }
 
+// Lanes of a one-round one-token workgroup for a 17- to 32-block row: a
+// half-wave quantizes each block.
+uint32_t onepass_lanes(uint32_t nb) { return nb <= 24u ? 768u : 1024u; }
+
 // Rows per workgroup: one per 8-lane team for I2_S and dense rows; for the
 // k-quants, whole rows of nb blocks over 64 teams of ni blocks each.
 uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
@@ -1639,10 +1654,10 @@ uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
 }
 
 template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false, uint32_t NT = kThreads,
-          bool FIX = false>
+          bool FIX = false, bool UNITS = FIX>
 void* kq_kernel() {
-  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX>)
-                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX>);
+  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>)
+                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>);
 }
 
 // The fixed-column kernels of the one-token, one-round launches (nullptr
@@ -1714,11 +1729,17 @@ void* kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool
 }
 
 // The one-token kernels with a half-wave for every block of a 17- to
-// 32-block activation (768 or 1024 lanes, one block per team).
-void* kq_onepass_kernel(uint32_t type_id, uint32_t nt) {
-  if (nt == 768u)
-    return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, 768u>() : kq_kernel<14, 1, 1, 4, false, false, 768u>();
-  return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, 1024u>() : kq_kernel<14, 1, 1, 4, false, false, 1024u>();
+// 32-block activation (768 or 1024 lanes, one block per team), on the
+// native rows or (`units`) the unit layout.
+template <uint32_t NT, bool UNITS>
+void* kq_onepass_kernel_nt(uint32_t type_id) {
+  return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, NT, false, UNITS>()
+                        : kq_kernel<14, 1, 1, 4, false, false, NT, false, UNITS>();
+}
+
+void* kq_onepass_kernel(uint32_t type_id, uint32_t nt, bool units) {
+  if (nt == 768u) return units ? kq_onepass_kernel_nt<768u, true>(type_id) : kq_onepass_kernel_nt<768u, false>(type_id);
+  return units ? kq_onepass_kernel_nt<1024u, true>(type_id) : kq_onepass_kernel_nt<1024u, false>(type_id);
 }
 
 // The norm-fused decode kernels: one token, four blocks per team (two for a
@@ -1837,7 +1858,17 @@ hipError_t launch_i2s_q8(GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0
 }  // namespace
 
 bool units_eligible(uint32_t type_id, size_t rows, size_t nb) {
-  return (type_id == 12u || type_id == 14u) && rows > 0 && nb > 0 && nb <= 128u && (nb & (nb - 1u)) == 0u;
+  // the kernels address the copy with 32-bit offsets
+  if ((type_id != 12u && type_id != 14u) || rows == 0 || nb == 0 || units_bytes(type_id, rows, nb) > UINT32_MAX)
+    return false;
+  // the fixed-column kernels
+  if (nb <= 128u && (nb & (nb - 1u)) == 0u) return true;
+  // the one-round kernels, whose workgroups then start whole groups
+  if (nb > 16u && nb <= 32u) {
+    const size_t per = (onepass_lanes(static_cast<uint32_t>(nb)) / 4u) / nb;
+    return per * nb % 16u == 0u;
+  }
+  return false;
 }
 
 size_t units_bytes(uint32_t type_id, size_t rows, size_t nb) {
@@ -1953,7 +1984,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
   uint32_t onepass_nt = 0u;
   if (T == 1 && FUSED && kquant && !norm && !pair_job && fq == 4u && nbl > 16u && nbl <= 32u &&
       tuning().kq_onepass) {
-    const uint32_t nt1 = nbl <= 24u ? 768u : 1024u;
+    const uint32_t nt1 = onepass_lanes(nbl);
     const uint32_t r1 = (nt1 / 4u) / nbl;
     uint32_t w1 = 0;
     for (uint32_t i = 0; i < jobs.n; i++) w1 += (jobs.j[i].rows + r1 - 1u) / r1;
@@ -2012,7 +2043,17 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
     uint32_t nt = kThreads, nit = ni;
     if (onepass_nt) {
-      k = kq_onepass_kernel(type_id, onepass_nt);
+      // On the matrices' unit-layout copies when every job has one and each
+      // workgroup's rows are whole groups of 16 blocks (contiguous rows:
+      // 2048x5632 takes 8 rows of 22 blocks, 11 groups), so each load
+      // instruction of a wave reads consecutive bytes. Tuning::kq_units =
+      // false keeps the native rows.
+      bool units = tuning().kq_units;
+      for (uint32_t i = 0; i < jobs.n; i++)
+        units = units && jobs.j[i].wu && jobs.j[i].il == 0u && (R * jobs.j[i].nb) % 16u == 0u;
+      k = kq_onepass_kernel(type_id, onepass_nt, units);
+      if (units)
+        for (uint32_t i = 0; i < jobs.n; i++) jobs.j[i].w = jobs.j[i].wu;
       nt = onepass_nt;
     } else if (balanced) {
       k = kq_wide_kernel(type_id, fq, ni, norm != nullptr, pair);
@@ -2039,7 +2080,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // every wave's rows starting a group of 16 blocks: the fixed-column walk
     // (BlockWalk) on those copies. Tuning::kq_fix = false keeps the general
     // walk on the native rows.
-    if (!onepass_nt && T == 1 && FUSED && fq == 1u && tuning().kq_fix) {
+    if (!onepass_nt && T == 1 && FUSED && fq == 1u && tuning().kq_fix && tuning().kq_units) {
       bool fix = true;
       for (uint32_t i = 0; i < jobs.n; i++) {
         const GemvJob& j = jobs.j[i];

@@ -94,6 +94,7 @@ struct Tuning {
   bool kq_fix = true;      // RUSTICIDE_HIP_KQ_FIX=0: the general block walk only
   bool kq_balance = true;  // RUSTICIDE_HIP_KQ_BALANCE=0: no one-workgroup-per-CU reshaping
   bool kq_onepass = true;  // RUSTICIDE_HIP_KQ_ONEPASS=0: no 768/1024-lane one-round quantization
+  bool kq_units = true;    // RUSTICIDE_HIP_KQ_UNITS=0: no kernel reads the unit-layout copies
   int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 (two-token kernel)
   int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
   int i2s_nt = 0;          // RUSTICIDE_HIP_I2S_NT=256|512|1024: threads per workgroup, one token
@@ -112,9 +113,9 @@ hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, cons
                                hipStream_t s);
 
 // The unit layout of a k-quant matrix whose rows hold nb blocks (a power of
-// two up to 128): the blocks in row-major order, cut into groups of 16, each
-// group stored as the 64 lanes of the wave that reads it in one step of the
-// fixed-column walk take it (the lane's 16-byte pieces side by side, then
+// two up to 128, or 22, 24 or 30: units_eligible): the blocks in
+// row-major order, cut into groups of 16, each group stored as the 64 lanes
+// of the wave that reads it in one step of the block walk take it (the lane's 16-byte pieces side by side, then
 // the per-block scales and d), so each of that wave's loads reads
 // consecutive bytes. A group past the last row repeats the last row. Bytes:
 // units_bytes(); launch_kq_units fills `dst` from the native rows.

@@ -44,9 +44,11 @@ VARIANTS = {
     # 17- to 32-block rows on 512 lanes (two rounds of quantization) instead
     # of 768 or 1024
     "no-onepass": {"RUSTICIDE_HIP_KQ_ONEPASS": "0"},
+    # every kernel on the native blocks, none on the unit-layout copies
+    "native": {"RUSTICIDE_HIP_KQ_UNITS": "0"},
 }
 SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_KQ_FIX",
-            "RUSTICIDE_HIP_KQ_BALANCE", "RUSTICIDE_HIP_KQ_ONEPASS")
+            "RUSTICIDE_HIP_KQ_BALANCE", "RUSTICIDE_HIP_KQ_ONEPASS", "RUSTICIDE_HIP_KQ_UNITS")
 
 
 @pytest.fixture(params=list(VARIANTS))
@@ -159,6 +161,8 @@ KQ_SHAPES = [
     (14, 19, 8192, [1, 2]),     # 32 blocks: two passes (one token: 1024 lanes)
     (12, 1000, 8192, [1]),      # 32 blocks, 125 workgroups of 1024 lanes
     (14, 333, 4608, [1, 2]),    # 18 blocks, 34 workgroups of 768 lanes
+    (14, 100, 6144, [1, 2]),    # 24 blocks: 8-row workgroups of 12 groups, the last of 4 rows
+    (12, 77, 7680, [1]),        # 30 blocks: 1024 lanes, 8 rows = 15 groups
     (12, 11, 256, [1, 2]),      # one block per row: 16 rows per wave
     (14, 2048, 5632, [1, 3]),   # Q6_K ffn_down: 4620-byte rows, padded stride
     (14, 45, 768, [1, 2, 9]),
@@ -520,6 +524,25 @@ def test_i2s_one_token_kernel_at_every_team_width(ctx, tuning, lanes, family):
 
 
 # ------------------------------------------------------------ batch rules
+
+
+def test_one_round_jobs_of_several_widths(ctx, variant):
+    # one launch of 17- to 32-block jobs: 22 and 24 blocks both have the
+    # unit-layout copy and 8-row workgroups of whole groups; a 23-block job
+    # (no copy) puts the whole launch on the native rows
+    width = 6144
+    specs = [(14, 2048, 5632), (14, 300, 6144), (14, 50, 5888)]
+    mats, datas = [], []
+    for i, (t, rows, cols) in enumerate(specs):
+        d = synth.matrix(t, rows, cols, seed=300 + i)
+        datas.append(d)
+        mats.append(R.Matrix.load(ctx, t, d, rows, cols))
+    x = synth.normal_f32(width, seed=78)
+    for n in (2, 3):
+        outs = [np.full(rows, np.nan, np.float32) for _, rows, _ in specs[:n]]
+        R.matmul_batch(ctx, x, 1, list(zip(mats[:n], outs)))
+        for (t, rows, cols), d, out in zip(specs, datas, outs):
+            assert_same_bits(out, oracle_matmul(t, d, rows, cols, x[:cols], 1), f"{n} jobs: {rows}x{cols}")
 
 
 def test_one_batch_mixes_formats_and_matches_per_token_calls(ctx, variant):
