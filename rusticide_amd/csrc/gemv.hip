@@ -346,6 +346,32 @@ __device__ __forceinline__ const uint8_t* unit_at(const WgRows& g, uint32_t r, u
   return m + ((row * nb + fb) >> 4) * ubytes;
 }
 
+// nb terms t[0], t[S], t[2S], ... summed in order from -0.0, the LDS reads
+// of each run of 8 (then 4) issued together: one read latency a run, not
+// one a term.
+template <int S>
+__device__ __forceinline__ float terms_sum(const float* t, uint32_t nb) {
+  float s = -0.0f;
+  uint32_t b = 0;
+  for (; b + 8u <= nb; b += 8u) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) v[k] = t[(b + k) * S];
+#pragma unroll
+    for (int k = 0; k < 8; k++) s += v[k];
+  }
+  if (b + 4u <= nb) {
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) v[k] = t[(b + k) * S];
+#pragma unroll
+    for (int k = 0; k < 4; k++) s += v[k];
+    b += 4u;
+  }
+  for (; b < nb; b++) s += t[b * S];
+  return s;
+}
+
 // Each row's block terms summed in block order from -0.0
 // (portable/int_dot/rows.rs:9-12,59) and written; PAIR writes
 // silu(gate) * up with silu_mul's expressions (portable/elementwise.rs:6-9).
@@ -355,9 +381,8 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
   if constexpr (PAIR) {
     static_assert(T == 1, "a gate/up pair serves one token");
     for (uint32_t r = threadIdx.x; r < g.nh; r += NT) {
-      float gs = -0.0f, us = -0.0f;
-      for (uint32_t b = 0; b < nb; b++) gs += terms[__umul24(r, nbmax) + b];
-      for (uint32_t b = 0; b < nb; b++) us += terms[__umul24(r + g.nh, nbmax) + b];
+      const float gs = terms_sum<1>(terms + __umul24(r, nbmax), nb);
+      const float us = terms_sum<1>(terms + __umul24(r + g.nh, nbmax), nb);
       const float den = 1.0f + expf_ref(-gs);
       const float sg = __fdiv_rn(gs, den);
       const size_t idx = static_cast<size_t>(g.row0 + r) * tokens + t0;
@@ -366,8 +391,7 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
   } else {
     for (uint32_t i = threadIdx.x; i < g.nrows * T; i += NT) {
       const uint32_t r = i / T, t = i - r * T;
-      float s = -0.0f;
-      for (uint32_t b = 0; b < nb; b++) s += terms[(__umul24(r, nbmax) + b) * T + t];
+      const float s = terms_sum<T>(terms + __umul24(r, nbmax) * T + t, nb);
       const size_t idx = static_cast<size_t>(row_of(g, r)) * tokens + t0 + t;
       if (idx < J.out_len) J.out[idx] = s;
     }
