@@ -36,7 +36,11 @@ FLAGS = [
 # either file): their accumulators are shifted and read by vector code every
 # K block, which the accumulation registers would force through copies, and
 # the 128-token tiles fit in 256 registers, two waves per SIMD.
+# The GEMV kernels' leading scalar arguments go into SGPRs before the first
+# instruction (gfx950 kernel-argument preload): the _pl kernel forms put the
+# activation's pointer and sizes first, so its loads wait on no argument load.
 SOURCE_FLAGS = {
+    "gemv.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=16"],
     "gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "gemm_i2s.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }

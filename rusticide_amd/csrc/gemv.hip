@@ -714,6 +714,18 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, co
   q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
+// The same kernel with the activation's scalars first: the build preloads
+// leading scalar arguments into SGPRs (-amdgpu-kernarg-preload-count), so the
+// activation's first loads need no kernel-argument load (kq_preloads).
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
+          bool UNITS = FIX>
+__global__ __launch_bounds__(NT) void gemv_q4k_kernel_pl(const float* __restrict__ x, size_t width, uint32_t R,
+                                                          uint32_t nbmax, size_t tokens, size_t t0, GemvJobs jobs,
+                                                          Q8Dev q, NormIn nrm) {
+  extern __shared__ __align__(16) uint8_t lds[];
+  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+}
+
 // Q6_K x Q8_K --------------------------------------------------------------
 // LDS: act [T][nbmax*256] i8 | d8 [T][nbmax] f32 | bias [T][nbmax*16] i32
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
@@ -850,6 +862,18 @@ __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, co
   static_assert(!FIX || T == 1, "fixed columns: one token");
   static_assert(!FIX || UNITS, "fixed columns read the unit layout");
   static_assert(!UNITS || !PAIR || FIX, "the general walk reads a pair's native rows");
+  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+}
+
+// The same kernel with the activation's scalars first: the build preloads
+// leading scalar arguments into SGPRs (-amdgpu-kernarg-preload-count), so the
+// activation's first loads need no kernel-argument load (kq_preloads).
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
+          bool UNITS = FIX>
+__global__ __launch_bounds__(NT) void gemv_q6k_kernel_pl(const float* __restrict__ x, size_t width, uint32_t R,
+                                                          uint32_t nbmax, size_t tokens, size_t t0, GemvJobs jobs,
+                                                          Q8Dev q, NormIn nrm) {
+  extern __shared__ __align__(16) uint8_t lds[];
   q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
@@ -1677,40 +1701,62 @@ uint32_t rows_per_wg(uint32_t type_id, uint32_t nb, uint32_t ni) {
   return R < 1u ? 1u : R;
 }
 
+// A k-quant GEMV kernel and the order of its arguments: `preload` kernels
+// are the _pl forms (the activation's scalars first, loaded into SGPRs before
+// the first instruction), the others take the jobs first.
+struct KqFn {
+  void* fn = nullptr;
+  bool preload = false;
+  explicit operator bool() const { return fn != nullptr; }
+};
+
+// Preloaded arguments measured faster for the decode's launches (TinyLlama
+// step 671.3-673.6 against 677.5-678.3 us) and slower for the eight-block
+// launches without a norm (the output-sized one-round GEMV, 32000x2048 Q6_K:
+// 11.20-11.23 against 10.99-11.10 us), which keep theirs in memory.
+template <int NI, bool NORM>
+constexpr bool kq_preloads() { return NI != 8 || NORM; }
+
 template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false, uint32_t NT = kThreads,
           bool FIX = false, bool UNITS = FIX>
-void* kq_kernel() {
-  return FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>)
-                   : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>);
+KqFn kq_kernel() {
+  if constexpr (kq_preloads<NI, NORM>())
+    return {FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel_pl<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>)
+                      : reinterpret_cast<void*>(gemv_q6k_kernel_pl<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>),
+            true};
+  else
+    return {FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>)
+                      : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>),
+            false};
 }
 
-// The fixed-column kernels of the one-token, one-round launches (nullptr
-// where none is built): 1, 2, 4 or 8 blocks per team (8: not for a pair);
+// The fixed-column kernels of the one-token, one-round launches (an empty
+// KqFn where none is built): 1, 2, 4 or 8 blocks per team (8: not for a pair);
 // norm-fused (pair or not) and plain.
 template <int FMT, uint32_t NT>
-void* kq_fix_kernel_nt(uint32_t ni, bool norm, bool pair) {
+KqFn kq_fix_kernel_nt(uint32_t ni, bool norm, bool pair) {
   if (norm && pair) {
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, true, NT, true>()
            : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, true, NT, true>()
            : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, true, NT, true>()
-                      : nullptr;
+                      : KqFn{};
   }
-  if (pair) return nullptr;
+  if (pair) return KqFn{};
   if (norm) {
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, false, NT, true>()
            : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, false, NT, true>()
            : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, false, NT, true>()
            : ni == 8u ? kq_kernel<FMT, 1, 8, 1, true, false, NT, true>()
-                      : nullptr;
+                      : KqFn{};
   }
   return ni == 1u ? kq_kernel<FMT, 1, 1, 1, false, false, NT, true>()
          : ni == 2u ? kq_kernel<FMT, 1, 2, 1, false, false, NT, true>()
          : ni == 4u ? kq_kernel<FMT, 1, 4, 1, false, false, NT, true>()
          : ni == 8u ? kq_kernel<FMT, 1, 8, 1, false, false, NT, true>()
-                    : nullptr;
+                    : KqFn{};
 }
 
-void* kq_fix_kernel(uint32_t type_id, uint32_t ni, bool norm, bool pair, uint32_t nt) {
+KqFn kq_fix_kernel(uint32_t type_id, uint32_t ni, bool norm, bool pair, uint32_t nt) {
   if (nt == kThreads)
     return type_id == 12u ? kq_fix_kernel_nt<12, kThreads>(ni, norm, pair)
                           : kq_fix_kernel_nt<14, kThreads>(ni, norm, pair);
@@ -1721,34 +1767,34 @@ void* kq_fix_kernel(uint32_t type_id, uint32_t ni, bool norm, bool pair, uint32_
 // The 512-lane one-token kernels: 128 teams of ni blocks each take the rows
 // that 64 teams of 2*ni take at 256 lanes (nullptr where none is built).
 template <int FMT>
-void* kq_wide_kernel_fmt(uint32_t fq, uint32_t ni, bool norm, bool pair) {
+KqFn kq_wide_kernel_fmt(uint32_t fq, uint32_t ni, bool norm, bool pair) {
   constexpr uint32_t W = 2u * kThreads;
   if (norm) {
-    if (fq != 1u) return nullptr;
+    if (fq != 1u) return KqFn{};
     if (pair) {
       return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, true, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, true, W>()
              : ni == 4u                                            ? kq_kernel<FMT, 1, 4, 1, true, true, W>()
-                                                                   : nullptr;
+                                                                   : KqFn{};
     }
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, true, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, true, false, W>()
            : ni == 4u ? kq_kernel<FMT, 1, 4, 1, true, false, W>()
            : ni == 8u ? kq_kernel<FMT, 1, 8, 1, true, false, W>()
-                      : nullptr;
+                      : KqFn{};
   }
-  if (pair) return nullptr;
+  if (pair) return KqFn{};
   if (fq == 1u)
     return ni == 1u ? kq_kernel<FMT, 1, 1, 1, false, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 1, false, false, W>()
            : ni == 4u ? kq_kernel<FMT, 1, 4, 1, false, false, W>()
            : ni == 8u ? kq_kernel<FMT, 1, 8, 1, false, false, W>()
-                      : nullptr;
+                      : KqFn{};
   if (fq == 4u)
     return ni == 1u ? kq_kernel<FMT, 1, 1, 4, false, false, W>() : ni == 2u ? kq_kernel<FMT, 1, 2, 4, false, false, W>()
            : ni == 4u                                              ? kq_kernel<FMT, 1, 4, 4, false, false, W>()
-                                                                   : nullptr;
-  return nullptr;
+                                                                   : KqFn{};
+  return KqFn{};
 }
 
-void* kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool pair) {
+KqFn kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool pair) {
   return type_id == 12u ? kq_wide_kernel_fmt<12>(fq, ni, norm, pair) : kq_wide_kernel_fmt<14>(fq, ni, norm, pair);
 }
 
@@ -1756,12 +1802,12 @@ void* kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool
 // 32-block activation (768 or 1024 lanes, one block per team), on the
 // native rows or (`units`) the unit layout.
 template <uint32_t NT, bool UNITS>
-void* kq_onepass_kernel_nt(uint32_t type_id) {
+KqFn kq_onepass_kernel_nt(uint32_t type_id) {
   return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, NT, false, UNITS>()
                         : kq_kernel<14, 1, 1, 4, false, false, NT, false, UNITS>();
 }
 
-void* kq_onepass_kernel(uint32_t type_id, uint32_t nt, bool units) {
+KqFn kq_onepass_kernel(uint32_t type_id, uint32_t nt, bool units) {
   if (nt == 768u) return units ? kq_onepass_kernel_nt<768u, true>(type_id) : kq_onepass_kernel_nt<768u, false>(type_id);
   return units ? kq_onepass_kernel_nt<1024u, true>(type_id) : kq_onepass_kernel_nt<1024u, false>(type_id);
 }
@@ -1769,7 +1815,7 @@ void* kq_onepass_kernel(uint32_t type_id, uint32_t nt, bool units) {
 // The norm-fused decode kernels: one token, four blocks per team (two for a
 // single-round launch that would leave most CUs idle), the row preloaded in
 // one (FQ 1) or four (FQ 4) rounds; `pair` for a gate/up job.
-void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair, uint32_t ni) {
+KqFn kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair, uint32_t ni) {
   if (ni == 8u && fq == 1u && !pair)
     return type_id == 12u ? kq_kernel<12, 1, 8, 1, true>() : kq_kernel<14, 1, 8, 1, true>();
   if (ni == 2u && fq == 1u) {
@@ -1785,7 +1831,7 @@ void* kq_norm_kernel(uint32_t type_id, uint32_t fq, bool pair, uint32_t ni) {
 }
 
 template <int FMT, int T, int FQ>
-void* kq_kernel_ni(uint32_t ni) {
+KqFn kq_kernel_ni(uint32_t ni) {
   // eight blocks per team: one-token fused launches only
   if constexpr (T == 1 && FQ != 0)
     if (ni == 8u) return kq_kernel<FMT, T, 8, FQ>();
@@ -1794,7 +1840,7 @@ void* kq_kernel_ni(uint32_t ni) {
 
 // fq: 0 (a separately quantized activation), 1 or 4 (fused, preload depth)
 template <int T>
-void* kq_kernel_for(uint32_t type_id, uint32_t ni, uint32_t fq) {
+KqFn kq_kernel_for(uint32_t type_id, uint32_t ni, uint32_t fq) {
   if (fq == 0u) return type_id == 12u ? kq_kernel_ni<12, T, 0>(ni) : kq_kernel_ni<14, T, 0>(ni);
   if (fq == 1u) return type_id == 12u ? kq_kernel_ni<12, T, 1>(ni) : kq_kernel_ni<14, T, 1>(ni);
   return type_id == 12u ? kq_kernel_ni<12, T, 4>(ni) : kq_kernel_ni<14, T, 4>(ni);
@@ -1868,7 +1914,7 @@ uint32_t choose_blocks_per_team(uint32_t type_id, uint32_t nb, uint32_t total_ro
     if (ni < floor_ni) continue;
     const uint32_t R = rows_per_wg(type_id, nb, ni);
     const uint32_t wgs = (total_rows + R - 1u) / R;
-    const int per_cu = resident_wgs_per_cu(kq_kernel_for<T>(type_id, ni, fq), lds_bytes<T>(type_id, nb, R));
+    const int per_cu = resident_wgs_per_cu(kq_kernel_for<T>(type_id, ni, fq).fn, lds_bytes<T>(type_id, nb, R));
     if (wgs <= static_cast<uint32_t>(per_cu * device_cus())) return ni;
   }
   return 4u;
@@ -2049,7 +2095,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // the fused kernels quantize blocks [0, nbmax) of x, which width covers
     const float* xin = FUSED ? x : nullptr;
     NormIn nrm{};
-    void* k;
+    KqFn k;
     if (norm) {
       // the squares of the row (and the rms) after the kernel's own LDS
       nrm = *norm;
@@ -2083,7 +2129,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       k = kq_wide_kernel(type_id, fq, ni, norm != nullptr, pair);
       nt = 2u * kThreads;
     } else if (wide8) {
-      if (void* kw = kq_wide_kernel(type_id, fq, 8u, norm != nullptr, pair)) {
+      if (const KqFn kw = kq_wide_kernel(type_id, fq, 8u, norm != nullptr, pair)) {
         k = kw;
         nt = 2u * kThreads;
       } else {
@@ -2092,7 +2138,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     } else if (T == 1 && FUSED && ni >= 2u) {
       const int forced = norm ? tuning().norm_nt : tuning().kq_nt;
       const bool wide = forced ? forced == 512 : wgs < static_cast<uint32_t>(device_cus());
-      void* kw = wide ? kq_wide_kernel(type_id, fq, ni / 2u, norm != nullptr, pair) : nullptr;
+      const KqFn kw = wide ? kq_wide_kernel(type_id, fq, ni / 2u, norm != nullptr, pair) : KqFn{};
       if (kw) {
         k = kw;
         nt = 2u * kThreads;
@@ -2115,7 +2161,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
         const uint32_t rpu = b != 0u && b < 16u ? 16u / b : 1u;
         fix = fix && (j.il ? (1u << (j.il - 1u)) % rpu == 0u : per % rpu == 0u);
       }
-      void* kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : nullptr;
+      const KqFn kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : KqFn{};
       if (kf) {
         k = kf;
         for (uint32_t i = 0; i < jobs.n; i++) {
@@ -2124,9 +2170,13 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
         }
       }
     }
-    void* args[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
-                    const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};
-    return hipLaunchKernel(k, dim3(wgs), dim3(nt), args, lds, s);
+    if (!k) return hipErrorNotSupported;
+    // the argument order of the kernel chosen (KqFn::preload)
+    void* args_jobs[] = {&jobs, const_cast<Q8Dev*>(&q), &xin, &width, const_cast<uint32_t*>(&R),
+                         const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};
+    void* args_pl[] = {&xin, &width, const_cast<uint32_t*>(&R), const_cast<uint32_t*>(&nbl), &tokens, &t0,
+                       &jobs, const_cast<Q8Dev*>(&q), &nrm};
+    return hipLaunchKernel(k.fn, dim3(wgs), dim3(nt), k.preload ? args_pl : args_jobs, lds, s);
   }
   if (tuning().i2s_one) {
     const hipError_t e = launch_i2s_q8<T>(jobs, q, tokens, t0, s, raw);
