@@ -612,14 +612,14 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   __builtin_amdgcn_sched_barrier(0);
   u32x4 hd[NI], c0[NI], c1[NI];
   // UNITS, unit layout: headers [16 teams][16] | qs[0..64) [64 lanes][16] |
-  // qs[64..128) [64 lanes][16]
+  // qs[64..128) [64 lanes][16]; the quants are read nontemporal
   const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
   auto issue = [&](int i) {
     const uint8_t* blk = walk.addr(i);
     if constexpr (UNITS) {
       hd[i] = load16(blk + 16u * utw);
-      c0[i] = load16(blk + 256u + 16u * ul);
-      c1[i] = load16(blk + 1280u + 16u * ul);
+      c0[i] = load16_nt(blk + 256u + 16u * ul);
+      c1[i] = load16_nt(blk + 1280u + 16u * ul);
     } else {
       hd[i] = load16(blk);
       c0[i] = load16(blk + 16u + 16u * p);
@@ -767,9 +767,9 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   auto issue = [&](int i) {
     const uint8_t* base = walk.addr(i);
     if constexpr (UNITS) {
-      A[i] = load16(base + 16u * ul);
-      B[i] = load16(base + 1024u + 16u * ul);
-      C[i] = load16(base + 2048u + 16u * ul);
+      A[i] = load16_nt(base + 16u * ul);  // nontemporal, as in q4k_body
+      B[i] = load16_nt(base + 1024u + 16u * ul);
+      C[i] = load16_nt(base + 2048u + 16u * ul);
       S[i] = *reinterpret_cast<const uint2*>(base + 3072u + 16u * utw + 8u * h);
       D[i] = *reinterpret_cast<const uint16_t*>(base + 3328u + 2u * utw);
     } else {
@@ -1283,7 +1283,7 @@ __global__ __launch_bounds__(NT) void gemv_i2s_one_kernel(GemvJobs jobs, const f
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
     const uint32_t c = min(cl + static_cast<uint32_t>(i * LPR), nchunk - 1u);
-    w[i] = load16(wrow + 16u * c);
+    w[i] = load16_nt(wrow + 16u * c);  // read once: nontemporal
   }
   // the scalars the stores need, loaded now rather than after the dot (the
   // compiler otherwise reloads them there, one dependent round trip each)
@@ -1507,7 +1507,7 @@ __global__ __launch_bounds__(256) void gemv_i2s_q8_kernel(GemvJobs jobs, Q8Dev q
 #pragma unroll
   for (int i = 0; i < CPL; i++) {
     const uint32_t c = min(cl + static_cast<uint32_t>(i * LPR), nchunk - 1u);
-    w[i] = load16(wrow + 16u * c);
+    w[i] = load16_nt(wrow + 16u * c);  // read once: nontemporal
   }
   __asm__ volatile("" ::"s"(out), "s"(out_len), "s"(scale), "s"(tokens), "s"(t0), "s"(raw));
   __builtin_amdgcn_sched_barrier(0);
