@@ -63,17 +63,17 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 WORKLOADS = {
     # name: (type_id, rows, cols, description, kernel the step launches)
     "q6k_lm_head": (14, 32000, 2048, "Q6_K x f32 GEMV 32000x2048 (TinyLlama lm_head), batch 1",
-                    "gemv_q6k_kernel<1, 8, 1, false, false, 512u, true>"),
+                    "gemv_q6k_kernel<1, 8, 1, false, false, 512u, true, true>"),
     "q6k_ffn_down": (14, 2048, 5632, "Q6_K x f32 GEMV 2048x5632 (TinyLlama ffn_down), batch 1",
-                     "gemv_q6k_kernel<1, 1, 4, false, false, 768u, false>"),
+                     "gemv_q6k_kernel_pl<1, 1, 4, false, false, 768u, false, true>"),
     "q4k_ffn_gate": (12, 5632, 2048, "Q4_K x f32 GEMV 5632x2048 (TinyLlama ffn_gate), batch 1",
-                     "gemv_q4k_kernel<1, 2, 1, false, false, 512u, true>"),
+                     "gemv_q4k_kernel_pl<1, 2, 1, false, false, 512u, true, true>"),
     "i2s_up": (36, 6912, 2560, "I2_S x int8 GEMV 6912x2560 (BitNet 2B4T up/gate), batch 1",
                "gemv_i2s_one_kernel<256u, 8, 5, true>"),
     "i2s_down": (36, 2560, 6912, "I2_S x int8 GEMV 2560x6912 (BitNet 2B4T down), batch 1",
                  "gemv_i2s_one_kernel<512u, 32, 4, true>"),
     "q4k_32000": (12, 32000, 2048, "Q4_K x f32 GEMV 32000x2048 (lm_head shape in Q4_K), batch 1",
-                  "gemv_q4k_kernel<1, 8, 1, false, false, 512u, true>"),
+                  "gemv_q4k_kernel<1, 8, 1, false, false, 512u, true, true>"),
 }
 HEADLINE = "q6k_lm_head"
 
