@@ -12,7 +12,12 @@ rows. Weights rotate over more than 1 GiB of distinct HBM copies, so the
 `value` is algorithmic GB/s of the whole step at wall clock:
 rows*row_bytes (+32 I2_S trailer) + 4*cols (f32 x) + 4*rows (f32 y).
 `roofline.achieved` is the same bytes over the average duration of the step's
-GEMV kernel, measured with HIP events on the stream it is launched on.
+GEMV kernel, measured with HIP events on the stream it is launched on, around
+`steps` launches that the host queues behind a bounded hold kernel
+(rh_hold_device) so that they run back to back. Every warm-up makes whole
+passes over the rotation of copies and lasts at least 50 ms, so the timed
+launches read copies whose pages are mapped and which the Infinity Cache no
+longer holds.
 `roofline.traffic` is the HBM bytes per launch read from the rocprofv3 counter
 summary in profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy of
 known size), when that summary covers the workload.
@@ -103,6 +108,37 @@ def load_rotation(ctx, name: str):
     return data, [one] + [R.Matrix.load(ctx, type_id, data, rows, cols) for _ in range(ncopies - 1)]
 
 
+WARM_MIN_S = 0.05  # every warm-up runs at least this long, whatever --warmup says
+
+
+def hold_us_for(launches: int, per_launch_host_us: float = 20.0) -> int:
+    """A hold long enough for the host to queue `launches` calls behind it."""
+    return int(min(100000, 1000 + per_launch_host_us * launches))
+
+
+def held_events(ctx, queue, launches: int, per_launch_host_us: float = 20.0):
+    """Per-launch device time of `launches` launches queued by `queue()`
+    behind a bounded hold (rh_hold_device), so that they run back to back:
+    HIP events on the stream the kernels run on, (start, end) around them.
+    Returns (us per launch, whether the host finished queueing inside the
+    hold, host microseconds per queued launch)."""
+    import rusticide_amd as R
+    from rusticide_amd import hip as H
+
+    stream = ctx.stream
+    hold = hold_us_for(launches, per_launch_host_us)
+    start, end = H.Event(), H.Event()
+    H.synchronize()
+    t = time.perf_counter()
+    R.hold(ctx, hold)
+    start.record(stream)
+    queue()
+    end.record(stream)
+    queued_s = time.perf_counter() - t
+    H.synchronize()
+    return 1e3 * start.elapsed_ms(end) / launches, queued_s < hold * 1e-6, queued_s * 1e6 / launches
+
+
 def measure_gpu(ctx, name: str, steps: int, warmup: int):
     import rusticide_amd as R
     from rusticide_amd import hip as H
@@ -115,53 +151,70 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
     out = H.DeviceArray(rows)
     stream = ctx.stream
     B = algorithmic_bytes(type_id, rows, cols)
+    # the handle arrays are built here, before any timed region: handles[0]
+    # starts the rotation at copy 0, handles[1] continues it where `steps`
+    # launches from copy 0 leave it
+    handles = [R.matrix_handles(mats, 0), R.matrix_handles(mats, steps % ncopies)]
 
-    def run(copies: int, n: int, first: int = 0) -> None:
+    def run(h, n: int) -> None:
         # the launches are queued from C (one rh_matmul_batch_device each):
         # a Python call per launch can take as long as the kernel itself
-        order = [mats[(first + i) % copies] for i in range(copies)]
-        R.matmul_batch_device_repeat(ctx, x, 1, order, out, n)
+        R.matmul_batch_device_repeat_handles(ctx, x, 1, h, out, n)
+
+    # warm-up: whole passes over every copy (each one's pages mapped and read
+    # once), at least `warmup` launches and WARM_MIN_S of them; the rotation
+    # is back at copy 0 when it ends
+    passes, t = max(1, math.ceil(warmup / ncopies)), time.perf_counter()
+    run(handles[0], passes * ncopies)
+    H.synchronize()
+    el = time.perf_counter() - t
+    more = math.ceil(max(0.0, WARM_MIN_S - el) / (el / passes))
+    if more:
+        run(handles[0], more * ncopies)
+        H.synchronize()
+    warm_launches = (passes + more) * ncopies
 
     # the timed region: `steps` steps bracketed by device synchronization,
-    # with events on the stream the step's one kernel runs on
-    run(ncopies, warmup)
-    H.synchronize()
+    # wall clock, with events on the stream the step's kernel runs on
     start, end = H.Event(), H.Event()
+    H.synchronize()
     t0 = time.perf_counter()
     start.record(stream)
-    run(ncopies, steps, warmup)
+    run(handles[0], steps)
     end.record(stream)
     H.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
-    kernel_us = 1e3 * start.elapsed_ms(end) / steps
+    unheld_us = 1e3 * start.elapsed_ms(end) / steps
     gpu_out = out.numpy()
+    # the same number of launches, continuing the rotation, queued behind a
+    # hold: the kernel's back-to-back time per launch, without the host's
+    # latency to the first launch
+    kernel_us, held, host_us = held_events(ctx, lambda: run(handles[1], steps), steps)
 
     # the same kernel on one cache-resident copy (Infinity Cache), labelled warm
-    run(1, warmup)
-    start.record(stream)
-    run(1, steps)
-    end.record(stream)
-    H.synchronize()
-    warm_us = 1e3 * start.elapsed_ms(end) / steps
+    one = R.matrix_handles(mats[:1])
+    run(one, max(warmup, 50))
+    warm_us = held_events(ctx, lambda: run(one, steps), steps)[0]
 
     # the unfused form for comparison: the GEMV alone on a pre-quantized activation
     kind = R.ROW if type_id == 36 else R.SUPER_BLOCK
     q8 = R.Q8(ctx).quantize(x, 1, kind)
-    for i in range(warmup):
-        R.dot_matrix_device(mats[i % ncopies], q8, out)
-    start.record(stream)
-    for i in range(steps):
-        R.dot_matrix_device(mats[i % ncopies], q8, out)
-    end.record(stream)
-    H.synchronize()
-    prequant_us = 1e3 * start.elapsed_ms(end) / steps
+    for i in range(ncopies):
+        R.dot_matrix_device(mats[i], q8, out)
+
+    def prequant():
+        for i in range(steps):
+            R.dot_matrix_device(mats[i % ncopies], q8, out)
+
+    prequant_us = held_events(ctx, prequant, steps, per_launch_host_us=60.0)[0]
     q8.free()
     for m in mats:
         m.free()
     return {
         "workload": name, "desc": desc, "kernel": kernel, "type_id": type_id, "rows": rows, "cols": cols,
         "bytes": B, "copies": ncopies, "ms_per_step": ms_per_step, "step_gbs": B / (ms_per_step * 1e-3) / 1e9,
-        "kernel_us": kernel_us, "kernel_gbs": B / (kernel_us * 1e-6) / 1e9,
+        "kernel_us": kernel_us, "kernel_gbs": B / (kernel_us * 1e-6) / 1e9, "held": held,
+        "host_us_per_launch": host_us, "unheld_kernel_us": unheld_us, "warmup_launches": warm_launches,
         "warm_kernel_us": warm_us, "warm_kernel_gbs": B / (warm_us * 1e-6) / 1e9,
         "prequantized_gemv_us": prequant_us,
         "data": data, "x": synth.normal_f32(cols, seed=2), "gpu_out": gpu_out,
@@ -170,8 +223,10 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
 
 def measure_stream_read(ctx, nbytes: int, copies: int, steps: int, warmup: int) -> float:
     """GB/s of a plain streaming read (rh_stream_read_device) of `nbytes` per
-    launch, rotated over the same number of copies as the headline: the
-    measured ceiling the GEMV kernel is compared with."""
+    launch, rotated over the same number of copies as the workload: the
+    measured ceiling the GEMV kernel is compared with. Warmed up and timed as
+    the GEMV is (a whole pass over the copies and WARM_MIN_S, then launches
+    queued behind a hold)."""
     import ctypes
     import rusticide_amd as R
     from rusticide_amd import hip as H
@@ -185,16 +240,20 @@ def measure_stream_read(ctx, nbytes: int, copies: int, steps: int, warmup: int) 
         b.fill_bytes(0x3C)
     ptrs = (ctypes.c_void_p * copies)(*[b.ptr.value for b in bufs])
     sink = H.DeviceArray(2048, dtype=np.uint32)
+
     # the launches are queued from C: a Python call per launch would take
     # longer than the ~9 us read and leave the GPU idle between launches
-    ctx.check(L.rh_stream_read_device(ctx.handle, ptrs, copies, n, warmup, sink.ptr))
+    def run(count: int) -> None:
+        ctx.check(L.rh_stream_read_device(ctx.handle, ptrs, copies, n, count, sink.ptr))
+
+    passes, t = max(1, math.ceil(warmup / copies)), time.perf_counter()
+    run(passes * copies)
     H.synchronize()
-    start, end = H.Event(), H.Event()
-    start.record(ctx.stream)
-    ctx.check(L.rh_stream_read_device(ctx.handle, ptrs, copies, n, steps, sink.ptr))
-    end.record(ctx.stream)
-    H.synchronize()
-    us = 1e3 * start.elapsed_ms(end) / steps
+    el = time.perf_counter() - t
+    more = math.ceil(max(0.0, WARM_MIN_S - el) / (el / passes))
+    if more:
+        run(more * copies)
+    us = held_events(ctx, lambda: run(steps), steps)[0]
     for b in bufs:
         b.free()
     sink.free()
@@ -288,7 +347,6 @@ def measure_gemm(ctx, token_counts=(128, 512, 2048), reps: int = 20):
     from rusticide_amd import hip as H
     from rusticide_amd import synth
 
-    stream = ctx.stream
     res = []
     for type_id, rows, cols, desc in GEMM_WORKLOADS:
         data = synth.i2s_matrix(rows, cols, seed=1) if type_id == 36 else synth.matrix(type_id, rows, cols, seed=1)
@@ -300,15 +358,14 @@ def measure_gemm(ctx, token_counts=(128, 512, 2048), reps: int = 20):
             q8 = R.Q8(ctx).quantize(x, T, kind)
 
             def timed(fn):
-                for i in range(3):
+                for i in range(4):
                     fn(i)
-                a, b = H.Event(), H.Event()
-                a.record(stream)
-                for i in range(reps):
-                    fn(i)
-                b.record(stream)
-                H.synchronize()
-                return 1e3 * a.elapsed_ms(b) / reps
+
+                def queue():
+                    for i in range(reps):
+                        fn(i)
+
+                return held_events(ctx, queue, reps, per_launch_host_us=100.0)[0]
 
             k_us = timed(lambda i: R.dot_matrix_device(mats[i % 4], q8, out))
             s_us = timed(lambda i: R.matmul_batch_device(ctx, x, T, [(mats[i % 4], out)]))
@@ -575,6 +632,8 @@ def main() -> int:
             "stream_read_gbs": round(r["stream_gbs"], 1),
             "frac_of_stream_read": round(r["kernel_gbs"] / r["stream_gbs"], 4),
             "prequantized_gemv_us": round(r["prequantized_gemv_us"], 3),
+            "unheld_kernel_us": round(r["unheld_kernel_us"], 3), "warmup_launches": r["warmup_launches"],
+            "host_us_per_launch": round(r["host_us_per_launch"], 2), "queued_inside_hold": r["held"],
             "kernel": r["kernel"], "hbm_traffic_bytes": traffic_for(n)}
         for n, r in results.items() if n != HEADLINE
     }
@@ -607,6 +666,7 @@ def main() -> int:
         "data": "synthetic",
         "config": {"workload": h["desc"], "rows": h["rows"], "cols": h["cols"], "tokens": 1,
                    "bytes_per_step": h["bytes"], "rotating_copies": h["copies"],
+                   "warmup_launches": h["warmup_launches"],
                    "step": "one launch: in-workgroup Q8_K quantize + Q6_K GEMV, weights rotated over >1 GiB"},
         "roofline": {"bound": "hbm", "achieved": round(h["kernel_gbs"], 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(h["kernel_gbs"] / HBM_PEAK_GBS, 4),
@@ -615,7 +675,13 @@ def main() -> int:
                      "warm_cache_resident_gbs": round(h["warm_kernel_gbs"], 1),
                      "stream_read_gbs": round(stream_gbs, 1),
                      "frac_of_stream_read": round(h["kernel_gbs"] / stream_gbs, 4),
-                     "prequantized_gemv_us": round(h["prequantized_gemv_us"], 3)},
+                     "prequantized_gemv_us": round(h["prequantized_gemv_us"], 3),
+                     "unheld_kernel_avg_us": round(h["unheld_kernel_us"], 3),
+                     "queued_inside_hold": h["held"],
+                     "host_us_per_launch": round(h["host_us_per_launch"], 2),
+                     "timing": "HIP events on the kernel's stream around `steps` launches queued behind a "
+                               "bounded hold (back to back); unheld_kernel_avg_us: events around the "
+                               "wall-clock timed region itself"},
         "cpu_baseline": cpu,
         "also": also,
     }

@@ -129,9 +129,12 @@ rh_status rh_matmul_batch_device(rh_ctx *ctx, const float *inputs, size_t inputs
  * bit for bit, and allocates nothing: the batch's quantized activations go
  * to a file-scope array of RH_NOALLOC_SCRATCH_BYTES on each GPU, whose
  * address rh_init looks up once per device, and K-split GEMMs run unsplit.
- * A batch whose quantized activations would not fit, about
- * 2 * tokens * width bytes plus a fifth of that, is refused with
- * RH_ERR_INVALID_ARGUMENT. Every call on a GPU shares that GPU's array:
+ * A batch whose quantized activations would not fit is refused with
+ * RH_ERR_INVALID_ARGUMENT. They take, with W = width rounded up to a
+ * multiple of 256 (at least 256), B = W / 32 rounded up to a multiple of 8
+ * and r(n) = n rounded up to a multiple of 256:
+ * 2 * r(tokens * W) + 6 * r(tokens * B * 4) bytes, about
+ * 2.75 * tokens * width (4096 tokens x 256 values, or 1489 x 1024, fit). Every call on a GPU shares that GPU's array:
  * calls that overlap on one GPU (other streams, other contexts, other
  * threads) race, and must be ordered by the caller. */
 enum { RH_NOALLOC_SCRATCH_BYTES = 4 << 20 };
@@ -201,6 +204,13 @@ rh_status rh_math_device(rh_ctx *ctx, uint32_t op, const float *a, const float *
 enum { RH_STREAM_READ_SINK_WORDS = 2048 };
 rh_status rh_stream_read_device(rh_ctx *ctx, const void *const *buffers, size_t n_buffers, size_t bytes,
                                 size_t launches, uint32_t *sink);
+/* Bench hook with no reference counterpart: one wave that occupies `stream`
+ * (NULL: the context's) for `microseconds` (at most RH_HOLD_MAX_US) of the
+ * device's constant-rate clock, then exits. Queued ahead of a timed run, it
+ * lets the host queue every launch before the first one starts, so events
+ * around the run time the launches back to back and not the host's pace. */
+enum { RH_HOLD_MAX_US = 100000 };
+rh_status rh_hold_device(rh_ctx *ctx, uint32_t microseconds, void *stream);
 /* Bench hook with no reference counterpart: `launches` calls of
  * rh_matmul_batch_device(ctx, inputs, inputs_len, tokens, {matrices[i %
  * n_matrices], out, out_len}, 1, stream), queued from C so that the host's
@@ -209,7 +219,9 @@ rh_status rh_matmul_batch_device_repeat(rh_ctx *ctx, const float *inputs, size_t
                                         const rh_matrix *const *matrices, size_t n_matrices, float *out,
                                         size_t out_len, size_t launches, void *stream);
 /* Tuning hook with no reference counterpart: re-reads the RUSTICIDE_HIP_*
- * kernel switches from the environment (rh_init reads them once). Every
+ * kernel switches from the environment (the process's first rh_init reads
+ * them; a reload publishes a new snapshot, which launches on any thread
+ * pick up whole). Every
  * switch gives the same bits; they select among equivalent kernels. */
 void rh_reload_tuning(void);
 /* Test hook with no reference counterpart: the ordered float sum the decoder

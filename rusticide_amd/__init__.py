@@ -109,6 +109,8 @@ def lib() -> ctypes.CDLL:
         L.rh_matmul_batch_device_repeat.restype = St
         L.rh_reload_tuning.argtypes = []
         L.rh_reload_tuning.restype = None
+        L.rh_hold_device.argtypes = [P, ctypes.c_uint32, P]
+        L.rh_hold_device.restype = St
         _lib = L
     return _lib
 
@@ -308,6 +310,28 @@ def matmul_batch_device_repeat(ctx: Context, inputs, tokens: int, matrices, out,
     ctx.check(lib().rh_matmul_batch_device_repeat(ctx.handle, _ptr(inputs), inputs.numel(), tokens, arr,
                                                   len(matrices), _ptr(out), out.numel(), launches,
                                                   stream or None))
+
+
+def matrix_handles(matrices, first: int = 0):
+    """A ctypes array of the matrices' handles, rotated to start at `first`
+    (built once, outside any timed region, for matmul_batch_device_repeat)."""
+    n = len(matrices)
+    order = [matrices[(first + i) % n] for i in range(n)]
+    return (ctypes.c_void_p * n)(*[ctypes.cast(m.handle, ctypes.c_void_p).value for m in order])
+
+
+def matmul_batch_device_repeat_handles(ctx: Context, inputs, tokens: int, handles, out, launches: int,
+                                       stream: int = 0) -> None:
+    """matmul_batch_device_repeat over a prebuilt handle array (matrix_handles)."""
+    ctx.check(lib().rh_matmul_batch_device_repeat(ctx.handle, _ptr(inputs), inputs.numel(), tokens, handles,
+                                                  len(handles), _ptr(out), out.numel(), launches,
+                                                  stream or None))
+
+
+def hold(ctx: Context, microseconds: int, stream: int = 0) -> None:
+    """Occupies the stream for `microseconds` with one bounded wave (a bench
+    hook): launches queued behind it start back to back."""
+    ctx.check(lib().rh_hold_device(ctx.handle, int(microseconds), stream or None))
 
 
 def reload_tuning() -> None:

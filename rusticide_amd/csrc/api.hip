@@ -7,6 +7,7 @@
 // activation kind once per batch on the device, then one grouped GEMV launch
 // per weight format covering every matrix of that format.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
@@ -351,7 +352,12 @@ void* scratch_ptr(int device) {
 namespace rh {
 
 namespace {
-Tuning g_tuning;
+// The current snapshot. A reload publishes a new one and never frees the
+// old: a launch on another thread may still be reading it (a few dozen bytes
+// per rh_reload_tuning call).
+const Tuning g_default_tuning{};
+std::atomic<const Tuning*> g_tuning{&g_default_tuning};
+std::once_flag g_tuning_once;
 
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
@@ -359,7 +365,7 @@ int env_int(const char* name, int dflt) {
 }
 }  // namespace
 
-const Tuning& tuning() { return g_tuning; }
+const Tuning& tuning() { return *g_tuning.load(std::memory_order_acquire); }
 
 void load_tuning() {
   Tuning t;
@@ -390,8 +396,10 @@ void load_tuning() {
   t.gemm_bn = bn == 64 || bn == 128 || bn == 256 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;
   t.attn_lds = env_int("RUSTICIDE_HIP_ATTN_LDS", 1) != 0;
-  g_tuning = t;
+  g_tuning.store(new Tuning(t), std::memory_order_release);
 }
+
+void init_tuning() { std::call_once(g_tuning_once, load_tuning); }
 
 int ctx_device(const rh_ctx* ctx) { return ctx->device; }
 uint64_t ctx_scratch_generation(const rh_ctx* ctx) { return ctx->scratch_gen; }
@@ -724,7 +732,7 @@ rh_status rh_init(int device, rh_ctx** out) {
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0) return RH_ERR_NO_DEVICE;
   rh_ctx* ctx = new (std::nothrow) rh_ctx();
   if (!ctx) return RH_ERR_OUT_OF_MEMORY;
-  load_tuning();
+  init_tuning();  // the first context reads the switches; rh_reload_tuning re-reads them
   ctx->device = device;
   if (hipSetDevice(device) != hipSuccess || hipStreamCreate(&ctx->stream) != hipSuccess) {
     delete ctx;

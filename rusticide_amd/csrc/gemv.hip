@@ -2160,6 +2160,9 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
         // interleave chunk, must be whole groups
         const uint32_t rpu = b != 0u && b < 16u ? 16u / b : 1u;
         fix = fix && (j.il ? (1u << (j.il - 1u)) % rpu == 0u : per % rpu == 0u);
+        // a pair's up rows start at workgroup row nh = min(per, rows - row0):
+        // the last workgroup's nh is whole groups only when rows is
+        fix = fix && (!pair || j.rows % rpu == 0u);
       }
       const KqFn kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : KqFn{};
       if (kf) {

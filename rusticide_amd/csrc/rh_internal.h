@@ -78,8 +78,9 @@ struct NormIn {
   uint32_t lds_offset = 0;  // filled by the launcher
 };
 
-// Kernel choices, read from the environment by rh_init (and
-// rh_reload_tuning) instead of on every launch. Every choice gives the same
+// Kernel choices, read from the environment by the first rh_init (and by
+// each rh_reload_tuning) instead of on every launch; each read publishes an
+// immutable snapshot, so a launch on another thread sees one whole snapshot. Every choice gives the same
 // bits; the switches exist to test and time one kernel against another.
 struct Tuning {
   // RUSTICIDE_HIP_GEMV: 0 the quantize-fused decode kernels (decode-sized
@@ -104,7 +105,8 @@ struct Tuning {
   bool attn_lds = true;    // RUSTICIDE_HIP_ATTN_LDS=0: the tiled attention step only
 };
 const Tuning& tuning();
-void load_tuning();
+void load_tuning();  // publish a fresh snapshot from the environment
+void init_tuning();  // load_tuning once per process
 
 // Launchers (stream-ordered; they return the launch status).
 hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, const Q8Dev& q,

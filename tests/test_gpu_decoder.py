@@ -499,3 +499,31 @@ def test_device_division_is_rounded_to_nearest(ctx):
     with np.errstate(all="ignore"):
         want = x / y
     _assert_same(_device_math(ctx, 2, x, y), want, x)
+
+
+@pytest.mark.parametrize("width,ffn", [(2048, 101), (256, 520)])
+def test_gate_up_pair_with_rows_that_end_mid_group(ctx, width, ffn):
+    # Q4_K gate/up whose row count is not a whole number of the regrouped
+    # copy's 16-block groups (2048 wide: 8 blocks a row, rows in pairs; 256
+    # wide: one block a row, rows in sixteens), with an F32 ffn_down so the
+    # decoder accepts any FFN width: the last workgroup's up rows start
+    # mid-group, and the one-token pair launch must still read the right
+    # blocks (feed_forward.rs:45-79 through the CPU path)
+    heads = width // 64
+    cfg = dict(SMALL, embedding_length=width, feed_forward_length=ffn, head_count=heads,
+               head_count_kv=heads // 2, block_count=1, context_length=64)
+    model = synth.decoder_model(cfg, seed=31)
+    rng = np.random.default_rng(32)
+    for b in model["blocks"]:
+        down = (0.05 * rng.standard_normal((width, ffn))).astype(np.float32)
+        b["ffn_down"] = (0, down.reshape(-1).view(np.uint8), width, ffn)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
+    tokens = rng.integers(0, cfg["vocab_size"], 9).astype(np.uint32)
+    for start, chunk in ((0, tokens[:5]), (5, tokens[5:6]), (6, tokens[6:7]), (7, tokens[7:9])):
+        g = gpu.forward_batch(chunk, start)
+        c = cpu.forward_batch(chunk, start)
+        assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
+    prompt = tokens[:6]
+    assert np.array_equal(gpu.generate_greedy(prompt, 12), cpu.generate_greedy(prompt, 12))
+    gpu.close()
+    cpu.close()

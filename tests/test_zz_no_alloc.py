@@ -67,7 +67,7 @@ def test_noalloc_equals_the_allocating_entry_point(ctx, first, second):
 
 
 def test_noalloc_refuses_batches_beyond_its_array(ctx):
-    # 4096 tokens of 2048 values need about 20 MB of quantized activations,
+    # 4096 tokens of 2048 values need 23,068,672 bytes of quantized activations,
     # more than the 4 MiB array: refused before any launch
     m = R.Matrix.load(ctx, R.Q4_K, synth.matrix(R.Q4_K, 16, 2048, seed=1), 16, 2048)
     x = H.DeviceArray(4096 * 2048)
