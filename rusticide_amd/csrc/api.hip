@@ -393,7 +393,7 @@ void load_tuning() {
   const int nt = env_int("RUSTICIDE_HIP_I2S_NT", 0);
   t.i2s_nt = nt == 256 || nt == 512 || nt == 1024 ? nt : 0;
   const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
-  t.gemm_bn = bn == 64 || bn == 128 || bn == 256 ? bn : 0;
+  t.gemm_bn = bn == 32 || bn == 64 || bn == 128 || bn == 256 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;
   t.attn_lds = env_int("RUSTICIDE_HIP_ATTN_LDS", 1) != 0;
   g_tuning.store(new Tuning(t), std::memory_order_release);

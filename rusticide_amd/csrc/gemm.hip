@@ -8,11 +8,12 @@
 //   Q6_K: isum = sum_s sc_s * sum_l (q-32)*a
 // and one float term per block, added in block order. Here the integers come
 // from int8 MFMA (v_mfma_i32_32x32x32_i8), exact in i32:
-//   * the sub-block scale is folded into the weight, w = sc*q (Q4_K: 0..945;
-//     Q6_K: sc*(q-32), -4096..4064), split into two int8 planes w = 128*hi +
-//     lo (lo in 0..127). Two accumulators take the hi and the lo plane side
-//     by side over the block's eight 32-deep steps (each activation fragment
-//     read from LDS once for both); isum = 128*hi + lo;
+//   * the sub-block scale is folded into the weight and the product split
+//     into two int8 planes: Q4_K w = sc*q with sc = 8*sh + sl, planes sh*q
+//     and sl*q (0..105), isum = 8*hi + lo; Q6_K w = sc*(q-32) = 128*hi + lo
+//     (lo in 0..127, hi in -32..31), isum = 128*hi + lo. Two accumulators
+//     take the planes side by side over the block's eight 32-deep steps, so
+//     each activation fragment is read from LDS once for both;
 //   * the Q4_K min term needs only the block sums: with bsum = 128*bh + bl
 //     (bl in 0..127), msum = 128 * sum_j m_j*bh_j + sum_j m_j*bl_j, two MFMAs
 //     whose 32-deep operands carry the eight (m_j, bl_j) / (m_j, bh_j) pairs
@@ -21,14 +22,8 @@
 // The float combine is the CPU path's, per block, in block order, one
 // accumulator per (row, token) in one lane.
 //
-// Tiles: a workgroup of 4 waves owns 64 rows x BN tokens; wave w computes rows
-// 32*(w&1).. and tokens (w>>1)*BN/2.. as BN/64 32x32 MFMA tiles. Per block:
-// weights are dequantized into LDS planes once per workgroup, the block's
-// activation tile and block-sum bytes are copied in, and the next block's raw
-// bytes are already in flight in registers while the MFMAs of this one run.
-//
 // Split K: when the row and token tiles give too few workgroups to fill the
-// chip (a 64-token prefill of a 2048-row matrix is 32 of them), blockIdx.z
+// chip (a 64-token prefill of a 2048-row matrix is 16 of them), blockIdx.z
 // takes a segment of seg_len blocks. Segment 0 forms the in-order sum over its
 // blocks as usual; every later segment stores each of its blocks' float terms,
 // and gemm_combine_kernel continues segment 0's sum with them in block order.
@@ -43,13 +38,10 @@ namespace rh {
 
 namespace {
 
-constexpr uint32_t kThreads = 256;
-constexpr uint32_t kBM = 64;        // rows per workgroup
 constexpr uint32_t kStride = 272;   // LDS bytes per 256-byte row: +16 spreads the banks
 
 typedef int32_t v4i __attribute__((ext_vector_type(4)));
 typedef int32_t v16i __attribute__((ext_vector_type(16)));
-typedef int16_t s16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t gemm_job(const GemvJobs& jobs, uint32_t wg) {
   uint32_t j = 0;
@@ -57,34 +49,6 @@ __device__ __forceinline__ uint32_t gemm_job(const GemvJobs& jobs, uint32_t wg) 
   for (uint32_t i = 1; i < static_cast<uint32_t>(kMaxJobs); i++)
     if (i < jobs.n && wg >= jobs.j[i].wg_begin) j = i;
   return j;
-}
-
-// Raw bytes one thread holds for one block of its row (thread = row*4 + p).
-// Q4_K: w[0] header (d, dmin, scales[12]), w[1..2] qs[32p..32p+32).
-// Q6_K: the GEMV kernels' lane windows for h = p>>1, gq = p&1: w[0] ql at
-// 64h+16gq, w[1] ql at 64h+32+16gq, w[2] qh at 32h+16gq, w[3] scales, w[4]
-// the fifth dwords of those windows and of the scales (holding d).
-struct WRaw {
-  u32x4 w[5];
-};
-
-template <int FMT>
-__device__ __forceinline__ void load_wraw(WRaw& x, const uint8_t* row, uint32_t b, uint32_t p) {
-  if (FMT == 12) {
-    const uint8_t* blk = row + static_cast<size_t>(b) * 144u;
-    x.w[0] = load16(blk);
-    x.w[1] = load16(blk + 16u + 32u * p);
-    x.w[2] = load16(blk + 32u + 32u * p);
-  } else {
-    const uint32_t h = p >> 1, gq = p & 1u;
-    const uint8_t* base = row + static_cast<size_t>(b) * 210u - 2u * (b & 1u);
-    x.w[0] = load16_a4(base + 64u * h + 16u * gq);
-    x.w[1] = load16_a4(base + 64u * h + 32u + 16u * gq);
-    x.w[2] = load16_a4(base + 128u + 32u * h + 16u * gq);
-    x.w[3] = load16_a4(base + 192u);
-    x.w[4] = u32x4{load4(base + 64u * h + 16u * gq + 16u), load4(base + 64u * h + 48u + 16u * gq),
-                   load4(base + 144u + 32u * h + 16u * gq), load4(base + 208u)};
-  }
 }
 
 // 6-bit scale and min of Q4_K sub-block j from the header dwords
@@ -100,92 +64,237 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& hd, uint32_t j, uint3
   }
 }
 
-// Four unsigned nibble bytes q (0..15) times sc (0..63) as the hi/lo planes:
-// the products are formed two at a time in 16-bit lanes (< 2^16, no carry).
-// Both factors are below 2^24, so the full-rate 24-bit multiply is exact.
-__device__ __forceinline__ void split4_u(uint32_t q, uint32_t sc, uint32_t& hi, uint32_t& lo) {
-  const uint32_t pe = __umul24(q & 0x00FF00FFu, sc);
-  const uint32_t po = __umul24((q >> 8) & 0x00FF00FFu, sc);
-  lo = (pe & 0x007F007Fu) | ((po & 0x007F007Fu) << 8);
-  hi = ((pe >> 7) & 0x00FF00FFu) | (((po >> 7) & 0x00FF00FFu) << 8);
-}
-
-// Four six-bit bytes q (0..63) as sc * (q - 32) (sc signed) in hi/lo planes:
-// w = 128*hi + lo, lo in 0..127, hi in -32..31 (two's complement bytes). The
-// products are formed two at a time in signed 16-bit lanes (|w| <= 4096).
-__device__ __forceinline__ void split4_s(uint32_t q, int32_t sc, uint32_t& hi, uint32_t& lo) {
-  const s16x2 scv{static_cast<int16_t>(sc), static_cast<int16_t>(sc)};
-  const s16x2 off{static_cast<int16_t>(-32 * sc), static_cast<int16_t>(-32 * sc)};
-  const uint32_t qe = q & 0x00FF00FFu, qo = (q >> 8) & 0x00FF00FFu;
-  const s16x2 we = __builtin_bit_cast(s16x2, qe) * scv + off;
-  const s16x2 wo = __builtin_bit_cast(s16x2, qo) * scv + off;
-  const uint32_t ue = __builtin_bit_cast(uint32_t, we), uo = __builtin_bit_cast(uint32_t, wo);
-  lo = (ue & 0x007F007Fu) | ((uo & 0x007F007Fu) << 8);
-  const s16x2 he = we >> static_cast<int16_t>(7), ho = wo >> static_cast<int16_t>(7);
-  hi = (__builtin_bit_cast(uint32_t, he) & 0x00FF00FFu) | ((__builtin_bit_cast(uint32_t, ho) & 0x00FF00FFu) << 8);
-}
-
-// LDS: hi [64][272] | lo [64][272] | act [BN][272] | mins [64][8] u8 |
-//      bsb [BN][16] (bl_0..7, bh_0..7) | rowd [64] float2 (d, dmin) | d8 [BN]
 // Terms of a split launch: plane 0 holds segment 0's sums, plane 1 + b -
 // seg_len the term of block b >= seg_len; each plane is [rows_pad][tokens]
-// over the launch's 64-row tiles.
+// over the launch's row tiles.
 struct SplitTerms {
   float* terms;       // nullptr: no split
   uint32_t seg_len;   // blocks per segment
-  uint32_t rows_pad;  // 64 x the launch's workgroups along rows
+  uint32_t rows_pad;  // kRowsWG x the launch's workgroups along rows
 };
 
-template <int FMT, int BN, bool SPLIT>
-__global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, size_t tokens, SplitTerms split) {
+// ------------------------------------------------------------ row-owning form
+// A workgroup of 4 waves owns kRowsWG = 128 rows x 32*NT tokens; wave w owns
+// rows 32w.. of the tile outright. Each lane loads the raw bytes of its own
+// row's block (lane = row + 32*g, g the lane's 16-deep half of every 32-deep
+// step) and dequantizes them straight into the MFMA A operand: no weight
+// plane passes through LDS and no two waves dequantize the same row. Only
+// the activation tile (the B operand, shared by the four waves) is staged in
+// LDS, double-buffered: block b+1's bytes are loaded into registers while
+// block b's MFMAs run and stored into the other buffer after them, one
+// barrier a block.
+//
+// Planes: Q4_K's w = sc*q is split along the scale, sc = 8*sh + sl (sh, sl
+// in 0..7), so each plane byte sh*q or sl*q (at most 105) is one packed
+// 16-bit multiply of four nibbles; isum = 8*hi + lo. Q6_K keeps w = sc*(q-32)
+// = 128*hi + lo. Both sums are exact in i32.
+//
+// Matrices with a regrouped copy (UNITS; launch_kq_units) are read from it:
+// the lane's pieces of a block sit at fixed 16-byte-aligned offsets of its
+// group of 16 blocks.
+constexpr uint32_t kRowsWG = 128;
+
+int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    cus = (hipGetDevice(&dev) == hipSuccess &&
+           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+              ? n
+              : 256;
+  }
+  return cus;
+}
+
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {
+  return __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, a) * __builtin_bit_cast(u16x2, b));
+}
+
+// The raw bytes one lane holds for one block of its row.
+// Q4_K: hd = d, dmin, scales[12]; qs[p] = qs[32p + 16g .. +16].
+// Q6_K: ql0[h] = ql[64h + 16g ..], ql1[h] = ql[64h + 32 + 16g ..],
+//       qh[h] = qh[32h + 16g ..], sc = scales[16], d in the low half of dw.
+template <int FMT>
+struct LaneRaw;
+template <>
+struct LaneRaw<12> {
+  u32x4 hd, qs[4];
+};
+template <>
+struct LaneRaw<14> {
+  u32x4 ql0[2], ql1[2], qh[2], sc;
+  uint32_t dw;
+};
+
+template <bool UNITS>
+__device__ __forceinline__ void load_lane_raw(LaneRaw<12>& x, const GemvJob& J, uint32_t row, uint32_t b,
+                                              uint32_t g) {
+  if (UNITS) {
+    const uint32_t e = row * J.nb + b, tw = e & 15u;
+    const uint8_t* u = J.wu + static_cast<size_t>(e >> 4) * 2304u;
+    x.hd = load16(u + 16u * tw);
+    x.qs[0] = load16(u + 256u + 64u * tw + 16u * g);
+    x.qs[1] = load16(u + 256u + 64u * tw + 32u + 16u * g);
+    x.qs[2] = load16(u + 1280u + 64u * tw + 16u * g);
+    x.qs[3] = load16(u + 1280u + 64u * tw + 32u + 16u * g);
+  } else {
+    const uint8_t* blk = J.w + static_cast<size_t>(row) * J.stride + b * 144u;
+    x.hd = load16(blk);
+#pragma unroll
+    for (uint32_t p = 0; p < 4u; p++) x.qs[p] = load16(blk + 16u + 32u * p + 16u * g);
+  }
+}
+
+template <bool UNITS>
+__device__ __forceinline__ void load_lane_raw(LaneRaw<14>& x, const GemvJob& J, uint32_t row, uint32_t b,
+                                              uint32_t g) {
+  if (UNITS) {
+    const uint32_t e = row * J.nb + b, tw = e & 15u;
+    const uint8_t* u = J.wu + static_cast<size_t>(e >> 4) * 3360u;
+#pragma unroll
+    for (uint32_t h = 0; h < 2u; h++) {
+      x.ql0[h] = load16(u + 64u * tw + 16u * (2u * h + g));
+      x.ql1[h] = load16(u + 1024u + 64u * tw + 16u * (2u * h + g));
+      x.qh[h] = load16(u + 2048u + 64u * tw + 16u * (2u * h + g));
+    }
+    x.sc = load16(u + 3072u + 16u * tw);
+    x.dw = *reinterpret_cast<const uint16_t*>(u + 3328u + 2u * tw);
+  } else {
+    // a 210-byte block starts 2-byte aligned: unaligned 16-byte loads, each
+    // inside the block
+    const uint8_t* blk = J.w + static_cast<size_t>(row) * J.stride + b * 210u;
+#pragma unroll
+    for (uint32_t h = 0; h < 2u; h++) {
+      x.ql0[h] = load16_any(blk + 64u * h + 16u * g);
+      x.ql1[h] = load16_any(blk + 64u * h + 32u + 16u * g);
+      x.qh[h] = load16_any(blk + 128u + 32u * h + 16u * g);
+    }
+    x.sc = load16_any(blk + 192u);
+    x.dw = *reinterpret_cast<const uint16_t*>(blk + 208u);
+  }
+}
+
+// The two A planes of 32-deep step kk for this lane (its row, k = 32kk + 16g ..).
+__device__ __forceinline__ void lane_planes(const LaneRaw<12>& x, uint32_t kk, uint32_t, v4i& hi, v4i& lo) {
+  uint32_t sc, m;
+  q4k_scale_min(x.hd, kk, sc, m);
+  const uint32_t sh = (sc >> 3) * 0x00010001u, sl = (sc & 7u) * 0x00010001u;
+  const u32x4 c = x.qs[kk >> 1];
+  const uint32_t s4 = 4u * (kk & 1u);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t nib = (c[i] >> s4) & 0x0F0F0F0Fu;
+    hi[i] = static_cast<int32_t>(pk_mul_u16(nib, sh));
+    lo[i] = static_cast<int32_t>(pk_mul_u16(nib, sl));
+  }
+}
+
+// Q6_K: four 6-bit bytes q as w = sc * (q - 32) in hi/lo planes (w = 128*hi
+// + lo, lo in 0..127). The bytes are spread into 16-bit lanes and multiplied
+// with one packed multiply-add each ((q - 32)*sc fits i16: |w| <= 4096),
+// then the planes' bytes are gathered back with v_perm_b32.
+__device__ __forceinline__ void q6_split(uint32_t q, int32_t sc, uint32_t& hi, uint32_t& lo) {
+  typedef int16_t i16x2 __attribute__((ext_vector_type(2)));
+  const i16x2 scv{static_cast<int16_t>(sc), static_cast<int16_t>(sc)};
+  const i16x2 off{static_cast<int16_t>(-32 * sc), static_cast<int16_t>(-32 * sc)};
+  // bytes 0,2 -> lanes of qe; bytes 1,3 -> lanes of qo (zero high bytes)
+  const uint32_t qe = __builtin_amdgcn_perm(0u, q, 0x0c020c00u);
+  const uint32_t qo = __builtin_amdgcn_perm(0u, q, 0x0c030c01u);
+  const i16x2 we = __builtin_bit_cast(i16x2, qe) * scv + off;
+  const i16x2 wo = __builtin_bit_cast(i16x2, qo) * scv + off;
+  const uint32_t ue = __builtin_bit_cast(uint32_t, we), uo = __builtin_bit_cast(uint32_t, wo);
+  // bytes (we.lo, wo.lo, we.hi, wo.hi) -> low byte of each 16-bit product
+  lo = __builtin_amdgcn_perm(uo, ue, 0x06020400u) & 0x7F7F7F7Fu;
+  const i16x2 he = we >> static_cast<int16_t>(7), ho = wo >> static_cast<int16_t>(7);
+  hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, ho), __builtin_bit_cast(uint32_t, he), 0x06020400u);
+}
+
+__device__ __forceinline__ void lane_planes(const LaneRaw<14>& x, uint32_t kk, uint32_t g, v4i& hi, v4i& lo) {
+  // k = 128h + 32r + l (q6_k.rs:13-43): ql[64h + 32(r&1) + l] (high nibble
+  // for r >= 2), qh[32h + l] bits 2r..2r+1, scale 8h + 2r + l/16
+  const uint32_t h = kk >> 2, r = kk & 3u;
+  const u32x4 ql = (r & 1u) ? x.ql1[h] : x.ql0[h];
+  const u32x4 qh = x.qh[h];
+  const uint32_t s = 8u * h + 2u * r + g;
+  const int32_t sc = __builtin_amdgcn_sbfe(static_cast<int32_t>(x.sc[s >> 2]), 8u * (s & 3u), 8);
+  const uint32_t nsh = 4u * (r >> 1);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t qv = ((ql[i] >> nsh) & 0x0F0F0F0Fu) | (((qh[i] >> (2u * r)) << 4) & 0x30303030u);
+    uint32_t hw, lw;
+    q6_split(qv, sc, hw, lw);
+    hi[i] = static_cast<int32_t>(hw);
+    lo[i] = static_cast<int32_t>(lw);
+  }
+}
+
+// Q4_K's mins as the msum MFMA's A operand (k = j in lane group 0): with
+// the activation's block sums as B (bsum_j = 128*bh_j + bl_j, bl_j in
+// 0..127), msum = 128 * sum_j m_j*bh_j + sum_j m_j*bl_j from two MFMAs.
+__device__ __forceinline__ v4i lane_mins(const LaneRaw<12>& x, uint32_t g) {
+  uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+  for (uint32_t j = 0; j < 8u; j++) {
+    uint32_t sc, m;
+    q4k_scale_min(x.hd, j, sc, m);
+    if (j < 4u) w0 |= m << (8u * j);
+    else w1 |= m << (8u * (j - 4u));
+  }
+  return v4i{g == 0 ? static_cast<int32_t>(w0) : 0, g == 0 ? static_cast<int32_t>(w1) : 0, 0, 0};
+}
+
+__device__ __forceinline__ float2 lane_d(const LaneRaw<12>& x) { return make_float2(f16_lo(x.hd.x), f16_hi(x.hd.x)); }
+__device__ __forceinline__ float2 lane_d(const LaneRaw<14>& x) { return make_float2(f16_lo(x.dw), 0.0f); }
+
+template <int NT>
+constexpr size_t rows_kernel_lds() {
+  // act [2][32NT][kStride] | d8 [2][32NT] | bs [2][32NT][16] | rowd [4][32]
+  return 2u * 32u * NT * kStride + 2u * 32u * NT * 4u + 2u * 32u * NT * 16u + 4u * 32u * 8u;
+}
+
+template <int FMT, int NT, bool UNITS, bool SPLIT>
+__global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev q, size_t tokens,
+                                                           SplitTerms split) {
+  constexpr uint32_t BN = 32u * NT;
   extern __shared__ __align__(16) uint8_t lds[];
-  int8_t* hiT = reinterpret_cast<int8_t*>(lds);
-  int8_t* loT = hiT + kBM * kStride;
-  int8_t* actT = loT + kBM * kStride;
-  uint8_t* minsT = reinterpret_cast<uint8_t*>(actT + BN * kStride);
-  uint8_t* bsT = minsT + kBM * 8u;
-  float2* rowd = reinterpret_cast<float2*>(bsT + BN * 16u);
-  float* d8T = reinterpret_cast<float*>(rowd + kBM);
+  int8_t* actT = reinterpret_cast<int8_t*>(lds);                          // [2][BN][kStride]
+  float* d8T = reinterpret_cast<float*>(lds + 2u * BN * kStride);         // [2][BN]
+  uint8_t* bsT = reinterpret_cast<uint8_t*>(d8T + 2u * BN);               // [2][BN][16]
+  float2* rowdT = reinterpret_cast<float2*>(bsT + 2u * BN * 16u);         // [4][32]
 
   const GemvJob& J = jobs.j[gemm_job(jobs, blockIdx.x)];
-  const uint32_t row0 = (blockIdx.x - J.wg_begin) * kBM;
+  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6, g = lane >> 5, ml = lane & 31u;
+  const uint32_t row0 = (blockIdx.x - J.wg_begin) * kRowsWG;
+  const uint32_t arow = min(row0 + 32u * wave + ml, J.rows - 1u);
   const uint32_t tok0 = blockIdx.y * BN;
   const uint32_t nb = J.nb;
   const uint32_t seg = SPLIT ? blockIdx.z : 0u;
   const uint32_t b_begin = SPLIT ? seg * split.seg_len : 0u;
   const uint32_t b_end = SPLIT ? min(nb, b_begin + split.seg_len) : nb;
   const bool store_terms = SPLIT && seg > 0u;
-  const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-  const uint32_t wm = wave & 1u, wn = wave >> 1;
-  constexpr int NT = BN / 64;  // 32x32 tiles per wave along tokens
-
-  // staging roles: one row quarter per thread for the weights, 16-byte
-  // chunks of the activation tile, one token's block sums for tid < BN
-  const uint32_t sr = tid >> 2, sp = tid & 3u;
-  const uint32_t srow = min(row0 + sr, J.rows - 1u);
-  const uint8_t* wrow = J.w + __umul24(srow, static_cast<uint32_t>(J.stride));
-  constexpr int ACH = BN * 16 / 256;  // activation chunks per thread
   const size_t T = tokens;
-  // the launch keeps tokens * qstride below 2^32 and both below 2^24: the
-  // activation offsets are exact 32-bit values from 24-bit multiplies
   const uint32_t last = static_cast<uint32_t>(T - 1);
   const uint32_t qs32 = static_cast<uint32_t>(q.qstride), bs32 = static_cast<uint32_t>(q.bstride);
-  const uint32_t stok = min(tok0 + (tid & (BN - 1)), last);
+  // staging: BN*256 activation bytes in 16-byte chunks over 256 threads; the
+  // first BN threads also take one token's d8 (and Q4_K block sums)
+  constexpr int ACH = static_cast<int>(BN) * 16 / 256;
+  const uint32_t stok = min(tok0 + (tid & (BN - 1u)), last);
 
-  WRaw wr;
+  LaneRaw<FMT> raw, nxt;
   u32x4 ar[ACH];
   u32x4 sr0{}, sr1{};
   float d8r = 0.0f;
-  auto prefetch = [&](uint32_t b) {
-    load_wraw<FMT>(wr, wrow, b, sp);
+  auto load_act = [&](uint32_t b) {
 #pragma unroll
     for (int c = 0; c < ACH; c++) {
-      const uint32_t chunk = tid + static_cast<uint32_t>(c) * kThreads;
-      const uint32_t n = chunk >> 4, k = (chunk & 15u) * 16u;
-      const uint32_t tok = min(tok0 + n, last);
-      ar[c] = load16(reinterpret_cast<const uint8_t*>(q.quants + (__umul24(tok, qs32) + b * 256u + k)));
+      const uint32_t chunk = tid + static_cast<uint32_t>(c) * 256u;
+      const uint32_t tok = min(tok0 + (chunk >> 4), last);
+      ar[c] = load16(reinterpret_cast<const uint8_t*>(q.quants + (__umul24(tok, qs32) + b * 256u +
+                                                                  (chunk & 15u) * 16u)));
     }
-    if (tid < static_cast<uint32_t>(BN)) {
+    if (tid < BN) {
       const uint32_t o = __umul24(stok, bs32) + b * 8u;
       d8r = q.scales[o];
       if (FMT == 12) {
@@ -194,44 +303,17 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
       }
     }
   };
-
-  v16i acc_i[NT], acc_m[NT];
-  float y[NT][16];
+  auto store_act = [&](uint32_t buf) {
+    int8_t* a = actT + buf * BN * kStride;
 #pragma unroll
-  for (int t = 0; t < NT; t++)
-#pragma unroll
-    for (int i = 0; i < 16; i++) y[t][i] = -0.0f;
-
-  if (b_begin < b_end) prefetch(b_begin);
-  for (uint32_t b = b_begin; b < b_end; b++) {
-    // raw bytes -> LDS planes
-    if (FMT == 12) {
-      const u32x4 hd = wr.w[0];
-      uint32_t sc0, m0, sc1, m1;
-      q4k_scale_min(hd, 2u * sp, sc0, m0);
-      q4k_scale_min(hd, 2u * sp + 1u, sc1, m1);
-      // qs[32p + l]: low nibble -> k = 64p + l (sub-block 2p), high -> 64p + 32 + l
-      uint32_t h0[8], l0[8], h1[8], l1[8];
-#pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const uint32_t v = wr.w[1 + (i >> 2)][i & 3];
-        split4_u(v & 0x0F0F0F0Fu, sc0, h0[i], l0[i]);
-        split4_u((v >> 4) & 0x0F0F0F0Fu, sc1, h1[i], l1[i]);
-      }
-      int8_t* hrow = hiT + sr * kStride + 64u * sp;
-      int8_t* lrow = loT + sr * kStride + 64u * sp;
-#pragma unroll
-      for (int i = 0; i < 8; i += 4) {
-        *reinterpret_cast<u32x4*>(hrow + 4 * i) = u32x4{h0[i], h0[i + 1], h0[i + 2], h0[i + 3]};
-        *reinterpret_cast<u32x4*>(lrow + 4 * i) = u32x4{l0[i], l0[i + 1], l0[i + 2], l0[i + 3]};
-        *reinterpret_cast<u32x4*>(hrow + 32 + 4 * i) = u32x4{h1[i], h1[i + 1], h1[i + 2], h1[i + 3]};
-        *reinterpret_cast<u32x4*>(lrow + 32 + 4 * i) = u32x4{l1[i], l1[i + 1], l1[i + 2], l1[i + 3]};
-      }
-      minsT[sr * 8u + 2u * sp] = static_cast<uint8_t>(m0);
-      minsT[sr * 8u + 2u * sp + 1u] = static_cast<uint8_t>(m1);
-      if (sp == 0) rowd[sr] = make_float2(f16_lo(hd.x), f16_hi(hd.x));
-      if (tid < static_cast<uint32_t>(BN)) {
-        // bsum_j = 128*bh_j + bl_j, bl_j in 0..127 (|bsum_j| <= 32*127)
+    for (int c = 0; c < ACH; c++) {
+      const uint32_t chunk = tid + static_cast<uint32_t>(c) * 256u;
+      *reinterpret_cast<u32x4*>(a + (chunk >> 4) * kStride + (chunk & 15u) * 16u) = ar[c];
+    }
+    if (tid < BN) {
+      d8T[buf * BN + tid] = d8r;
+      if (FMT == 12) {
+        // bsum_j = 128*bh_j + bl_j, bl_j in 0..127 (|bsum_j| <= 32*128)
         const int32_t s8[8] = {static_cast<int32_t>(sr0.x), static_cast<int32_t>(sr0.y),
                                static_cast<int32_t>(sr0.z), static_cast<int32_t>(sr0.w),
                                static_cast<int32_t>(sr1.x), static_cast<int32_t>(sr1.y),
@@ -242,146 +324,107 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
           bl[j >> 2] |= (static_cast<uint32_t>(s8[j]) & 0x7fu) << (8 * (j & 3));
           bh[j >> 2] |= (static_cast<uint32_t>(s8[j] >> 7) & 0xffu) << (8 * (j & 3));
         }
-        *reinterpret_cast<u32x4*>(bsT + tid * 16u) = u32x4{bl[0], bl[1], bh[0], bh[1]};
+        *reinterpret_cast<u32x4*>(bsT + (buf * BN + tid) * 16u) = u32x4{bl[0], bl[1], bh[0], bh[1]};
       }
-    } else {
-      const uint32_t h = sp >> 1, gq = sp & 1u;
-      const uint32_t sh = 2u * (b & 1u);
-      const u32x4 A = wr.w[0], B = wr.w[1], C = wr.w[2], W = wr.w[3], E = wr.w[4];
-      const u32x4 a{__builtin_amdgcn_alignbyte(A.y, A.x, sh), __builtin_amdgcn_alignbyte(A.z, A.y, sh),
-                    __builtin_amdgcn_alignbyte(A.w, A.z, sh), __builtin_amdgcn_alignbyte(E.x, A.w, sh)};
-      const u32x4 bq{__builtin_amdgcn_alignbyte(B.y, B.x, sh), __builtin_amdgcn_alignbyte(B.z, B.y, sh),
-                     __builtin_amdgcn_alignbyte(B.w, B.z, sh), __builtin_amdgcn_alignbyte(E.y, B.w, sh)};
-      const u32x4 c{__builtin_amdgcn_alignbyte(C.y, C.x, sh), __builtin_amdgcn_alignbyte(C.z, C.y, sh),
-                    __builtin_amdgcn_alignbyte(C.w, C.z, sh), __builtin_amdgcn_alignbyte(E.z, C.w, sh)};
-      const uint32_t X0 = __builtin_amdgcn_alignbyte(W.y, W.x, sh);
-      const uint32_t X1 = __builtin_amdgcn_alignbyte(W.z, W.y, sh);
-      const uint32_t X2 = __builtin_amdgcn_alignbyte(W.w, W.z, sh);
-      const uint32_t X3 = __builtin_amdgcn_alignbyte(E.w, W.w, sh);
-      const uint32_t slo = h ? X2 : X0, shi = h ? X3 : X1;
-      // run r, 16-group gq: scales[8h + 2r + gq] (int_dot.rs:199)
-      int32_t scr[4];
-      scr[0] = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq, 8);
-      scr[1] = __builtin_amdgcn_sbfe(static_cast<int32_t>(slo), 8u * gq + 16u, 8);
-      scr[2] = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq, 8);
-      scr[3] = __builtin_amdgcn_sbfe(static_cast<int32_t>(shi), 8u * gq + 16u, 8);
-      // element 128h + 32r + 16gq + l holds run r's value l (q6_k.rs:13-43)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        uint32_t hw[4], lw[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const uint32_t qv = r == 0 ? (a[k] & 0x0F0F0F0Fu) | ((c[k] << 4) & 0x30303030u)
-                            : r == 1 ? (bq[k] & 0x0F0F0F0Fu) | ((c[k] << 2) & 0x30303030u)
-                            : r == 2 ? ((a[k] >> 4) & 0x0F0F0F0Fu) | (c[k] & 0x30303030u)
-                                     : ((bq[k] >> 4) & 0x0F0F0F0Fu) | ((c[k] >> 2) & 0x30303030u);
-          split4_s(qv, scr[r], hw[k], lw[k]);
-        }
-        const uint32_t k0 = 128u * h + 32u * static_cast<uint32_t>(r) + 16u * gq;
-        *reinterpret_cast<u32x4*>(hiT + sr * kStride + k0) = u32x4{hw[0], hw[1], hw[2], hw[3]};
-        *reinterpret_cast<u32x4*>(loT + sr * kStride + k0) = u32x4{lw[0], lw[1], lw[2], lw[3]};
-      }
-      if (sp == 0) rowd[sr] = make_float2(f16_lo(E.w >> (8u * sh)), 0.0f);
     }
-#pragma unroll
-    for (int cch = 0; cch < ACH; cch++) {
-      const uint32_t chunk = tid + static_cast<uint32_t>(cch) * kThreads;
-      *reinterpret_cast<u32x4*>(actT + (chunk >> 4) * kStride + (chunk & 15u) * 16u) = ar[cch];
-    }
-    if (tid < static_cast<uint32_t>(BN)) d8T[tid] = d8r;
-    __syncthreads();
-    if (b + 1u < b_end) prefetch(b + 1u);
+  };
 
-    const uint32_t arow = 32u * wm + (lane & 31u);
-    const uint32_t g = lane >> 5;  // the lane's 16-byte k group of a 32-deep step
-    uint32_t bcol[NT];
+  float y[NT][16];
 #pragma unroll
-    for (int t = 0; t < NT; t++) bcol[t] = static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
+  for (int t = 0; t < NT; t++)
 #pragma unroll
-    for (int t = 0; t < NT; t++) acc_i[t] = v16i{};
-    v16i acc_l[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc_l[t] = v16i{};
-    // hi and lo planes side by side per 32-deep step: each activation
-    // fragment is read from LDS once
+    for (int i = 0; i < 16; i++) y[t][i] = -0.0f;
+
+  if (b_begin < b_end) {
+    load_lane_raw<UNITS>(raw, J, arow, b_begin, g);
+    load_act(b_begin);
+    store_act(0u);
+    __syncthreads();
+  }
+  for (uint32_t b = b_begin; b < b_end; b++) {
+    const uint32_t cur = (b - b_begin) & 1u;
+    const bool more = b + 1u < b_end;
+    if (more) {
+      // the next block's weights go out a whole block ahead: each lane's
+      // 16-byte pieces come from 32 different rows, a long round trip
+      load_lane_raw<UNITS>(nxt, J, arow, b + 1u, g);
+      load_act(b + 1u);
+    }
+    // this block's (d, dmin) of the wave's rows, for the D layout's rows
+    if (g == 0) rowdT[wave * 32u + ml] = lane_d(raw);
+    const int8_t* a = actT + cur * BN * kStride;
+    v16i acc_h[NT], acc_l[NT];
 #pragma unroll
     for (uint32_t kk = 0; kk < 8u; kk++) {
-      const uint32_t ko = 32u * kk + 16u * g;
-      const v4i Ah = *reinterpret_cast<const v4i*>(hiT + arow * kStride + ko);
-      const v4i Al = *reinterpret_cast<const v4i*>(loT + arow * kStride + ko);
+      v4i Ah, Al;
+      lane_planes(raw, kk, g, Ah, Al);
 #pragma unroll
       for (int t = 0; t < NT; t++) {
-        const v4i Bv = *reinterpret_cast<const v4i*>(actT + bcol[t] * kStride + ko);
-        acc_i[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah, Bv, acc_i[t], 0, 0, 0);
-        acc_l[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al, Bv, acc_l[t], 0, 0, 0);
+        const v4i Bv = *reinterpret_cast<const v4i*>(a + (32u * t + ml) * kStride + 32u * kk + 16u * g);
+        acc_h[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Ah, Bv, kk ? acc_h[t] : v16i{}, 0, 0, 0);
+        acc_l[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Al, Bv, kk ? acc_l[t] : v16i{}, 0, 0, 0);
       }
     }
-    if (FMT == 12) {
-      // msum: (m_j, bh_j) then x128, then (m_j, bl_j), in lane group 0
-      const uint32_t mw0 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u) : 0u;
-      const uint32_t mw1 = g == 0 ? *reinterpret_cast<const uint32_t*>(minsT + arow * 8u + 4u) : 0u;
-      const v4i Am{static_cast<int32_t>(mw0), static_cast<int32_t>(mw1), 0, 0};
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const u32x4 bs = *reinterpret_cast<const u32x4*>(bsT + bcol[t] * 16u);
-        const v4i Bh{g == 0 ? static_cast<int32_t>(bs.z) : 0, g == 0 ? static_cast<int32_t>(bs.w) : 0, 0, 0};
-        acc_m[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bh, v16i{}, 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 16; i++) acc_m[t][i] <<= 7;
-        const v4i Bl{g == 0 ? static_cast<int32_t>(bs.x) : 0, g == 0 ? static_cast<int32_t>(bs.y) : 0, 0, 0};
-        acc_m[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bl, acc_m[t], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++)
-#pragma unroll
-      for (int i = 0; i < 16; i++) acc_i[t][i] = (acc_i[t][i] << 7) + acc_l[t][i];
-    // the block's float term per (row, token), added in block order
-    // (D layout: lane n + 32*((m/4)%2), register 4*(m/8) + m%4)
-    float d8n[NT];
-#pragma unroll
-    for (int t = 0; t < NT; t++) d8n[t] = d8T[bcol[t]];
+    v4i Am{};
+    if constexpr (FMT == 12) Am = lane_mins(raw, g);
     float* plane = store_terms ? split.terms + static_cast<size_t>(1u + b - split.seg_len) * split.rows_pad * T
                                : nullptr;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const uint32_t m = 32u * wm + 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
-      const float2 dd = rowd[m];
+    for (int t = 0; t < NT; t++) {
+      const uint32_t tl = 32u * t + ml;  // the lane's token column of this tile
+      const float d8 = d8T[cur * BN + tl];
+      v16i acc_m{};
+      if constexpr (FMT == 12) {
+        const u32x4 bs = *reinterpret_cast<const u32x4*>(bsT + (cur * BN + tl) * 16u);
+        const v4i Bh{g == 0 ? static_cast<int32_t>(bs.z) : 0, g == 0 ? static_cast<int32_t>(bs.w) : 0, 0, 0};
+        const v4i Bl{g == 0 ? static_cast<int32_t>(bs.x) : 0, g == 0 ? static_cast<int32_t>(bs.y) : 0, 0, 0};
+        acc_m = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bh, v16i{}, 0, 0, 0);
 #pragma unroll
-      for (int t = 0; t < NT; t++) {
+        for (int i = 0; i < 16; i++) acc_m[i] <<= 7;
+        acc_m = __builtin_amdgcn_mfma_i32_32x32x32_i8(Am, Bl, acc_m, 0, 0, 0);
+      }
+      // the block's float term per (row, token), added in block order
+      // (D layout: lane n + 32*((m/4)%2), register 4*(m/8) + m%4)
+#pragma unroll
+      for (int i = 0; i < 16; i++) {
+        const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
+        const float2 dd = rowdT[wave * 32u + m];
+        const int32_t isum = FMT == 12 ? (acc_h[t][i] << 3) + acc_l[t][i] : (acc_h[t][i] << 7) + acc_l[t][i];
         float term;
-        if (FMT == 12) {
+        if constexpr (FMT == 12) {
           // int_dot.rs:169: d8 * d.mul_add(isum, -(dmin * msum))
-          const float neg = -(dd.y * static_cast<float>(acc_m[t][i]));
-          term = d8n[t] * __builtin_fmaf(dd.x, static_cast<float>(acc_i[t][i]), neg);
+          const float neg = -(dd.y * static_cast<float>(acc_m[i]));
+          term = d8 * __builtin_fmaf(dd.x, static_cast<float>(isum), neg);
         } else {
           // int_dot.rs:203: (d * d8) * isum
-          const float s = dd.x * d8n[t];
-          term = s * static_cast<float>(acc_i[t][i]);
+          const float sd = dd.x * d8;
+          term = sd * static_cast<float>(isum);
         }
         if (store_terms) {
-          const size_t tok = tok0 + static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
-          if (tok < T) plane[static_cast<size_t>(blockIdx.x * kBM + m) * T + tok] = term;
+          const size_t tok = tok0 + tl;
+          if (tok < T) plane[static_cast<size_t>(blockIdx.x * kRowsWG + 32u * wave + m) * T + tok] = term;
         } else {
           y[t][i] += term;
         }
       }
     }
+    if (more) {
+      store_act(cur ^ 1u);
+      raw = nxt;
+    }
     __syncthreads();
   }
   if (store_terms) return;
-
-  const uint32_t g = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 16; i++) {
-    const uint32_t m = 32u * wm + 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
-    const uint32_t row = row0 + m;
+    const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
+    const uint32_t row = row0 + 32u * wave + m;
     if (row >= J.rows) continue;
 #pragma unroll
     for (int t = 0; t < NT; t++) {
-      const size_t tok = tok0 + static_cast<uint32_t>(BN / 2) * wn + 32u * static_cast<uint32_t>(t) + (lane & 31u);
+      const size_t tok = tok0 + 32u * t + ml;
       if (SPLIT) {  // segment 0 of a split launch: plane 0
-        if (tok < T) split.terms[static_cast<size_t>(blockIdx.x * kBM + m) * T + tok] = y[t][i];
+        if (tok < T) split.terms[static_cast<size_t>(blockIdx.x * kRowsWG + 32u * wave + m) * T + tok] = y[t][i];
         continue;
       }
       const size_t idx = static_cast<size_t>(row) * T + tok;
@@ -396,7 +439,8 @@ __global__ __launch_bounds__(256) void gemm_kq_kernel(GemvJobs jobs, Q8Dev q, si
 // multiple of 64 of them) and keeps eight planes of loads in flight; the
 // additions stay one plane at a time, in block order.
 __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const float* __restrict__ terms,
-                                                           uint32_t planes, uint32_t rows_pad, size_t tokens) {
+                                                           uint32_t planes, uint32_t rows_pad, size_t tokens,
+                                                           uint32_t bm) {
   const size_t n = static_cast<size_t>(rows_pad) * tokens;
   const size_t idx = (static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x) * 4u;
   if (idx >= n) return;
@@ -414,25 +458,20 @@ __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const 
   for (int e = 0; e < 4; e++) {
     const uint32_t grow = static_cast<uint32_t>((idx + e) / tokens);
     const size_t tok = idx + e - static_cast<size_t>(grow) * tokens;
-    const GemvJob& J = jobs.j[gemm_job(jobs, grow / kBM)];
-    const uint32_t row = grow - J.wg_begin * kBM;
+    const GemvJob& J = jobs.j[gemm_job(jobs, grow / bm)];
+    const uint32_t row = grow - J.wg_begin * bm;
     const size_t o = static_cast<size_t>(row) * tokens + tok;
     if (row < J.rows && o < J.out_len) J.out[o] = y[e];
   }
 }
 
-int token_tile(size_t tokens) {
-  // Tuning::gemm_bn forces the token tile (64 or 128 here), for tuning
-  if (const int bn = tuning().gemm_bn) return bn == 256 ? 128 : bn;
-  return tokens >= 512 ? 128 : 64;
-}
-
-// Workgroups along rows, with each job's first one recorded in wg_begin.
-uint32_t row_tiles(GemvJobs& jobs) {
+// Workgroups along rows (tiles of bm rows), with each job's first one
+// recorded in wg_begin.
+uint32_t row_tiles(GemvJobs& jobs, uint32_t bm) {
   uint32_t wgs = 0;
   for (uint32_t i = 0; i < jobs.n; i++) {
     jobs.j[i].wg_begin = wgs;
-    wgs += (jobs.j[i].rows + kBM - 1u) / kBM;
+    wgs += (jobs.j[i].rows + bm - 1u) / bm;
   }
   return wgs;
 }
@@ -441,53 +480,96 @@ struct SplitPlan {
   uint32_t segs = 1, seg_len = 0, planes = 0, rows_pad = 0;
 };
 
-// Splits K when the launch has fewer than kSplitBelow workgroups, aiming at
+// Splits K when the launch has fewer than `below` workgroups, aiming at
 // kSplitTarget; every job must have the same block count. Below 2 blocks, or
 // with Tuning::gemm_split off, nothing is split.
-constexpr uint32_t kSplitBelow = 128, kSplitTarget = 512;
+constexpr uint32_t kSplitTarget = 512;
 
-SplitPlan plan_split(GemvJobs jobs, size_t tokens) {
+SplitPlan plan_split(GemvJobs jobs, size_t tokens, uint32_t bm, uint32_t bn, uint32_t below) {
   SplitPlan p;
-  const uint32_t wgs = row_tiles(jobs);
+  const uint32_t wgs = row_tiles(jobs, bm);
   if (wgs == 0 || jobs.n == 0) return p;
   const uint32_t nb = jobs.j[0].nb;
   for (uint32_t i = 1; i < jobs.n; i++)
     if (jobs.j[i].nb != nb) return p;
   if (!tuning().gemm_split) return p;
-  const size_t tiles = (tokens + token_tile(tokens) - 1) / token_tile(tokens);
-  const size_t base = static_cast<size_t>(wgs) * tiles;
-  if (nb < 2 || base >= kSplitBelow) return p;
+  const size_t base = static_cast<size_t>(wgs) * ((tokens + bn - 1) / bn);
+  if (nb < 2 || base >= below) return p;
   const uint32_t want = static_cast<uint32_t>(std::min<size_t>(nb, (kSplitTarget + base - 1) / base));
   if (want < 2) return p;
   p.seg_len = (nb + want - 1) / want;
   p.segs = (nb + p.seg_len - 1) / p.seg_len;
   if (p.segs < 2) return SplitPlan{};
   p.planes = 1 + nb - p.seg_len;
-  p.rows_pad = wgs * kBM;
+  p.rows_pad = wgs * bm;
   return p;
 }
 
-template <int FMT, int BN>
-hipError_t launch_bn(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPlan& plan, float* terms,
-                     hipStream_t s) {
-  const uint32_t wgs = row_tiles(jobs);
+// The launch a batch gets: 32*nt tokens a workgroup, on the regrouped copies
+// when every job has one (units), and the K split.
+struct GemmPlan {
+  bool units = false;
+  int nt = 2, bn = 64;
+  SplitPlan split;
+};
+
+GemmPlan plan_gemm(const GemvJobs& jobs, size_t tokens) {
+  GemmPlan g;
+  GemvJobs jj = jobs;
+  g.units = jobs.n > 0;
+  for (uint32_t i = 0; i < jobs.n; i++) g.units = g.units && jobs.j[i].wu;
+  const uint32_t wgs = row_tiles(jj, kRowsWG);
+  const uint32_t cus = static_cast<uint32_t>(device_cus());
+  if (const int bn = tuning().gemm_bn) {
+    g.nt = bn <= 32 ? 1 : 2;
+  } else {
+    // two 32-token tiles a wave (half the dequantization per MFMA) when
+    // that still gives every CU a workgroup
+    g.nt = static_cast<size_t>(wgs) * ((tokens + 63) / 64) >= cus ? 2 : 1;
+  }
+  g.bn = 32 * g.nt;
+  // K is split below half a workgroup per CU when rows are long (16 blocks
+  // or more) or the grid is under a quarter of the CUs; a short row split
+  // over a moderate grid measured slower than unsplit (Q4_K 5632x2048 x 64
+  // tokens, 88 workgroups: 19.5 against 15.7 us)
+  uint32_t below = cus / 2u;
+  if (jobs.n && jobs.j[0].nb < 16u && static_cast<size_t>(wgs) * ((tokens + g.bn - 1) / g.bn) >= cus / 4u)
+    below = 0;
+  g.split = plan_split(jj, tokens, kRowsWG, static_cast<uint32_t>(g.bn), below);
+  return g;
+}
+
+template <int FMT, int NT, bool UNITS>
+hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPlan& plan, float* terms,
+                       hipStream_t s) {
+  const uint32_t wgs = row_tiles(jobs, kRowsWG);
   if (wgs == 0) return hipSuccess;
-  const uint32_t tiles = static_cast<uint32_t>((tokens + BN - 1) / BN);
-  const size_t lds = 2u * kBM * kStride + BN * kStride + kBM * 8u + BN * 16u + kBM * 8u + BN * 4u;
+  const uint32_t tiles = static_cast<uint32_t>((tokens + 32u * NT - 1) / (32u * NT));
+  constexpr size_t lds = rows_kernel_lds<NT>();
   const bool split = plan.segs > 1 && terms;
   if (!split) {
-    hipLaunchKernelGGL((gemm_kq_kernel<FMT, BN, false>), dim3(wgs, tiles), dim3(kThreads), lds, s, jobs, q, tokens,
-                       SplitTerms{nullptr, 0u, 0u});
+    hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, UNITS, false>), dim3(wgs, tiles), dim3(256), lds, s, jobs, q,
+                       tokens, SplitTerms{nullptr, 0u, 0u});
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((gemm_kq_kernel<FMT, BN, true>), dim3(wgs, tiles, plan.segs), dim3(kThreads), lds, s, jobs, q,
-                     tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad});
+  hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, UNITS, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
+                     jobs, q, tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad});
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n = static_cast<size_t>(plan.rows_pad) * tokens;  // a multiple of 64
   hipLaunchKernelGGL(gemm_combine_kernel, dim3(static_cast<uint32_t>((n / 4u + 255u) / 256u)), dim3(256), 0, s, jobs,
-                     terms, plan.planes, plan.rows_pad, tokens);
+                     terms, plan.planes, plan.rows_pad, tokens, kRowsWG);
   return hipGetLastError();
+}
+
+template <int FMT>
+hipError_t launch_rows_fmt(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, const GemmPlan& g, float* terms,
+                           hipStream_t s) {
+  if (g.nt == 2)
+    return g.units ? launch_rows<FMT, 2, true>(jobs, q, tokens, g.split, terms, s)
+                   : launch_rows<FMT, 2, false>(jobs, q, tokens, g.split, terms, s);
+  return g.units ? launch_rows<FMT, 1, true>(jobs, q, tokens, g.split, terms, s)
+                 : launch_rows<FMT, 1, false>(jobs, q, tokens, g.split, terms, s);
 }
 
 }  // namespace
@@ -498,7 +580,7 @@ bool gemm_fits(size_t tokens, size_t qstride) {
 
 size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens) {
   if (tokens == 0 || (type_id != 12u && type_id != 14u)) return 0;
-  const SplitPlan p = plan_split(jobs, tokens);
+  const SplitPlan p = plan_gemm(jobs, tokens).split;
   return p.segs > 1 ? static_cast<size_t>(p.planes) * p.rows_pad * tokens * sizeof(float) : 0;
 }
 
@@ -506,14 +588,9 @@ hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, s
                        hipStream_t s) {
   if (tokens == 0) return hipSuccess;
   if (!gemm_fits(tokens, q.qstride)) return hipErrorInvalidValue;
-  const SplitPlan plan = plan_split(jobs, tokens);
-  const int bn = token_tile(tokens);
-  if (type_id == 12u)
-    return bn == 128 ? launch_bn<12, 128>(jobs, q, tokens, plan, terms, s)
-                     : launch_bn<12, 64>(jobs, q, tokens, plan, terms, s);
-  if (type_id == 14u)
-    return bn == 128 ? launch_bn<14, 128>(jobs, q, tokens, plan, terms, s)
-                     : launch_bn<14, 64>(jobs, q, tokens, plan, terms, s);
+  const GemmPlan g = plan_gemm(jobs, tokens);
+  if (type_id == 12u) return launch_rows_fmt<12>(jobs, q, tokens, g, terms, s);
+  if (type_id == 14u) return launch_rows_fmt<14>(jobs, q, tokens, g, terms, s);
   return hipErrorInvalidValue;
 }
 

@@ -100,7 +100,7 @@ struct Tuning {
   int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
   int i2s_nt = 0;          // RUSTICIDE_HIP_I2S_NT=256|512|1024: threads per workgroup, one token
   bool i2s_one = true;     // RUSTICIDE_HIP_I2S_ONE=0: one token on the two-token kernel
-  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=64|128 (k-quants), 64|128|256 (I2_S)
+  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=32|64 (k-quants), 64|128|256 (I2_S)
   bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
   bool attn_lds = true;    // RUSTICIDE_HIP_ATTN_LDS=0: the tiled attention step only
 };
