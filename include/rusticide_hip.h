@@ -82,14 +82,14 @@ const char *rh_adapter_name(void);
 void *rh_stream(rh_ctx *ctx);
 
 /* Matrix::load_on (crates/rusticide-model/src/weights.rs:53-98) + the upload:
- * validates `len` against rows x cols for `type_id`, copies the native
- * blocks to HBM once (rows padded to a 16-byte stride), and for I2_S parses
- * and validates the trailer scale (weights.rs:190-202). F16 is widened to
- * f32 as `widen` does (weights.rs:241-247). A Q4_K or Q6_K matrix whose rows
- * hold 1, 2, 4, ... 128 blocks, or 22, 24 or 30 (5632, 6144 or 7680
- * values), also gets a second copy of its blocks,
- * regrouped so that one-token GEMVs read them in contiguous runs (the same
- * bytes again; skipped, with no error, when HBM cannot hold it). */
+ * validates `len` against rows x cols for `type_id`, copies the blocks to
+ * HBM once and for I2_S parses and validates the trailer scale
+ * (weights.rs:190-202). F16 is widened to f32 as `widen` does
+ * (weights.rs:241-247). I2_S and f32 rows sit at a 16-byte stride; Q4_K and
+ * Q6_K blocks are regrouped on the host during the upload into groups of 16
+ * consecutive blocks laid out the way the kernels' waves read them (the
+ * same bytes, one copy; the in-place repack of Adapter::prepare_matrix,
+ * crates/rusticide-kernels/src/adapter.rs:70-83). */
 rh_status rh_matrix_load(rh_ctx *ctx, uint32_t type_id, const void *data, size_t len,
                          size_t rows, size_t cols, rh_matrix **out);
 /* Frees the matrix; valid before or after its context is destroyed. */
@@ -99,7 +99,8 @@ size_t rh_matrix_cols(const rh_matrix *m);
 uint32_t rh_matrix_type(const rh_matrix *m);
 /* Weights::Ternary::scale (matmul.rs:41-45); 0 for other formats. */
 float rh_matrix_ternary_scale(const rh_matrix *m);
-/* Bytes of HBM the matrix occupies (with the regrouped copy, if any). */
+/* Bytes of HBM the matrix occupies: its blocks (Q4_K / Q6_K rounded up to
+ * whole groups of 16), plus 256 bytes of slack rounded to 256. */
 size_t rh_matrix_device_bytes(const rh_matrix *m);
 
 /* Matrix::copy_row (weights.rs:120-150): dequantizes row `index` into the

@@ -49,9 +49,6 @@ struct rh_matrix {
   float scale = 0.0f;
   uint8_t* data = nullptr;
   size_t bytes = 0;
-  // the same blocks in the unit layout (launch_kq_units) for the one-token
-  // fixed-column GEMVs, or null
-  uint8_t* units = nullptr;
 };
 
 struct rh_q8 {
@@ -230,7 +227,7 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
       if (kind != RH_TYPE_F32 && m->nblocks < nb) nb = m->nblocks;
       GemvJob& j = g.j[g.n++];
       j.w = m->data;
-      j.wu = nb == m->nblocks ? m->units : nullptr;
+      j.ub = static_cast<uint32_t>(m->nblocks);
       j.stride = static_cast<uint32_t>(m->stride);
       j.rows = static_cast<uint32_t>(rows);
       j.nb = static_cast<uint32_t>(nb);
@@ -384,7 +381,6 @@ void load_tuning() {
   t.kq_fix = env_int("RUSTICIDE_HIP_KQ_FIX", 1) != 0;
   t.kq_balance = env_int("RUSTICIDE_HIP_KQ_BALANCE", 1) != 0;
   t.kq_onepass = env_int("RUSTICIDE_HIP_KQ_ONEPASS", 1) != 0;
-  t.kq_units = env_int("RUSTICIDE_HIP_KQ_UNITS", 1) != 0;
   const int gr = env_int("RUSTICIDE_HIP_I2S_GROUPS", 0);
   t.i2s_groups = gr == 1 || gr == 2 || gr == 4 ? gr : 0;
   const int lpr = env_int("RUSTICIDE_HIP_I2S_LPR", 0);
@@ -424,7 +420,7 @@ rh_status matmul_norm_device(rh_ctx* ctx, const float* hidden, const NormIn& nor
       j.stride = static_cast<uint32_t>(m->stride);
       j.rows = static_cast<uint32_t>(rows);
       j.nb = static_cast<uint32_t>(m->nblocks < cover ? m->nblocks : cover);
-      j.wu = j.nb == m->nblocks ? m->units : nullptr;
+      j.ub = static_cast<uint32_t>(m->nblocks);
       j.out = jobs[i].out;
       j.out_len = jobs[i].out_len;
       j.scale = m->scale;
@@ -450,10 +446,7 @@ rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn
   GemvJob& j = g.j[g.n++];
   j.w = gate->data;
   j.w2 = up->data;
-  if (gate->units && up->units) {
-    j.wu = gate->units;
-    j.wu2 = up->units;
-  }
+  j.ub = static_cast<uint32_t>(gate->nblocks);
   j.stride = static_cast<uint32_t>(gate->stride);
   j.rows = static_cast<uint32_t>(rows);
   j.nb = static_cast<uint32_t>(gate->nblocks);
@@ -484,7 +477,7 @@ rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg) {
 }
 
 const uint8_t* matrix_data(const rh_matrix* m) { return m->data; }
-size_t matrix_stride(const rh_matrix* m) { return m->stride; }
+size_t matrix_pitch(const rh_matrix* m) { return is_kquant(m->type_id) ? m->nblocks : m->stride; }
 
 rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t len, size_t rows, size_t cols,
                          PendingUpload* out) {
@@ -541,7 +534,8 @@ rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
     // the GEMV kernels address a matrix with 24-bit row indices and 32-bit
     // byte offsets
     if (rows >= (size_t{1} << 24) || m->stride >= (size_t{1} << 24) ||
-        rows * m->stride + kPad > size_t{0xffffffffu}) {
+        rows * m->stride + kPad > size_t{0xffffffffu} ||
+        (is_kquant(type_id) && units_bytes(type_id, rows, m->nblocks) + kPad > size_t{0xffffffffu})) {
       delete m;
       return fail(ctx, RH_ERR_SHAPE_MISMATCH, "matrix exceeds 2^24 rows or 4 GiB of blocks");
     }
@@ -567,7 +561,10 @@ rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
     delete m;
     return fail(ctx, RH_ERR_MISSING_KERNEL, "no kernel reads this block format");
   }
-  m->bytes = round_up(rows * m->stride + kPad, 256);
+  // Q4_K / Q6_K live in the unit layout (rh_device.h), whole groups of 16
+  // blocks; I2_S and dense rows at the 16-byte stride. kPad bytes of zeros
+  // follow either.
+  m->bytes = round_up((is_kquant(type_id) ? units_bytes(type_id, rows, m->nblocks) : rows * m->stride) + kPad, 256);
   hipError_t e = hipMalloc(reinterpret_cast<void**>(&m->data), m->bytes);
   if (e != hipSuccess) {
     delete m;
@@ -583,9 +580,64 @@ namespace {
 constexpr size_t kStageBytes = size_t{32} << 20;  // per pinned staging buffer
 constexpr size_t kCopySlice = size_t{2} << 20;    // least bytes one host thread copies
 
-// Bytes [lo, hi) of a matrix's device image: row r's data at r * stride,
-// zeros in the gaps between rows and after the last one.
+// Group g of a k-quant matrix in the unit layout (rh_device.h) into dst,
+// from its blocks back to back in src (blocks past the last are zeros).
+void unit_group_image(const rh_matrix* m, const uint8_t* src, size_t g, uint8_t* dst) {
+  const size_t total = m->rows * m->nblocks;
+  if (m->type_id == RH_TYPE_Q4_K) {
+    for (size_t tw = 0; tw < 16; tw++) {
+      const size_t e = 16 * g + tw;
+      if (e >= total) {
+        std::memset(dst + 16 * tw, 0, 16);
+        std::memset(dst + 256 + 64 * tw, 0, 64);
+        std::memset(dst + 1280 + 64 * tw, 0, 64);
+        continue;
+      }
+      const uint8_t* b = src + e * 144;
+      std::memcpy(dst + 16 * tw, b, 16);
+      std::memcpy(dst + 256 + 64 * tw, b + 16, 64);
+      std::memcpy(dst + 1280 + 64 * tw, b + 80, 64);
+    }
+    return;
+  }
+  for (size_t tw = 0; tw < 16; tw++) {
+    const size_t e = 16 * g + tw;
+    uint8_t zero[210] = {};
+    const uint8_t* b = e < total ? src + e * 210 : zero;
+    for (size_t h = 0; h < 2; h++) {
+      std::memcpy(dst + 64 * tw + 32 * h, b + 64 * h, 32);
+      std::memcpy(dst + 1024 + 64 * tw + 32 * h, b + 64 * h + 32, 32);
+    }
+    std::memcpy(dst + 2048 + 64 * tw, b + 128, 64);
+    std::memcpy(dst + 3072 + 16 * tw, b + 192, 16);
+    std::memcpy(dst + 3328 + 2 * tw, b + 208, 2);
+  }
+}
+
+// Bytes [lo, hi) of a matrix's device image: for Q4_K / Q6_K the unit
+// layout, for I2_S and dense rows row r's data at r * stride; zeros in the
+// gaps between rows and after the last one.
 void image_range(const rh_matrix* m, const uint8_t* src, size_t lo, size_t hi, uint8_t* dst) {
+  if (is_kquant(m->type_id)) {
+    const size_t gb = m->type_id == RH_TYPE_Q4_K ? 16 * 144 : 16 * 210;
+    const size_t body = units_bytes(m->type_id, m->rows, m->nblocks);
+    uint8_t tmp[16 * 210];
+    for (size_t pos = lo; pos < hi;) {
+      if (pos >= body) {
+        std::memset(dst + (pos - lo), 0, hi - pos);
+        return;
+      }
+      const size_t g = pos / gb, in = pos - g * gb, take = std::min(hi - pos, gb - in);
+      if (in == 0 && take == gb) {
+        unit_group_image(m, src, g, dst + (pos - lo));
+      } else {  // a group cut by the range: build it whole, copy the part
+        unit_group_image(m, src, g, tmp);
+        std::memcpy(dst + (pos - lo), tmp + in, take);
+      }
+      pos += take;
+    }
+    return;
+  }
   const size_t body = m->rows * m->stride;
   size_t pos = lo;
   while (pos < hi) {
@@ -698,19 +750,6 @@ rh_status matrix_upload(rh_ctx* ctx, PendingUpload* p, size_t n) {
     rh_status st = flush();
     if (st != RH_OK) return st;
   }
-  // the unit-layout copies, from the uploaded rows (a matrix without one,
-  // for want of memory or an eligible shape, takes the general block walk)
-  for (size_t i = 0; i < n; i++) {
-    rh_matrix* m = p[i].m;
-    if (m->units || !units_eligible(m->type_id, m->rows, m->nblocks)) continue;
-    void* u = nullptr;
-    if (hipMalloc(&u, units_bytes(m->type_id, m->rows, m->nblocks)) != hipSuccess) {
-      (void)hipGetLastError();
-      continue;
-    }
-    m->units = static_cast<uint8_t*>(u);
-    RH_HIP(ctx, launch_kq_units(m->type_id, m->data, m->stride, m->rows, m->nblocks, m->units, ctx->stream));
-  }
   RH_HIP(ctx, hipStreamSynchronize(ctx->stream));
   return RH_OK;
 }
@@ -793,7 +832,6 @@ void rh_matrix_free(rh_matrix* m) {
   hipSetDevice(m->device);
   hipDeviceSynchronize();
   hipFree(m->data);
-  if (m->units) hipFree(m->units);
   delete m;
 }
 
@@ -803,7 +841,7 @@ uint32_t rh_matrix_type(const rh_matrix* m) { return m ? m->type_id : 0; }
 float rh_matrix_ternary_scale(const rh_matrix* m) { return m ? m->scale : 0.0f; }
 size_t rh_matrix_device_bytes(const rh_matrix* m) {
   if (!m) return 0;
-  return m->bytes + (m->units ? units_bytes(m->type_id, m->rows, m->nblocks) : 0);
+  return m->bytes;
 }
 
 rh_status rh_matrix_copy_row(rh_ctx* ctx, const rh_matrix* m, size_t index, float* out,
@@ -832,8 +870,8 @@ rh_status rh_matrix_copy_row(rh_ctx* ctx, const rh_matrix* m, size_t index, floa
   if (st != RH_OK) return st;
   float* d = static_cast<float*>(ctx->buf[kOut]);
   if (nb) {
-    RH_HIP(ctx, launch_dequantize_row(m->type_id, row, static_cast<uint32_t>(nb), m->scale, d, nb * bs,
-                                      ctx->stream));
+    RH_HIP(ctx, launch_dequantize_row(m->type_id, m->data, matrix_pitch(m), static_cast<uint32_t>(index),
+                                      static_cast<uint32_t>(nb), m->scale, d, nb * bs, ctx->stream));
     RH_HIP(ctx, hipMemcpyAsync(out, d, nb * bs * 4, hipMemcpyDeviceToHost, ctx->stream));
   }
   RH_HIP(ctx, hipStreamSynchronize(ctx->stream));

@@ -1,6 +1,6 @@
-// gemm.hip -- prefill GEMM on gfx950 matrix cores: Q4_K / Q6_K weights in
-// their native GGUF blocks against Q8_K-quantized activations of many tokens,
-// bit-identical to rusticide's CPU integer path.
+// gemm.hip -- prefill GEMM on gfx950 matrix cores: Q4_K / Q6_K weights (their
+// GGUF blocks, in the unit layout of rh_device.h) against Q8_K-quantized
+// activations of many tokens, bit-identical to rusticide's CPU integer path.
 //
 // The CPU path (crates/rusticide-kernels/src/portable/int_dot.rs:142-204)
 // forms, per 256-weight super-block b of row r and token t, exact integers
@@ -89,9 +89,8 @@ struct SplitTerms {
 // 16-bit multiply of four nibbles; isum = 8*hi + lo. Q6_K keeps w = sc*(q-32)
 // = 128*hi + lo. Both sums are exact in i32.
 //
-// Matrices with a regrouped copy (UNITS; launch_kq_units) are read from it:
-// the lane's pieces of a block sit at fixed 16-byte-aligned offsets of its
-// group of 16 blocks.
+// The matrices are in the unit layout (rh_device.h): the lane's pieces of a
+// block sit at fixed 16-byte-aligned offsets of its group of 16 blocks.
 constexpr uint32_t kRowsWG = 128;
 
 int device_cus() {
@@ -128,52 +127,32 @@ struct LaneRaw<14> {
   uint32_t dw;
 };
 
-template <bool UNITS>
+// The lane's pieces of block b of its row from the unit layout (rh_device.h):
+// block e = row * ub + b sits at position tw of group e >> 4, every piece at
+// a 16-byte-aligned offset.
 __device__ __forceinline__ void load_lane_raw(LaneRaw<12>& x, const GemvJob& J, uint32_t row, uint32_t b,
                                               uint32_t g) {
-  if (UNITS) {
-    const uint32_t e = row * J.nb + b, tw = e & 15u;
-    const uint8_t* u = J.wu + static_cast<size_t>(e >> 4) * 2304u;
-    x.hd = load16(u + 16u * tw);
-    x.qs[0] = load16(u + 256u + 64u * tw + 16u * g);
-    x.qs[1] = load16(u + 256u + 64u * tw + 32u + 16u * g);
-    x.qs[2] = load16(u + 1280u + 64u * tw + 16u * g);
-    x.qs[3] = load16(u + 1280u + 64u * tw + 32u + 16u * g);
-  } else {
-    const uint8_t* blk = J.w + static_cast<size_t>(row) * J.stride + b * 144u;
-    x.hd = load16(blk);
-#pragma unroll
-    for (uint32_t p = 0; p < 4u; p++) x.qs[p] = load16(blk + 16u + 32u * p + 16u * g);
-  }
+  const uint32_t e = row * J.ub + b, tw = e & 15u;
+  const uint8_t* u = J.w + static_cast<size_t>(e >> 4) * kUnitBytesQ4;
+  x.hd = load16(u + 16u * tw);
+  x.qs[0] = load16(u + 256u + 64u * tw + 16u * g);
+  x.qs[1] = load16(u + 256u + 64u * tw + 32u + 16u * g);
+  x.qs[2] = load16(u + 1280u + 64u * tw + 16u * g);
+  x.qs[3] = load16(u + 1280u + 64u * tw + 32u + 16u * g);
 }
 
-template <bool UNITS>
 __device__ __forceinline__ void load_lane_raw(LaneRaw<14>& x, const GemvJob& J, uint32_t row, uint32_t b,
                                               uint32_t g) {
-  if (UNITS) {
-    const uint32_t e = row * J.nb + b, tw = e & 15u;
-    const uint8_t* u = J.wu + static_cast<size_t>(e >> 4) * 3360u;
+  const uint32_t e = row * J.ub + b, tw = e & 15u;
+  const uint8_t* u = J.w + static_cast<size_t>(e >> 4) * kUnitBytesQ6;
 #pragma unroll
-    for (uint32_t h = 0; h < 2u; h++) {
-      x.ql0[h] = load16(u + 64u * tw + 16u * (2u * h + g));
-      x.ql1[h] = load16(u + 1024u + 64u * tw + 16u * (2u * h + g));
-      x.qh[h] = load16(u + 2048u + 64u * tw + 16u * (2u * h + g));
-    }
-    x.sc = load16(u + 3072u + 16u * tw);
-    x.dw = *reinterpret_cast<const uint16_t*>(u + 3328u + 2u * tw);
-  } else {
-    // a 210-byte block starts 2-byte aligned: unaligned 16-byte loads, each
-    // inside the block
-    const uint8_t* blk = J.w + static_cast<size_t>(row) * J.stride + b * 210u;
-#pragma unroll
-    for (uint32_t h = 0; h < 2u; h++) {
-      x.ql0[h] = load16_any(blk + 64u * h + 16u * g);
-      x.ql1[h] = load16_any(blk + 64u * h + 32u + 16u * g);
-      x.qh[h] = load16_any(blk + 128u + 32u * h + 16u * g);
-    }
-    x.sc = load16_any(blk + 192u);
-    x.dw = *reinterpret_cast<const uint16_t*>(blk + 208u);
+  for (uint32_t h = 0; h < 2u; h++) {
+    x.ql0[h] = load16(u + 64u * tw + 16u * (2u * h + g));
+    x.ql1[h] = load16(u + 1024u + 64u * tw + 16u * (2u * h + g));
+    x.qh[h] = load16(u + 2048u + 64u * tw + 16u * (2u * h + g));
   }
+  x.sc = load16(u + 3072u + 16u * tw);
+  x.dw = *reinterpret_cast<const uint16_t*>(u + 3328u + 2u * tw);
 }
 
 // The two A planes of 32-deep step kk for this lane (its row, k = 32kk + 16g ..).
@@ -254,7 +233,7 @@ constexpr size_t rows_kernel_lds() {
   return 2u * 32u * NT * kStride + 2u * 32u * NT * 4u + 2u * 32u * NT * 16u + 4u * 32u * 8u;
 }
 
-template <int FMT, int NT, bool UNITS, bool SPLIT>
+template <int FMT, int NT, bool SPLIT>
 __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev q, size_t tokens,
                                                            SplitTerms split) {
   constexpr uint32_t BN = 32u * NT;
@@ -336,7 +315,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
     for (int i = 0; i < 16; i++) y[t][i] = -0.0f;
 
   if (b_begin < b_end) {
-    load_lane_raw<UNITS>(raw, J, arow, b_begin, g);
+    load_lane_raw(raw, J, arow, b_begin, g);
     load_act(b_begin);
     store_act(0u);
     __syncthreads();
@@ -347,7 +326,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
     if (more) {
       // the next block's weights go out a whole block ahead: each lane's
       // 16-byte pieces come from 32 different rows, a long round trip
-      load_lane_raw<UNITS>(nxt, J, arow, b + 1u, g);
+      load_lane_raw(nxt, J, arow, b + 1u, g);
       load_act(b + 1u);
     }
     // this block's (d, dmin) of the wave's rows, for the D layout's rows
@@ -505,10 +484,8 @@ SplitPlan plan_split(GemvJobs jobs, size_t tokens, uint32_t bm, uint32_t bn, uin
   return p;
 }
 
-// The launch a batch gets: 32*nt tokens a workgroup, on the regrouped copies
-// when every job has one (units), and the K split.
+// The launch a batch gets: 32*nt tokens a workgroup, and the K split.
 struct GemmPlan {
-  bool units = false;
   int nt = 2, bn = 64;
   SplitPlan split;
 };
@@ -516,8 +493,6 @@ struct GemmPlan {
 GemmPlan plan_gemm(const GemvJobs& jobs, size_t tokens) {
   GemmPlan g;
   GemvJobs jj = jobs;
-  g.units = jobs.n > 0;
-  for (uint32_t i = 0; i < jobs.n; i++) g.units = g.units && jobs.j[i].wu;
   const uint32_t wgs = row_tiles(jj, kRowsWG);
   const uint32_t cus = static_cast<uint32_t>(device_cus());
   if (const int bn = tuning().gemm_bn) {
@@ -539,7 +514,7 @@ GemmPlan plan_gemm(const GemvJobs& jobs, size_t tokens) {
   return g;
 }
 
-template <int FMT, int NT, bool UNITS>
+template <int FMT, int NT>
 hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPlan& plan, float* terms,
                        hipStream_t s) {
   const uint32_t wgs = row_tiles(jobs, kRowsWG);
@@ -548,11 +523,11 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
   constexpr size_t lds = rows_kernel_lds<NT>();
   const bool split = plan.segs > 1 && terms;
   if (!split) {
-    hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, UNITS, false>), dim3(wgs, tiles), dim3(256), lds, s, jobs, q,
+    hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, false>), dim3(wgs, tiles), dim3(256), lds, s, jobs, q,
                        tokens, SplitTerms{nullptr, 0u, 0u});
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, UNITS, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
+  hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
                      jobs, q, tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad});
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
@@ -565,11 +540,8 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
 template <int FMT>
 hipError_t launch_rows_fmt(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, const GemmPlan& g, float* terms,
                            hipStream_t s) {
-  if (g.nt == 2)
-    return g.units ? launch_rows<FMT, 2, true>(jobs, q, tokens, g.split, terms, s)
-                   : launch_rows<FMT, 2, false>(jobs, q, tokens, g.split, terms, s);
-  return g.units ? launch_rows<FMT, 1, true>(jobs, q, tokens, g.split, terms, s)
-                 : launch_rows<FMT, 1, false>(jobs, q, tokens, g.split, terms, s);
+  return g.nt == 2 ? launch_rows<FMT, 2>(jobs, q, tokens, g.split, terms, s)
+                   : launch_rows<FMT, 1>(jobs, q, tokens, g.split, terms, s);
 }
 
 }  // namespace

@@ -325,18 +325,9 @@ __device__ __forceinline__ uint32_t row_of(const WgRows& g, uint32_t r) {
   return ((__umul24(r >> g.cs, g.nwg) + g.w) << g.cs) | (r & g.mask);
 }
 
-// Block b of workgroup row r (matrices stay below 4 GiB and 2^24 rows:
-// 24-bit multiplies, 32-bit offsets).
-template <bool PAIR>
-__device__ __forceinline__ const uint8_t* block_at(const GemvJob& J, const WgRows& g, uint32_t r, uint32_t boff) {
-  const bool second = PAIR && r >= g.nh;
-  const uint8_t* m = g.w1 + (second ? g.d2 : 0u);
-  const uint32_t row = PAIR ? g.row0 + (second ? r - g.nh : r) : row_of(g, r);
-  return m + (__umul24(row, static_cast<uint32_t>(J.stride)) + boff);
-}
-
-// The group of 16 blocks (unit layout, launch_kq_units) holding block fb of
-// workgroup row r: a wave's step reads one group, its team tw at position tw.
+// The group of 16 blocks (the unit layout, rh_device.h) holding block fb of
+// workgroup row r, for the fixed-column walk: a wave's step reads one group,
+// its team tw at position tw.
 template <bool PAIR>
 __device__ __forceinline__ const uint8_t* unit_at(const WgRows& g, uint32_t r, uint32_t fb, uint32_t nb,
                                                   uint32_t ubytes) {
@@ -401,20 +392,18 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
 // Where a team finds its blocks. A workgroup's teams take team blocks
 // g = team + i * NT/4, i = 0..NI-1, of its rows x nb blocks in row-major
 // order. The general walk divides each g into (row g / nb, block g % nb) and
-// reads the matrix's native rows.
+// finds that block's group and position in the unit layout (rh_device.h);
+// when a wave's 16 teams take the 16 blocks of one group, its loads read
+// consecutive bytes.
 // FIX (nb a power of two up to NT/4: rows of 256, 512, ... values): g % nb
 // is the same for every i, so the team keeps one
 // block column fb, its row advances by step = NT/4/nb an iteration, and the
 // activation a team reads is the same for all of its blocks and leaves the
-// loop. FIX reads the unit layout (launch_kq_units): a wave's 16 teams take
-// the 16 blocks of one group, and the group's address advances by a constant
-// stride (row_of is affine in i: step is a whole number of interleaved
-// chunks, and the launcher checks that every wave's rows start a group).
-// UNITS without FIX: the general walk on the unit layout. A wave's 16 teams
-// take team blocks 16w..16w+15 (+ i * NT/4), one group when the workgroup's
-// first block starts one (the launcher checks: contiguous rows, R * nb a
-// multiple of 16, no pair).
-template <bool PAIR, uint32_t NT, bool FIX, bool UNITS = FIX>
+// loop. A wave's 16 teams take the 16 blocks of one group, each at its own
+// position, and the group's address advances by a constant stride (row_of is
+// affine in i: step is a whole number of interleaved chunks, and the
+// launcher checks that every wave's rows start a group).
+template <bool PAIR, uint32_t NT, bool FIX>
 struct BlockWalk {
   const GemvJob& J;
   const WgRows& wr;
@@ -455,9 +444,11 @@ struct BlockWalk {
       b = g - __umul24(r, nb);
     }
   }
-  // the address of team block i; a spare team re-reads a block of its own
-  __device__ __forceinline__ const uint8_t* addr(int i) const {
+  // the group of team block i and the block's position tw in it; a spare
+  // team re-reads a block of its own
+  __device__ __forceinline__ const uint8_t* addr(int i, uint32_t& tw) const {
     if constexpr (FIX) {
+      tw = team & 15u;
       const uint32_t r = r0 + static_cast<uint32_t>(i) * step;
       if constexpr (PAIR) return r < wr.nrows ? unit_at<true>(wr, r, fb, nb, 16u * bbytes) : p0;
       return r < wr.nrows ? p0 + static_cast<uint32_t>(i) * delta : p0;
@@ -466,8 +457,12 @@ struct BlockWalk {
       const uint32_t g = team + static_cast<uint32_t>(i) * (NT / 4u);
       const uint32_t gg = g < total ? g : 0u;
       const uint32_t r = static_cast<uint32_t>((static_cast<float>(gg) + 0.5f) * inv_nb), b = gg - __umul24(r, nb);
-      if constexpr (UNITS) return unit_at<PAIR>(wr, r, b, nb, 16u * bbytes);
-      return block_at<PAIR>(J, wr, r, __umul24(b, bbytes));
+      const bool second = PAIR && r >= wr.nh;
+      const uint8_t* m = wr.w1 + (second ? wr.d2 : 0u);
+      const uint32_t row = PAIR ? wr.row0 + (second ? r - wr.nh : r) : row_of(wr, r);
+      const uint32_t e = row * J.ub + b;  // the matrix's unit blocks stay below 2^32
+      tw = e & 15u;
+      return m + (e >> 4) * (16u * bbytes);
     }
   }
 };
@@ -588,7 +583,7 @@ __device__ __forceinline__ float q6k_term(const Q6Dec& q, const u32x4& a0, const
 // NORM (T = 1, the whole row in the preload): x is the hidden state and the
 // kernel applies the NormIn residual add and RMSNorm before quantizing.
 // FIX: see BlockWalk (one token).
-template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX, bool UNITS>
+template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX>
 __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const float* __restrict__ x, size_t width,
                                          uint32_t R, uint32_t nbmax, size_t tokens, size_t t0, const NormIn& nrm,
                                          uint8_t* lds) {
@@ -599,7 +594,7 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   float* terms = reinterpret_cast<float*>(sums + T * nbmax * 8u);
 
   const WgRows wr = wg_rows<PAIR>(J, R);
-  const BlockWalk<PAIR, NT, FIX, UNITS> walk(J, wr, 144u);
+  const BlockWalk<PAIR, NT, FIX> walk(J, wr, 144u);
   const uint32_t p = threadIdx.x & 3u;
 
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
@@ -611,20 +606,15 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
   // issue order: the prologue waits only for these)
   __builtin_amdgcn_sched_barrier(0);
   u32x4 hd[NI], c0[NI], c1[NI];
-  // UNITS, unit layout: headers [16 teams][16] | qs[0..64) [64 lanes][16] |
-  // qs[64..128) [64 lanes][16]; the quants are read nontemporal
-  const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
+  // the unit layout (rh_device.h): the block's header at 16 tw, the lane's
+  // pieces of qs[0..64) and qs[64..128) at 256 / 1280 + 64 tw + 16p; the
+  // quants are read nontemporal (once per launch)
   auto issue = [&](int i) {
-    const uint8_t* blk = walk.addr(i);
-    if constexpr (UNITS) {
-      hd[i] = load16(blk + 16u * utw);
-      c0[i] = load16_nt(blk + 256u + 16u * ul);
-      c1[i] = load16_nt(blk + 1280u + 16u * ul);
-    } else {
-      hd[i] = load16(blk);
-      c0[i] = load16(blk + 16u + 16u * p);
-      c1[i] = load16(blk + 80u + 16u * p);
-    }
+    uint32_t tw;
+    const uint8_t* grp = walk.addr(i, tw);
+    hd[i] = load16(grp + 16u * tw);
+    c0[i] = load16_nt(grp + 256u + 64u * tw + 16u * p);
+    c1[i] = load16_nt(grp + 1280u + 64u * tw + 16u * p);
   };
   constexpr int ahead = issue_ahead<NI, NORM>();
 #pragma unroll
@@ -702,28 +692,24 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
 // a kernel of its own rather than a branch in one: at the join of two walks
 // the compiler merges their pending loads and then waits for the activation
 // before issuing the first weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
-          bool UNITS = FIX>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
 __global__ __launch_bounds__(NT) void gemv_q4k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
   static_assert(!FIX || T == 1, "fixed columns: one token");
-  static_assert(!FIX || UNITS, "fixed columns read the unit layout");
-  static_assert(!UNITS || !PAIR || FIX, "the general walk reads a pair's native rows");
-  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // The same kernel with the activation's scalars first: the build preloads
 // leading scalar arguments into SGPRs (-amdgpu-kernarg-preload-count), so the
 // activation's first loads need no kernel-argument load (kq_preloads).
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
-          bool UNITS = FIX>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
 __global__ __launch_bounds__(NT) void gemv_q4k_kernel_pl(const float* __restrict__ x, size_t width, uint32_t R,
                                                           uint32_t nbmax, size_t tokens, size_t t0, GemvJobs jobs,
                                                           Q8Dev q, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
-  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+  q4k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // Q6_K x Q8_K --------------------------------------------------------------
@@ -731,7 +717,7 @@ __global__ __launch_bounds__(NT) void gemv_q4k_kernel_pl(const float* __restrict
 //      (-32 * the activation sum of each 16-run) | terms [R][nbmax][T] f32
 // FQ: 0 reads the activation q holds; 1 or 4 quantizes x in the kernel,
 // preloading FQ blocks per half-wave before the weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX, bool UNITS>
+template <int T, int NI, int FQ, bool NORM, bool PAIR, uint32_t NT, bool FIX>
 __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const float* __restrict__ x, size_t width,
                                          uint32_t R, uint32_t nbmax, size_t tokens, size_t t0, const NormIn& nrm,
                                          uint8_t* lds) {
@@ -742,14 +728,12 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   float* terms = reinterpret_cast<float*>(bias + T * nbmax * 16u);
 
   const WgRows wr = wg_rows<PAIR>(J, R);
-  const BlockWalk<PAIR, NT, FIX, UNITS> walk(J, wr, 210u);
+  const BlockWalk<PAIR, NT, FIX> walk(J, wr, 210u);
   const uint32_t p = threadIdx.x & 3u;
   const uint32_t h = p >> 1, gq = p & 1u;
 
   // A, B: ql[64h+16gq..], ql[64h+32+16gq..]; C: qh[32h+16gq..]; S: the
-  // eight scales of half h at 192+8h; D: d at 208 (q6_k.rs:13-43). Blocks are
-  // 210 bytes, so every load but D's is only 2-byte aligned; each stays
-  // inside its block.
+  // eight scales of half h; D: d (q6_k.rs:13-43).
   const XGeom xg = x_geom<T>(FQ ? x + t0 * width : nullptr, width, nbmax);
   XRound<FQ ? FQ : 1> xr;
   if (FQ) load_x_round<FQ ? FQ : 1, NT>(xr, xg, 0u);
@@ -761,24 +745,17 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
   u32x4 A[NI], B[NI], C[NI];
   uint2 S[NI];
   uint32_t D[NI];
-  // UNITS, unit layout: A [64 lanes][16] | B [64][16] | C [64][16] | the
-  // scales [16 teams][16] | d [16 teams][2]
-  const uint32_t ul = threadIdx.x & 63u, utw = ul >> 2;
+  // the unit layout (rh_device.h): the lane's pieces A, B, C at
+  // 64 tw + 16p, 1024 + 64 tw + 16p, 2048 + 64 tw + 16p (nontemporal, as in
+  // q4k_body), the block's scales at 3072 + 16 tw, d at 3328 + 2 tw
   auto issue = [&](int i) {
-    const uint8_t* base = walk.addr(i);
-    if constexpr (UNITS) {
-      A[i] = load16_nt(base + 16u * ul);  // nontemporal, as in q4k_body
-      B[i] = load16_nt(base + 1024u + 16u * ul);
-      C[i] = load16_nt(base + 2048u + 16u * ul);
-      S[i] = *reinterpret_cast<const uint2*>(base + 3072u + 16u * utw + 8u * h);
-      D[i] = *reinterpret_cast<const uint16_t*>(base + 3328u + 2u * utw);
-    } else {
-      A[i] = load16_any(base + 64u * h + 16u * gq);
-      B[i] = load16_any(base + 64u * h + 32u + 16u * gq);
-      C[i] = load16_any(base + 128u + 32u * h + 16u * gq);
-      S[i] = load8_any(base + 192u + 8u * h);
-      D[i] = *reinterpret_cast<const uint16_t*>(base + 208u);
-    }
+    uint32_t tw;
+    const uint8_t* grp = walk.addr(i, tw);
+    A[i] = load16_nt(grp + 64u * tw + 16u * p);
+    B[i] = load16_nt(grp + 1024u + 64u * tw + 16u * p);
+    C[i] = load16_nt(grp + 2048u + 64u * tw + 16u * p);
+    S[i] = *reinterpret_cast<const uint2*>(grp + 3072u + 16u * tw + 8u * h);
+    D[i] = *reinterpret_cast<const uint16_t*>(grp + 3328u + 2u * tw);
   };
   constexpr int ahead = issue_ahead<NI, NORM>();
 #pragma unroll
@@ -853,62 +830,24 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
 // a kernel of its own rather than a branch in one: at the join of two walks
 // the compiler merges their pending loads and then waits for the activation
 // before issuing the first weights.
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
-          bool UNITS = FIX>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
 __global__ __launch_bounds__(NT) void gemv_q6k_kernel(GemvJobs jobs, Q8Dev q, const float* __restrict__ x,
                                                        size_t width, uint32_t R, uint32_t nbmax, size_t tokens,
                                                        size_t t0, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
   static_assert(!FIX || T == 1, "fixed columns: one token");
-  static_assert(!FIX || UNITS, "fixed columns read the unit layout");
-  static_assert(!UNITS || !PAIR || FIX, "the general walk reads a pair's native rows");
-  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
+  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // The same kernel with the activation's scalars first: the build preloads
 // leading scalar arguments into SGPRs (-amdgpu-kernarg-preload-count), so the
 // activation's first loads need no kernel-argument load (kq_preloads).
-template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false,
-          bool UNITS = FIX>
+template <int T, int NI, int FQ, bool NORM, bool PAIR = false, uint32_t NT = kThreads, bool FIX = false>
 __global__ __launch_bounds__(NT) void gemv_q6k_kernel_pl(const float* __restrict__ x, size_t width, uint32_t R,
                                                           uint32_t nbmax, size_t tokens, size_t t0, GemvJobs jobs,
                                                           Q8Dev q, NormIn nrm) {
   extern __shared__ __align__(16) uint8_t lds[];
-  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
-}
-
-// The unit layout (launch_kq_units): one thread per (group of 16 blocks,
-// lane), the lane's pieces of its team's block as the fixed-column kernels'
-// lane l = 4*tw + p loads them (tw the team in the wave, p its lane).
-template <int FMT>
-__global__ __launch_bounds__(256) void kq_units_kernel(const uint8_t* __restrict__ src, uint32_t stride,
-                                                       uint32_t rows, uint32_t nb, uint32_t groups,
-                                                       uint8_t* __restrict__ dst) {
-  constexpr uint32_t bb = FMT == 12 ? 144u : 210u;
-  const uint32_t gid = blockIdx.x * 256u + threadIdx.x;
-  const uint32_t grp = gid >> 6, l = gid & 63u;
-  if (grp >= groups) return;
-  const uint32_t tw = l >> 2, p = l & 3u;
-  const uint32_t blk = grp * 16u + tw;
-  uint32_t row = blk / nb;
-  const uint32_t col = blk - row * nb;
-  row = row < rows ? row : rows - 1u;
-  const uint8_t* b = src + static_cast<size_t>(row) * stride + col * bb;
-  uint8_t* u = dst + static_cast<size_t>(grp) * (16u * bb);
-  if (FMT == 12) {
-    if (p == 0) *reinterpret_cast<u32x4*>(u + 16u * tw) = load16(b);
-    *reinterpret_cast<u32x4*>(u + 256u + 16u * l) = load16(b + 16u + 16u * p);
-    *reinterpret_cast<u32x4*>(u + 1280u + 16u * l) = load16(b + 80u + 16u * p);
-  } else {
-    const uint32_t h = p >> 1, gq = p & 1u;
-    *reinterpret_cast<u32x4*>(u + 16u * l) = load16_any(b + 64u * h + 16u * gq);
-    *reinterpret_cast<u32x4*>(u + 1024u + 16u * l) = load16_any(b + 64u * h + 32u + 16u * gq);
-    *reinterpret_cast<u32x4*>(u + 2048u + 16u * l) = load16_any(b + 128u + 32u * h + 16u * gq);
-    if (p == 0) {
-      *reinterpret_cast<u32x4*>(u + 3072u + 16u * tw) = load16_any(b + 192u);
-      *reinterpret_cast<uint16_t*>(u + 3328u + 2u * tw) = *reinterpret_cast<const uint16_t*>(b + 208u);
-    }
-  }
+  q6k_body<T, NI, FQ, NORM, PAIR, NT, FIX>(jobs.j[find_job(jobs)], q, x, width, R, nbmax, tokens, t0, nrm, lds);
 }
 
 // I2_S x I8_S --------------------------------------------------------------
@@ -1624,8 +1563,8 @@ __global__ __launch_bounds__(256) void gemv_dense_kernel(GemvJobs jobs, const fl
 }
 
 // Dequantize one row (Matrix::copy_row, model/src/weights.rs:120-150) -------
-__global__ __launch_bounds__(256) void dequantize_row_kernel(uint32_t type_id, const uint8_t* row,
-                                                             uint32_t nb, float scale, float* out,
+__global__ __launch_bounds__(256) void dequantize_row_kernel(uint32_t type_id, const uint8_t* m, size_t pitch,
+                                                             uint32_t row, uint32_t nb, float scale, float* out,
                                                              size_t out_len) {
   const uint32_t bs = type_id == 36u ? 128u : 256u;
   const size_t n = min(static_cast<size_t>(nb) * bs, out_len);
@@ -1633,37 +1572,10 @@ __global__ __launch_bounds__(256) void dequantize_row_kernel(uint32_t type_id, c
        e += static_cast<size_t>(gridDim.x) * kThreads) {
     const uint32_t b = static_cast<uint32_t>(e / bs), l = static_cast<uint32_t>(e % bs);
     float v;
-    if (type_id == 12u) {  // quantize/src/q4_k.rs:32-66
-      const uint8_t* blk = row + static_cast<size_t>(b) * 144u;
-      const float d = f16_lo(load4(blk)), dmin = f16_hi(load4(blk));
-      const uint32_t j = l / 32u, li = l % 32u;
-      const uint8_t* s = blk + 4;
-      uint32_t sc, m;
-      if (j < 4u) {
-        sc = s[j] & 63u;
-        m = s[j + 4u] & 63u;
-      } else {
-        sc = (s[j + 4u] & 0x0Fu) | ((s[j - 4u] >> 6) << 4);
-        m = (s[j + 4u] >> 4) | ((s[j] >> 6) << 4);
-      }
-      const uint8_t qb = blk[16u + 32u * (j / 2u) + li];
-      const uint32_t qv = (j & 1u) ? (qb >> 4) : (qb & 0x0Fu);
-      const float ds = d * static_cast<float>(sc), dm = dmin * static_cast<float>(m);
-      const float prod = ds * static_cast<float>(qv);
-      v = prod - dm;
-    } else if (type_id == 14u) {  // quantize/src/q6_k.rs:13-43
-      const uint8_t* blk = row + static_cast<size_t>(b) * 210u;
-      const float d = f16_lo(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
-      const uint32_t hh = l / 128u, rr = (l % 128u) / 32u, li = l % 32u;
-      const uint8_t low = blk[64u * hh + 32u * (rr & 1u) + li];
-      const uint8_t high = blk[128u + 32u * hh + li];
-      const uint32_t nib = rr < 2u ? (low & 0x0Fu) : (low >> 4);
-      const int32_t qv = static_cast<int32_t>(nib | (((high >> (2u * rr)) & 3u) << 4)) - 32;
-      const float sc = static_cast<float>(static_cast<int8_t>(blk[192u + 8u * hh + 2u * rr + li / 16u]));
-      const float ds = d * sc;
-      v = ds * static_cast<float>(qv);
+    if (type_id == 12u || type_id == 14u) {
+      v = unit_weight(m, type_id, row * static_cast<uint32_t>(pitch) + b, l);
     } else {  // quantize/src/i2_s.rs:15-21 then i2_s_apply_scale (:33-37)
-      const uint8_t byte = row[static_cast<size_t>(b) * 32u + l % 32u];
+      const uint8_t byte = m[static_cast<size_t>(row) * pitch + static_cast<size_t>(b) * 32u + l % 32u];
       const uint32_t code = (byte >> (6u - 2u * (l / 32u))) & 3u;
       const float c = static_cast<float>(code) - 1.0f;
       v = c * scale;
@@ -1718,15 +1630,15 @@ template <int NI, bool NORM>
 constexpr bool kq_preloads() { return NI != 8 || NORM; }
 
 template <int FMT, int T, int NI, int FQ, bool NORM = false, bool PAIR = false, uint32_t NT = kThreads,
-          bool FIX = false, bool UNITS = FIX>
+          bool FIX = false>
 KqFn kq_kernel() {
   if constexpr (kq_preloads<NI, NORM>())
-    return {FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel_pl<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>)
-                      : reinterpret_cast<void*>(gemv_q6k_kernel_pl<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>),
+    return {FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel_pl<T, NI, FQ, NORM, PAIR, NT, FIX>)
+                      : reinterpret_cast<void*>(gemv_q6k_kernel_pl<T, NI, FQ, NORM, PAIR, NT, FIX>),
             true};
   else
-    return {FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>)
-                      : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX, UNITS>),
+    return {FMT == 12 ? reinterpret_cast<void*>(gemv_q4k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX>)
+                      : reinterpret_cast<void*>(gemv_q6k_kernel<T, NI, FQ, NORM, PAIR, NT, FIX>),
             false};
 }
 
@@ -1799,17 +1711,15 @@ KqFn kq_wide_kernel(uint32_t type_id, uint32_t fq, uint32_t ni, bool norm, bool 
 }
 
 // The one-token kernels with a half-wave for every block of a 17- to
-// 32-block activation (768 or 1024 lanes, one block per team), on the
-// native rows or (`units`) the unit layout.
-template <uint32_t NT, bool UNITS>
+// 32-block activation (768 or 1024 lanes, one block per team).
+template <uint32_t NT>
 KqFn kq_onepass_kernel_nt(uint32_t type_id) {
-  return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, NT, false, UNITS>()
-                        : kq_kernel<14, 1, 1, 4, false, false, NT, false, UNITS>();
+  return type_id == 12u ? kq_kernel<12, 1, 1, 4, false, false, NT, false>()
+                        : kq_kernel<14, 1, 1, 4, false, false, NT, false>();
 }
 
-KqFn kq_onepass_kernel(uint32_t type_id, uint32_t nt, bool units) {
-  if (nt == 768u) return units ? kq_onepass_kernel_nt<768u, true>(type_id) : kq_onepass_kernel_nt<768u, false>(type_id);
-  return units ? kq_onepass_kernel_nt<1024u, true>(type_id) : kq_onepass_kernel_nt<1024u, false>(type_id);
+KqFn kq_onepass_kernel(uint32_t type_id, uint32_t nt) {
+  return nt == 768u ? kq_onepass_kernel_nt<768u>(type_id) : kq_onepass_kernel_nt<1024u>(type_id);
 }
 
 // The norm-fused decode kernels: one token, four blocks per team (two for a
@@ -1927,39 +1837,9 @@ hipError_t launch_i2s_q8(GemvJobs jobs, const Q8Dev& q, size_t tokens, size_t t0
 
 }  // namespace
 
-bool units_eligible(uint32_t type_id, size_t rows, size_t nb) {
-  // the kernels address the copy with 32-bit offsets
-  if ((type_id != 12u && type_id != 14u) || rows == 0 || nb == 0 || units_bytes(type_id, rows, nb) > UINT32_MAX)
-    return false;
-  // the fixed-column kernels
-  if (nb <= 128u && (nb & (nb - 1u)) == 0u) return true;
-  // the one-round kernels, whose workgroups then start whole groups
-  if (nb > 16u && nb <= 32u) {
-    const size_t per = (onepass_lanes(static_cast<uint32_t>(nb)) / 4u) / nb;
-    return per * nb % 16u == 0u;
-  }
-  return false;
-}
-
 size_t units_bytes(uint32_t type_id, size_t rows, size_t nb) {
   const size_t groups = (rows * nb + 15u) / 16u;
   return groups * 16u * (type_id == 12u ? 144u : 210u);
-}
-
-hipError_t launch_kq_units(uint32_t type_id, const uint8_t* src, size_t stride, size_t rows, size_t nb, uint8_t* dst,
-                           hipStream_t s) {
-  if (!units_eligible(type_id, rows, nb)) return hipErrorInvalidValue;
-  const uint32_t groups = static_cast<uint32_t>((rows * nb + 15u) / 16u);
-  const uint32_t threads = groups * 64u;
-  if (type_id == 12u)
-    hipLaunchKernelGGL(kq_units_kernel<12>, dim3((threads + 255u) / 256u), dim3(256), 0, s, src,
-                       static_cast<uint32_t>(stride), static_cast<uint32_t>(rows), static_cast<uint32_t>(nb), groups,
-                       dst);
-  else
-    hipLaunchKernelGGL(kq_units_kernel<14>, dim3((threads + 255u) / 256u), dim3(256), 0, s, src,
-                       static_cast<uint32_t>(stride), static_cast<uint32_t>(rows), static_cast<uint32_t>(nb), groups,
-                       dst);
-  return hipGetLastError();
 }
 
 namespace {
@@ -2113,17 +1993,10 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
     // 12.9). Tuning::kq_nt and Tuning::norm_nt force it.
     uint32_t nt = kThreads, nit = ni;
     if (onepass_nt) {
-      // On the matrices' unit-layout copies when every job has one and each
-      // workgroup's rows are whole groups of 16 blocks (contiguous rows:
-      // 2048x5632 takes 8 rows of 22 blocks, 11 groups), so each load
-      // instruction of a wave reads consecutive bytes. Tuning::kq_units =
-      // false keeps the native rows.
-      bool units = tuning().kq_units;
-      for (uint32_t i = 0; i < jobs.n; i++)
-        units = units && jobs.j[i].wu && jobs.j[i].il == 0u && (R * jobs.j[i].nb) % 16u == 0u;
-      k = kq_onepass_kernel(type_id, onepass_nt, units);
-      if (units)
-        for (uint32_t i = 0; i < jobs.n; i++) jobs.j[i].w = jobs.j[i].wu;
+      // each workgroup's rows are whole groups of 16 blocks where R * nb is a
+      // multiple of 16 (2048x5632 takes 8 rows of 22 blocks, 11 groups), so
+      // each load instruction of a wave reads consecutive bytes
+      k = kq_onepass_kernel(type_id, onepass_nt);
       nt = onepass_nt;
     } else if (balanced) {
       k = kq_wide_kernel(type_id, fq, ni, norm != nullptr, pair);
@@ -2146,16 +2019,15 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
       }
     }
     // One token, one preload round, and every job's blocks a power of two
-    // no larger than the teams, in a matrix with a unit-layout copy, with
-    // every wave's rows starting a group of 16 blocks: the fixed-column walk
-    // (BlockWalk) on those copies. Tuning::kq_fix = false keeps the general
-    // walk on the native rows.
-    if (!onepass_nt && T == 1 && FUSED && fq == 1u && tuning().kq_fix && tuning().kq_units) {
+    // no larger than the teams covering whole rows, with every wave's rows
+    // starting a group of 16 blocks: the fixed-column walk (BlockWalk).
+    // Tuning::kq_fix = false keeps the general walk.
+    if (!onepass_nt && T == 1 && FUSED && fq == 1u && tuning().kq_fix) {
       bool fix = true;
       for (uint32_t i = 0; i < jobs.n; i++) {
         const GemvJob& j = jobs.j[i];
         const uint32_t b = j.nb;
-        fix = fix && b != 0u && (b & (b - 1u)) == 0u && b <= nt / 4u && j.wu && (!pair || j.wu2);
+        fix = fix && b != 0u && (b & (b - 1u)) == 0u && b <= nt / 4u && b == j.ub;
         // rows per group of 16 blocks; a workgroup's first row, and an
         // interleave chunk, must be whole groups
         const uint32_t rpu = b != 0u && b < 16u ? 16u / b : 1u;
@@ -2165,13 +2037,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
         fix = fix && (!pair || j.rows % rpu == 0u);
       }
       const KqFn kf = fix ? kq_fix_kernel(type_id, nit, norm != nullptr, pair, nt) : KqFn{};
-      if (kf) {
-        k = kf;
-        for (uint32_t i = 0; i < jobs.n; i++) {
-          jobs.j[i].w = jobs.j[i].wu;
-          if (pair) jobs.j[i].w2 = jobs.j[i].wu2;
-        }
-      }
+      if (kf) k = kf;
     }
     if (!k) return hipErrorNotSupported;
     // the argument order of the kernel chosen (KqFn::preload)
@@ -2478,14 +2344,14 @@ hipError_t launch_gemv_fused(uint32_t type_id, const GemvJobs& jobs, const float
   }
 }
 
-hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
-                                 float* out, size_t out_len, hipStream_t s) {
+hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* mat, size_t pitch, uint32_t row, uint32_t nb,
+                                 float scale, float* out, size_t out_len, hipStream_t s) {
   const size_t n = static_cast<size_t>(nb) * (type_id == 36u ? 128u : 256u);
   const size_t m = n < out_len ? n : out_len;
   if (m == 0) return hipSuccess;
   const uint32_t grid = static_cast<uint32_t>((m + kThreads - 1) / kThreads);
   hipLaunchKernelGGL(dequantize_row_kernel, dim3(grid < 1024u ? grid : 1024u), dim3(kThreads), 0, s,
-                     type_id, row, nb, scale, out, out_len);
+                     type_id, mat, pitch, row, nb, scale, out, out_len);
   return hipGetLastError();
 }
 

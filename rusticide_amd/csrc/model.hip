@@ -40,56 +40,23 @@ constexpr uint32_t kNormThreads = 256;
 
 
 
-// Token rows of token_embd into hidden (Matrix::copy_row, weights.rs:120-150).
-// Element e of a token_embd row (Matrix::copy_row's dequantization).
-__device__ __forceinline__ float embed_value(uint32_t type_id, const uint8_t* row, uint32_t e) {
-  {
-    float v;
-    if (type_id == 0u) {
-      v = reinterpret_cast<const float*>(row)[e];
-    } else if (type_id == 12u) {  // quantize/src/q4_k.rs:32-66
-      const uint32_t b = e / 256u, l = e % 256u;
-      const uint8_t* blk = row + static_cast<size_t>(b) * 144u;
-      const float d = f16_lo(load4(blk)), dmin = f16_hi(load4(blk));
-      const uint32_t j = l / 32u, li = l % 32u;
-      const uint8_t* s = blk + 4;
-      uint32_t sc, m;
-      if (j < 4u) {
-        sc = s[j] & 63u;
-        m = s[j + 4u] & 63u;
-      } else {
-        sc = (s[j + 4u] & 0x0Fu) | ((s[j - 4u] >> 6) << 4);
-        m = (s[j + 4u] >> 4) | ((s[j] >> 6) << 4);
-      }
-      const uint8_t qb = blk[16u + 32u * (j / 2u) + li];
-      const uint32_t qv = (j & 1u) ? (qb >> 4) : (qb & 0x0Fu);
-      const float ds = d * static_cast<float>(sc), dm = dmin * static_cast<float>(m);
-      const float prod = ds * static_cast<float>(qv);
-      v = prod - dm;
-    } else {  // Q6_K, quantize/src/q6_k.rs:13-43
-      const uint32_t b = e / 256u, l = e % 256u;
-      const uint8_t* blk = row + static_cast<size_t>(b) * 210u;
-      const float d = f16_lo(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
-      const uint32_t hh = l / 128u, rr = (l % 128u) / 32u, li = l % 32u;
-      const uint8_t low = blk[64u * hh + 32u * (rr & 1u) + li];
-      const uint8_t high = blk[128u + 32u * hh + li];
-      const uint32_t nib = rr < 2u ? (low & 0x0Fu) : (low >> 4);
-      const int32_t qv = static_cast<int32_t>(nib | (((high >> (2u * rr)) & 3u) << 4)) - 32;
-      const float sc = static_cast<float>(static_cast<int8_t>(blk[192u + 8u * hh + 2u * rr + li / 16u]));
-      const float ds = d * sc;
-      v = ds * static_cast<float>(qv);
-    }
-    return v;
-  }
+// Element e of row `row` of token_embd (Matrix::copy_row's dequantization,
+// weights.rs:120-150): f32 rows of `pitch` bytes, or Q4_K / Q6_K in the unit
+// layout with `pitch` blocks a row.
+__device__ __forceinline__ float embed_value(uint32_t type_id, const uint8_t* data, size_t pitch, uint32_t row,
+                                             uint32_t e) {
+  if (type_id == 0u) return reinterpret_cast<const float*>(data + static_cast<size_t>(row) * pitch)[e];
+  return unit_weight(data, type_id, row * static_cast<uint32_t>(pitch) + e / 256u, e % 256u);
 }
 
-__global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint8_t* data, size_t stride,
+// Token rows of token_embd into hidden.
+__global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint8_t* data, size_t pitch,
                                                     const uint32_t* tokens, uint32_t width, float* hidden) {
   const uint32_t t = blockIdx.y;
-  const uint8_t* row = data + static_cast<size_t>(tokens[t]) * stride;
+  const uint32_t row = tokens[t];
   float* out = hidden + static_cast<size_t>(t) * width;
   for (uint32_t e = blockIdx.x * 256u + threadIdx.x; e < width; e += gridDim.x * 256u)
-    out[e] = embed_value(type_id, row, e);
+    out[e] = embed_value(type_id, data, pitch, row, e);
 }
 
 // hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t]),
@@ -774,13 +741,6 @@ __device__ __forceinline__ int32_t total_key(float f) {
   return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
 }
 
-// Greedy pick over the logits: NaN as -inf, max by total order, the last
-// maximum wins; out[0] = token, out[1] = 1 when some logit is finite. When
-// `tokens` is given the token is also appended at tokens[count[0]] (the
-// generation's record), count[0] advanced, and count[1] set for good once a
-// pick finds no finite logit. When `hidden` is given, the picked token's
-// embedding row (emb_type blocks at emb_data, emb_stride bytes per row) is
-// written there: the next step's input.
 // (key, index) as one unsigned 64-bit value in the pick's order: the
 // total-order key (made unsigned) above the index (a larger index wins a
 // tie: the last maximum). Keys of real logits are above INT32_MIN (a NaN
@@ -808,14 +768,15 @@ __device__ __forceinline__ uint64_t wave_max_code(uint64_t c) {
 // `tokens` is given the token is also appended at tokens[count[0]] (the
 // generation's record), count[0] advanced, and count[1] set for good once a
 // pick finds no finite logit. When `hidden` is given, the picked token's
-// embedding row (emb_type blocks at emb_data, emb_stride bytes per row) is
+// embedding row (token_embd's type emb_type at emb_data, row pitch
+// emb_pitch as matrix_pitch gives it) is
 // written there: the next step's input.
 // Each thread issues all of its loads (32 a pass, clamped into range) before
 // it looks at any, and the record's count is read first of all: the pick
 // waits on one memory round trip, not one per eight loads.
 __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint32_t n, uint32_t* out,
                                                       uint32_t* tokens, uint32_t* count, uint32_t emb_type,
-                                                      const uint8_t* emb_data, size_t emb_stride, uint32_t width,
+                                                      const uint8_t* emb_data, size_t emb_pitch, uint32_t width,
                                                       float* hidden) {
   constexpr uint32_t kPer = 32;
   __shared__ uint32_t shi[16], slo[16], sfin[16];
@@ -869,8 +830,7 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint3
   }
   if (!hidden) return;  // uniform
   __syncthreads();
-  const uint8_t* row = emb_data + static_cast<size_t>(s_pick) * emb_stride;
-  for (uint32_t e = threadIdx.x; e < width; e += 1024u) hidden[e] = embed_value(emb_type, row, e);
+  for (uint32_t e = threadIdx.x; e < width; e += 1024u) hidden[e] = embed_value(emb_type, emb_data, emb_pitch, s_pick, e);
 }
 
 // the float functions of the kernels above, one per element (test hook)
@@ -1068,7 +1028,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   hipStream_t s = d->stream;
   const rh_matrix* E = d->token_embd;
   hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, nn), dim3(256), 0, s, rh_matrix_type(E),
-                     matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
+                     matrix_data(E), matrix_pitch(E), tokens, w, d->hidden);
   RHD(hipGetLastError());
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
   const size_t norm_lds = add_norm_lds(w);
@@ -1136,7 +1096,7 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start,
   const rh_matrix* E = d->token_embd;
   if (!embedded) {
     hipLaunchKernelGGL(embed_kernel, dim3((w + 255u) / 256u, 1u), dim3(256), 0, s, rh_matrix_type(E),
-                       matrix_data(E), matrix_stride(E), tokens, w, d->hidden);
+                       matrix_data(E), matrix_pitch(E), tokens, w, d->hidden);
     RHD(hipGetLastError());
   }
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
@@ -1606,7 +1566,7 @@ rh_status rh_decoder_generate_greedy(rh_decoder* d, const uint32_t* prompt, size
     // on the norm-fused path the pick also writes the next step's embedding
     const rh_matrix* E = d->token_embd;
     hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, d->logits, static_cast<uint32_t>(d->c.vocab_size),
-                       d->pick, d->record, d->count, rh_matrix_type(E), matrix_data(E), matrix_stride(E),
+                       d->pick, d->record, d->count, rh_matrix_type(E), matrix_data(E), matrix_pitch(E),
                        static_cast<uint32_t>(d->c.embedding_length), d->fuse_norm ? d->hidden : nullptr);
     RHD(hipGetLastError());
     emitted++;

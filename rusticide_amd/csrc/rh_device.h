@@ -585,4 +585,77 @@ __device__ __forceinline__ void quantize_super_block(const float (&f)[4], uint32
   if (lane < 8u) q.scales[b0 + lane] = step;
 }
 
+// ---------------------------------------------------------------- unit layout
+// Q4_K and Q6_K matrices live in HBM once, in the unit layout: the blocks in
+// row-major order (block e = row * blocks_per_row + column), cut into groups
+// of 16, each group laid out the way a wave of 16 four-lane teams reads it
+// (lane l = 4 * tw + p of the team at position tw). Group g of a matrix
+// starts at g * kUnitBytes{Q4,Q6}; block e is at position tw = e & 15 of
+// group e >> 4.
+//   Q4_K (2304 bytes): headers (d, dmin, scales[12]) [16][16] at 16 tw |
+//     qs[0..64) of block tw at 256 + 64 tw | qs[64..128) at 1280 + 64 tw.
+//   Q6_K (3360 bytes): ql[64h + x], x < 32, at 64 tw + 32h + x |
+//     ql[64h + 32 + x] at 1024 + 64 tw + 32h + x | qh[c] at 2048 + 64 tw + c |
+//     scales[16] at 3072 + 16 tw | d at 3328 + 2 tw.
+// So a team lane p's 16-byte pieces of its block sit at one offset each
+// (Q4_K: 256 + 64 tw + 16p, 1280 + 64 tw + 16p; Q6_K: 64 tw + 16p,
+// 1024 + 64 tw + 16p, 2048 + 64 tw + 16p), and a wave whose 16 teams read the
+// 16 blocks of a group reads 1 KB of consecutive bytes per load.
+constexpr uint32_t kUnitBytesQ4 = 16u * 144u;
+constexpr uint32_t kUnitBytesQ6 = 16u * 210u;
+
+__device__ __forceinline__ const uint8_t* unit_group(const uint8_t* m, uint32_t type_id, uint32_t e) {
+  return m + static_cast<size_t>(e >> 4) * (type_id == 12u ? kUnitBytesQ4 : kUnitBytesQ6);
+}
+
+// Byte c of block e in its GGUF order (Q4_K 0..143, Q6_K 0..209).
+__device__ __forceinline__ uint8_t unit_byte(const uint8_t* m, uint32_t type_id, uint32_t e, uint32_t c) {
+  const uint8_t* g = unit_group(m, type_id, e);
+  const uint32_t tw = e & 15u;
+  if (type_id == 12u) {
+    if (c < 16u) return g[16u * tw + c];
+    c -= 16u;
+    return c < 64u ? g[256u + 64u * tw + c] : g[1280u + 64u * tw + (c - 64u)];
+  }
+  if (c < 128u) {
+    const uint32_t h = c >> 6, x = c & 63u;
+    return x < 32u ? g[64u * tw + 32u * h + x] : g[1024u + 64u * tw + 32u * h + (x - 32u)];
+  }
+  if (c < 192u) return g[2048u + 64u * tw + (c - 128u)];
+  if (c < 208u) return g[3072u + 16u * tw + (c - 192u)];
+  return g[3328u + 2u * tw + (c - 208u)];
+}
+
+// Weight l (0..255) of Q4_K / Q6_K block e, dequantized as Matrix::copy_row
+// does (quantize/src/q4_k.rs:32-66, q6_k.rs:13-43), from the unit layout.
+__device__ __forceinline__ float unit_weight(const uint8_t* m, uint32_t type_id, uint32_t e, uint32_t l) {
+  auto byte = [&](uint32_t c) { return static_cast<uint32_t>(unit_byte(m, type_id, e, c)); };
+  if (type_id == 12u) {
+    const float d = f16_lo(byte(0) | (byte(1) << 8)), dmin = f16_lo(byte(2) | (byte(3) << 8));
+    const uint32_t j = l / 32u, li = l % 32u;
+    uint32_t sc, mn;
+    if (j < 4u) {
+      sc = byte(4u + j) & 63u;
+      mn = byte(8u + j) & 63u;
+    } else {
+      sc = (byte(8u + j) & 0x0Fu) | ((byte(j) >> 6) << 4);
+      mn = (byte(8u + j) >> 4) | ((byte(4u + j) >> 6) << 4);
+    }
+    const uint32_t qb = byte(16u + 32u * (j / 2u) + li);
+    const uint32_t qv = (j & 1u) ? (qb >> 4) : (qb & 0x0Fu);
+    const float ds = d * static_cast<float>(sc), dm = dmin * static_cast<float>(mn);
+    const float prod = ds * static_cast<float>(qv);
+    return prod - dm;
+  }
+  const float d = f16_lo(byte(208) | (byte(209) << 8));
+  const uint32_t hh = l / 128u, rr = (l % 128u) / 32u, li = l % 32u;
+  const uint32_t low = byte(64u * hh + 32u * (rr & 1u) + li);
+  const uint32_t high = byte(128u + 32u * hh + li);
+  const uint32_t nib = rr < 2u ? (low & 0x0Fu) : (low >> 4);
+  const int32_t qv = static_cast<int32_t>(nib | (((high >> (2u * rr)) & 3u) << 4)) - 32;
+  const float sc = static_cast<float>(static_cast<int8_t>(byte(192u + 8u * hh + 2u * rr + li / 16u)));
+  const float ds = d * sc;
+  return ds * static_cast<float>(qv);
+}
+
 }  // namespace rh

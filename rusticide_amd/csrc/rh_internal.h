@@ -34,14 +34,16 @@ struct Q8Dev {
 
 // One matrix of a grouped launch.
 struct GemvJob {
-  const uint8_t* w;     // row-major native blocks (or f32 rows)
-  // A second matrix of w's shape and stride (the up projection beside the
-  // gate one): the norm-fused k-quant launch then writes silu(w x) * (w2 x)
-  // to out instead of w x.
+  // Q4_K / Q6_K: the matrix in the unit layout (rh_device.h); I2_S: rows of
+  // `stride` bytes; dense: f32 rows
+  const uint8_t* w;
+  // A second matrix of w's shape (the up projection beside the gate one):
+  // the norm-fused k-quant launch then writes silu(w x) * (w2 x) to out
+  // instead of w x.
   const uint8_t* w2;
   float* out;           // out[row * tokens + token]
   size_t out_len;
-  uint32_t stride;      // bytes between rows (a matrix stays below 4 GiB)
+  uint32_t stride;      // bytes between rows (I2_S, dense; a matrix stays below 4 GiB)
   uint32_t rows;        // rows to compute (already bounded by out_len)
   uint32_t nb;          // blocks per row both operands cover
   float scale;          // I2_S tensor scale
@@ -51,14 +53,11 @@ struct GemvJob {
   // one window of the matrix (the launcher sets it only when the rows tile
   // the grid exactly).
   uint32_t il = 0;
-  // The matrices' copies in the unit layout (launch_kq_units), or null; set
-  // only when the job covers whole rows (nb = the matrix's blocks per row).
-  // The launcher swaps them into w and w2 when it takes the fixed-column walk.
-  const uint8_t* wu = nullptr;
-  const uint8_t* wu2 = nullptr;
+  uint32_t ub = 0;      // the matrix's blocks per row: block (r, b) is unit block r * ub + b
+  uint32_t pad_ = 0;
 };
-// 72 bytes: every launch's kernel arguments hold kMaxJobs of these
-static_assert(sizeof(GemvJob) == 72, "GemvJob packs into 72 bytes");
+// 64 bytes: every launch's kernel arguments hold kMaxJobs of these
+static_assert(sizeof(GemvJob) == 64, "GemvJob packs into 64 bytes");
 
 struct GemvJobs {
   GemvJob j[kMaxJobs];
@@ -95,7 +94,6 @@ struct Tuning {
   bool kq_fix = true;      // RUSTICIDE_HIP_KQ_FIX=0: the general block walk only
   bool kq_balance = true;  // RUSTICIDE_HIP_KQ_BALANCE=0: no one-workgroup-per-CU reshaping
   bool kq_onepass = true;  // RUSTICIDE_HIP_KQ_ONEPASS=0: no 768/1024-lane one-round quantization
-  bool kq_units = true;    // RUSTICIDE_HIP_KQ_UNITS=0: no kernel reads the unit-layout copies
   int i2s_groups = 0;      // RUSTICIDE_HIP_I2S_GROUPS=1|2|4 (two-token kernel)
   int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
   int i2s_nt = 0;          // RUSTICIDE_HIP_I2S_NT=256|512|1024: threads per workgroup, one token
@@ -114,17 +112,9 @@ hipError_t launch_quantize_super(const float* x, size_t width, size_t tokens, co
 hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, const Q8Dev& q,
                                hipStream_t s);
 
-// The unit layout of a k-quant matrix whose rows hold nb blocks (a power of
-// two up to 128, or 22, 24 or 30: units_eligible): the blocks in
-// row-major order, cut into groups of 16, each group stored as the 64 lanes
-// of the wave that reads it in one step of the block walk take it (the lane's 16-byte pieces side by side, then
-// the per-block scales and d), so each of that wave's loads reads
-// consecutive bytes. A group past the last row repeats the last row. Bytes:
-// units_bytes(); launch_kq_units fills `dst` from the native rows.
+// Bytes of a k-quant matrix of rows x nb blocks in the unit layout
+// (rh_device.h): whole groups of 16 blocks.
 size_t units_bytes(uint32_t type_id, size_t rows, size_t nb);
-bool units_eligible(uint32_t type_id, size_t rows, size_t nb);
-hipError_t launch_kq_units(uint32_t type_id, const uint8_t* src, size_t stride, size_t rows, size_t nb, uint8_t* dst,
-                           hipStream_t s);
 
 // Grouped GEMV for one format: tokens [t0, t0+tn) of `tokens` total.
 hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, const float* x,
@@ -177,7 +167,9 @@ uint64_t ctx_scratch_generation(const rh_ctx* ctx);
 // Records `msg` as the context's rh_last_error and returns `st`.
 rh_status set_last_error(rh_ctx* ctx, rh_status st, const std::string& msg);
 const uint8_t* matrix_data(const rh_matrix* m);
-size_t matrix_stride(const rh_matrix* m);
+// What locates a row: its byte stride for f32 rows, its block count for a
+// k-quant matrix in the unit layout.
+size_t matrix_pitch(const rh_matrix* m);
 
 // A matrix checked and allocated on the device (Matrix::load_on's checks,
 // model/src/weights.rs:53-98) whose image is not uploaded yet: `src` holds
@@ -194,8 +186,10 @@ rh_status matrix_prepare(rh_ctx* ctx, uint32_t type_id, const void* data, size_t
 // allocated for the caller to free.
 rh_status matrix_upload(rh_ctx* ctx, PendingUpload* p, size_t n);
 
-hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* row, uint32_t nb, float scale,
-                                 float* out, size_t out_len, hipStream_t s);
+// Row `row` of matrix data `m` (pitch: matrix_pitch), its first nb blocks
+// dequantized into out (at most out_len values).
+hipError_t launch_dequantize_row(uint32_t type_id, const uint8_t* m, size_t pitch, uint32_t row, uint32_t nb,
+                                 float scale, float* out, size_t out_len, hipStream_t s);
 
 // rh_matmul_batch_device for one token whose activation the k-quant
 // kernels form themselves from the hidden state: normalize(hidden + delta) *

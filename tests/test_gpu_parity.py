@@ -44,11 +44,9 @@ VARIANTS = {
     # 17- to 32-block rows on 512 lanes (two rounds of quantization) instead
     # of 768 or 1024
     "no-onepass": {"RUSTICIDE_HIP_KQ_ONEPASS": "0"},
-    # every kernel on the native blocks, none on the unit-layout copies
-    "native": {"RUSTICIDE_HIP_KQ_UNITS": "0"},
 }
 SWITCHES = ("RUSTICIDE_HIP_GEMV", "RUSTICIDE_HIP_GEMV_NI", "RUSTICIDE_HIP_KQ_NT", "RUSTICIDE_HIP_KQ_FIX",
-            "RUSTICIDE_HIP_KQ_BALANCE", "RUSTICIDE_HIP_KQ_ONEPASS", "RUSTICIDE_HIP_KQ_UNITS")
+            "RUSTICIDE_HIP_KQ_BALANCE", "RUSTICIDE_HIP_KQ_ONEPASS")
 
 
 @pytest.fixture(params=list(VARIANTS))
