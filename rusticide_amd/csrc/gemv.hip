@@ -366,9 +366,11 @@ __device__ __forceinline__ float terms_sum(const float* t, uint32_t nb) {
 // Each row's block terms summed in block order from -0.0
 // (portable/int_dot/rows.rs:9-12,59) and written; PAIR writes
 // silu(gate) * up with silu_mul's expressions (portable/elementwise.rs:6-9).
-template <int T, bool PAIR, uint32_t NT = kThreads>
+// PICK (one token, a norm-fused launch): with `pick` set, the workgroup also
+// writes the greedy pick's partial over its rows to pick[blockIdx.x].
+template <int T, bool PAIR, uint32_t NT = kThreads, bool PICK = false>
 __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, const float* terms, uint32_t nb,
-                                           uint32_t nbmax, size_t tokens, size_t t0) {
+                                           uint32_t nbmax, size_t tokens, size_t t0, PickPart* pick = nullptr) {
   if constexpr (PAIR) {
     static_assert(T == 1, "a gate/up pair serves one token");
     for (uint32_t r = threadIdx.x; r < g.nh; r += NT) {
@@ -380,11 +382,42 @@ __device__ __forceinline__ void write_rows(const GemvJob& J, const WgRows& g, co
       if (idx < J.out_len) J.out[idx] = sg * us;
     }
   } else {
+    const bool want = PICK && pick != nullptr;  // uniform
+    uint64_t best = 0;
+    uint32_t fin = 0;
     for (uint32_t i = threadIdx.x; i < g.nrows * T; i += NT) {
       const uint32_t r = i / T, t = i - r * T;
       const float s = terms_sum<T>(terms + __umul24(r, nbmax) * T + t, nb);
-      const size_t idx = static_cast<size_t>(row_of(g, r)) * tokens + t0 + t;
-      if (idx < J.out_len) J.out[idx] = s;
+      const uint32_t row = row_of(g, r);
+      const size_t idx = static_cast<size_t>(row) * tokens + t0 + t;
+      if (idx < J.out_len) {
+        J.out[idx] = s;
+        if (want) {
+          fin |= __builtin_isfinite(s) ? 1u : 0u;
+          const uint64_t c = pick_code(total_key(s != s ? -INFINITY : s), row);
+          best = c > best ? c : best;
+        }
+      }
+    }
+    if constexpr (PICK) {
+      if (!want) return;
+      __shared__ uint64_t s_best[NT / 64u];
+      __shared__ uint32_t s_fin[NT / 64u];
+      best = wave_max_code(best);
+      fin = __ballot(fin != 0u) ? 1u : 0u;
+      if ((threadIdx.x & 63u) == 0) {
+        s_best[threadIdx.x >> 6] = best;
+        s_fin[threadIdx.x >> 6] = fin;
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        PickPart part{0, 0, 0};
+        for (uint32_t w = 0; w < NT / 64u; w++) {
+          part.code = s_best[w] > part.code ? s_best[w] : part.code;
+          part.fin |= s_fin[w];
+        }
+        pick[blockIdx.x] = part;
+      }
     }
   }
 }
@@ -685,7 +718,7 @@ __device__ __forceinline__ void q4k_body(const GemvJob& J, const Q8Dev& q, const
     }
   }
   __syncthreads();
-  write_rows<T, PAIR, NT>(J, wr, terms, J.nb, nbmax, tokens, t0);
+  write_rows<T, PAIR, NT, NORM && !PAIR && T == 1>(J, wr, terms, J.nb, nbmax, tokens, t0, nrm.pick);
 }
 
 // FIX: every job's nb is a power of two up to NT/4 (the launch checks). It is
@@ -823,7 +856,7 @@ __device__ __forceinline__ void q6k_body(const GemvJob& J, const Q8Dev& q, const
     }
   }
   __syncthreads();
-  write_rows<T, PAIR, NT>(J, wr, terms, J.nb, nbmax, tokens, t0);
+  write_rows<T, PAIR, NT, NORM && !PAIR && T == 1>(J, wr, terms, J.nb, nbmax, tokens, t0, nrm.pick);
 }
 
 // FIX: every job's nb is a power of two up to NT/4 (the launch checks). It is
@@ -2045,6 +2078,7 @@ hipError_t launch_t(uint32_t type_id, GemvJobs jobs, const Q8Dev& q, const float
                          const_cast<uint32_t*>(&nbl), &tokens, &t0, &nrm};
     void* args_pl[] = {&xin, &width, const_cast<uint32_t*>(&R), const_cast<uint32_t*>(&nbl), &tokens, &t0,
                        &jobs, const_cast<Q8Dev*>(&q), &nrm};
+    if (norm && norm->grid_out) *norm->grid_out = wgs;
     return hipLaunchKernel(k.fn, dim3(wgs), dim3(nt), k.preload ? args_pl : args_jobs, lds, s);
   }
   if (tuning().i2s_one) {

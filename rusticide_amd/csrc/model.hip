@@ -735,33 +735,6 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const 
   hf[i] = s * up[static_cast<size_t>(e) * n + t];
 }
 
-// f32::total_cmp's order as an i32 key.
-__device__ __forceinline__ int32_t total_key(float f) {
-  const int32_t b = __float_as_int(f);
-  return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
-}
-
-// (key, index) as one unsigned 64-bit value in the pick's order: the
-// total-order key (made unsigned) above the index (a larger index wins a
-// tie: the last maximum). Keys of real logits are above INT32_MIN (a NaN
-// enters as -inf), so 0 stands for "no logit".
-__device__ __forceinline__ uint64_t pick_code(int32_t key, uint32_t idx) {
-  return (static_cast<uint64_t>(static_cast<uint32_t>(key) ^ 0x80000000u) << 32) | idx;
-}
-
-// The maximum code over the wave, in every lane: the keys first, then the
-// indices among the lanes holding the largest key.
-__device__ __forceinline__ uint64_t wave_max_code(uint64_t c) {
-  uint32_t hi = static_cast<uint32_t>(c >> 32);
-  uint32_t m = half_max_u32(hi);
-  m = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 0)),
-          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 32)));
-  uint32_t lo = hi == m ? static_cast<uint32_t>(c) : 0u;
-  lo = half_max_u32(lo);
-  lo = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), 0)),
-           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), 32)));
-  return (static_cast<uint64_t>(m) << 32) | lo;
-}
 
 // Greedy pick over the logits: NaN as -inf, max by total order, the last
 // maximum wins; out[0] = token, out[1] = 1 when some logit is finite. When
@@ -774,33 +747,15 @@ __device__ __forceinline__ uint64_t wave_max_code(uint64_t c) {
 // Each thread issues all of its loads (32 a pass, clamped into range) before
 // it looks at any, and the record's count is read first of all: the pick
 // waits on one memory round trip, not one per eight loads.
-__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint32_t n, uint32_t* out,
-                                                      uint32_t* tokens, uint32_t* count, uint32_t emb_type,
-                                                      const uint8_t* emb_data, size_t emb_pitch, uint32_t width,
-                                                      float* hidden) {
-  constexpr uint32_t kPer = 32;
+// The pick's end over a 1024-thread workgroup, each thread holding the best
+// code and the finite flag of its share: the workgroup's maximum goes to
+// out / the record, and (hidden set) the picked row of token_embd to hidden.
+__device__ __forceinline__ void pick_finish(uint64_t best, uint32_t fin, uint32_t cnt, uint32_t* out,
+                                            uint32_t* tokens, uint32_t* count, uint32_t emb_type,
+                                            const uint8_t* emb_data, size_t emb_pitch, uint32_t width,
+                                            float* hidden) {
   __shared__ uint32_t shi[16], slo[16], sfin[16];
   __shared__ uint32_t s_pick;
-  uint32_t cnt = 0;
-  if (tokens && threadIdx.x == 0) cnt = count[0];
-  uint64_t best = 0;
-  uint32_t fin = 0;
-  for (uint32_t base = 0; base < n; base += kPer * 1024u) {  // uniform
-    float v[kPer];
-#pragma unroll
-    for (uint32_t j = 0; j < kPer; j++) {
-      const uint32_t i = base + threadIdx.x + j * 1024u;
-      v[j] = logits[i < n ? i : n - 1u];
-    }
-#pragma unroll
-    for (uint32_t j = 0; j < kPer; j++) {
-      const uint32_t i = base + threadIdx.x + j * 1024u;
-      const bool in = i < n;
-      fin |= in && __builtin_isfinite(v[j]) ? 1u : 0u;
-      const uint64_t c = pick_code(total_key(v[j] != v[j] ? -INFINITY : v[j]), i);
-      best = in && c > best ? c : best;
-    }
-  }
   best = wave_max_code(best);
   fin = __ballot(fin != 0u) ? 1u : 0u;
   const uint32_t wv = threadIdx.x >> 6;
@@ -831,6 +786,53 @@ __global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint3
   if (!hidden) return;  // uniform
   __syncthreads();
   for (uint32_t e = threadIdx.x; e < width; e += 1024u) hidden[e] = embed_value(emb_type, emb_data, emb_pitch, s_pick, e);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* logits, uint32_t n, uint32_t* out,
+                                                      uint32_t* tokens, uint32_t* count, uint32_t emb_type,
+                                                      const uint8_t* emb_data, size_t emb_pitch, uint32_t width,
+                                                      float* hidden) {
+  constexpr uint32_t kPer = 32;
+  uint32_t cnt = 0;
+  if (tokens && threadIdx.x == 0) cnt = count[0];
+  uint64_t best = 0;
+  uint32_t fin = 0;
+  for (uint32_t base = 0; base < n; base += kPer * 1024u) {  // uniform
+    float v[kPer];
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t i = base + threadIdx.x + j * 1024u;
+      v[j] = logits[i < n ? i : n - 1u];
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kPer; j++) {
+      const uint32_t i = base + threadIdx.x + j * 1024u;
+      const bool in = i < n;
+      fin |= in && __builtin_isfinite(v[j]) ? 1u : 0u;
+      const uint64_t c = pick_code(total_key(v[j] != v[j] ? -INFINITY : v[j]), i);
+      best = in && c > best ? c : best;
+    }
+  }
+  pick_finish(best, fin, cnt, out, tokens, count, emb_type, emb_data, emb_pitch, width, hidden);
+}
+
+// The same pick from the output launch's per-workgroup partials (PickPart,
+// written by the norm-fused output GEMV): n records of 16 bytes instead of
+// every logit. The maximum of maxima is the maximum, in the same order.
+__global__ __launch_bounds__(1024) void argmax_parts_kernel(const PickPart* parts, uint32_t n, uint32_t* out,
+                                                            uint32_t* tokens, uint32_t* count, uint32_t emb_type,
+                                                            const uint8_t* emb_data, size_t emb_pitch,
+                                                            uint32_t width, float* hidden) {
+  uint32_t cnt = 0;
+  if (tokens && threadIdx.x == 0) cnt = count[0];
+  uint64_t best = 0;
+  uint32_t fin = 0;
+  for (uint32_t i = threadIdx.x; i < n; i += 1024u) {
+    const PickPart p = parts[i];
+    best = p.code > best ? p.code : best;
+    fin |= p.fin;
+  }
+  pick_finish(best, fin, cnt, out, tokens, count, emb_type, emb_data, emb_pitch, width, hidden);
 }
 
 // the float functions of the kernels above, one per element (test hook)
@@ -899,6 +901,10 @@ struct rh_decoder {
   float* logits = nullptr;
   uint32_t* tokens = nullptr;  // the chunk's token ids
   uint32_t* pick = nullptr;    // argmax: [token, any finite]
+  // the output launch's per-workgroup pick partials, and how many the last
+  // one-token forward wrote (0: none; the pick then reads the logits)
+  PickPart* pick_parts = nullptr;
+  uint32_t pick_n = 0;
   uint32_t* record = nullptr;  // generated tokens
   uint32_t* count = nullptr;   // [recorded, a pick found no finite logit]
   size_t record_cap = 0;
@@ -1020,6 +1026,7 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start,
 // `embedded`: a one-token forward on the norm-fused path whose embedding row
 // the greedy pick already wrote to hidden.
 rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t start, bool embedded = false) {
+  d->pick_n = 0;  // set again by a one-token output launch that writes pick partials
   if (n == 1 && d->fuse_norm) return forward_one_fused(d, tokens, start, embedded);
   const rh_decoder_config& c = d->c;
   const uint32_t w = static_cast<uint32_t>(c.embedding_length), kv = static_cast<uint32_t>(d->kv);
@@ -1181,6 +1188,8 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start,
     fo.delta = pending;
     fo.weight = d->output_norm;
     fo.eps = c.rms_norm_eps;
+    fo.pick = d->pick_parts;
+    fo.grid_out = &d->pick_n;
     const rh_job lm{out, d->logits, c.vocab_size};
     RHS(matmul_norm_device(d->ctx, h, fo, w, &lm, 1, s));
   } else {
@@ -1388,6 +1397,7 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
   const size_t cache = c.block_count * c.context_length * d->kv;
   ok = ok && dmalloc(&d->keys, cache) == hipSuccess && dmalloc(&d->values, cache) == hipSuccess &&
        dmalloc(&d->logits, c.vocab_size) == hipSuccess && dmalloc(&d->pick, 2) == hipSuccess &&
+       dmalloc(&d->pick_parts, c.vocab_size) == hipSuccess &&
        dmalloc(&d->count, 2) == hipSuccess;
   if (!ok) {
     rh_decoder_free(d);
@@ -1438,7 +1448,7 @@ void rh_decoder_free(rh_decoder* d) {
   for (void* p : {static_cast<void*>(d->output_norm), static_cast<void*>(d->rope_cos),
                   static_cast<void*>(d->rope_sin), static_cast<void*>(d->keys), static_cast<void*>(d->values),
                   static_cast<void*>(d->logits), static_cast<void*>(d->pick), static_cast<void*>(d->record),
-                  static_cast<void*>(d->count)})
+                  static_cast<void*>(d->count), static_cast<void*>(d->pick_parts)})
     if (p) hipFree(p);
   delete d;
 }
@@ -1461,6 +1471,7 @@ constexpr size_t kMaxGraphs = 8;
 // replay it while no buffer it captured has moved. A failed capture leaves
 // the eager result and no graph.
 rh_status forward_cached(rh_decoder* d, size_t n, size_t start) {
+  d->pick_n = 0;  // a replayed batch writes no pick partials
   if (n < 2 || !d->use_graphs) return forward_device(d, d->tokens, n, start);
   const uint64_t cg = ctx_scratch_generation(d->ctx);
   for (size_t i = 0; i < d->graphs.size(); i++) {
@@ -1565,9 +1576,15 @@ rh_status rh_decoder_generate_greedy(rh_decoder* d, const uint32_t* prompt, size
   for (size_t i = 0; i < max_tokens; i++) {
     // on the norm-fused path the pick also writes the next step's embedding
     const rh_matrix* E = d->token_embd;
-    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, d->logits, static_cast<uint32_t>(d->c.vocab_size),
-                       d->pick, d->record, d->count, rh_matrix_type(E), matrix_data(E), matrix_pitch(E),
-                       static_cast<uint32_t>(d->c.embedding_length), d->fuse_norm ? d->hidden : nullptr);
+    float* next = d->fuse_norm ? d->hidden : nullptr;
+    const uint32_t width = static_cast<uint32_t>(d->c.embedding_length);
+    if (d->pick_n)  // the last forward was a one-token step whose output launch wrote partials
+      hipLaunchKernelGGL(argmax_parts_kernel, dim3(1), dim3(1024), 0, s, d->pick_parts, d->pick_n, d->pick,
+                         d->record, d->count, rh_matrix_type(E), matrix_data(E), matrix_pitch(E), width, next);
+    else
+      hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, d->logits,
+                         static_cast<uint32_t>(d->c.vocab_size), d->pick, d->record, d->count, rh_matrix_type(E),
+                         matrix_data(E), matrix_pitch(E), width, next);
     RHD(hipGetLastError());
     emitted++;
     if (position == d->c.context_length) break;

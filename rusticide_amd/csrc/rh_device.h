@@ -585,6 +585,45 @@ __device__ __forceinline__ void quantize_super_block(const float (&f)[4], uint32
   if (lane < 8u) q.scales[b0 + lane] = step;
 }
 
+// ---------------------------------------------------------------- greedy pick
+// (sampling/src/filters.rs:37-43: NaN as -inf, f32::total_cmp, the last
+// maximum wins)
+// f32::total_cmp's order as an i32 key.
+__device__ __forceinline__ int32_t total_key(float f) {
+  const int32_t b = __float_as_int(f);
+  return b ^ static_cast<int32_t>(static_cast<uint32_t>(b >> 31) >> 1);
+}
+
+// (key, index) as one unsigned 64-bit value in the pick's order: the
+// total-order key (made unsigned) above the index (a larger index wins a
+// tie: the last maximum). Keys of real logits are above INT32_MIN (a NaN
+// enters as -inf), so 0 stands for "no logit".
+__device__ __forceinline__ uint64_t pick_code(int32_t key, uint32_t idx) {
+  return (static_cast<uint64_t>(static_cast<uint32_t>(key) ^ 0x80000000u) << 32) | idx;
+}
+
+// The maximum code over the wave, in every lane: the keys first, then the
+// indices among the lanes holding the largest key.
+__device__ __forceinline__ uint64_t wave_max_code(uint64_t c) {
+  uint32_t hi = static_cast<uint32_t>(c >> 32);
+  uint32_t m = half_max_u32(hi);
+  m = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 0)),
+          static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(m), 32)));
+  uint32_t lo = hi == m ? static_cast<uint32_t>(c) : 0u;
+  lo = half_max_u32(lo);
+  lo = max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), 0)),
+           static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(lo), 32)));
+  return (static_cast<uint64_t>(m) << 32) | lo;
+}
+
+// The pick's partial over a set of logits (one workgroup's rows): the
+// largest code and whether any logit is finite.
+struct PickPart {
+  uint64_t code;
+  uint32_t fin;
+  uint32_t pad;
+};
+
 // ---------------------------------------------------------------- unit layout
 // Q4_K and Q6_K matrices live in HBM once, in the unit layout: the blocks in
 // row-major order (block e = row * blocks_per_row + column), cut into groups

@@ -69,12 +69,18 @@ struct GemvJobs {
 // null), x = (v / sqrt(mean(v*v) + eps)) * weight, the sum of squares in
 // element order (transformer/src/norm.rs:10-14, portable/norm.rs:8-14). The
 // launch's first workgroup writes v to hidden_out when that is set.
+struct PickPart;  // rh_device.h
 struct NormIn {
   const float* delta = nullptr;
   const float* weight = nullptr;
   float eps = 0.0f;
   float* hidden_out = nullptr;
   uint32_t lds_offset = 0;  // filled by the launcher
+  // One job of one-token rows: each workgroup also writes the greedy pick's
+  // partial over its rows to pick[workgroup] (a device array), and the
+  // launcher stores the workgroup count in *grid_out (host memory).
+  PickPart* pick = nullptr;
+  uint32_t* grid_out = nullptr;
 };
 
 // Kernel choices, read from the environment by the first rh_init (and by
