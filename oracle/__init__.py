@@ -78,6 +78,12 @@ def lib():
             getattr(L, name).argtypes = [P, S, P, P, P, S]
             getattr(L, name).restype = ctypes.c_float
         L.orc_ternary_dot.argtypes = [P, S, P, P, S]
+        L.orc_avx2_available.restype = ctypes.c_int
+        L.orc_avx2_prepare.argtypes = [ctypes.c_uint32, P, S, S]
+        L.orc_avx2_prepare.restype = P
+        L.orc_avx2_free.argtypes = [P]
+        L.orc_avx2_matvec.argtypes = [P, P, S, P, S, ctypes.c_int]
+        L.orc_avx2_matvec.restype = ctypes.c_int
         L.orc_ternary_dot.restype = ctypes.c_int32
         L.orc_ternary_product.argtypes = [P, S, P, P, P, S, ctypes.c_float]
         L.orc_ternary_product.restype = ctypes.c_float
@@ -258,6 +264,38 @@ def matmul_batch(inputs, tokens: int, jobs, threads: int = 1) -> None:
 
 def matvec_batch(x, jobs, threads: int = 1) -> None:
     matmul_batch(x, 1, jobs, threads)
+
+
+class Avx2Matrix:
+    """A Q4_K / Q6_K matrix repacked into the reference's eight-row avx2 units
+    (rh_avx2.c): the CPU baseline's timing of rusticide's x86 kernels."""
+
+    def __init__(self, type_id: int, data, rows: int, row_bytes: int):
+        self._data = np.ascontiguousarray(data, np.uint8)
+        self.rows = rows
+        self.h = lib().orc_avx2_prepare(type_id, self._data.ctypes.data, rows, row_bytes)
+        if not self.h:
+            raise ValueError("the avx2 units need avx2+fma, Q4_K/Q6_K and rows a multiple of 8")
+
+    @staticmethod
+    def available() -> bool:
+        return bool(lib().orc_avx2_available())
+
+    def matvec(self, x, out, threads: int = 1) -> bool:
+        """out[r] = row r . x; False when x quantizes to the quant -128 (out untouched)."""
+        x = np.ascontiguousarray(x, np.float32)
+        return bool(lib().orc_avx2_matvec(self.h, x.ctypes.data, x.size, out.ctypes.data, out.size, threads))
+
+    def close(self) -> None:
+        if self.h:
+            lib().orc_avx2_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 def ternary_dot_matrix_i32(data, row_bytes_: int, inputs, tokens: int) -> np.ndarray:

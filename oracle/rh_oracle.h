@@ -97,6 +97,20 @@ void orc_ternary_dot_matrix_i32(const uint8_t *data, size_t data_len, size_t row
                                 const float *inputs, size_t inputs_len, size_t tokens,
                                 int32_t *out, size_t out_len);
 
+/* ------------------------------------------- the avx2 adapter (rh_avx2.c)
+ * The reference's x86 Q4_K / Q6_K kernels (crates/rusticide-simd/src/avx2/
+ * {q4_k,q6_k}/vector.rs) over its eight-row units (group/{q4_k,q6_k}.rs),
+ * for the CPU baseline. prepare: NULL unless the CPU has avx2 and fma, the
+ * format is Q4_K / Q6_K and rows is a multiple of 8. matvec: one token
+ * (Q8_K-quantized here) against every row, threads workers; 0 when the
+ * activation holds the quant -128 (the reference then keeps the portable
+ * kernel), else 1. */
+typedef struct orc_avx2_matrix orc_avx2_matrix;
+int orc_avx2_available(void);
+orc_avx2_matrix *orc_avx2_prepare(uint32_t type_id, const uint8_t *data, size_t rows, size_t row_bytes);
+void orc_avx2_free(orc_avx2_matrix *m);
+int orc_avx2_matvec(const orc_avx2_matrix *m, const float *x, size_t len, float *out, size_t out_len, int threads);
+
 /* ------------------------------------------------------------- decoder */
 
 /* DecoderConfig (crates/rusticide-transformer/src/config.rs:19-33), llama
