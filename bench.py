@@ -22,8 +22,8 @@ longer holds.
 summary in profiles/ (FETCH_SIZE + WRITE_SIZE, calibrated on a device copy of
 known size), when that summary covers the workload.
 
-`also.prefill_gemm` is the MFMA path at the prefill shapes: Q4_K 5632x2048
-and I2_S 6912x2560 weights against 128, 512 and 2048 tokens (the whole
+`also.prefill_gemm` is the MFMA path at the prefill shapes: Q4_K 5632x2048,
+Q6_K 2048x5632 and I2_S 6912x2560 weights against 128, 512 and 2048 tokens (the whole
 matmul_batch step and the GEMM kernel alone on pre-quantized activations), as
 int8 MFMA utilisation against the 5.0 POPS dense peak, counting
 2*rows*cols*tokens operations.
@@ -39,6 +39,11 @@ The model reaches the device as a GGUF file (rusticide_amd.gguf writes it to
 a temporary file): `gguf_load` times mapping and parsing it (rh_gguf_open)
 and the upload of its tensors to HBM (rh_gguf_model_load), beside a plain
 copy from page-locked host memory, the ceiling of any upload.
+
+`cpu_baseline` is the reference's CPU path on this job's share of the host's
+cores, restated in C (oracle/): for Q4_K/Q6_K the avx2 restatement of its x86
+adapter (rh_avx2.c, eight-row units, the repack done before timing), with the
+portable scalar restatement's figure beside it.
 
 Prints one JSON line on stdout; progress goes to stderr.
 """
@@ -68,17 +73,17 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.json")
 WORKLOADS = {
     # name: (type_id, rows, cols, description, kernel the step launches)
     "q6k_lm_head": (14, 32000, 2048, "Q6_K x f32 GEMV 32000x2048 (TinyLlama lm_head), batch 1",
-                    "gemv_q6k_kernel<1, 8, 1, false, false, 512u, true, true>"),
+                    "gemv_q6k_kernel<1, 8, 1, false, false, 512u, true>"),
     "q6k_ffn_down": (14, 2048, 5632, "Q6_K x f32 GEMV 2048x5632 (TinyLlama ffn_down), batch 1",
-                     "gemv_q6k_kernel_pl<1, 1, 4, false, false, 768u, false, true>"),
+                     "gemv_q6k_kernel_pl<1, 1, 4, false, false, 768u, false>"),
     "q4k_ffn_gate": (12, 5632, 2048, "Q4_K x f32 GEMV 5632x2048 (TinyLlama ffn_gate), batch 1",
-                     "gemv_q4k_kernel_pl<1, 2, 1, false, false, 512u, true, true>"),
+                     "gemv_q4k_kernel_pl<1, 2, 1, false, false, 512u, true>"),
     "i2s_up": (36, 6912, 2560, "I2_S x int8 GEMV 6912x2560 (BitNet 2B4T up/gate), batch 1",
                "gemv_i2s_one_kernel<256u, 8, 5, true>"),
     "i2s_down": (36, 2560, 6912, "I2_S x int8 GEMV 2560x6912 (BitNet 2B4T down), batch 1",
                  "gemv_i2s_one_kernel<512u, 32, 4, true>"),
     "q4k_32000": (12, 32000, 2048, "Q4_K x f32 GEMV 32000x2048 (lm_head shape in Q4_K), batch 1",
-                  "gemv_q4k_kernel<1, 8, 1, false, false, 512u, true, true>"),
+                  "gemv_q4k_kernel<1, 8, 1, false, false, 512u, true>"),
 }
 HEADLINE = "q6k_lm_head"
 
@@ -102,8 +107,7 @@ def load_rotation(ctx, name: str):
     data = synth.matrix(type_id, rows, cols, seed=1)
     one = R.Matrix.load(ctx, type_id, data, rows, cols)
     # copies enough that the bytes one launch reads, over all of them, pass
-    # ROTATE_BYTES (a k-quant matrix also holds a regrouped copy, which the
-    # one-token kernels read instead of its native rows)
+    # ROTATE_BYTES
     ncopies = max(2, math.ceil(ROTATE_BYTES / algorithmic_bytes(type_id, rows, cols)))
     return data, [one] + [R.Matrix.load(ctx, type_id, data, rows, cols) for _ in range(ncopies - 1)]
 
@@ -362,6 +366,7 @@ def measure_cpu(res: dict, seconds: float):
     v_gbs = res["bytes"] / (el_v / n_v) / 1e9
     return {
         "value": round(v_gbs, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+        "label": "avx2 restatement",
         "sample": (f"the avx2 C restatement of the reference's x86 adapter (eight-row units, "
                    f"vpmaddubsw/vpmaddwd, its repack done before timing): {n_v} full {rows}x{cols} GEMVs "
                    f"incl. activation quantization, {el_v:.2f} s wall on {where}; "
@@ -565,7 +570,7 @@ def traffic_for(name: str):
 
 def pmc_probe(steps: int) -> int:
     """A short, fixed sequence for `rocprofv3 --pmc` runs: each GEMV workload's
-    step on rotating copies, the prefill GEMM at 2048 tokens, then
+    step on rotating copies, the prefill GEMMs at 512 and 2048 tokens, then
     device-to-device copies of a known size (the calibration for the
     counters)."""
     import rusticide_amd as R
@@ -583,18 +588,20 @@ def pmc_probe(steps: int) -> int:
         for m in mats:
             m.free()
         log(f"[pmc] {name}: {steps} steps")
-    # the prefill GEMM at 2048 tokens, for its MFMA / VALU / LDS counters
-    rows, cols, T = 5632, 2048, 2048
-    m = R.Matrix.load(ctx, 12, synth.matrix(12, rows, cols, seed=1), rows, cols)
-    x = H.DeviceArray.from_numpy(synth.normal_f32(T * cols, seed=2))
-    out = H.DeviceArray(rows * T)
-    q8 = R.Q8(ctx).quantize(x, T, R.SUPER_BLOCK)
-    for _ in range(5):
-        R.dot_matrix_device(m, q8, out)
-    H.synchronize()
-    q8.free()
-    m.free()
-    log(f"[pmc] prefill GEMM Q4_K {rows}x{cols} x {T} tokens: 5 launches")
+    # the prefill GEMMs, for their MFMA / VALU / LDS counters: Q4_K ffn_gate
+    # and Q6_K ffn_down at 512 and 2048 tokens, five launches each, in order
+    for type_id, rows, cols in ((12, 5632, 2048), (14, 2048, 5632)):
+        m = R.Matrix.load(ctx, type_id, synth.matrix(type_id, rows, cols, seed=1), rows, cols)
+        for T in (512, 2048):
+            x = H.DeviceArray.from_numpy(synth.normal_f32(T * cols, seed=2))
+            out = H.DeviceArray(rows * T)
+            q8 = R.Q8(ctx).quantize(x, T, R.SUPER_BLOCK)
+            for _ in range(5):
+                R.dot_matrix_device(m, q8, out)
+            H.synchronize()
+            q8.free()
+            log(f"[pmc] prefill GEMM type {type_id} {rows}x{cols} x {T} tokens: 5 launches")
+        m.free()
     n = 256 * 2 ** 20
     a, b = H.DeviceArray(n // 4), H.DeviceArray(n // 4)
     a.fill_bytes(1)
