@@ -503,8 +503,8 @@ def test_device_division_is_rounded_to_nearest(ctx):
 
 @pytest.mark.parametrize("width,ffn", [(2048, 101), (256, 520)])
 def test_gate_up_pair_with_rows_that_end_mid_group(ctx, width, ffn):
-    # Q4_K gate/up whose row count is not a whole number of the regrouped
-    # copy's 16-block groups (2048 wide: 8 blocks a row, rows in pairs; 256
+    # Q4_K gate/up whose row count is not a whole number of the unit
+    # layout's 16-block groups (2048 wide: 8 blocks a row, rows in pairs; 256
     # wide: one block a row, rows in sixteens), with an F32 ffn_down so the
     # decoder accepts any FFN width: the last workgroup's up rows start
     # mid-group, and the one-token pair launch must still read the right
