@@ -348,6 +348,17 @@ void* scratch_ptr(int device) {
 
 namespace rh {
 
+int device_cus() {
+  static const int cus = [] {
+    int dev = 0, n = 0;
+    return hipGetDevice(&dev) == hipSuccess &&
+                   hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+               ? n
+               : 256;
+  }();
+  return cus;
+}
+
 namespace {
 // The current snapshot. A reload publishes a new one and never frees the
 // old: a launch on another thread may still be reading it (a few dozen bytes
@@ -389,7 +400,7 @@ void load_tuning() {
   const int nt = env_int("RUSTICIDE_HIP_I2S_NT", 0);
   t.i2s_nt = nt == 256 || nt == 512 || nt == 1024 ? nt : 0;
   const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
-  t.gemm_bn = bn == 32 || bn == 64 || bn == 128 || bn == 256 ? bn : 0;
+  t.gemm_bn = bn == 32 || bn == 64 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;
   t.attn_lds = env_int("RUSTICIDE_HIP_ATTN_LDS", 1) != 0;
   g_tuning.store(new Tuning(t), std::memory_order_release);

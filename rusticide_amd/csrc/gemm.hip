@@ -93,18 +93,6 @@ struct SplitTerms {
 // block sit at fixed 16-byte-aligned offsets of its group of 16 blocks.
 constexpr uint32_t kRowsWG = 128;
 
-int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    cus = (hipGetDevice(&dev) == hipSuccess &&
-           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-              ? n
-              : 256;
-  }
-  return cus;
-}
-
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ uint32_t pk_mul_u16(uint32_t a, uint32_t b) {

@@ -1809,18 +1809,6 @@ int resident_wgs_per_cu(const void* kernel, size_t lds) {
   return n;
 }
 
-int device_cus() {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 0;
-    cus = (hipGetDevice(&dev) == hipSuccess &&
-           hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-              ? n
-              : 256;
-  }
-  return cus;
-}
-
 // The 64 teams of a workgroup cover at most 64 * NI blocks: a row of nb
 // blocks needs NI >= nb / 64.
 uint32_t min_blocks_per_team(uint32_t nb) {

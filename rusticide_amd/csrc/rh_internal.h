@@ -104,7 +104,7 @@ struct Tuning {
   int i2s_lpr = 0;         // RUSTICIDE_HIP_I2S_LPR=8|16|32|64: lanes per row, one token
   int i2s_nt = 0;          // RUSTICIDE_HIP_I2S_NT=256|512|1024: threads per workgroup, one token
   bool i2s_one = true;     // RUSTICIDE_HIP_I2S_ONE=0: one token on the two-token kernel
-  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=32|64 (k-quants), 64|128|256 (I2_S)
+  int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=32|64: tokens a GEMM workgroup
   bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
   bool attn_lds = true;    // RUSTICIDE_HIP_ATTN_LDS=0: the tiled attention step only
 };
@@ -145,6 +145,9 @@ bool norm_fusable(uint32_t type_id, size_t width, uint32_t nbmax);
 // across workgroups (0: it does not split). launch_gemm splits only when
 // `terms` holds that many bytes; without it the launch runs unsplit.
 size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens);
+// Compute units of the current device when first asked (256 if the query
+// fails); the launch shapes are sized by it.
+int device_cus();
 // rh_matmul_batch_device for k-quant jobs on an activation already quantized
 // to Q8_K in `q` (width / 256 super-blocks for each of `tokens` tokens).
 rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tokens, const rh_job* jobs,

@@ -356,6 +356,29 @@ def test_i2s_prefill_gemm_is_bit_exact(ctx, rows, cols, token_counts):
                          f"{rows}x{cols} tokens={tokens}")
 
 
+@pytest.mark.parametrize("bn", ["32", "64"])
+def test_i2s_gemm_token_tiles(ctx, tuning, bn):
+    # the I2_S GEMM at both token tiles: ragged rows (a wave's rows past the
+    # end) and tokens, one block, 54 blocks (the loads three blocks ahead run
+    # past the last block), two jobs in one launch; its i32 dots against the
+    # CPU path's
+    tuning.set("RUSTICIDE_HIP_GEMM_BN", bn)
+    for rows, cols, tokens in ((300, 384, 77), (33, 128, 9), (2560, 6912, 40), (257, 1024, 130), (64, 256, 33)):
+        data = synth.i2s_matrix(rows, cols, seed=rows * 3 + cols)
+        m = R.Matrix.load(ctx, 36, data, rows, cols)
+        x = synth.normal_f32(tokens * cols, seed=tokens + cols)
+        raw = ctx.ternary_dot_i32(m, x, tokens)
+        want = O.ternary_dot_matrix_i32(data[: rows * cols // 4], cols // 4, x, tokens)
+        assert np.array_equal(raw, want), f"{rows}x{cols} tokens={tokens} bn={bn}"
+    specs = [(96, synth.i2s_matrix(96, 512, seed=1)), (200, synth.i2s_matrix(200, 512, seed=2))]
+    mats = [R.Matrix.load(ctx, 36, d, r, 512) for r, d in specs]
+    x = synth.normal_f32(50 * 512, seed=9)
+    outs = [np.full(r * 50, np.nan, np.float32) for r, _ in specs]
+    R.matmul_batch(ctx, x, 50, list(zip(mats, outs)))
+    for (r, d), out in zip(specs, outs):
+        assert_same_bits(out, oracle_matmul(36, d, r, 512, x, 50, scale=0.02), f"two jobs, rows {r}")
+
+
 def test_i2s_prefill_gemm_every_code_and_hostile_activations(ctx):
     # random packed bytes use code 3 (+2, i2_s.rs:96-104); activations with
     # NaN, infinities and zeros exercise the I8_S rules (q8.rs:38-49,99-105);
