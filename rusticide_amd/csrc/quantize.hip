@@ -16,10 +16,9 @@ __global__ __launch_bounds__(256) void quantize_super_kernel(const float* __rest
   const uint32_t sb = blockIdx.x * 4u + (threadIdx.x >> 6);
   const size_t t = blockIdx.y;
   if (sb >= n_super) return;  // wave-uniform
-  const float* v = x + t * width + static_cast<size_t>(sb) * 256u;
-  float f[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) f[i] = v[lane * 4u + i];
+  // one 16-byte load a lane (rows are whole super blocks, x 16-byte aligned)
+  const float4 v = *reinterpret_cast<const float4*>(x + t * width + static_cast<size_t>(sb) * 256u + lane * 4u);
+  const float f[4] = {v.x, v.y, v.z, v.w};
   quantize_super_block(f, lane, t, sb, q);
 }
 

@@ -534,32 +534,31 @@ template <class Q>
 __device__ __forceinline__ void quantize_super_block(const float (&f)[4], uint32_t lane, size_t t, uint32_t sb,
                                                      const Q& q) {
   // amax: f32::max folded from 0.0 (q8.rs:12-14,19-25). Comparisons keep a
-  // NaN from ever entering the running maximum, as maxNum does.
+  // NaN from ever entering the running maximum, as maxNum does; the result
+  // is a non-negative float or +inf, whose bits order like u32 (DPP within
+  // each half-wave, then the two halves).
   float amax = 0.0f;
 #pragma unroll
   for (int i = 0; i < 4; i++) {
     float m = __builtin_fabsf(f[i]);
     amax = m > amax ? m : amax;
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    float o = __shfl_xor(amax, off, 64);
-    amax = o > amax ? o : amax;
-  }
+  const uint32_t ab = half_max_u32(__float_as_uint(amax));
+  amax = __uint_as_float(max(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ab), 0)),
+                             static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(ab), 32))));
   // The first element, in order, whose magnitude is amax (q8.rs:26-32).
   uint32_t idx = 256u;
 #pragma unroll
   for (int i = 3; i >= 0; i--)
     if (__builtin_fabsf(f[i]) == amax) idx = lane * 4u + i;
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    uint32_t o = static_cast<uint32_t>(__shfl_xor(static_cast<int>(idx), off, 64));
-    idx = o < idx ? o : idx;
-  }
+  idx = half_min_u32(idx);
+  idx = min(static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idx), 0)),
+            static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(idx), 32)));
   // the owner of element idx broadcasts it (no dependent reload)
   const uint32_t sel = idx & 3u;
   const float mine = sel == 0 ? f[0] : sel == 1 ? f[1] : sel == 2 ? f[2] : f[3];
-  const float owned = __shfl(mine, static_cast<int>((idx >> 2) & 63u), 64);
+  const float owned =
+      __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mine), static_cast<int>((idx >> 2) & 63u)));
   const float max = idx < 256u ? owned : 0.0f;
   const float inverse = (max == 0.0f) ? 0.0f : __fdiv_rn(-127.0f, max);
   const float step = (max == 0.0f) ? 0.0f : __fdiv_rn(1.0f, inverse);
@@ -575,13 +574,15 @@ __device__ __forceinline__ void quantize_super_block(const float (&f)[4], uint32
   uint32_t packed = (static_cast<uint32_t>(qv[0]) & 0xffu) | ((static_cast<uint32_t>(qv[1]) & 0xffu) << 8) |
                     ((static_cast<uint32_t>(qv[2]) & 0xffu) << 16) | (static_cast<uint32_t>(qv[3]) << 24);
   *reinterpret_cast<uint32_t*>(q.quants + t * q.qstride + static_cast<size_t>(sb) * 256u + lane * 4u) = packed;
-  // sums per 16 (4 lanes) and per 32 (8 lanes)
-  int32_t s16 = s + __shfl_xor(s, 1, 64);
-  s16 += __shfl_xor(s16, 2, 64);
-  int32_t s32 = s16 + __shfl_xor(s16, 4, 64);
+  // sums per 16 (a quad: quad_perm swaps) and per 32 (two quads: the
+  // half-row mirror)
+  uint32_t s16 = static_cast<uint32_t>(s);
+  s16 += dpp<0xB1>(s16);
+  s16 += dpp<0x4E>(s16);
+  const uint32_t s32 = s16 + dpp<0x141>(s16);
   const size_t b0 = t * q.bstride + static_cast<size_t>(sb) * 8u;
-  if ((lane & 3u) == 0) q.sums16[2 * t * q.bstride + static_cast<size_t>(sb) * 16u + lane / 4u] = s16;
-  if ((lane & 7u) == 0) q.sums[b0 + lane / 8u] = s32;
+  if ((lane & 3u) == 0) q.sums16[2 * t * q.bstride + static_cast<size_t>(sb) * 16u + lane / 4u] = static_cast<int32_t>(s16);
+  if ((lane & 7u) == 0) q.sums[b0 + lane / 8u] = static_cast<int32_t>(s32);
   if (lane < 8u) q.scales[b0 + lane] = step;
 }
 
