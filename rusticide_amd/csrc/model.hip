@@ -735,6 +735,43 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const 
   hf[i] = s * up[static_cast<size_t>(e) * n + t];
 }
 
+// silu_mul_kernel's values for tokens t0 .. t0+3 (t0 = 4 blockIdx.y) of the
+// 256-value block blockIdx.x, quantized to Q8_K into q as quantize_super_kernel
+// would from hf: one launch instead of two, and hf never leaves the chip.
+// Thread i reads weight row 256 blockIdx.x + i of gate and up, the four
+// tokens side by side (one 16-byte load when n is a multiple of 4); wave w
+// then quantizes token t0 + w's block from LDS.
+__global__ __launch_bounds__(256) void silu_quant_kernel(const float* gate, const float* up, uint32_t n, Q8Dev q) {
+  __shared__ __align__(16) float blk[4][256];
+  const uint32_t tid = threadIdx.x, sb = blockIdx.x, t0 = 4u * blockIdx.y;
+  const size_t at = static_cast<size_t>(sb * 256u + tid) * n + t0;
+  float g[4], u[4];
+  if ((n & 3u) == 0) {
+    const float4 gv = *reinterpret_cast<const float4*>(gate + at);
+    const float4 uv = *reinterpret_cast<const float4*>(up + at);
+    g[0] = gv.x, g[1] = gv.y, g[2] = gv.z, g[3] = gv.w;
+    u[0] = uv.x, u[1] = uv.y, u[2] = uv.z, u[3] = uv.w;
+  } else {
+#pragma unroll
+    for (uint32_t j = 0; j < 4u; j++) {
+      const bool in = t0 + j < n;
+      g[j] = in ? gate[at + j] : 0.0f;
+      u[j] = in ? up[at + j] : 0.0f;
+    }
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < 4u; j++) {
+    const float den = 1.0f + expf_ref(-g[j]);
+    blk[j][tid] = __fdiv_rn(g[j], den) * u[j];
+  }
+  __syncthreads();
+  const uint32_t w = tid >> 6, lane = tid & 63u;
+  if (t0 + w >= n) return;
+  const float4 v = reinterpret_cast<const float4*>(blk[w])[lane];
+  const float f[4] = {v.x, v.y, v.z, v.w};
+  quantize_super_block(f, lane, t0 + w, sb, q);
+}
+
 
 // Greedy pick over the logits: NaN as -inf, max by total order, the last
 // maximum wins; out[0] = token, out[1] = 1 when some logit is finite. When
@@ -895,6 +932,7 @@ struct rh_decoder {
   float* hidden2 = nullptr;  // the residual's other buffer on the norm-fused path
   bool fuse_norm = false;    // one-token forwards fold each RMSNorm into the GEMV after it
   bool quant_norm = false;   // batches quantize the normed rows in the norm kernel
+  bool quant_ffn = false;    // batches quantize silu(gate) * up in silu_quant_kernel
   bool fuse_output_norm = false;  // one-token forwards fold the output norm into the output matrix's launch
   Q8Dev q8;                  // that activation, for up to `cap` tokens
   float *q = nullptr, *mixed = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
@@ -981,8 +1019,10 @@ hipError_t ensure_acts(rh_decoder* d, size_t n) {
     free_acts(d);
     return e;
   }
-  // the Q8_K activation of a batch (the layout ensure_q8 gives matmul_batch)
-  const size_t qstride = (w + 255u) / 256u * 256u, bstride = (qstride / 32u + 7u) / 8u * 8u;
+  // the Q8_K activation of a batch (the layout ensure_q8 gives matmul_batch),
+  // wide enough for either matrix input: a normed row (w) or the FFN's (f)
+  const size_t wq = w > f ? w : f;
+  const size_t qstride = (wq + 255u) / 256u * 256u, bstride = (qstride / 32u + 7u) / 8u * 8u;
   if ((e = dmalloc(&d->q8.quants, n * qstride)) != hipSuccess ||
       (e = dmalloc(&d->q8.scales, n * bstride)) != hipSuccess || (e = dmalloc(&d->q8.sums, n * bstride)) != hipSuccess ||
       (e = dmalloc(&d->q8.sums16, 2 * n * bstride)) != hipSuccess) {
@@ -1001,10 +1041,18 @@ rh_status mm(rh_decoder* d, const float* in, size_t n, size_t width, std::initia
   return rh_matmul_batch_device(d->ctx, in, n * width, n, v.data(), v.size(), d->stream);
 }
 
-// mm over the decoder's Q8_K activation (d->q8, which a QUANT norm filled).
+// The decoder's Q8_K activation as rows of `width` values (a multiple of 256).
+Q8Dev q8_for(const rh_decoder* d, size_t width) {
+  Q8Dev q = d->q8;
+  q.n_blocks = width / 256u * 8u;
+  return q;
+}
+
+// mm over the decoder's Q8_K activation (d->q8, which a QUANT norm or
+// silu_quant_kernel filled) for rows of `width` values.
 rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_job> jobs) {
   std::vector<rh_job> v(jobs);
-  return matmul_q8_device(d->ctx, d->q8, width, n, v.data(), v.size(), d->stream);
+  return matmul_q8_device(d->ctx, q8_for(d, width), width, n, v.data(), v.size(), d->stream);
 }
 
 #define RHD(expr)                                   \
@@ -1074,11 +1122,18 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
       RHS(mm_q8(d, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
     else
       RHS(mm(d, d->normed, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
-    const size_t total = n * f;
-    hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255u) / 256u)), dim3(256), 0, s, d->gate,
-                       d->up, nn, f, d->hf);
-    RHD(hipGetLastError());
-    RHS(mm(d, d->hf, n, f, {{b.down, d->delta, n * w}}));
+    if (d->quant_ffn && n >= 2) {
+      hipLaunchKernelGGL(silu_quant_kernel, dim3(f / 256u, (nn + 3u) / 4u), dim3(256), 0, s, d->gate, d->up, nn,
+                         q8_for(d, f));
+      RHD(hipGetLastError());
+      RHS(mm_q8(d, n, f, {{b.down, d->delta, n * w}}));
+    } else {
+      const size_t total = n * f;
+      hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255u) / 256u)), dim3(256), 0, s,
+                         d->gate, d->up, nn, f, d->hf);
+      RHD(hipGetLastError());
+      RHS(mm(d, d->hf, n, f, {{b.down, d->delta, n * w}}));
+    }
     pending = d->delta;
   }
   // the last residual for every token, then the last token's output norm
@@ -1431,6 +1486,11 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
   d->use_graphs = genv && genv[0] == '1';
   const char* qenv = std::getenv("RUSTICIDE_HIP_NORM_QUANT");
   d->quant_norm = quant && !(qenv && qenv[0] == '0');
+  // likewise the FFN's down input, when every down matrix is a k-quant
+  bool qffn = c.feed_forward_length % 256 == 0;
+  for (const rh_decoder::Block& b : d->blocks)
+    qffn = qffn && is_kquant_matrix(b.down) && rh_matrix_cols(b.down) == c.feed_forward_length;
+  d->quant_ffn = qffn && !(qenv && qenv[0] == '0');
   *out = d;
   return RH_OK;
 }
