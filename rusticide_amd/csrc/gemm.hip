@@ -402,27 +402,34 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
 
 // The end of a split launch: per (row, token), segment 0's sum plus the later
 // blocks' terms, one addition at a time in block order.
-// Each thread owns four consecutive (row, token) slots (a plane holds a
-// multiple of 64 of them) and keeps eight planes of loads in flight; the
-// additions stay one plane at a time, in block order.
+// Each thread owns two consecutive (row, token) slots (a plane holds a
+// multiple of 64 of them) and requests up to kCombineAhead planes at once,
+// clamped to the last plane, before its first addition: the combine waits on
+// memory once for up to that many planes (a 64-token prefill's planes number
+// 8-21), not once per plane. The additions stay one plane at a time, in block
+// order.
+constexpr uint32_t kCombineAhead = 24;
+
 __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const float* __restrict__ terms,
                                                            uint32_t planes, uint32_t rows_pad, size_t tokens,
                                                            uint32_t bm) {
   const size_t n = static_cast<size_t>(rows_pad) * tokens;
-  const size_t idx = (static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x) * 4u;
+  const size_t idx = (static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x) * 2u;
   if (idx >= n) return;
-  f32x4 y = *reinterpret_cast<const f32x4*>(terms + idx);
-  uint32_t p = 1;
-  for (; p + 8u <= planes; p += 8u) {
-    f32x4 v[8];
+  f32x2 y = *reinterpret_cast<const f32x2*>(terms + idx);
+  for (uint32_t p0 = 1; p0 < planes; p0 += kCombineAhead) {
+    f32x2 v[kCombineAhead];
 #pragma unroll
-    for (int k = 0; k < 8; k++) v[k] = *reinterpret_cast<const f32x4*>(terms + static_cast<size_t>(p + k) * n + idx);
+    for (uint32_t k = 0; k < kCombineAhead; k++) {
+      const uint32_t p = min(p0 + k, planes - 1u);
+      v[k] = *reinterpret_cast<const f32x2*>(terms + static_cast<size_t>(p) * n + idx);
+    }
 #pragma unroll
-    for (int k = 0; k < 8; k++) y += v[k];
+    for (uint32_t k = 0; k < kCombineAhead; k++)
+      if (p0 + k < planes) y += v[k];
   }
-  for (; p < planes; p++) y += *reinterpret_cast<const f32x4*>(terms + static_cast<size_t>(p) * n + idx);
 #pragma unroll
-  for (int e = 0; e < 4; e++) {
+  for (int e = 0; e < 2; e++) {
     const uint32_t grow = static_cast<uint32_t>((idx + e) / tokens);
     const size_t tok = idx + e - static_cast<size_t>(grow) * tokens;
     const GemvJob& J = jobs.j[gemm_job(jobs, grow / bm)];
@@ -520,7 +527,7 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const size_t n = static_cast<size_t>(plan.rows_pad) * tokens;  // a multiple of 64
-  hipLaunchKernelGGL(gemm_combine_kernel, dim3(static_cast<uint32_t>((n / 4u + 255u) / 256u)), dim3(256), 0, s, jobs,
+  hipLaunchKernelGGL(gemm_combine_kernel, dim3(static_cast<uint32_t>((n / 2u + 255u) / 256u)), dim3(256), 0, s, jobs,
                      terms, plan.planes, plan.rows_pad, tokens, kRowsWG);
   return hipGetLastError();
 }

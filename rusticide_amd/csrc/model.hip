@@ -61,20 +61,19 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint
 
 // hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t]),
 // then normed[t] = normalize(hidden[t], weight) for tokens t >= norm_from.
-// One workgroup per token; each thread keeps its PER elements (e = tid +
-// 256k) in registers from the first load to the last store, so every global
-// load is issued up front.
+// One workgroup of TH threads per token; each thread keeps its PER elements
+// (e = tid + TH k) in registers from the first load to the last store, so
+// every global load is issued up front.
 constexpr uint32_t kMaxNormPer = 32;  // widths up to 256 * 32 = 8192
 
 // QUANT: the normalized row is not stored as f32 but quantized to Q8_K into
 // q8 (token t - norm_from), as quantize_super_kernel would from the f32 row;
 // width must then be a multiple of 256.
-template <uint32_t PER, bool QUANT = false>
-__global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restrict__ hidden,
-                                                                const float* __restrict__ delta, uint32_t n,
-                                                                uint32_t width, const float* __restrict__ weight,
-                                                                float eps, uint32_t norm_from,
-                                                                float* __restrict__ normed, Q8Dev q8) {
+template <uint32_t PER, bool QUANT, uint32_t TH>
+__global__ __launch_bounds__(TH) void add_norm_kernel(float* __restrict__ hidden, const float* __restrict__ delta,
+                                                      uint32_t n, uint32_t width, const float* __restrict__ weight,
+                                                      float eps, uint32_t norm_from, float* __restrict__ normed,
+                                                      Q8Dev q8) {
   extern __shared__ __align__(16) float sq[];
   __shared__ float s_rms;
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -83,7 +82,7 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
   float v[PER], wt[PER], dl[PER];
 #pragma unroll
   for (uint32_t k = 0; k < PER; k++) {
-    const uint32_t e = tid + k * kNormThreads;
+    const uint32_t e = tid + k * TH;
     if (e < width) {
       v[k] = h[e];
       if (delta) dl[k] = delta[static_cast<size_t>(e) * n + t];
@@ -93,7 +92,7 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
   if (delta) {
 #pragma unroll
     for (uint32_t k = 0; k < PER; k++) {
-      const uint32_t e = tid + k * kNormThreads;
+      const uint32_t e = tid + k * TH;
       if (e < width) {
         v[k] += dl[k];
         h[e] = v[k];
@@ -103,7 +102,7 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
   if (!norm) return;
 #pragma unroll
   for (uint32_t k = 0; k < PER; k++) {
-    const uint32_t e = tid + k * kNormThreads;
+    const uint32_t e = tid + k * TH;
     if (e < width) {
       const float s = v[k] * v[k];
       sq[wave_sum_index(e)] = s;
@@ -127,12 +126,12 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
     // wave then quantizes a 256-value block at a time
 #pragma unroll
     for (uint32_t k = 0; k < PER; k++) {
-      const uint32_t e = tid + k * kNormThreads;
+      const uint32_t e = tid + k * TH;
       if (e < width) sq[e] = __fdiv_rn(v[k], rms) * wt[k];
     }
     __syncthreads();
     const uint32_t lane = tid & 63u;
-    for (uint32_t sb = tid >> 6; sb < width / 256u; sb += kNormThreads / 64u) {
+    for (uint32_t sb = tid >> 6; sb < width / 256u; sb += TH / 64u) {
       float f[4];
 #pragma unroll
       for (int i = 0; i < 4; i++) f[i] = sq[sb * 256u + lane * 4u + static_cast<uint32_t>(i)];
@@ -143,7 +142,7 @@ __global__ __launch_bounds__(kNormThreads) void add_norm_kernel(float* __restric
   float* o = normed + static_cast<size_t>(t - norm_from) * width;
 #pragma unroll
   for (uint32_t k = 0; k < PER; k++) {
-    const uint32_t e = tid + k * kNormThreads;
+    const uint32_t e = tid + k * TH;
     if (e < width) {
       const float x = __fdiv_rn(v[k], rms);
       o[e] = x * wt[k];
@@ -160,13 +159,24 @@ size_t add_norm_lds(uint32_t width) {
   return (n > width ? n : width) * 4u;
 }
 
-// The add_norm_kernel instance for a row width (<= 256 * kMaxNormPer).
+// The add_norm_kernel instance for a row width (<= 256 * kMaxNormPer) and
+// its workgroup size: rows of 2048 values or more take 512 threads, so that
+// eight waves quantize eight 256-value blocks at once (a 2048-wide QUANT
+// norm of 64 tokens: 5.1 against 5.9 us with 256 threads).
+struct AddNorm {
+  AddNormFn fn;
+  uint32_t threads;
+};
+
 template <bool QUANT = false>
-AddNormFn add_norm_for(uint32_t width) {
-  if (width <= 4u * kNormThreads) return add_norm_kernel<4, QUANT>;
-  if (width <= 8u * kNormThreads) return add_norm_kernel<8, QUANT>;
-  if (width <= 16u * kNormThreads) return add_norm_kernel<16, QUANT>;
-  return add_norm_kernel<kMaxNormPer, QUANT>;
+AddNorm add_norm_for(uint32_t width) {
+  if (width >= 2048u) {
+    if (width <= 4u * 512u) return {add_norm_kernel<4, QUANT, 512>, 512u};
+    if (width <= 8u * 512u) return {add_norm_kernel<8, QUANT, 512>, 512u};
+    return {add_norm_kernel<kMaxNormPer / 2u, QUANT, 512>, 512u};
+  }
+  if (width <= 4u * kNormThreads) return {add_norm_kernel<4, QUANT, kNormThreads>, kNormThreads};
+  return {add_norm_kernel<8, QUANT, kNormThreads>, kNormThreads};
 }
 
 // q/k/v from the projections (stored by weight row, x[e*n + t]): q rotated
@@ -342,13 +352,26 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
   const uint32_t hd = HD ? HD : head_dim;
   const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const uint32_t rows = start + t + 1u;
-  const uint32_t tr = tile_rows(hd);
   float* qh = sh;                      // [kMaxHeadDim]
   float* red = sh + kMaxHeadDim;       // [64]
   float* w = red + 64;                 // [rows rounded up to 4]
   float* vt = w + ((rows + 3u) & ~3u);  // [2][kVTile * 64]
   const uint32_t off = (h / group) * hd;
-  if (tid < hd) qh[tid] = q[static_cast<size_t>(t) * width + h * hd + tid];
+  // Loads that wait on nothing go out together: the query head, (head_dim
+  // 64) this thread's first key row (row min(tid, rows - 1), so that the
+  // load is unconditional) and the first value tile; the workgroup then
+  // waits on memory once before the scores and not again before the mix.
+  const float qv = tid < hd ? q[static_cast<size_t>(t) * width + h * hd + tid] : 0.0f;
+  f32x4 k4[16];
+  if constexpr (HD == 64u) {
+    const float* kr = kcache + static_cast<size_t>(min(tid, rows - 1u)) * kv + off;
+#pragma unroll
+    for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
+  }
+  const uint32_t tr = tile_rows(hd);
+  VTileRegs<HD> regs;
+  regs.load(vcache, kv, off, hd, 0u, rows < tr ? rows : tr);
+  if (tid < hd) qh[tid] = qv;
   __syncthreads();
   // dot (float.rs:23-36): eight fused lanes over whole chunks, lanes summed
   // in order from -0.0, then the unfused tail summed from -0.0. One cached
@@ -359,9 +382,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float tail = -0.0f;
     if constexpr (HD == 64u) {
-      f32x4 k4[16];
+      if (i != tid) {
 #pragma unroll
-      for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
+        for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
+      }
       lanes64(qh, k4, acc);
     } else {
       const uint32_t chunks = hd / 8u;
@@ -382,8 +406,6 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
   // Value tiles are staged through LDS by every thread, a tile ahead of
   // the first wave's chain of fused adds.
   const uint32_t tiles = (rows + tr - 1u) / tr;
-  VTileRegs<HD> regs;
-  regs.load(vcache, kv, off, hd, 0u, rows < tr ? rows : tr);
   regs.store(vt, hd, rows < tr ? rows : tr);
   __syncthreads();
   float acc = 0.0f;
@@ -1087,15 +1109,15 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   RHD(hipGetLastError());
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
   const size_t norm_lds = add_norm_lds(w);
-  const AddNormFn norm_fn = add_norm_for(w);
+  const AddNorm norm_fn = add_norm_for(w);
   // a batch whose normed rows feed only k-quant GEMMs gets them as Q8_K
   // straight from the norm kernel
   const bool qn = d->quant_norm && n >= 2;
-  const AddNormFn norm_in = qn ? add_norm_for<true>(w) : norm_fn;
+  const AddNorm norm_in = qn ? add_norm_for<true>(w) : norm_fn;
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
     const rh_decoder::Block& b = d->blocks[l];
-    hipLaunchKernelGGL(norm_in, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+    hipLaunchKernelGGL(norm_in.fn, dim3(nn), dim3(norm_in.threads), norm_lds, s, d->hidden, pending, nn, w,
                        b.attn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
     RHD(hipGetLastError());
     if (qn)
@@ -1115,7 +1137,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                        static_cast<uint32_t>(start), d->mixed);
     RHD(hipGetLastError());
     RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
-    hipLaunchKernelGGL(norm_in, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, d->delta, nn, w,
+    hipLaunchKernelGGL(norm_in.fn, dim3(nn), dim3(norm_in.threads), norm_lds, s, d->hidden, d->delta, nn, w,
                        b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
     RHD(hipGetLastError());
     if (qn)
@@ -1137,7 +1159,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
     pending = d->delta;
   }
   // the last residual for every token, then the last token's output norm
-  hipLaunchKernelGGL(norm_fn, dim3(nn), dim3(kNormThreads), norm_lds, s, d->hidden, pending, nn, w,
+  hipLaunchKernelGGL(norm_fn.fn, dim3(nn), dim3(norm_fn.threads), norm_lds, s, d->hidden, pending, nn, w,
                      d->output_norm, c.rms_norm_eps, nn - 1u, d->normed, Q8Dev{});
   RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
@@ -1248,8 +1270,9 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start,
     const rh_job lm{out, d->logits, c.vocab_size};
     RHS(matmul_norm_device(d->ctx, h, fo, w, &lm, 1, s));
   } else {
-    hipLaunchKernelGGL(add_norm_for(w), dim3(1), dim3(kNormThreads), add_norm_lds(w), s, h, pending, 1u,
-                       w, d->output_norm, c.rms_norm_eps, 0u, d->normed, Q8Dev{});
+    const AddNorm an = add_norm_for(w);
+    hipLaunchKernelGGL(an.fn, dim3(1), dim3(an.threads), add_norm_lds(w), s, h, pending, 1u, w, d->output_norm,
+                       c.rms_norm_eps, 0u, d->normed, Q8Dev{});
     RHD(hipGetLastError());
     RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
   }

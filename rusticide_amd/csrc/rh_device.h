@@ -21,6 +21,7 @@ typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 // memcpy, which keeps register arrays of it in scratch when they live across
 // branches; arrays of this type stay in registers.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
