@@ -352,26 +352,13 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
   const uint32_t hd = HD ? HD : head_dim;
   const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
   const uint32_t rows = start + t + 1u;
+  const uint32_t tr = tile_rows(hd);
   float* qh = sh;                      // [kMaxHeadDim]
   float* red = sh + kMaxHeadDim;       // [64]
   float* w = red + 64;                 // [rows rounded up to 4]
   float* vt = w + ((rows + 3u) & ~3u);  // [2][kVTile * 64]
   const uint32_t off = (h / group) * hd;
-  // Loads that wait on nothing go out together: the query head, (head_dim
-  // 64) this thread's first key row (row min(tid, rows - 1), so that the
-  // load is unconditional) and the first value tile; the workgroup then
-  // waits on memory once before the scores and not again before the mix.
-  const float qv = tid < hd ? q[static_cast<size_t>(t) * width + h * hd + tid] : 0.0f;
-  f32x4 k4[16];
-  if constexpr (HD == 64u) {
-    const float* kr = kcache + static_cast<size_t>(min(tid, rows - 1u)) * kv + off;
-#pragma unroll
-    for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
-  }
-  const uint32_t tr = tile_rows(hd);
-  VTileRegs<HD> regs;
-  regs.load(vcache, kv, off, hd, 0u, rows < tr ? rows : tr);
-  if (tid < hd) qh[tid] = qv;
+  if (tid < hd) qh[tid] = q[static_cast<size_t>(t) * width + h * hd + tid];
   __syncthreads();
   // dot (float.rs:23-36): eight fused lanes over whole chunks, lanes summed
   // in order from -0.0, then the unfused tail summed from -0.0. One cached
@@ -382,10 +369,9 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     float tail = -0.0f;
     if constexpr (HD == 64u) {
-      if (i != tid) {
+      f32x4 k4[16];
 #pragma unroll
-        for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
-      }
+      for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
       lanes64(qh, k4, acc);
     } else {
       const uint32_t chunks = hd / 8u;
@@ -406,6 +392,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
   // Value tiles are staged through LDS by every thread, a tile ahead of
   // the first wave's chain of fused adds.
   const uint32_t tiles = (rows + tr - 1u) / tr;
+  VTileRegs<HD> regs;
+  regs.load(vcache, kv, off, hd, 0u, rows < tr ? rows : tr);
   regs.store(vt, hd, rows < tr ? rows : tr);
   __syncthreads();
   float acc = 0.0f;
@@ -420,6 +408,123 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
     __syncthreads();
   }
   if (tid < hd) mixed[static_cast<size_t>(t) * width + h * hd + tid] = acc;
+}
+
+// attention_kernel<64> for the G query heads of one kv head (G = 4 or 8):
+// one workgroup per (kv head, token) forms the G heads' scores, softmaxes
+// and value mixes with attention_kernel's arithmetic, reading each key and
+// value row once for all G heads (a 64-token prefill of 32/4 heads: 256
+// workgroups instead of 2048). The scores give each head 256 / G lanes (one
+// row a lane per pass); the mix gives every thread the output lane
+// tid % 64 of heads tid / 64 + 4k. With QUANT the G heads' outputs, G / 4
+// whole 256-value blocks of the token's mixed row, are quantized to Q8_K
+// into q8 as quantize_super_kernel would from that row, and not stored.
+template <uint32_t G, bool QUANT>
+__global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const float* q, const float* kcache,
+                                                                       const float* vcache, uint32_t width,
+                                                                       uint32_t kv, float scale, uint32_t start,
+                                                                       float* mixed, Q8Dev q8) {
+  static_assert(G == 4u || G == 8u, "four or eight query heads per kv head");
+  constexpr uint32_t HD = 64u, L = kAttnThreads / G;  // lanes per head in the scores
+  extern __shared__ __align__(16) float sh[];
+  const uint32_t g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+  const uint32_t rows = start + t + 1u, ws = (rows + 3u) & ~3u;
+  float* qh = sh;                // [G][64]; with QUANT later the outputs
+  float* red = qh + G * HD;      // [64]
+  float* w = red + 64;           // [G][ws]
+  float* vt = w + G * ws;        // [2][kVTile * 64]
+  const uint32_t off = g * HD;
+  // the first value tile goes out with the query heads (its registers stay
+  // live over the scores' loop only as 16 floats)
+  VTileRegs<HD> regs;
+  regs.load(vcache, kv, off, HD, 0u, rows < kVTile ? rows : kVTile);
+  for (uint32_t i = tid; i < G * HD; i += kAttnThreads) qh[i] = q[static_cast<size_t>(t) * width + g * G * HD + i];
+  __syncthreads();
+  const uint32_t j = tid / L, i0 = tid % L;
+  float* wj = w + j * ws;
+  float mx = -INFINITY;
+  for (uint32_t i = i0; i < rows; i += L) {
+    const float* kr = kcache + static_cast<size_t>(i) * kv + off;
+    f32x4 k4[16];
+#pragma unroll
+    for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    lanes64(qh + j * HD, k4, acc);
+    const float score = score_from_lanes(acc, -0.0f, scale);
+    wj[i] = score;
+    mx = fmaxf(mx, score);
+  }
+  // softmax_rows per head: the maximum over the head's lanes (an aligned
+  // half-wave, or a whole wave), exp, the sum in order from 0.0 on one lane
+  // of the head, the division
+  mx = max_key_float(half_max_u32(max_key(mx)));
+  if constexpr (L == 64u)
+    mx = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
+               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)));
+  for (uint32_t i = i0; i < rows; i += L) wj[i] = expf_ref(wj[i] - mx);
+  __syncthreads();
+  if (i0 == 0) red[j] = ordered_sum(wj, rows, 0.0f);  // portable/norm.rs: `let mut sum = 0.0`
+  __syncthreads();
+  const float sum = red[j];
+  for (uint32_t i = i0; i < rows; i += L) wj[i] = __fdiv_rn(wj[i], sum);
+  regs.store(vt, HD, rows < kVTile ? rows : kVTile);
+  __syncthreads();
+  // mix_rows: each output lane's chain of fused adds over the rows in order
+  const uint32_t d = tid & 63u, jp = tid >> 6;
+  float acc[G / 4u];
+#pragma unroll
+  for (uint32_t k = 0; k < G / 4u; k++) acc[k] = 0.0f;
+  const uint32_t tiles = (rows + kVTile - 1u) / kVTile;
+  for (uint32_t tile = 0; tile < tiles; tile++) {
+    const uint32_t r0 = tile * kVTile;
+    const uint32_t count = rows - r0 < kVTile ? rows - r0 : kVTile;
+    const bool more = tile + 1u < tiles;
+    const uint32_t nr0 = r0 + kVTile, ncount = more ? (rows - nr0 < kVTile ? rows - nr0 : kVTile) : 0u;
+    if (more) regs.load(vcache, kv, off, HD, nr0, ncount);
+    const float* cur = vt + (tile & 1u) * kVTile * 64u;
+    uint32_t r = 0;
+    for (; r + 16u <= count; r += 16u) {
+      float v[16];
+#pragma unroll
+      for (int k = 0; k < 16; k++) v[k] = cur[(r + k) * HD + d];
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+#pragma unroll
+        for (uint32_t h = 0; h < G / 4u; h++) acc[h] = __builtin_fmaf(v[k], w[(jp + 4u * h) * ws + r0 + r + k], acc[h]);
+    }
+    for (; r < count; r++) {
+      const float v = cur[r * HD + d];
+#pragma unroll
+      for (uint32_t h = 0; h < G / 4u; h++) acc[h] = __builtin_fmaf(v, w[(jp + 4u * h) * ws + r0 + r], acc[h]);
+    }
+    if (more) regs.store(vt + ((tile + 1u) & 1u) * kVTile * 64u, HD, ncount);
+    __syncthreads();
+  }
+  if constexpr (!QUANT) {
+#pragma unroll
+    for (uint32_t h = 0; h < G / 4u; h++)
+      mixed[static_cast<size_t>(t) * width + (g * G + jp + 4u * h) * HD + d] = acc[h];
+  } else {
+    // block h of the group holds heads 4h .. 4h + 3, head jp + 4h at jp * 64
+#pragma unroll
+    for (uint32_t h = 0; h < G / 4u; h++) qh[h * 256u + jp * HD + d] = acc[h];
+    __syncthreads();
+    const uint32_t wave = tid >> 6, lane = tid & 63u;
+    if (wave < G / 4u) {
+      const f32x4 v = reinterpret_cast<const f32x4*>(qh + wave * 256u)[lane];
+      const float f[4] = {v[0], v[1], v[2], v[3]};
+      quantize_super_block(f, lane, t, g * G / 4u + wave, q8);
+    }
+  }
+}
+
+using AttnGroupFn = void (*)(const float*, const float*, const float*, uint32_t, uint32_t, float, uint32_t, float*,
+                            Q8Dev);
+constexpr size_t kMaxLdsBytes = 160u * 1024u;  // a gfx950 workgroup's LDS
+
+// LDS floats attention_group_kernel needs for `rows` cached rows.
+inline size_t attention_group_lds_floats(size_t group, size_t rows) {
+  return group * 64u + 64u + group * ((rows + 3u) & ~size_t{3}) + 2u * kVTile * 64u;
 }
 
 // Value tile rows r0.. (below `rows`) of one kv head for head_dim 64, a
@@ -955,6 +1060,7 @@ struct rh_decoder {
   bool fuse_norm = false;    // one-token forwards fold each RMSNorm into the GEMV after it
   bool quant_norm = false;   // batches quantize the normed rows in the norm kernel
   bool quant_ffn = false;    // batches quantize silu(gate) * up in silu_quant_kernel
+  bool quant_attn = false;   // batches quantize the attention output in attention_group_kernel
   bool fuse_output_norm = false;  // one-token forwards fold the output norm into the output matrix's launch
   Q8Dev q8;                  // that activation, for up to `cap` tokens
   float *q = nullptr, *mixed = nullptr, *gate = nullptr, *up = nullptr, *hf = nullptr;
@@ -1130,13 +1236,29 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
     hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn, w,
                        kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
     RHD(hipGetLastError());
-    const size_t att_lds = attention_lds_floats(start + n) * 4u;
-    hipLaunchKernelGGL(hd == 64u ? attention_kernel<64> : attention_kernel<0>,
-                       dim3(static_cast<uint32_t>(c.head_count), nn), dim3(kAttnThreads), att_lds, s, d->q, kc, vc,
-                       w, kv, hd, static_cast<uint32_t>(c.head_count / c.head_count_kv), scale,
-                       static_cast<uint32_t>(start), d->mixed);
-    RHD(hipGetLastError());
-    RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
+    const uint32_t grp = static_cast<uint32_t>(c.head_count / c.head_count_kv);
+    const size_t glds = attention_group_lds_floats(grp, start + n) * 4u;
+    if (hd == 64u && (grp == 4u || grp == 8u) && glds <= kMaxLdsBytes) {
+      // the kv head's query heads together; the output as the O matrix's
+      // Q8_K operand when it takes one
+      const bool qa = d->quant_attn;
+      const AttnGroupFn fn = grp == 8u ? (qa ? attention_group_kernel<8, true> : attention_group_kernel<8, false>)
+                                       : (qa ? attention_group_kernel<4, true> : attention_group_kernel<4, false>);
+      hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(c.head_count_kv), nn), dim3(kAttnThreads), glds, s, d->q, kc,
+                         vc, w, kv, scale, static_cast<uint32_t>(start), d->mixed, q8_for(d, w));
+      RHD(hipGetLastError());
+      if (qa)
+        RHS(mm_q8(d, n, w, {{b.o, d->delta, n * w}}));
+      else
+        RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
+    } else {
+      const size_t att_lds = attention_lds_floats(start + n) * 4u;
+      hipLaunchKernelGGL(hd == 64u ? attention_kernel<64> : attention_kernel<0>,
+                         dim3(static_cast<uint32_t>(c.head_count), nn), dim3(kAttnThreads), att_lds, s, d->q, kc,
+                         vc, w, kv, hd, grp, scale, static_cast<uint32_t>(start), d->mixed);
+      RHD(hipGetLastError());
+      RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
+    }
     hipLaunchKernelGGL(norm_in.fn, dim3(nn), dim3(norm_in.threads), norm_lds, s, d->hidden, d->delta, nn, w,
                        b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
     RHD(hipGetLastError());
@@ -1514,6 +1636,13 @@ rh_status rh_decoder_new(rh_ctx* ctx, const rh_decoder_config* config, const rh_
   for (const rh_decoder::Block& b : d->blocks)
     qffn = qffn && is_kquant_matrix(b.down) && rh_matrix_cols(b.down) == c.feed_forward_length;
   d->quant_ffn = qffn && !(qenv && qenv[0] == '0');
+  // and the attention output, the O matrix's input, where the grouped
+  // attention kernel forms it (head_dim 64, four or eight heads a kv head)
+  const size_t grp = c.head_count_kv ? c.head_count / c.head_count_kv : 0;
+  bool qattn = c.head_dim == 64 && (grp == 4 || grp == 8) && w % 256 == 0;
+  for (const rh_decoder::Block& b : d->blocks)
+    qattn = qattn && is_kquant_matrix(b.o) && rh_matrix_cols(b.o) == w;
+  d->quant_attn = qattn && !(qenv && qenv[0] == '0');
   *out = d;
   return RH_OK;
 }

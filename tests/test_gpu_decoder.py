@@ -194,6 +194,23 @@ def test_head_dims_other_than_64_take_the_generic_attention(ctx, norm_path, head
     cpu.close()
 
 
+@pytest.mark.parametrize("heads,kv_heads,width", [(8, 2, 512), (16, 2, 1024)])
+def test_grouped_attention_matches_the_cpu_path(ctx, norm_path, heads, kv_heads, width):
+    # attention_group_kernel (head_dim 64, four or eight query heads a kv
+    # head) in batched forwards, its output stored or, with the norms'
+    # quantization on, quantized for the O matrix; against the CPU path
+    cfg = dict(SMALL, embedding_length=width, head_count=heads, head_count_kv=kv_heads, head_dim=64)
+    model = synth.decoder_model(cfg, seed=heads)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
+    tokens = np.random.default_rng(heads).integers(0, cfg["vocab_size"], 70).astype(np.uint32)
+    for start, chunk in ((0, tokens[:64]), (64, tokens[64:69]), (69, tokens[69:70])):
+        g, c = gpu.forward_batch(chunk, start), cpu.forward_batch(chunk, start)
+        assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
+    assert np.array_equal(gpu.generate_greedy(tokens, 12), cpu.generate_greedy(tokens, 12))
+    gpu.close()
+    cpu.close()
+
+
 def test_contexts_past_64_kib_of_attention_lds(ctx):
     # the attention kernels keep a context's weights in one workgroup's LDS:
     # at 9,000 rows that is more than 64 KiB (gfx950 gives a workgroup
