@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
         if (tok < T) split.terms[static_cast<size_t>(blockIdx.x * kRowsWG + 32u * wave + m) * T + tok] = y[t][i];
         continue;
       }
-      const size_t idx = static_cast<size_t>(row) * T + tok;
+      const size_t idx = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
       if (tok < T && idx < J.out_len) J.out[idx] = y[t][i];
     }
   }
@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const 
     const size_t tok = idx + e - static_cast<size_t>(grow) * tokens;
     const GemvJob& J = jobs.j[gemm_job(jobs, grow / bm)];
     const uint32_t row = grow - J.wg_begin * bm;
-    const size_t o = static_cast<size_t>(row) * tokens + tok;
+    const size_t o = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * tokens + tok;
     if (row < J.rows && o < J.out_len) J.out[o] = y[e];
   }
 }

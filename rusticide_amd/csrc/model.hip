@@ -59,7 +59,8 @@ __global__ __launch_bounds__(256) void embed_kernel(uint32_t type_id, const uint
     out[e] = embed_value(type_id, data, pitch, row, e);
 }
 
-// hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t]),
+// hidden[t] (+= the residual delta, stored by weight row: delta[e*n + t],
+// or with TM token-major: delta[t*width + e]),
 // then normed[t] = normalize(hidden[t], weight) for tokens t >= norm_from.
 // One workgroup of TH threads per token; each thread keeps its PER elements
 // (e = tid + TH k) in registers from the first load to the last store, so
@@ -69,7 +70,7 @@ constexpr uint32_t kMaxNormPer = 32;  // widths up to 256 * 32 = 8192
 // QUANT: the normalized row is not stored as f32 but quantized to Q8_K into
 // q8 (token t - norm_from), as quantize_super_kernel would from the f32 row;
 // width must then be a multiple of 256.
-template <uint32_t PER, bool QUANT, uint32_t TH>
+template <uint32_t PER, bool QUANT, uint32_t TH, bool TM>
 __global__ __launch_bounds__(TH) void add_norm_kernel(float* __restrict__ hidden, const float* __restrict__ delta,
                                                       uint32_t n, uint32_t width, const float* __restrict__ weight,
                                                       float eps, uint32_t norm_from, float* __restrict__ normed,
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(TH) void add_norm_kernel(float* __restrict__ hidden
     const uint32_t e = tid + k * TH;
     if (e < width) {
       v[k] = h[e];
-      if (delta) dl[k] = delta[static_cast<size_t>(e) * n + t];
+      if (delta) dl[k] = TM ? delta[static_cast<size_t>(t) * width + e] : delta[static_cast<size_t>(e) * n + t];
       if (norm) wt[k] = weight[e];
     }
   }
@@ -168,15 +169,15 @@ struct AddNorm {
   uint32_t threads;
 };
 
-template <bool QUANT = false>
+template <bool QUANT = false, bool TM = false>
 AddNorm add_norm_for(uint32_t width) {
   if (width >= 2048u) {
-    if (width <= 4u * 512u) return {add_norm_kernel<4, QUANT, 512>, 512u};
-    if (width <= 8u * 512u) return {add_norm_kernel<8, QUANT, 512>, 512u};
-    return {add_norm_kernel<kMaxNormPer / 2u, QUANT, 512>, 512u};
+    if (width <= 4u * 512u) return {add_norm_kernel<4, QUANT, 512, TM>, 512u};
+    if (width <= 8u * 512u) return {add_norm_kernel<8, QUANT, 512, TM>, 512u};
+    return {add_norm_kernel<kMaxNormPer / 2u, QUANT, 512, TM>, 512u};
   }
-  if (width <= 4u * kNormThreads) return {add_norm_kernel<4, QUANT, kNormThreads>, kNormThreads};
-  return {add_norm_kernel<8, QUANT, kNormThreads>, kNormThreads};
+  if (width <= 4u * kNormThreads) return {add_norm_kernel<4, QUANT, kNormThreads, TM>, kNormThreads};
+  return {add_norm_kernel<8, QUANT, kNormThreads, TM>, kNormThreads};
 }
 
 // q/k/v from the projections (stored by weight row, x[e*n + t]): q rotated
@@ -1178,9 +1179,9 @@ Q8Dev q8_for(const rh_decoder* d, size_t width) {
 
 // mm over the decoder's Q8_K activation (d->q8, which a QUANT norm or
 // silu_quant_kernel filled) for rows of `width` values.
-rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_job> jobs) {
+rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_job> jobs, bool token_major = false) {
   std::vector<rh_job> v(jobs);
-  return matmul_q8_device(d->ctx, q8_for(d, width), width, n, v.data(), v.size(), d->stream);
+  return matmul_q8_device(d->ctx, q8_for(d, width), width, n, v.data(), v.size(), d->stream, token_major);
 }
 
 #define RHD(expr)                                   \
@@ -1215,11 +1216,18 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   RHD(hipGetLastError());
   const float scale = ::sqrtf(static_cast<float>(c.head_dim));
   const size_t norm_lds = add_norm_lds(w);
-  const AddNorm norm_fn = add_norm_for(w);
+  const uint32_t grp = static_cast<uint32_t>(c.head_count / c.head_count_kv);
+  const size_t glds = attention_group_lds_floats(grp, start + n) * 4u;
+  const bool grouped = hd == 64u && (grp == 4u || grp == 8u) && glds <= kMaxLdsBytes;
+  // when both producers of the residual delta (the O and down matrices) are
+  // k-quant GEMMs over Q8_K operands, they store it token-major and the
+  // norms read it coalesced
+  const bool tm = grouped && d->quant_attn && d->quant_ffn && n >= rh_gemm_min_tokens();
+  const AddNorm norm_fn = tm ? add_norm_for<false, true>(w) : add_norm_for(w);
   // a batch whose normed rows feed only k-quant GEMMs gets them as Q8_K
   // straight from the norm kernel
   const bool qn = d->quant_norm && n >= 2;
-  const AddNorm norm_in = qn ? add_norm_for<true>(w) : norm_fn;
+  const AddNorm norm_in = qn ? (tm ? add_norm_for<true, true>(w) : add_norm_for<true>(w)) : norm_fn;
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
     const rh_decoder::Block& b = d->blocks[l];
@@ -1236,9 +1244,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
     hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn, w,
                        kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
     RHD(hipGetLastError());
-    const uint32_t grp = static_cast<uint32_t>(c.head_count / c.head_count_kv);
-    const size_t glds = attention_group_lds_floats(grp, start + n) * 4u;
-    if (hd == 64u && (grp == 4u || grp == 8u) && glds <= kMaxLdsBytes) {
+    if (grouped) {
       // the kv head's query heads together; the output as the O matrix's
       // Q8_K operand when it takes one
       const bool qa = d->quant_attn;
@@ -1248,7 +1254,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                          vc, w, kv, scale, static_cast<uint32_t>(start), d->mixed, q8_for(d, w));
       RHD(hipGetLastError());
       if (qa)
-        RHS(mm_q8(d, n, w, {{b.o, d->delta, n * w}}));
+        RHS(mm_q8(d, n, w, {{b.o, d->delta, n * w}}, tm));
       else
         RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
     } else {
@@ -1270,7 +1276,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
       hipLaunchKernelGGL(silu_quant_kernel, dim3(f / 256u, (nn + 3u) / 4u), dim3(256), 0, s, d->gate, d->up, nn,
                          q8_for(d, f));
       RHD(hipGetLastError());
-      RHS(mm_q8(d, n, f, {{b.down, d->delta, n * w}}));
+      RHS(mm_q8(d, n, f, {{b.down, d->delta, n * w}}, tm));
     } else {
       const size_t total = n * f;
       hipLaunchKernelGGL(silu_mul_kernel, dim3(static_cast<uint32_t>((total + 255u) / 256u)), dim3(256), 0, s,

@@ -41,7 +41,7 @@ struct GemvJob {
   // the norm-fused k-quant launch then writes silu(w x) * (w2 x) to out
   // instead of w x.
   const uint8_t* w2;
-  float* out;           // out[row * tokens + token]
+  float* out;           // out[row * tokens + token] (token-major: out[token * rows + row])
   size_t out_len;
   uint32_t stride;      // bytes between rows (I2_S, dense; a matrix stays below 4 GiB)
   uint32_t rows;        // rows to compute (already bounded by out_len)
@@ -54,7 +54,7 @@ struct GemvJob {
   // the grid exactly).
   uint32_t il = 0;
   uint32_t ub = 0;      // the matrix's blocks per row: block (r, b) is unit block r * ub + b
-  uint32_t pad_ = 0;
+  uint32_t tmajor = 0;  // k-quant GEMM only: 1 stores out token-major
 };
 // 64 bytes: every launch's kernel arguments hold kMaxJobs of these
 static_assert(sizeof(GemvJob) == 64, "GemvJob packs into 64 bytes");
@@ -150,8 +150,10 @@ size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens);
 int device_cus();
 // rh_matmul_batch_device for k-quant jobs on an activation already quantized
 // to Q8_K in `q` (width / 256 super-blocks for each of `tokens` tokens).
+// token_major: the outputs are stored out[token * rows + row] (same values);
+// only the GEMM path stores so, so tokens must be at least rh_gemm_min_tokens().
 rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tokens, const rh_job* jobs,
-                           size_t n_jobs, hipStream_t s);
+                           size_t n_jobs, hipStream_t s, bool token_major = false);
 // Whether a k-quant GEMM can address a batch: the quantized activation's
 // offsets (tokens x qstride bytes) are 32-bit.
 bool gemm_fits(size_t tokens, size_t qstride);
