@@ -415,11 +415,14 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
 // one workgroup per (kv head, token) forms the G heads' scores, softmaxes
 // and value mixes with attention_kernel's arithmetic, reading each key and
 // value row once for all G heads (a 64-token prefill of 32/4 heads: 256
-// workgroups instead of 2048). The scores give each head 256 / G lanes (one
-// row a lane per pass); the mix gives every thread the output lane
-// tid % 64 of heads tid / 64 + 4k. With QUANT the G heads' outputs, G / 4
-// whole 256-value blocks of the token's mixed row, are quantized to Q8_K
-// into q8 as quantize_super_kernel would from that row, and not stored.
+// workgroups instead of 2048). In the scores thread tid takes head tid % G
+// and rows tid / G + (256 / G) k: the G lanes of a row read its 16-byte
+// pieces together, so a load instruction touches 64 / G rows, not 64 (a
+// 64-row score pass: 1.3 against 3.9 us); the mix gives every thread the
+// output lane tid % 64 of heads tid / 64 + 4k. With QUANT the G heads'
+// outputs, G / 4 whole 256-value blocks of the token's mixed row, are
+// quantized to Q8_K into q8 as quantize_super_kernel would from that row,
+// and not stored.
 template <uint32_t G, bool QUANT>
 __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const float* q, const float* kcache,
                                                                        const float* vcache, uint32_t width,
@@ -429,9 +432,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
   constexpr uint32_t HD = 64u, L = kAttnThreads / G;  // lanes per head in the scores
   extern __shared__ __align__(16) float sh[];
   const uint32_t g = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
-  const uint32_t rows = start + t + 1u, ws = (rows + 3u) & ~3u;
-  float* qh = sh;                // [G][64]; with QUANT later the outputs
-  float* red = qh + G * HD;      // [64]
+  constexpr uint32_t QS = HD + 4u;  // LDS floats per query head: the G heads' reads fall on distinct banks
+  // ws: LDS floats per head's weights, 4 more than a multiple of 4, so that
+  // the G lanes summing the G heads at once read distinct banks
+  const uint32_t rows = start + t + 1u, ws = ((rows + 3u) & ~3u) + 4u;
+  float* qh = sh;                // [G][QS]; with QUANT later the outputs
+  float* red = qh + G * QS;      // [64]: the waves' maxima, then the sums
   float* w = red + 64;           // [G][ws]
   float* vt = w + G * ws;        // [2][kVTile * 64]
   const uint32_t off = g * HD;
@@ -439,9 +445,10 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
   // live over the scores' loop only as 16 floats)
   VTileRegs<HD> regs;
   regs.load(vcache, kv, off, HD, 0u, rows < kVTile ? rows : kVTile);
-  for (uint32_t i = tid; i < G * HD; i += kAttnThreads) qh[i] = q[static_cast<size_t>(t) * width + g * G * HD + i];
+  for (uint32_t i = tid; i < G * HD; i += kAttnThreads)
+    qh[(i / HD) * QS + i % HD] = q[static_cast<size_t>(t) * width + g * G * HD + i];
   __syncthreads();
-  const uint32_t j = tid / L, i0 = tid % L;
+  const uint32_t j = tid % G, i0 = tid / G;
   float* wj = w + j * ws;
   float mx = -INFINITY;
   for (uint32_t i = i0; i < rows; i += L) {
@@ -450,23 +457,25 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
 #pragma unroll
     for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    lanes64(qh + j * HD, k4, acc);
+    lanes64(qh + j * QS, k4, acc);
     const float score = score_from_lanes(acc, -0.0f, scale);
     wj[i] = score;
     mx = fmaxf(mx, score);
   }
-  // softmax_rows per head: the maximum over the head's lanes (an aligned
-  // half-wave, or a whole wave), exp, the sum in order from 0.0 on one lane
-  // of the head, the division
-  mx = max_key_float(half_max_u32(max_key(mx)));
-  if constexpr (L == 64u)
-    mx = fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 0)),
-               __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mx), 32)));
+  // softmax_rows per head: the maximum over the head's lanes (exact in any
+  // order; every lane's is a number, fmaxf having dropped NaN scores), exp,
+  // the sum in order from 0.0 on one lane of the head, the division
+  const uint32_t wave = tid >> 6;
+#pragma unroll
+  for (uint32_t o = G; o < 64u; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, static_cast<int>(o), 64));
+  if ((tid & 63u) < G) red[wave * G + j] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[j], red[G + j]), fmaxf(red[2u * G + j], red[3u * G + j]));
   for (uint32_t i = i0; i < rows; i += L) wj[i] = expf_ref(wj[i] - mx);
   __syncthreads();
-  if (i0 == 0) red[j] = ordered_sum(wj, rows, 0.0f);  // portable/norm.rs: `let mut sum = 0.0`
+  if (i0 == 0) red[32u + j] = ordered_sum(wj, rows, 0.0f);  // portable/norm.rs: `let mut sum = 0.0`
   __syncthreads();
-  const float sum = red[j];
+  const float sum = red[32u + j];
   for (uint32_t i = i0; i < rows; i += L) wj[i] = __fdiv_rn(wj[i], sum);
   regs.store(vt, HD, rows < kVTile ? rows : kVTile);
   __syncthreads();
@@ -510,7 +519,7 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
 #pragma unroll
     for (uint32_t h = 0; h < G / 4u; h++) qh[h * 256u + jp * HD + d] = acc[h];
     __syncthreads();
-    const uint32_t wave = tid >> 6, lane = tid & 63u;
+    const uint32_t lane = tid & 63u;
     if (wave < G / 4u) {
       const f32x4 v = reinterpret_cast<const f32x4*>(qh + wave * 256u)[lane];
       const float f[4] = {v[0], v[1], v[2], v[3]};
@@ -525,7 +534,7 @@ constexpr size_t kMaxLdsBytes = 160u * 1024u;  // a gfx950 workgroup's LDS
 
 // LDS floats attention_group_kernel needs for `rows` cached rows.
 inline size_t attention_group_lds_floats(size_t group, size_t rows) {
-  return group * 64u + 64u + group * ((rows + 3u) & ~size_t{3}) + 2u * kVTile * 64u;
+  return group * 68u + 64u + group * (((rows + 3u) & ~size_t{3}) + 4u) + 2u * kVTile * 64u;
 }
 
 // Value tile rows r0.. (below `rows`) of one kv head for head_dim 64, a
