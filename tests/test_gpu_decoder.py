@@ -211,6 +211,24 @@ def test_grouped_attention_matches_the_cpu_path(ctx, norm_path, heads, kv_heads,
     cpu.close()
 
 
+def test_grouped_attention_one_token_forwards_without_norm_fusion(ctx, monkeypatch):
+    # RUSTICIDE_HIP_NORM_FUSE=0 with the quantizing kernels on: one-token
+    # forwards take the batched path, where the grouped attention's Q8_K
+    # output feeds the O matrix's one-token GEMV
+    monkeypatch.setenv("RUSTICIDE_HIP_NORM_FUSE", "0")
+    monkeypatch.delenv("RUSTICIDE_HIP_NORM_QUANT", raising=False)
+    cfg = dict(SMALL, embedding_length=1024, head_count=16, head_count_kv=2, head_dim=64)
+    model = synth.decoder_model(cfg, seed=61)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
+    tokens = np.random.default_rng(61).integers(0, cfg["vocab_size"], 20).astype(np.uint32)
+    for start, chunk in ((0, tokens[:16]), (16, tokens[16:17]), (17, tokens[17:20])):
+        g, c = gpu.forward_batch(chunk, start), cpu.forward_batch(chunk, start)
+        assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
+    assert np.array_equal(gpu.generate_greedy(tokens, 8), cpu.generate_greedy(tokens, 8))
+    gpu.close()
+    cpu.close()
+
+
 def test_contexts_past_64_kib_of_attention_lds(ctx):
     # the attention kernels keep a context's weights in one workgroup's LDS:
     # at 9,000 rows that is more than 64 KiB (gfx950 gives a workgroup
