@@ -199,14 +199,17 @@ def test_grouped_attention_matches_the_cpu_path(ctx, norm_path, heads, kv_heads,
     # attention_group_kernel (head_dim 64, four or eight query heads a kv
     # head) in batched forwards, its output stored or, with the norms'
     # quantization on, quantized for the O matrix; against the CPU path
-    cfg = dict(SMALL, embedding_length=width, head_count=heads, head_count_kv=kv_heads, head_dim=64)
+    # chunks after the first reach past one 64-row value tile and start
+    # mid-context (the cached rows before `start` and the chunk's own)
+    cfg = dict(SMALL, embedding_length=width, head_count=heads, head_count_kv=kv_heads, head_dim=64,
+               context_length=256)
     model = synth.decoder_model(cfg, seed=heads)
     gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=8)
-    tokens = np.random.default_rng(heads).integers(0, cfg["vocab_size"], 70).astype(np.uint32)
-    for start, chunk in ((0, tokens[:64]), (64, tokens[64:69]), (69, tokens[69:70])):
-        g, c = gpu.forward_batch(chunk, start), cpu.forward_batch(chunk, start)
+    tokens = np.random.default_rng(heads).integers(0, cfg["vocab_size"], 200).astype(np.uint32)
+    for start, end in ((0, 64), (64, 69), (69, 70), (70, 134), (134, 200)):
+        g, c = gpu.forward_batch(tokens[start:end], start), cpu.forward_batch(tokens[start:end], start)
         assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
-    assert np.array_equal(gpu.generate_greedy(tokens, 12), cpu.generate_greedy(tokens, 12))
+    assert np.array_equal(gpu.generate_greedy(tokens[:70], 12), cpu.generate_greedy(tokens[:70], 12))
     gpu.close()
     cpu.close()
 
