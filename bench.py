@@ -33,7 +33,10 @@ TinyLlama-1.1B-shaped model in the Q4_K_M mix (22 layers, 2048 hidden, 32/4
 heads of 64, FFN 5632, vocab 32000; Q6_K lm_head and even-layer ffn_down),
 a 64-token prompt then 128 greedy tokens (generate.rs:35-124), f32 KV cache.
 tok/s = 128 / decode wall time, where decode time is a 129-token generation
-less a 1-token one (both include the same prefill). The CPU oracle decodes a
+less a 1-token one (both include the same prefill, and each pick is followed
+by its forward, as generate.rs:83-111 does); the prefill figure is the
+prompt's own forward (Decoder.forward_batch) to its last logits, with the
+1-token generation beside it. The CPU oracle decodes a
 few of the same tokens on the host cores beside it and must pick the same ones.
 The model reaches the device as a GGUF file (rusticide_amd.gguf writes it to
 a temporary file): `gguf_load` times mapping and parsing it (rh_gguf_open)
@@ -510,7 +513,7 @@ def measure_decode(ctx, reps: int, prompt_len: int = 64, new_tokens: int = 128):
         f"({load['upload_gbs']:.1f} GB/s host to HBM; a pinned-buffer copy reaches {h2d:.1f} GB/s)")
     prompt = np.random.default_rng(1).integers(0, synth.TINYLLAMA["vocab_size"], prompt_len).astype(np.uint32)
     tokens = dec.generate_greedy(prompt, new_tokens + 1)  # warm-up
-    decode_s, prefill_s = [], []
+    decode_s, gen1_s, prefill_s = [], [], []
     for _ in range(reps):
         t = time.perf_counter()
         dec.generate_greedy(prompt, 1)
@@ -520,7 +523,14 @@ def measure_decode(ctx, reps: int, prompt_len: int = 64, new_tokens: int = 128):
         tn = time.perf_counter() - t
         assert np.array_equal(got, tokens), "greedy decode is not deterministic"
         decode_s.append(tn - t1)
-        prefill_s.append(t1)
+        gen1_s.append(t1)
+        # the prefill alone: the prompt's forward to its last logits (a
+        # one-token generation also picks and, as generate.rs:83-111 does
+        # after every pick, runs the picked token's forward)
+        dec.reset()
+        t = time.perf_counter()
+        dec.forward_batch(prompt, 0)
+        prefill_s.append(time.perf_counter() - t)
     dec.close()
     gm.free()
     f.close()
@@ -530,7 +540,8 @@ def measure_decode(ctx, reps: int, prompt_len: int = 64, new_tokens: int = 128):
     return {
         "model": model, "prompt": prompt, "tokens": tokens[:new_tokens],
         "tok_s": new_tokens / d, "us_per_token": d / new_tokens * 1e6,
-        "prefill_ms": float(np.median(prefill_s)) * 1e3, "bytes_per_token": per_token,
+        "prefill_ms": float(np.median(prefill_s)) * 1e3, "generate_1_ms": float(np.median(gen1_s)) * 1e3,
+        "bytes_per_token": per_token,
         "gbs": per_token / (d / new_tokens) / 1e9, "gguf_load": load,
     }
 
@@ -668,7 +679,8 @@ def main() -> int:
     if args.decode_reps > 0:
         e2e = measure_decode(ctx, args.decode_reps)
         log(f"[bench] e2e decode: {e2e['tok_s']:.1f} tok/s ({e2e['us_per_token']:.1f} us/token, "
-            f"{e2e['gbs']:.0f} GB/s of compulsory bytes), prefill 64 tokens {e2e['prefill_ms']:.2f} ms")
+            f"{e2e['gbs']:.0f} GB/s of compulsory bytes), prefill 64 tokens {e2e['prefill_ms']:.2f} ms "
+                f"(a one-token generation, prefill + pick + the pick's forward: {e2e['generate_1_ms']:.2f} ms)")
     cpu = None if args.no_cpu else measure_cpu(h, args.cpu_seconds)
     if cpu:
         log(f"[bench] cpu baseline: {cpu['value']} GB/s ({cpu['sample']})")
@@ -695,7 +707,7 @@ def main() -> int:
             "workload": "TinyLlama-1.1B-shaped Q4_K_M random-init model, 64-token prompt + 128 greedy tokens, "
                         "batch 1, f32 KV cache",
             "tok_s": round(e2e["tok_s"], 1), "us_per_token": round(e2e["us_per_token"], 1),
-            "prefill_64_ms": round(e2e["prefill_ms"], 3),
+            "prefill_64_ms": round(e2e["prefill_ms"], 3), "generate_1_ms": round(e2e["generate_1_ms"], 3),
             "bytes_per_token": e2e["bytes_per_token"], "compulsory_gbs": round(e2e["gbs"], 1),
             "hbm_frac": round(e2e["gbs"] / HBM_PEAK_GBS, 4),
             "gguf_load": {k: (round(v, 2) if isinstance(v, float) else v) for k, v in e2e["gguf_load"].items()},
