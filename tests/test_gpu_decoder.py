@@ -214,6 +214,23 @@ def test_grouped_attention_matches_the_cpu_path(ctx, norm_path, heads, kv_heads,
     cpu.close()
 
 
+@pytest.mark.parametrize("tokens", [200, 320])
+def test_long_batches_store_the_residual_token_major_without_a_split(ctx, tokens):
+    # batches long enough that the O and down GEMMs run unsplit store the
+    # residual delta token-major from the GEMM epilogue itself (shorter ones
+    # through the split-K combine); a single forward_batch against the CPU path
+    cfg = dict(SMALL, embedding_length=1024, head_count=16, head_count_kv=2, head_dim=64, context_length=512)
+    model = synth.decoder_model(cfg, seed=71)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=16)
+    seq = np.random.default_rng(tokens).integers(0, cfg["vocab_size"], tokens + 1).astype(np.uint32)
+    g, c = gpu.forward_batch(seq[:tokens], 0), cpu.forward_batch(seq[:tokens], 0)
+    assert same_bits(g, c), f"max |diff| {diff(g, c)}"
+    g, c = gpu.forward_batch(seq[tokens:], tokens), cpu.forward_batch(seq[tokens:], tokens)
+    assert same_bits(g, c), f"next token: max |diff| {diff(g, c)}"
+    gpu.close()
+    cpu.close()
+
+
 def test_grouped_attention_one_token_forwards_without_norm_fusion(ctx, monkeypatch):
     # RUSTICIDE_HIP_NORM_FUSE=0 with the quantizing kernels on: one-token
     # forwards take the batched path, where the grouped attention's Q8_K
