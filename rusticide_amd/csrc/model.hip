@@ -251,6 +251,20 @@ struct VTileRegs {
       }
     }
   }
+  // load() for head_dim HD, rows from `start` on read from vnew (the batch's
+  // value projection, token-major with rows of kv floats) instead of vcache
+  __device__ __forceinline__ void load_split(const float* vcache, const float* vnew, uint32_t start, uint32_t kv,
+                                             uint32_t off, uint32_t r0, uint32_t count) {
+    static_assert(HD != 0, "head_dim fixed");
+#pragma unroll
+    for (uint32_t k = 0; k < kPer; k++) {
+      const uint32_t f = threadIdx.x + k * kAttnThreads;
+      const uint32_t r = f / (HD / 4u), c = f % (HD / 4u);
+      const uint32_t row = r0 + (r < count ? r : count - 1u);
+      const float* src = row >= start ? vnew + static_cast<size_t>(row - start) * kv : vcache + static_cast<size_t>(row) * kv;
+      v[k] = *reinterpret_cast<const T*>(src + off + 4u * c);
+    }
+  }
   __device__ __forceinline__ void store(float* tile, uint32_t hd, uint32_t count) const {
 #pragma unroll
     for (uint32_t k = 0; k < kPer; k++) {
@@ -423,11 +437,18 @@ __global__ __launch_bounds__(kAttnThreads) void attention_kernel(const float* q,
 // outputs, G / 4 whole 256-value blocks of the token's mixed row, are
 // quantized to Q8_K into q8 as quantize_super_kernel would from that row,
 // and not stored.
-template <uint32_t G, bool QUANT>
-__global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const float* q, const float* kcache,
-                                                                       const float* vcache, uint32_t width,
-                                                                       uint32_t kv, float scale, uint32_t start,
-                                                                       float* mixed, Q8Dev q8) {
+// With ROPE, qkv_post_kernel's work for the batch is done here too, so it
+// needs no launch of its own: q is the raw query projection, token-major;
+// keys and values of the batch's rows (start on) come raw from kr and vr
+// (token-major, kv floats a row), the keys rotated as they are read, and
+// the workgroups of a kv head's token t append its row start + t to the
+// caches (no workgroup of the launch reads those cache rows).
+template <uint32_t G, bool QUANT, bool ROPE>
+__global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const float* q, float* kcache, float* vcache,
+                                                                       uint32_t width, uint32_t kv, float scale,
+                                                                       uint32_t start, float* mixed, Q8Dev q8,
+                                                                       const float* kr, const float* vr,
+                                                                       const float* rcos, const float* rsin) {
   static_assert(G == 4u || G == 8u, "four or eight query heads per kv head");
   constexpr uint32_t HD = 64u, L = kAttnThreads / G;  // lanes per head in the scores
   extern __shared__ __align__(16) float sh[];
@@ -443,19 +464,75 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
   const uint32_t off = g * HD;
   // the first value tile goes out with the query heads (its registers stay
   // live over the scores' loop only as 16 floats)
+  constexpr uint32_t kPairs = HD / 2u;
   VTileRegs<HD> regs;
-  regs.load(vcache, kv, off, HD, 0u, rows < kVTile ? rows : kVTile);
-  for (uint32_t i = tid; i < G * HD; i += kAttnThreads)
-    qh[(i / HD) * QS + i % HD] = q[static_cast<size_t>(t) * width + g * G * HD + i];
+  if constexpr (ROPE)
+    regs.load_split(vcache, vr, start, kv, off, 0u, rows < kVTile ? rows : kVTile);
+  else
+    regs.load(vcache, kv, off, HD, 0u, rows < kVTile ? rows : kVTile);
+  if constexpr (ROPE) {
+    // qkv_post_kernel's rotation of the G query heads (pair p of head j), and
+    // of this token's key row into the cache (threads of the first head)
+    const uint32_t pos = start + t;
+    for (uint32_t pi = tid; pi < G * kPairs; pi += kAttnThreads) {
+      const uint32_t jh = pi / kPairs, p = pi % kPairs;
+      const float* src = q + static_cast<size_t>(t) * width + (g * G + jh) * HD;
+      const float lo = src[2u * p], hi = src[2u * p + 1u];
+      const float c = rcos[static_cast<size_t>(pos) * kPairs + p], sn = rsin[static_cast<size_t>(pos) * kPairs + p];
+      const float hs = hi * sn, ls = lo * sn;
+      qh[jh * QS + 2u * p] = __builtin_fmaf(lo, c, -hs);
+      qh[jh * QS + 2u * p + 1u] = __builtin_fmaf(hi, c, ls);
+      if (jh == 0u) {
+        const float* ks = kr + static_cast<size_t>(t) * kv + off;
+        const float klo = ks[2u * p], khi = ks[2u * p + 1u];
+        const float khs = khi * sn, kls = klo * sn;
+        float* kd = kcache + static_cast<size_t>(pos) * kv + off;
+        kd[2u * p] = __builtin_fmaf(klo, c, -khs);
+        kd[2u * p + 1u] = __builtin_fmaf(khi, c, kls);
+      }
+    }
+    if (tid >= 64u && tid < 64u + HD / 4u)
+      reinterpret_cast<f32x4*>(vcache + static_cast<size_t>(pos) * kv + off)[tid - 64u] =
+          reinterpret_cast<const f32x4*>(vr + static_cast<size_t>(t) * kv + off)[tid - 64u];
+  } else {
+    for (uint32_t i = tid; i < G * HD; i += kAttnThreads)
+      qh[(i / HD) * QS + i % HD] = q[static_cast<size_t>(t) * width + g * G * HD + i];
+  }
   __syncthreads();
   const uint32_t j = tid % G, i0 = tid / G;
   float* wj = w + j * ws;
   float mx = -INFINITY;
   for (uint32_t i = i0; i < rows; i += L) {
-    const float* kr = kcache + static_cast<size_t>(i) * kv + off;
+    // ROPE: a batch row (i >= start) is read raw and rotated here with
+    // qkv_post_kernel's expressions; the rotation's table loads are
+    // unconditional (a cached row drops their result)
+    const bool fresh = ROPE && i >= start;
+    const float* krow = fresh ? kr + static_cast<size_t>(i - start) * kv + off : kcache + static_cast<size_t>(i) * kv + off;
     f32x4 k4[16];
 #pragma unroll
-    for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(kr)[c];
+    for (int c = 0; c < 16; c++) k4[c] = reinterpret_cast<const f32x4*>(krow)[c];
+    if constexpr (ROPE) {
+      f32x4 cs[8], sn[8];
+#pragma unroll
+      for (int c = 0; c < 8; c++) {
+        cs[c] = reinterpret_cast<const f32x4*>(rcos + static_cast<size_t>(i) * kPairs)[c];
+        sn[c] = reinterpret_cast<const f32x4*>(rsin + static_cast<size_t>(i) * kPairs)[c];
+      }
+#pragma unroll
+      for (int c = 0; c < 16; c++) {
+        f32x4 r = k4[c];
+#pragma unroll
+        for (int u = 0; u < 2; u++) {
+          // pair 2c + u: elements 2u, 2u + 1 of the chunk
+          const float co = cs[c >> 1][2 * (c & 1) + u], si = sn[c >> 1][2 * (c & 1) + u];
+          const float lo = k4[c][2 * u], hi = k4[c][2 * u + 1];
+          const float hs = hi * si, ls = lo * si;
+          r[2 * u] = __builtin_fmaf(lo, co, -hs);
+          r[2 * u + 1] = __builtin_fmaf(hi, co, ls);
+        }
+        k4[c] = fresh ? r : k4[c];
+      }
+    }
     float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     lanes64(qh + j * QS, k4, acc);
     const float score = score_from_lanes(acc, -0.0f, scale);
@@ -490,7 +567,12 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
     const uint32_t count = rows - r0 < kVTile ? rows - r0 : kVTile;
     const bool more = tile + 1u < tiles;
     const uint32_t nr0 = r0 + kVTile, ncount = more ? (rows - nr0 < kVTile ? rows - nr0 : kVTile) : 0u;
-    if (more) regs.load(vcache, kv, off, HD, nr0, ncount);
+    if (more) {
+      if constexpr (ROPE)
+        regs.load_split(vcache, vr, start, kv, off, nr0, ncount);
+      else
+        regs.load(vcache, kv, off, HD, nr0, ncount);
+    }
     const float* cur = vt + (tile & 1u) * kVTile * 64u;
     uint32_t r = 0;
     for (; r + 16u <= count; r += 16u) {
@@ -528,8 +610,8 @@ __global__ __launch_bounds__(kAttnThreads) void attention_group_kernel(const flo
   }
 }
 
-using AttnGroupFn = void (*)(const float*, const float*, const float*, uint32_t, uint32_t, float, uint32_t, float*,
-                            Q8Dev);
+using AttnGroupFn = void (*)(const float*, float*, float*, uint32_t, uint32_t, float, uint32_t, float*, Q8Dev,
+                            const float*, const float*, const float*, const float*);
 constexpr size_t kMaxLdsBytes = 160u * 1024u;  // a gfx950 workgroup's LDS
 
 // LDS floats attention_group_kernel needs for `rows` cached rows.
@@ -1236,6 +1318,9 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   // a batch whose normed rows feed only k-quant GEMMs gets them as Q8_K
   // straight from the norm kernel
   const bool qn = d->quant_norm && n >= 2;
+  // with those and the token-major path, the QKV GEMM stores q, k and v
+  // token-major too and the grouped attention does qkv_post_kernel's work
+  const bool rope_in_attn = tm && qn;
   const AddNorm norm_in = qn ? (tm ? add_norm_for<true, true>(w) : add_norm_for<true>(w)) : norm_fn;
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
@@ -1244,23 +1329,31 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                        b.attn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
     RHD(hipGetLastError());
     if (qn)
-      RHS(mm_q8(d, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
+      RHS(mm_q8(d, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}, rope_in_attn));
     else
       RHS(mm(d, d->normed, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
     float* kc = d->keys + l * c.context_length * kv;
     float* vc = d->values + l * c.context_length * kv;
-    const uint32_t work = w / 2u + kv / 2u + kv;
-    hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn, w,
-                       kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
-    RHD(hipGetLastError());
+    if (!rope_in_attn) {
+      const uint32_t work = w / 2u + kv / 2u + kv;
+      hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn,
+                         w, kv, hd, d->rope_cos, d->rope_sin, static_cast<uint32_t>(start), d->q, kc, vc);
+      RHD(hipGetLastError());
+    }
     if (grouped) {
       // the kv head's query heads together; the output as the O matrix's
       // Q8_K operand when it takes one
       const bool qa = d->quant_attn;
-      const AttnGroupFn fn = grp == 8u ? (qa ? attention_group_kernel<8, true> : attention_group_kernel<8, false>)
-                                       : (qa ? attention_group_kernel<4, true> : attention_group_kernel<4, false>);
-      hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(c.head_count_kv), nn), dim3(kAttnThreads), glds, s, d->q, kc,
-                         vc, w, kv, scale, static_cast<uint32_t>(start), d->mixed, q8_for(d, w));
+      AttnGroupFn fn;
+      if (grp == 8u)
+        fn = rope_in_attn ? attention_group_kernel<8, true, true>
+                          : qa ? attention_group_kernel<8, true, false> : attention_group_kernel<8, false, false>;
+      else
+        fn = rope_in_attn ? attention_group_kernel<4, true, true>
+                          : qa ? attention_group_kernel<4, true, false> : attention_group_kernel<4, false, false>;
+      hipLaunchKernelGGL(fn, dim3(static_cast<uint32_t>(c.head_count_kv), nn), dim3(kAttnThreads), glds, s,
+                         rope_in_attn ? d->qr : d->q, kc, vc, w, kv, scale, static_cast<uint32_t>(start), d->mixed,
+                         q8_for(d, w), d->kr, d->vr, d->rope_cos, d->rope_sin);
       RHD(hipGetLastError());
       if (qa)
         RHS(mm_q8(d, n, w, {{b.o, d->delta, n * w}}, tm));
