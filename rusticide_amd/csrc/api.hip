@@ -168,7 +168,8 @@ size_t rows_for(const rh_matrix* m, size_t out_len, size_t tokens) {
 // launches quantize d_in themselves.
 rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t tokens, const rh_job* jobs,
                       size_t n_jobs, const Q8Dev& super_q, const Q8Dev& row_q, hipStream_t s,
-                      int32_t* raw, unsigned fused, bool allow_split = true, bool token_major = false) {
+                      int32_t* raw, unsigned fused, bool allow_split = true, bool token_major = false,
+                      SplitOut* defer = nullptr) {
   rh_status st = RH_OK;
   const uint32_t kinds[4] = {RH_TYPE_Q4_K, RH_TYPE_Q6_K, RH_TYPE_I2_S, RH_TYPE_F32};
   for (uint32_t kind : kinds) {
@@ -186,7 +187,7 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
           if (es != RH_OK) return es;
           terms = static_cast<float*>(ctx->buf[kTerms]);
         }
-        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, terms, s));
+        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, terms, s, defer));
         g = GemvJobs{};
         nbmax = 0;
         return RH_OK;
@@ -470,14 +471,16 @@ rh_status matmul_norm_silu_device(rh_ctx* ctx, const float* hidden, const NormIn
 }
 
 rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tokens, const rh_job* jobs,
-                           size_t n_jobs, hipStream_t s, bool token_major) {
+                           size_t n_jobs, hipStream_t s, bool token_major, SplitOut* defer) {
   if (!ctx || (!jobs && n_jobs) || tokens == 0) return RH_ERR_INVALID_ARGUMENT;
+  if (defer && (!token_major || n_jobs != 1)) return RH_ERR_INVALID_ARGUMENT;
+  if (defer) *defer = SplitOut{};
   for (size_t i = 0; i < n_jobs; i++)
     if (!jobs[i].weights || !is_kquant(jobs[i].weights->type_id) || (!jobs[i].out && jobs[i].out_len))
       return fail(ctx, RH_ERR_INVALID_ARGUMENT, "a pre-quantized job is not a k-quant matrix with an output");
   if (token_major && tokens < g_gemm_min_tokens)
     return fail(ctx, RH_ERR_INVALID_ARGUMENT, "token-major outputs need the GEMM path's token count");
-  return launch_jobs(ctx, nullptr, width, tokens, jobs, n_jobs, q, q, s, nullptr, 0u, true, token_major);
+  return launch_jobs(ctx, nullptr, width, tokens, jobs, n_jobs, q, q, s, nullptr, 0u, true, token_major, defer);
 }
 
 // Calls made without a context keep their message per thread

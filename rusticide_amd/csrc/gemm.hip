@@ -71,7 +71,13 @@ struct SplitTerms {
   float* terms;       // nullptr: no split
   uint32_t seg_len;   // blocks per segment
   uint32_t rows_pad;  // kRowsWG x the launch's workgroups along rows
+  uint32_t tmajor;    // 1: each plane token-major, [token][rows_pad]
 };
+
+// Offset of (padded row r, token t) within a plane.
+__device__ __forceinline__ size_t plane_at(const SplitTerms& sp, uint32_t r, size_t t, size_t tokens) {
+  return sp.tmajor ? t * sp.rows_pad + r : static_cast<size_t>(r) * tokens + t;
+}
 
 // ------------------------------------------------------------ row-owning form
 // A workgroup of 4 waves owns kRowsWG = 128 rows x 32*NT tokens; wave w owns
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
         }
         if (store_terms) {
           const size_t tok = tok0 + tl;
-          if (tok < T) plane[static_cast<size_t>(blockIdx.x * kRowsWG + 32u * wave + m) * T + tok] = term;
+          if (tok < T) plane[plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T)] = term;
         } else {
           y[t][i] += term;
         }
@@ -391,7 +397,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
     for (int t = 0; t < NT; t++) {
       const size_t tok = tok0 + 32u * t + ml;
       if (SPLIT) {  // segment 0 of a split launch: plane 0
-        if (tok < T) split.terms[static_cast<size_t>(blockIdx.x * kRowsWG + 32u * wave + m) * T + tok] = y[t][i];
+        if (tok < T) split.terms[plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T)] = y[t][i];
         continue;
       }
       const size_t idx = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
@@ -511,7 +517,7 @@ GemmPlan plan_gemm(const GemvJobs& jobs, size_t tokens) {
 
 template <int FMT, int NT>
 hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPlan& plan, float* terms,
-                       hipStream_t s) {
+                       hipStream_t s, SplitOut* defer) {
   const uint32_t wgs = row_tiles(jobs, kRowsWG);
   if (wgs == 0) return hipSuccess;
   const uint32_t tiles = static_cast<uint32_t>((tokens + 32u * NT - 1) / (32u * NT));
@@ -519,13 +525,17 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
   const bool split = plan.segs > 1 && terms;
   if (!split) {
     hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, false>), dim3(wgs, tiles), dim3(256), lds, s, jobs, q,
-                       tokens, SplitTerms{nullptr, 0u, 0u});
+                       tokens, SplitTerms{nullptr, 0u, 0u, 0u});
     return hipGetLastError();
   }
   hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
-                     jobs, q, tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad});
+                     jobs, q, tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad, defer ? 1u : 0u});
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  if (defer) {  // the caller sums the token-major planes in block order itself
+    *defer = SplitOut{terms, plan.planes, plan.rows_pad};
+    return hipSuccess;
+  }
   const size_t n = static_cast<size_t>(plan.rows_pad) * tokens;  // a multiple of 64
   hipLaunchKernelGGL(gemm_combine_kernel, dim3(static_cast<uint32_t>((n / 2u + 255u) / 256u)), dim3(256), 0, s, jobs,
                      terms, plan.planes, plan.rows_pad, tokens, kRowsWG);
@@ -534,9 +544,9 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
 
 template <int FMT>
 hipError_t launch_rows_fmt(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, const GemmPlan& g, float* terms,
-                           hipStream_t s) {
-  return g.nt == 2 ? launch_rows<FMT, 2>(jobs, q, tokens, g.split, terms, s)
-                   : launch_rows<FMT, 1>(jobs, q, tokens, g.split, terms, s);
+                           hipStream_t s, SplitOut* defer) {
+  return g.nt == 2 ? launch_rows<FMT, 2>(jobs, q, tokens, g.split, terms, s, defer)
+                   : launch_rows<FMT, 1>(jobs, q, tokens, g.split, terms, s, defer);
 }
 
 }  // namespace
@@ -552,12 +562,13 @@ size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens) {
 }
 
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
-                       hipStream_t s) {
+                       hipStream_t s, SplitOut* defer) {
+  if (defer) *defer = SplitOut{};
   if (tokens == 0) return hipSuccess;
   if (!gemm_fits(tokens, q.qstride)) return hipErrorInvalidValue;
   const GemmPlan g = plan_gemm(jobs, tokens);
-  if (type_id == 12u) return launch_rows_fmt<12>(jobs, q, tokens, g, terms, s);
-  if (type_id == 14u) return launch_rows_fmt<14>(jobs, q, tokens, g, terms, s);
+  if (type_id == 12u) return launch_rows_fmt<12>(jobs, q, tokens, g, terms, s, defer);
+  if (type_id == 14u) return launch_rows_fmt<14>(jobs, q, tokens, g, terms, s, defer);
   return hipErrorInvalidValue;
 }
 

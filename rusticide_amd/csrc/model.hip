@@ -70,11 +70,17 @@ constexpr uint32_t kMaxNormPer = 32;  // widths up to 256 * 32 = 8192
 // QUANT: the normalized row is not stored as f32 but quantized to Q8_K into
 // q8 (token t - norm_from), as quantize_super_kernel would from the f32 row;
 // width must then be a multiple of 256.
-template <uint32_t PER, bool QUANT, uint32_t TH, bool TM>
+// PL: the delta is a split GEMM's token-major planes (SplitOut: planes
+// `np` of rows_pad x n floats each, at `pl`), summed here in plane order as
+// gemm_combine_kernel would, so that GEMM needs no combine launch.
+constexpr uint32_t kPlaneBatch = 8;  // planes requested at once
+
+template <uint32_t PER, bool QUANT, uint32_t TH, bool TM, bool PL = false>
 __global__ __launch_bounds__(TH) void add_norm_kernel(float* __restrict__ hidden, const float* __restrict__ delta,
                                                       uint32_t n, uint32_t width, const float* __restrict__ weight,
                                                       float eps, uint32_t norm_from, float* __restrict__ normed,
-                                                      Q8Dev q8) {
+                                                      Q8Dev q8, const float* __restrict__ pl, uint32_t np,
+                                                      uint32_t rows_pad) {
   extern __shared__ __align__(16) float sq[];
   __shared__ float s_rms;
   const uint32_t t = blockIdx.x, tid = threadIdx.x;
@@ -90,7 +96,28 @@ __global__ __launch_bounds__(TH) void add_norm_kernel(float* __restrict__ hidden
       if (norm) wt[k] = weight[e];
     }
   }
-  if (delta) {
+  if constexpr (PL) {
+    // plane 0, then planes 1.. one addition at a time; each batch of planes
+    // requested before its first addition (indices clamped to the last)
+    const size_t psz = static_cast<size_t>(rows_pad) * n;
+    const float* base = pl + static_cast<size_t>(t) * rows_pad;
+    for (uint32_t p0 = 0; p0 < np; p0 += kPlaneBatch) {
+      float pv[kPlaneBatch][PER];
+#pragma unroll
+      for (uint32_t j = 0; j < kPlaneBatch; j++)
+#pragma unroll
+        for (uint32_t k = 0; k < PER; k++) {
+          const uint32_t e = min(tid + k * TH, width - 1u);
+          pv[j][k] = base[static_cast<size_t>(min(p0 + j, np - 1u)) * psz + e];
+        }
+#pragma unroll
+      for (uint32_t j = 0; j < kPlaneBatch; j++)
+#pragma unroll
+        for (uint32_t k = 0; k < PER; k++)
+          if (p0 + j < np) dl[k] = p0 + j == 0 ? pv[j][k] : dl[k] + pv[j][k];
+    }
+  }
+  if (delta || PL) {
 #pragma unroll
     for (uint32_t k = 0; k < PER; k++) {
       const uint32_t e = tid + k * TH;
@@ -151,7 +178,8 @@ __global__ __launch_bounds__(TH) void add_norm_kernel(float* __restrict__ hidden
   }
 }
 
-using AddNormFn = void (*)(float*, const float*, uint32_t, uint32_t, const float*, float, uint32_t, float*, Q8Dev);
+using AddNormFn = void (*)(float*, const float*, uint32_t, uint32_t, const float*, float, uint32_t, float*, Q8Dev,
+                          const float*, uint32_t, uint32_t);
 
 // Dynamic LDS of add_norm_kernel: the squares in the ordered sum's layout
 // (at least width floats, which the QUANT form reuses for the row).
@@ -169,15 +197,15 @@ struct AddNorm {
   uint32_t threads;
 };
 
-template <bool QUANT = false, bool TM = false>
+template <bool QUANT = false, bool TM = false, bool PL = false>
 AddNorm add_norm_for(uint32_t width) {
   if (width >= 2048u) {
-    if (width <= 4u * 512u) return {add_norm_kernel<4, QUANT, 512, TM>, 512u};
-    if (width <= 8u * 512u) return {add_norm_kernel<8, QUANT, 512, TM>, 512u};
-    return {add_norm_kernel<kMaxNormPer / 2u, QUANT, 512, TM>, 512u};
+    if (width <= 4u * 512u) return {add_norm_kernel<4, QUANT, 512, TM, PL>, 512u};
+    if (width <= 8u * 512u) return {add_norm_kernel<8, QUANT, 512, TM, PL>, 512u};
+    return {add_norm_kernel<kMaxNormPer / 2u, QUANT, 512, TM, PL>, 512u};
   }
-  if (width <= 4u * kNormThreads) return {add_norm_kernel<4, QUANT, kNormThreads, TM>, kNormThreads};
-  return {add_norm_kernel<8, QUANT, kNormThreads, TM>, kNormThreads};
+  if (width <= 4u * kNormThreads) return {add_norm_kernel<4, QUANT, kNormThreads, TM, PL>, kNormThreads};
+  return {add_norm_kernel<8, QUANT, kNormThreads, TM, PL>, kNormThreads};
 }
 
 // q/k/v from the projections (stored by weight row, x[e*n + t]): q rotated
@@ -1270,9 +1298,11 @@ Q8Dev q8_for(const rh_decoder* d, size_t width) {
 
 // mm over the decoder's Q8_K activation (d->q8, which a QUANT norm or
 // silu_quant_kernel filled) for rows of `width` values.
-rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_job> jobs, bool token_major = false) {
+// defer: a split launch leaves its token-major planes there (SplitOut).
+rh_status mm_q8(rh_decoder* d, size_t n, size_t width, std::initializer_list<rh_job> jobs, bool token_major = false,
+                SplitOut* defer = nullptr) {
   std::vector<rh_job> v(jobs);
-  return matmul_q8_device(d->ctx, q8_for(d, width), width, n, v.data(), v.size(), d->stream, token_major);
+  return matmul_q8_device(d->ctx, q8_for(d, width), width, n, v.data(), v.size(), d->stream, token_major, defer);
 }
 
 #define RHD(expr)                                   \
@@ -1322,11 +1352,13 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   // token-major too and the grouped attention does qkv_post_kernel's work
   const bool rope_in_attn = tm && qn;
   const AddNorm norm_in = qn ? (tm ? add_norm_for<true, true>(w) : add_norm_for<true>(w)) : norm_fn;
+  // the FFN norm that sums a split O launch's planes itself (no combine)
+  const AddNorm norm_pl = qn ? add_norm_for<true, true, true>(w) : add_norm_for<false, true, true>(w);
   const float* pending = nullptr;  // the residual the next norm adds first
   for (size_t l = 0; l < d->blocks.size(); l++) {
     const rh_decoder::Block& b = d->blocks[l];
     hipLaunchKernelGGL(norm_in.fn, dim3(nn), dim3(norm_in.threads), norm_lds, s, d->hidden, pending, nn, w,
-                       b.attn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
+                       b.attn_norm, c.rms_norm_eps, 0u, d->normed, d->q8, nullptr, 0u, 0u);
     RHD(hipGetLastError());
     if (qn)
       RHS(mm_q8(d, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}, rope_in_attn));
@@ -1334,6 +1366,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
       RHS(mm(d, d->normed, n, w, {{b.q, d->qr, n * w}, {b.k, d->kr, n * kv}, {b.v, d->vr, n * kv}}));
     float* kc = d->keys + l * c.context_length * kv;
     float* vc = d->values + l * c.context_length * kv;
+    SplitOut o_planes;
     if (!rope_in_attn) {
       const uint32_t work = w / 2u + kv / 2u + kv;
       hipLaunchKernelGGL(qkv_post_kernel, dim3((work + 255u) / 256u, nn), dim3(256), 0, s, d->qr, d->kr, d->vr, nn,
@@ -1356,7 +1389,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                          q8_for(d, w), d->kr, d->vr, d->rope_cos, d->rope_sin);
       RHD(hipGetLastError());
       if (qa)
-        RHS(mm_q8(d, n, w, {{b.o, d->delta, n * w}}, tm));
+        RHS(mm_q8(d, n, w, {{b.o, d->delta, n * w}}, tm, tm ? &o_planes : nullptr));
       else
         RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
     } else {
@@ -1367,8 +1400,13 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
       RHD(hipGetLastError());
       RHS(mm(d, d->mixed, n, w, {{b.o, d->delta, n * w}}));
     }
-    hipLaunchKernelGGL(norm_in.fn, dim3(nn), dim3(norm_in.threads), norm_lds, s, d->hidden, d->delta, nn, w,
-                       b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8);
+    if (o_planes.planes)
+      hipLaunchKernelGGL(norm_pl.fn, dim3(nn), dim3(norm_pl.threads), norm_lds, s, d->hidden, nullptr, nn, w,
+                         b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8, o_planes.terms, o_planes.planes,
+                         o_planes.rows_pad);
+    else
+      hipLaunchKernelGGL(norm_in.fn, dim3(nn), dim3(norm_in.threads), norm_lds, s, d->hidden, d->delta, nn, w,
+                         b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8, nullptr, 0u, 0u);
     RHD(hipGetLastError());
     if (qn)
       RHS(mm_q8(d, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
@@ -1390,7 +1428,7 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
   }
   // the last residual for every token, then the last token's output norm
   hipLaunchKernelGGL(norm_fn.fn, dim3(nn), dim3(norm_fn.threads), norm_lds, s, d->hidden, pending, nn, w,
-                     d->output_norm, c.rms_norm_eps, nn - 1u, d->normed, Q8Dev{});
+                     d->output_norm, c.rms_norm_eps, nn - 1u, d->normed, Q8Dev{}, nullptr, 0u, 0u);
   RHD(hipGetLastError());
   const rh_matrix* out = d->output ? d->output : d->token_embd;
   RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
@@ -1502,7 +1540,7 @@ rh_status forward_one_fused(rh_decoder* d, const uint32_t* tokens, size_t start,
   } else {
     const AddNorm an = add_norm_for(w);
     hipLaunchKernelGGL(an.fn, dim3(1), dim3(an.threads), add_norm_lds(w), s, h, pending, 1u, w, d->output_norm,
-                       c.rms_norm_eps, 0u, d->normed, Q8Dev{});
+                       c.rms_norm_eps, 0u, d->normed, Q8Dev{}, nullptr, 0u, 0u);
     RHD(hipGetLastError());
     RHS(mm(d, d->normed, 1, w, {{out, d->logits, c.vocab_size}}));
   }

@@ -122,6 +122,16 @@ hipError_t launch_quantize_row(const float* x, size_t width, size_t tokens, cons
 // (rh_device.h): whole groups of 16 blocks.
 size_t units_bytes(uint32_t type_id, size_t rows, size_t nb);
 
+// A split launch's planes left for the caller to sum (SplitOut.planes == 0:
+// the launch was not split and stored its outputs itself). Plane p holds, at
+// [token][rows_pad] over the launch's row tiles (a job's rows from its
+// wg_begin * 128 on), segment 0's in-order sum for p = 0 and block
+// seg_len + p - 1's term after it; the outputs are plane 0 plus planes 1..
+// in order, one addition at a time.
+struct SplitOut {
+  const float* terms = nullptr;
+  uint32_t planes = 0, rows_pad = 0;
+};
 // Grouped GEMV for one format: tokens [t0, t0+tn) of `tokens` total.
 hipError_t launch_gemv(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, const float* x,
                        size_t width, size_t tokens, size_t t0, size_t tn, hipStream_t s,
@@ -152,13 +162,17 @@ int device_cus();
 // to Q8_K in `q` (width / 256 super-blocks for each of `tokens` tokens).
 // token_major: the outputs are stored out[token * rows + row] (same values);
 // only the GEMM path stores so, so tokens must be at least rh_gemm_min_tokens().
+// defer (token_major only): a split launch leaves its planes there for the
+// caller (see launch_gemm); one k-quant job.
 rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tokens, const rh_job* jobs,
-                           size_t n_jobs, hipStream_t s, bool token_major = false);
+                           size_t n_jobs, hipStream_t s, bool token_major = false, SplitOut* defer = nullptr);
 // Whether a k-quant GEMM can address a batch: the quantized activation's
 // offsets (tokens x qstride bytes) are 32-bit.
 bool gemm_fits(size_t tokens, size_t qstride);
+// With defer, a split launch stores its planes token-major and leaves them
+// in *defer instead of combining them.
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
-                       hipStream_t s);
+                       hipStream_t s, SplitOut* defer = nullptr);
 // Prefill GEMM on int8 MFMA for I2_S against the I8_S activation q; with
 // `raw` the i32 dots go there instead of the scaled outputs.
 hipError_t launch_gemm_i2s(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, int32_t* raw, hipStream_t s);
