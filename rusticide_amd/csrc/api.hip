@@ -33,6 +33,9 @@ struct rh_ctx {
   // bumped whenever a scratch slot moves: graphs that captured the old
   // addresses must not be replayed
   uint64_t scratch_gen = 0;
+  // the split GEMMs' tile arrival counters (kFixupTiles, zero between
+  // launches); nullptr: every split GEMM combines in a launch of its own
+  uint32_t* tile_counters = nullptr;
   // pinned staging for matrix uploads, made on the first one
   uint8_t* stage[2] = {};
   hipEvent_t stage_done[2] = {};
@@ -187,7 +190,7 @@ rh_status launch_jobs(rh_ctx* ctx, const float* d_in, size_t width, size_t token
           if (es != RH_OK) return es;
           terms = static_cast<float*>(ctx->buf[kTerms]);
         }
-        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, terms, s, defer));
+        RH_HIP(ctx, launch_gemm(kind, g, q, tokens, terms, s, defer, ctx->tile_counters));
         g = GemvJobs{};
         nbmax = 0;
         return RH_OK;
@@ -404,6 +407,7 @@ void load_tuning() {
   const int bn = env_int("RUSTICIDE_HIP_GEMM_BN", 0);
   t.gemm_bn = bn == 32 || bn == 64 ? bn : 0;
   t.gemm_split = env_int("RUSTICIDE_HIP_GEMM_SPLIT", 1) != 0;
+  t.gemm_fixup = env_int("RUSTICIDE_HIP_GEMM_FIXUP", 1) != 0;
   t.attn_lds = env_int("RUSTICIDE_HIP_ATTN_LDS", 1) != 0;
   g_tuning.store(new Tuning(t), std::memory_order_release);
 }
@@ -794,6 +798,15 @@ rh_status rh_init(int device, rh_ctx** out) {
     delete ctx;
     return RH_ERR_DEVICE;
   }
+  // the split GEMMs' arrival counters, zeroed once; without them split
+  // GEMMs combine in a launch of their own
+  if (hipMalloc(&ctx->tile_counters, kFixupTiles * sizeof(uint32_t)) != hipSuccess ||
+      hipMemset(ctx->tile_counters, 0, kFixupTiles * sizeof(uint32_t)) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    (void)hipGetLastError();
+    if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
+    ctx->tile_counters = nullptr;
+  }
   // the allocation-free entry point's array on this device; a failure only
   // disables that entry point (it reports the error)
   const hipError_t se = scratch_setup(device);
@@ -811,6 +824,7 @@ void rh_destroy(rh_ctx* ctx) {
   hipStreamSynchronize(ctx->stream);
   for (void* b : ctx->buf)
     if (b) hipFree(b);
+  if (ctx->tile_counters) hipFree(ctx->tile_counters);
   for (int b = 0; b < 2; b++) {
     if (ctx->stage[b]) hipHostFree(ctx->stage[b]);
     if (ctx->stage_done[b]) hipEventDestroy(ctx->stage_done[b]);

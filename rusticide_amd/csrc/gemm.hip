@@ -68,15 +68,106 @@ __device__ __forceinline__ void q4k_scale_min(const u32x4& hd, uint32_t j, uint3
 // seg_len the term of block b >= seg_len; each plane is [rows_pad][tokens]
 // over the launch's row tiles.
 struct SplitTerms {
-  float* terms;       // nullptr: no split
-  uint32_t seg_len;   // blocks per segment
-  uint32_t rows_pad;  // kRowsWG x the launch's workgroups along rows
-  uint32_t tmajor;    // 1: each plane token-major, [token][rows_pad]
+  float* terms;        // nullptr: no split
+  uint32_t seg_len;    // blocks per segment
+  uint32_t rows_pad;   // kRowsWG x the launch's workgroups along rows
+  uint32_t tmajor;     // 1: each plane token-major, [token][rows_pad]
+  uint32_t planes;     // 1 + blocks - seg_len
+  uint32_t* counters;  // non-null: the tiles' arrival counts (split_fixup)
 };
 
 // Offset of (padded row r, token t) within a plane.
 __device__ __forceinline__ size_t plane_at(const SplitTerms& sp, uint32_t r, size_t t, size_t tokens) {
   return sp.tmajor ? t * sp.rows_pad + r : static_cast<size_t>(r) * tokens + t;
+}
+
+constexpr uint32_t kRowsWG = 128;  // rows a GEMM workgroup owns
+
+// ------------------------------------------------------------ split fixup
+// The end of a split launch without gemm_combine_kernel. Each workgroup, its
+// planes stored, counts itself in at its tile's counter (device scope); the
+// last of the tile's gridDim.z segments to arrive sums the tile's planes,
+// plane 0 then planes 1.. one addition at a time as gemm_combine_kernel
+// does (the same bits), stores the outputs and sets the counter back to 0
+// for the next launch. No workgroup waits on another. Plane layout
+// [rows_pad][tokens]; tokens a multiple of 4 (the host checks), so a
+// thread's four consecutive tokens are one 16-byte load.
+//
+// Coherence without cache maintenance: the workgroups of a tile may sit on
+// different XCDs, whose L2 caches are not coherent with one another. The
+// planes are therefore stored device-coherent (relaxed device-scope atomic
+// stores: sc1, written through the L2) and read device-coherent (sc1 buffer
+// loads); each wave waits for its stores to complete (vmcnt(0)) before the
+// workgroup's barrier, and one lane's counter increment follows the
+// barrier, so a workgroup that finds the count complete reads every plane
+// as stored. A release/acquire pair of fences instead writes back and
+// invalidates the whole L2 of an XCD per workgroup: a 64-token prefill
+// measured 2.35 ms that way against 2.04 with the separate combine launch.
+constexpr uint32_t kFixupPlanes = 8;  // planes requested at once per slot
+constexpr int kCoherentSc1 = 16;      // cache-policy bit sc1 of a buffer load
+constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9 buffer resource: raw 32-bit dwords
+
+// A plane value, stored device-coherent when a fixup reads it.
+__device__ __forceinline__ void store_plane(float* p, float v, bool coherent) {
+  if (coherent) __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else *p = v;
+}
+
+template <int NT>
+__device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTerms& sp, size_t T, uint32_t tok0,
+                                            uint32_t* last) {
+  // every wave's plane stores complete before one lane counts the
+  // workgroup in
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  uint32_t* const ctr = sp.counters + blockIdx.y * gridDim.x + blockIdx.x;
+  if (threadIdx.x == 0)
+    *last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u == gridDim.z;
+  __syncthreads();
+  if (!*last) return;
+  // slots of four tokens: 8*NT a row, kRowsWG rows, kSlots a thread; byte
+  // offsets within the planes (below 4 GiB, the host checks)
+  constexpr uint32_t kCols = 8u * NT, kSlots = kRowsWG * kCols / 256u, kAhead = kFixupPlanes / NT;
+  const uint32_t cols = static_cast<uint32_t>(min(static_cast<size_t>(32u * NT), T - tok0)) / 4u;
+  const uint32_t n4 = 4u * sp.rows_pad * static_cast<uint32_t>(T);
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(sp.terms, 0, static_cast<int>(n4 * sp.planes), kBufferRsrcWord3);
+  uint32_t base[kSlots];
+  f32x4 y[kSlots];
+#pragma unroll
+  for (uint32_t k = 0; k < kSlots; k++) {
+    const uint32_t sl = threadIdx.x + 256u * k, r = sl / kCols, c = sl % kCols;
+    base[k] = 4u * ((blockIdx.x * kRowsWG + r) * static_cast<uint32_t>(T) + tok0 + 4u * (c < cols ? c : 0u));
+    y[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base[k], 0, kCoherentSc1));
+  }
+  for (uint32_t p0 = 1; p0 < sp.planes; p0 += kAhead) {
+    f32x4 v[kAhead][kSlots];
+#pragma unroll
+    for (uint32_t j = 0; j < kAhead; j++)
+#pragma unroll
+      for (uint32_t k = 0; k < kSlots; k++)
+        v[j][k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rs, min(p0 + j, sp.planes - 1u) * n4 + base[k], 0, kCoherentSc1));
+#pragma unroll
+    for (uint32_t j = 0; j < kAhead; j++)
+#pragma unroll
+      for (uint32_t k = 0; k < kSlots; k++)
+        if (p0 + j < sp.planes) y[k] += v[j][k];
+  }
+  const GemvJob& J = jobs.j[gemm_job(jobs, blockIdx.x)];
+#pragma unroll
+  for (uint32_t k = 0; k < kSlots; k++) {
+    const uint32_t sl = threadIdx.x + 256u * k, r = sl / kCols, c = sl % kCols;
+    const uint32_t row = (blockIdx.x - J.wg_begin) * kRowsWG + r;
+    if (c >= cols || row >= J.rows) continue;
+#pragma unroll
+    for (uint32_t e = 0; e < 4u; e++) {
+      const size_t tok = tok0 + 4u * c + e;
+      const size_t o = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
+      if (o < J.out_len) J.out[o] = y[k][e];
+    }
+  }
+  if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ------------------------------------------------------------ row-owning form
@@ -97,7 +188,6 @@ __device__ __forceinline__ size_t plane_at(const SplitTerms& sp, uint32_t r, siz
 //
 // The matrices are in the unit layout (rh_device.h): the lane's pieces of a
 // block sit at fixed 16-byte-aligned offsets of its group of 16 blocks.
-constexpr uint32_t kRowsWG = 128;
 
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
@@ -375,7 +465,9 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
         }
         if (store_terms) {
           const size_t tok = tok0 + tl;
-          if (tok < T) plane[plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T)] = term;
+          if (tok < T)
+            store_plane(plane + plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T), term,
+                        split.counters != nullptr);
         } else {
           y[t][i] += term;
         }
@@ -387,22 +479,28 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
     }
     __syncthreads();
   }
-  if (store_terms) return;
+  if (!store_terms) {
 #pragma unroll
-  for (int i = 0; i < 16; i++) {
-    const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
-    const uint32_t row = row0 + 32u * wave + m;
-    if (row >= J.rows) continue;
+    for (int i = 0; i < 16; i++) {
+      const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
+      const uint32_t row = row0 + 32u * wave + m;
 #pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const size_t tok = tok0 + 32u * t + ml;
-      if (SPLIT) {  // segment 0 of a split launch: plane 0
-        if (tok < T) split.terms[plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T)] = y[t][i];
-        continue;
+      for (int t = 0; t < NT; t++) {
+        const size_t tok = tok0 + 32u * t + ml;
+        if (SPLIT) {  // segment 0 of a split launch: plane 0 (padded rows too)
+          if (tok < T)
+            store_plane(split.terms + plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T), y[t][i],
+                        split.counters != nullptr);
+          continue;
+        }
+        const size_t idx = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
+        if (row < J.rows && tok < T && idx < J.out_len) J.out[idx] = y[t][i];
       }
-      const size_t idx = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
-      if (tok < T && idx < J.out_len) J.out[idx] = y[t][i];
     }
+  }
+  if constexpr (SPLIT) {
+    __shared__ uint32_t fix_last;
+    if (split.counters) split_fixup<NT>(jobs, split, T, tok0, &fix_last);
   }
 }
 
@@ -517,7 +615,7 @@ GemmPlan plan_gemm(const GemvJobs& jobs, size_t tokens) {
 
 template <int FMT, int NT>
 hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const SplitPlan& plan, float* terms,
-                       hipStream_t s, SplitOut* defer) {
+                       hipStream_t s, SplitOut* defer, uint32_t* counters) {
   const uint32_t wgs = row_tiles(jobs, kRowsWG);
   if (wgs == 0) return hipSuccess;
   const uint32_t tiles = static_cast<uint32_t>((tokens + 32u * NT - 1) / (32u * NT));
@@ -525,13 +623,21 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
   const bool split = plan.segs > 1 && terms;
   if (!split) {
     hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, false>), dim3(wgs, tiles), dim3(256), lds, s, jobs, q,
-                       tokens, SplitTerms{nullptr, 0u, 0u, 0u});
+                       tokens, SplitTerms{nullptr, 0u, 0u, 0u, 0u, nullptr});
     return hipGetLastError();
   }
+  // the last segment of each tile sums its planes (split_fixup) when the
+  // tiles fit the counters, the tokens come in fours and the planes' byte
+  // offsets in 31 bits
+  const bool fixup = !defer && counters && tokens % 4u == 0 &&
+                     static_cast<size_t>(wgs) * tiles <= kFixupTiles && tuning().gemm_fixup &&
+                     static_cast<size_t>(plan.planes) * plan.rows_pad * tokens * sizeof(float) <= 0x7fffffffu;
   hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
-                     jobs, q, tokens, SplitTerms{terms, plan.seg_len, plan.rows_pad, defer ? 1u : 0u});
+                     jobs, q, tokens,
+                     SplitTerms{terms, plan.seg_len, plan.rows_pad, defer ? 1u : 0u, plan.planes,
+                                fixup ? counters : nullptr});
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || fixup) return e;
   if (defer) {  // the caller sums the token-major planes in block order itself
     *defer = SplitOut{terms, plan.planes, plan.rows_pad};
     return hipSuccess;
@@ -544,9 +650,9 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
 
 template <int FMT>
 hipError_t launch_rows_fmt(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, const GemmPlan& g, float* terms,
-                           hipStream_t s, SplitOut* defer) {
-  return g.nt == 2 ? launch_rows<FMT, 2>(jobs, q, tokens, g.split, terms, s, defer)
-                   : launch_rows<FMT, 1>(jobs, q, tokens, g.split, terms, s, defer);
+                           hipStream_t s, SplitOut* defer, uint32_t* counters) {
+  return g.nt == 2 ? launch_rows<FMT, 2>(jobs, q, tokens, g.split, terms, s, defer, counters)
+                   : launch_rows<FMT, 1>(jobs, q, tokens, g.split, terms, s, defer, counters);
 }
 
 }  // namespace
@@ -562,13 +668,13 @@ size_t gemm_split_bytes(uint32_t type_id, const GemvJobs& jobs, size_t tokens) {
 }
 
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
-                       hipStream_t s, SplitOut* defer) {
+                       hipStream_t s, SplitOut* defer, uint32_t* counters) {
   if (defer) *defer = SplitOut{};
   if (tokens == 0) return hipSuccess;
   if (!gemm_fits(tokens, q.qstride)) return hipErrorInvalidValue;
   const GemmPlan g = plan_gemm(jobs, tokens);
-  if (type_id == 12u) return launch_rows_fmt<12>(jobs, q, tokens, g, terms, s, defer);
-  if (type_id == 14u) return launch_rows_fmt<14>(jobs, q, tokens, g, terms, s, defer);
+  if (type_id == 12u) return launch_rows_fmt<12>(jobs, q, tokens, g, terms, s, defer, counters);
+  if (type_id == 14u) return launch_rows_fmt<14>(jobs, q, tokens, g, terms, s, defer, counters);
   return hipErrorInvalidValue;
 }
 

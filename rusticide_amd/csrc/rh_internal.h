@@ -106,6 +106,7 @@ struct Tuning {
   bool i2s_one = true;     // RUSTICIDE_HIP_I2S_ONE=0: one token on the two-token kernel
   int gemm_bn = 0;         // RUSTICIDE_HIP_GEMM_BN=32|64: tokens a GEMM workgroup
   bool gemm_split = true;  // RUSTICIDE_HIP_GEMM_SPLIT=0
+  bool gemm_fixup = true;  // RUSTICIDE_HIP_GEMM_FIXUP=0: a split GEMM's planes summed by gemm_combine_kernel
   bool attn_lds = true;    // RUSTICIDE_HIP_ATTN_LDS=0: the tiled attention step only
 };
 const Tuning& tuning();
@@ -169,10 +170,17 @@ rh_status matmul_q8_device(rh_ctx* ctx, const Q8Dev& q, size_t width, size_t tok
 // Whether a k-quant GEMM can address a batch: the quantized activation's
 // offsets (tokens x qstride bytes) are 32-bit.
 bool gemm_fits(size_t tokens, size_t qstride);
+// Tiles (row tiles x token tiles) of a split k-quant GEMM launch whose
+// last-arriving segment sums the planes itself: `counters` of launch_gemm
+// holds this many u32, all zero between launches (each launch leaves them
+// so); larger launches, and batches whose token count is not a multiple of
+// 4, sum them in a gemm_combine_kernel launch. Launches that share the
+// counters must not overlap (one stream).
+constexpr uint32_t kFixupTiles = 16384;
 // With defer, a split launch stores its planes token-major and leaves them
 // in *defer instead of combining them.
 hipError_t launch_gemm(uint32_t type_id, const GemvJobs& jobs, const Q8Dev& q, size_t tokens, float* terms,
-                       hipStream_t s, SplitOut* defer = nullptr);
+                       hipStream_t s, SplitOut* defer = nullptr, uint32_t* counters = nullptr);
 // Prefill GEMM on int8 MFMA for I2_S against the I8_S activation q; with
 // `raw` the i32 dots go there instead of the scaled outputs.
 hipError_t launch_gemm_i2s(const GemvJobs& jobs, const Q8Dev& q, size_t tokens, int32_t* raw, hipStream_t s);

@@ -310,6 +310,41 @@ def test_split_k_gives_the_unsplit_bits(ctx, tuning, type_id, rows, cols, tokens
     assert_same_bits(split, oracle_matmul(type_id, data, rows, cols, x, tokens, threads=16))
 
 
+@pytest.mark.parametrize("tokens", [64, 36, 12])
+def test_split_k_tile_fixup_matches_the_combine_launch(ctx, tuning, tokens):
+    # a split launch whose token count is a multiple of 4 sums each tile's
+    # planes in the tile's last-arriving workgroup (device-scope arrival
+    # counters, reset by that workgroup); RUSTICIDE_HIP_GEMM_FIXUP=0 sums them
+    # in gemm_combine_kernel. Jobs whose rows end mid-tile (two in one Q4_K
+    # launch), a 21-plane Q6_K launch, the calls repeated and interleaved so
+    # that a counter left non-zero shows
+    cols = 2048
+    specs = [(12, 300, synth.matrix(12, 300, cols, seed=11)), (12, 45, synth.matrix(12, 45, cols, seed=12)),
+             (14, 100, synth.matrix(14, 100, cols, seed=14))]
+    mats = [R.Matrix.load(ctx, t, d, rows, cols) for t, rows, d in specs]
+    big = synth.matrix(14, 2048, 5632, seed=13)
+    mbig = R.Matrix.load(ctx, 14, big, 2048, 5632)
+    x = synth.normal_f32(tokens * cols, seed=21 + tokens)
+    xb = synth.normal_f32(tokens * 5632, seed=22 + tokens)
+
+    def run():
+        outs = [np.full(rows * tokens, np.nan, np.float32) for _, rows, _ in specs]
+        R.matmul_batch(ctx, x, tokens, list(zip(mats, outs)))
+        ob = np.full(2048 * tokens, np.nan, np.float32)
+        R.matmul_batch(ctx, xb, tokens, [(mbig, ob)])
+        return outs + [ob]
+
+    first = [run() for _ in range(3)]
+    tuning.set("RUSTICIDE_HIP_GEMM_FIXUP", "0")
+    combined = run()
+    for outs in first:
+        for a, b in zip(outs, combined):
+            assert_same_bits(a, b, f"tokens={tokens}")
+    for (t, rows, d), out in zip(specs, combined[:-1]):
+        assert_same_bits(out, oracle_matmul(t, d, rows, cols, x, tokens), f"type {t} rows {rows}")
+    assert_same_bits(combined[-1], oracle_matmul(14, big, 2048, 5632, xb, tokens, threads=16))
+
+
 def test_prefill_gemm_batch_of_projections_and_hostile_bytes(ctx):
     # Q/K/V in one batch (attention.rs:215-223) on the GEMM, plus random block
     # bytes (f16 inf/NaN scales) that must compute what the CPU path computes
