@@ -104,6 +104,12 @@ constexpr uint32_t kRowsWG = 128;  // rows a GEMM workgroup owns
 // invalidates the whole L2 of an XCD per workgroup: a 64-token prefill
 // measured 2.35 ms that way against 2.04 with the separate combine launch.
 constexpr uint32_t kFixupPlanes = 8;  // planes requested at once per slot
+// Launches of more planes combine in gemm_combine_kernel: one workgroup
+// reading a tile's planes in several rounds is slower than the separate
+// launch (a 64-token prefill's 21-plane down GEMMs: 18.4-21.2 us with the
+// fixup against 16.3-18.9 with the combine; its 8-plane QKV GEMM 11.8
+// against 14.5).
+constexpr uint32_t kFixupMaxPlanes = 1 + kFixupPlanes;
 constexpr int kCoherentSc1 = 16;      // cache-policy bit sc1 of a buffer load
 constexpr int kBufferRsrcWord3 = 0x00020000;  // gfx9 buffer resource: raw 32-bit dwords
 
@@ -626,11 +632,12 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
                        tokens, SplitTerms{nullptr, 0u, 0u, 0u, 0u, nullptr});
     return hipGetLastError();
   }
-  // the last segment of each tile sums its planes (split_fixup) when the
-  // tiles fit the counters, the tokens come in fours and the planes' byte
-  // offsets in 31 bits
+  // the last segment of each tile sums its planes (split_fixup) when they
+  // are few, the tiles fit the counters, the tokens come in fours and the
+  // planes' byte offsets in 31 bits
   const bool fixup = !defer && counters && tokens % 4u == 0 &&
                      static_cast<size_t>(wgs) * tiles <= kFixupTiles && tuning().gemm_fixup &&
+                     plan.planes <= kFixupMaxPlanes &&
                      static_cast<size_t>(plan.planes) * plan.rows_pad * tokens * sizeof(float) <= 0x7fffffffu;
   hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
                      jobs, q, tokens,

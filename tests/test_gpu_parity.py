@@ -312,12 +312,13 @@ def test_split_k_gives_the_unsplit_bits(ctx, tuning, type_id, rows, cols, tokens
 
 @pytest.mark.parametrize("tokens", [64, 36, 12])
 def test_split_k_tile_fixup_matches_the_combine_launch(ctx, tuning, tokens):
-    # a split launch whose token count is a multiple of 4 sums each tile's
-    # planes in the tile's last-arriving workgroup (device-scope arrival
-    # counters, reset by that workgroup); RUSTICIDE_HIP_GEMM_FIXUP=0 sums them
-    # in gemm_combine_kernel. Jobs whose rows end mid-tile (two in one Q4_K
-    # launch), a 21-plane Q6_K launch, the calls repeated and interleaved so
-    # that a counter left non-zero shows
+    # a split launch of up to 9 planes whose token count is a multiple of 4
+    # sums each tile's planes in the tile's last-arriving workgroup
+    # (device-scope arrival counters, reset by that workgroup);
+    # RUSTICIDE_HIP_GEMM_FIXUP=0 sums them in gemm_combine_kernel. Jobs whose
+    # rows end mid-tile (two in one Q4_K launch), a 21-plane Q6_K launch
+    # (always combined) between them, the calls repeated so that a counter
+    # left non-zero shows
     cols = 2048
     specs = [(12, 300, synth.matrix(12, 300, cols, seed=11)), (12, 45, synth.matrix(12, 45, cols, seed=12)),
              (14, 100, synth.matrix(14, 100, cols, seed=14))]
