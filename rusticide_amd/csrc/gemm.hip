@@ -119,6 +119,27 @@ __device__ __forceinline__ void store_plane(float* p, float v, bool coherent) {
   else *p = v;
 }
 
+// A lane's 16 values of one token into a plane: register 4q + u holds row
+// 8q + 4g + u of the wave's 32 (the MFMA's D layout), so a token-major
+// plane takes them as four 16-byte stores of four consecutive rows (a store
+// instruction then writes 32 bytes a token instead of 4).
+__device__ __forceinline__ void store_lane_plane(const SplitTerms& sp, float* plane, uint32_t r0, uint32_t g,
+                                                 size_t tok, size_t T, const float (&v)[16]) {
+  const bool coherent = sp.counters != nullptr;
+  if (sp.tmajor && !coherent) {
+    float* p = plane + tok * sp.rows_pad + r0 + 4u * g;
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      *reinterpret_cast<f32x4*>(p + 8u * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < 16; i++) {
+    const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
+    store_plane(plane + plane_at(sp, r0 + m, tok, T), v[i], coherent);
+  }
+}
+
 template <int NT>
 __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTerms& sp, size_t T, uint32_t tok0,
                                             uint32_t* last) {
@@ -454,6 +475,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
       }
       // the block's float term per (row, token), added in block order
       // (D layout: lane n + 32*((m/4)%2), register 4*(m/8) + m%4)
+      float tv[16];
 #pragma unroll
       for (int i = 0; i < 16; i++) {
         const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
@@ -469,15 +491,11 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
           const float sd = dd.x * d8;
           term = sd * static_cast<float>(isum);
         }
-        if (store_terms) {
-          const size_t tok = tok0 + tl;
-          if (tok < T)
-            store_plane(plane + plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T), term,
-                        split.counters != nullptr);
-        } else {
-          y[t][i] += term;
-        }
+        if (store_terms) tv[i] = term;
+        else y[t][i] += term;
       }
+      if (store_terms && tok0 + tl < T)
+        store_lane_plane(split, plane, blockIdx.x * kRowsWG + 32u * wave, g, tok0 + tl, T, tv);
     }
     if (more) {
       store_act(cur ^ 1u);
@@ -485,7 +503,27 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
     }
     __syncthreads();
   }
-  if (!store_terms) {
+  if (SPLIT && !store_terms) {  // segment 0 of a split launch: plane 0 (padded rows too)
+#pragma unroll
+    for (int t = 0; t < NT; t++)
+      if (tok0 + 32u * t + ml < T)
+        store_lane_plane(split, split.terms, blockIdx.x * kRowsWG + 32u * wave, g, tok0 + 32u * t + ml, T, y[t]);
+  } else if (!SPLIT && J.tmajor && J.rows % 4u == 0) {
+    // token-major outputs, four consecutive rows a 16-byte store (whole
+    // groups of four rows are inside the job or past it)
+#pragma unroll
+    for (int t = 0; t < NT; t++) {
+      const size_t tok = tok0 + 32u * t + ml;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const uint32_t row = row0 + 32u * wave + 8u * static_cast<uint32_t>(q) + 4u * g;
+        const size_t idx = tok * J.rows + row;
+        if (row < J.rows && tok < T && idx + 4u <= J.out_len)
+          *reinterpret_cast<f32x4*>(J.out + idx) =
+              f32x4{y[t][4 * q], y[t][4 * q + 1], y[t][4 * q + 2], y[t][4 * q + 3]};
+      }
+    }
+  } else if (!SPLIT) {
 #pragma unroll
     for (int i = 0; i < 16; i++) {
       const uint32_t m = 8u * static_cast<uint32_t>(i >> 2) + 4u * g + static_cast<uint32_t>(i & 3);
@@ -493,12 +531,6 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
 #pragma unroll
       for (int t = 0; t < NT; t++) {
         const size_t tok = tok0 + 32u * t + ml;
-        if (SPLIT) {  // segment 0 of a split launch: plane 0 (padded rows too)
-          if (tok < T)
-            store_plane(split.terms + plane_at(split, blockIdx.x * kRowsWG + 32u * wave + m, tok, T), y[t][i],
-                        split.counters != nullptr);
-          continue;
-        }
         const size_t idx = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
         if (row < J.rows && tok < T && idx < J.out_len) J.out[idx] = y[t][i];
       }
