@@ -508,7 +508,7 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
     for (int t = 0; t < NT; t++)
       if (tok0 + 32u * t + ml < T)
         store_lane_plane(split, split.terms, blockIdx.x * kRowsWG + 32u * wave, g, tok0 + 32u * t + ml, T, y[t]);
-  } else if (!SPLIT && J.tmajor && J.rows % 4u == 0) {
+  } else if (!SPLIT && J.tmajor && J.rows % 4u == 0 && (reinterpret_cast<uintptr_t>(J.out) & 15u) == 0) {
     // token-major outputs, four consecutive rows a 16-byte store (whole
     // groups of four rows are inside the job or past it)
 #pragma unroll
@@ -552,9 +552,11 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
 // order.
 constexpr uint32_t kCombineAhead = 24;
 
+// tmajor: the planes are [tokens][rows_pad] (written so for token-major
+// outputs, which are then stored in runs of consecutive rows).
 __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const float* __restrict__ terms,
                                                            uint32_t planes, uint32_t rows_pad, size_t tokens,
-                                                           uint32_t bm) {
+                                                           uint32_t bm, uint32_t tmajor) {
   const size_t n = static_cast<size_t>(rows_pad) * tokens;
   const size_t idx = (static_cast<size_t>(blockIdx.x) * 256u + threadIdx.x) * 2u;
   if (idx >= n) return;
@@ -569,6 +571,27 @@ __global__ __launch_bounds__(256) void gemm_combine_kernel(GemvJobs jobs, const 
 #pragma unroll
     for (uint32_t k = 0; k < kCombineAhead; k++)
       if (p0 + k < planes) y += v[k];
+  }
+  if (tmajor) {
+    // both slots are one token's rows grow, grow + 1 of one row tile
+    const size_t tok = idx / rows_pad;
+    const uint32_t grow = static_cast<uint32_t>(idx - tok * rows_pad);
+    const GemvJob& J = jobs.j[gemm_job(jobs, grow / bm)];
+    const uint32_t row = grow - J.wg_begin * bm;
+    if (J.tmajor) {
+      const size_t o = tok * J.rows + row;
+      if (row + 1u < J.rows && o + 2u <= J.out_len && (reinterpret_cast<uintptr_t>(J.out + o) & 7u) == 0) {
+        *reinterpret_cast<f32x2*>(J.out + o) = y;
+        return;
+      }
+    }
+#pragma unroll
+    for (uint32_t e = 0; e < 2u; e++) {
+      const uint32_t r = row + e;
+      const size_t o = J.tmajor ? tok * J.rows + r : static_cast<size_t>(r) * tokens + tok;
+      if (r < J.rows && o < J.out_len) J.out[o] = y[e];
+    }
+    return;
   }
 #pragma unroll
   for (int e = 0; e < 2; e++) {
@@ -671,10 +694,13 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
                      static_cast<size_t>(wgs) * tiles <= kFixupTiles && tuning().gemm_fixup &&
                      plan.planes <= kFixupMaxPlanes &&
                      static_cast<size_t>(plan.planes) * plan.rows_pad * tokens * sizeof(float) <= 0x7fffffffu;
+  // token-major planes for the caller, and for the combine of token-major
+  // outputs (its reads and stores then both run along rows); the fixup reads
+  // [rows_pad][tokens] planes (every job of a launch has the same tmajor)
+  const uint32_t tplanes = defer || (!fixup && jobs.j[0].tmajor) ? 1u : 0u;
   hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
                      jobs, q, tokens,
-                     SplitTerms{terms, plan.seg_len, plan.rows_pad, defer ? 1u : 0u, plan.planes,
-                                fixup ? counters : nullptr});
+                     SplitTerms{terms, plan.seg_len, plan.rows_pad, tplanes, plan.planes, fixup ? counters : nullptr});
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess || fixup) return e;
   if (defer) {  // the caller sums the token-major planes in block order itself
@@ -683,7 +709,7 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
   }
   const size_t n = static_cast<size_t>(plan.rows_pad) * tokens;  // a multiple of 64
   hipLaunchKernelGGL(gemm_combine_kernel, dim3(static_cast<uint32_t>((n / 2u + 255u) / 256u)), dim3(256), 0, s, jobs,
-                     terms, plan.planes, plan.rows_pad, tokens, kRowsWG);
+                     terms, plan.planes, plan.rows_pad, tokens, kRowsWG, tplanes);
   return hipGetLastError();
 }
 
