@@ -89,9 +89,11 @@ constexpr uint32_t kRowsWG = 128;  // rows a GEMM workgroup owns
 // last of the tile's gridDim.z segments to arrive sums the tile's planes,
 // plane 0 then planes 1.. one addition at a time as gemm_combine_kernel
 // does (the same bits), stores the outputs and sets the counter back to 0
-// for the next launch. No workgroup waits on another. Plane layout
-// [rows_pad][tokens]; tokens a multiple of 4 (the host checks), so a
-// thread's four consecutive tokens are one 16-byte load.
+// for the next launch. No workgroup waits on another. Tokens come in
+// multiples of 4 (the host checks): a thread's slot is four consecutive
+// tokens of a row in [rows_pad][tokens] planes, or four consecutive rows of
+// a token in token-major planes (token-major outputs), one 16-byte load
+// either way.
 //
 // Coherence without cache maintenance: the workgroups of a tile may sit on
 // different XCDs, whose L2 caches are not coherent with one another. The
@@ -122,15 +124,27 @@ __device__ __forceinline__ void store_plane(float* p, float v, bool coherent) {
 // A lane's 16 values of one token into a plane: register 4q + u holds row
 // 8q + 4g + u of the wave's 32 (the MFMA's D layout), so a token-major
 // plane takes them as four 16-byte stores of four consecutive rows (a store
-// instruction then writes 32 bytes a token instead of 4).
+// instruction then writes 32 bytes a token instead of 4); device-coherent
+// ones (a fixup reads them) as sc1 buffer stores.
 __device__ __forceinline__ void store_lane_plane(const SplitTerms& sp, float* plane, uint32_t r0, uint32_t g,
                                                  size_t tok, size_t T, const float (&v)[16]) {
   const bool coherent = sp.counters != nullptr;
-  if (sp.tmajor && !coherent) {
-    float* p = plane + tok * sp.rows_pad + r0 + 4u * g;
+  if (sp.tmajor) {
+    const size_t at = static_cast<size_t>(plane - sp.terms) + tok * sp.rows_pad + r0 + 4u * g;
+    if (coherent) {
+      const uint32_t bytes = 4u * sp.rows_pad * static_cast<uint32_t>(T) * sp.planes;  // below 2^31
+      const __amdgpu_buffer_rsrc_t rs =
+          __builtin_amdgcn_make_buffer_rsrc(sp.terms, 0, static_cast<int>(bytes), kBufferRsrcWord3);
+#pragma unroll
+      for (int q = 0; q < 4; q++)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}), rs,
+            static_cast<int>(4u * (static_cast<uint32_t>(at) + 8u * q)), 0, kCoherentSc1);
+      return;
+    }
 #pragma unroll
     for (int q = 0; q < 4; q++)
-      *reinterpret_cast<f32x4*>(p + 8u * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+      *reinterpret_cast<f32x4*>(sp.terms + at + 8u * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
     return;
   }
 #pragma unroll
@@ -152,19 +166,27 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
     *last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u == gridDim.z;
   __syncthreads();
   if (!*last) return;
-  // slots of four tokens: 8*NT a row, kRowsWG rows, kSlots a thread; byte
-  // offsets within the planes (below 4 GiB, the host checks)
+  // kSlots slots a thread: [rows_pad][tokens] planes, slot (row sl / kCols,
+  // tokens 4 (sl % kCols) ..); token-major planes, slot (token sl / 32, rows
+  // 4 (sl % 32) ..). Byte offsets within the planes (below 2^31, the host
+  // checks); slots past the tile's tokens read its first and store nothing
   constexpr uint32_t kCols = 8u * NT, kSlots = kRowsWG * kCols / 256u, kAhead = kFixupPlanes / NT;
-  const uint32_t cols = static_cast<uint32_t>(min(static_cast<size_t>(32u * NT), T - tok0)) / 4u;
-  const uint32_t n4 = 4u * sp.rows_pad * static_cast<uint32_t>(T);
+  const uint32_t tw = static_cast<uint32_t>(min(static_cast<size_t>(32u * NT), T - tok0));
+  const uint32_t n4 = 4u * sp.rows_pad * static_cast<uint32_t>(T), R0 = blockIdx.x * kRowsWG;
   const __amdgpu_buffer_rsrc_t rs =
       __builtin_amdgcn_make_buffer_rsrc(sp.terms, 0, static_cast<int>(n4 * sp.planes), kBufferRsrcWord3);
   uint32_t base[kSlots];
   f32x4 y[kSlots];
 #pragma unroll
   for (uint32_t k = 0; k < kSlots; k++) {
-    const uint32_t sl = threadIdx.x + 256u * k, r = sl / kCols, c = sl % kCols;
-    base[k] = 4u * ((blockIdx.x * kRowsWG + r) * static_cast<uint32_t>(T) + tok0 + 4u * (c < cols ? c : 0u));
+    const uint32_t sl = threadIdx.x + 256u * k;
+    if (sp.tmajor) {
+      const uint32_t t = sl / 32u, rq = sl % 32u;
+      base[k] = 4u * ((tok0 + (t < tw ? t : 0u)) * sp.rows_pad + R0 + 4u * rq);
+    } else {
+      const uint32_t r = sl / kCols, c = sl % kCols;
+      base[k] = 4u * ((R0 + r) * static_cast<uint32_t>(T) + tok0 + 4u * (4u * c < tw ? c : 0u));
+    }
     y[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base[k], 0, kCoherentSc1));
   }
   for (uint32_t p0 = 1; p0 < sp.planes; p0 += kAhead) {
@@ -182,16 +204,34 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
         if (p0 + j < sp.planes) y[k] += v[j][k];
   }
   const GemvJob& J = jobs.j[gemm_job(jobs, blockIdx.x)];
+  const bool runs = J.tmajor && J.rows % 4u == 0 && (reinterpret_cast<uintptr_t>(J.out) & 15u) == 0;
 #pragma unroll
   for (uint32_t k = 0; k < kSlots; k++) {
-    const uint32_t sl = threadIdx.x + 256u * k, r = sl / kCols, c = sl % kCols;
-    const uint32_t row = (blockIdx.x - J.wg_begin) * kRowsWG + r;
-    if (c >= cols || row >= J.rows) continue;
+    const uint32_t sl = threadIdx.x + 256u * k;
+    if (sp.tmajor) {
+      const uint32_t t = sl / 32u, row = (blockIdx.x - J.wg_begin) * kRowsWG + 4u * (sl % 32u);
+      const size_t tok = tok0 + t;
+      if (t >= tw || row >= J.rows) continue;
+      if (runs) {  // four rows of the token, one 16-byte store
+        const size_t o = tok * J.rows + row;
+        if (o + 4u <= J.out_len) *reinterpret_cast<f32x4*>(J.out + o) = y[k];
+        continue;
+      }
 #pragma unroll
-    for (uint32_t e = 0; e < 4u; e++) {
-      const size_t tok = tok0 + 4u * c + e;
-      const size_t o = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
-      if (o < J.out_len) J.out[o] = y[k][e];
+      for (uint32_t e = 0; e < 4u; e++) {
+        const size_t o = J.tmajor ? tok * J.rows + row + e : static_cast<size_t>(row + e) * T + tok;
+        if (row + e < J.rows && o < J.out_len) J.out[o] = y[k][e];
+      }
+    } else {
+      const uint32_t r = sl / kCols, c = sl % kCols;
+      const uint32_t row = (blockIdx.x - J.wg_begin) * kRowsWG + r;
+      if (4u * c >= tw || row >= J.rows) continue;
+#pragma unroll
+      for (uint32_t e = 0; e < 4u; e++) {
+        const size_t tok = tok0 + 4u * c + e;
+        const size_t o = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
+        if (o < J.out_len) J.out[o] = y[k][e];
+      }
     }
   }
   if (threadIdx.x == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -694,10 +734,10 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
                      static_cast<size_t>(wgs) * tiles <= kFixupTiles && tuning().gemm_fixup &&
                      plan.planes <= kFixupMaxPlanes &&
                      static_cast<size_t>(plan.planes) * plan.rows_pad * tokens * sizeof(float) <= 0x7fffffffu;
-  // token-major planes for the caller, and for the combine of token-major
-  // outputs (its reads and stores then both run along rows); the fixup reads
-  // [rows_pad][tokens] planes (every job of a launch has the same tmajor)
-  const uint32_t tplanes = defer || (!fixup && jobs.j[0].tmajor) ? 1u : 0u;
+  // token-major planes for the caller, and for the combine or fixup of
+  // token-major outputs (its reads and stores then both run along rows;
+  // every job of a launch has the same tmajor)
+  const uint32_t tplanes = defer || jobs.j[0].tmajor ? 1u : 0u;
   hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
                      jobs, q, tokens,
                      SplitTerms{terms, plan.seg_len, plan.rows_pad, tplanes, plan.planes, fixup ? counters : nullptr});
