@@ -986,14 +986,25 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* gate, const 
 // 256-value block blockIdx.x, quantized to Q8_K into q as quantize_super_kernel
 // would from hf: one launch instead of two, and hf never leaves the chip.
 // Thread i reads weight row 256 blockIdx.x + i of gate and up, the four
-// tokens side by side (one 16-byte load when n is a multiple of 4); wave w
-// then quantizes token t0 + w's block from LDS.
-__global__ __launch_bounds__(256) void silu_quant_kernel(const float* gate, const float* up, uint32_t n, Q8Dev q) {
+// tokens side by side (one 16-byte load when n is a multiple of 4; TM: gate
+// and up token-major, rows of fw values, so each token's load runs along
+// the rows); wave w then quantizes token t0 + w's block from LDS.
+template <bool TM>
+__global__ __launch_bounds__(256) void silu_quant_kernel(const float* gate, const float* up, uint32_t n, uint32_t fw,
+                                                         Q8Dev q) {
   __shared__ __align__(16) float blk[4][256];
   const uint32_t tid = threadIdx.x, sb = blockIdx.x, t0 = 4u * blockIdx.y;
   const size_t at = static_cast<size_t>(sb * 256u + tid) * n + t0;
   float g[4], u[4];
-  if ((n & 3u) == 0) {
+  if constexpr (TM) {
+#pragma unroll
+    for (uint32_t j = 0; j < 4u; j++) {
+      // tokens past n read token n - 1 (wave j then stores nothing)
+      const size_t o = static_cast<size_t>(min(t0 + j, n - 1u)) * fw + sb * 256u + tid;
+      g[j] = gate[o];
+      u[j] = up[o];
+    }
+  } else if ((n & 3u) == 0) {
     const float4 gv = *reinterpret_cast<const float4*>(gate + at);
     const float4 uv = *reinterpret_cast<const float4*>(up + at);
     g[0] = gv.x, g[1] = gv.y, g[2] = gv.z, g[3] = gv.w;
@@ -1409,12 +1420,14 @@ rh_status forward_device(rh_decoder* d, const uint32_t* tokens, size_t n, size_t
                          b.ffn_norm, c.rms_norm_eps, 0u, d->normed, d->q8, nullptr, 0u, 0u);
     RHD(hipGetLastError());
     if (qn)
-      RHS(mm_q8(d, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
+      RHS(mm_q8(d, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}, tm));
     else
       RHS(mm(d, d->normed, n, w, {{b.gate, d->gate, n * f}, {b.up, d->up, n * f}}));
     if (d->quant_ffn && n >= 2) {
-      hipLaunchKernelGGL(silu_quant_kernel, dim3(f / 256u, (nn + 3u) / 4u), dim3(256), 0, s, d->gate, d->up, nn,
-                         q8_for(d, f));
+      // gate and up are token-major where the k-quant GEMM stored them so
+      hipLaunchKernelGGL(tm && qn ? silu_quant_kernel<true> : silu_quant_kernel<false>,
+                         dim3(f / 256u, (nn + 3u) / 4u),
+                         dim3(256), 0, s, d->gate, d->up, nn, f, q8_for(d, f));
       RHD(hipGetLastError());
       RHS(mm_q8(d, n, f, {{b.down, d->delta, n * w}}, tm));
     } else {
