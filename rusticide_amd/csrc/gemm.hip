@@ -154,9 +154,14 @@ __device__ __forceinline__ void store_lane_plane(const SplitTerms& sp, float* pl
   }
 }
 
+// Token-major outputs from [rows_pad][tokens] planes go through `tile`
+// (LDS, 32*NT tokens x kTileStride floats): the sums are stored there by row
+// and read back by token, so the outputs are stored in runs of four rows.
+constexpr uint32_t kTileStride = kRowsWG + 4u;
+
 template <int NT>
 __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTerms& sp, size_t T, uint32_t tok0,
-                                            uint32_t* last) {
+                                            uint32_t* last, float* tile) {
   // every wave's plane stores complete before one lane counts the
   // workgroup in
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -222,6 +227,10 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
         const size_t o = J.tmajor ? tok * J.rows + row + e : static_cast<size_t>(row + e) * T + tok;
         if (row + e < J.rows && o < J.out_len) J.out[o] = y[k][e];
       }
+    } else if (J.tmajor) {  // into the tile, by row
+      const uint32_t r = sl / kCols, c = sl % kCols;
+#pragma unroll
+      for (uint32_t e = 0; e < 4u; e++) tile[(4u * c + e) * kTileStride + r] = y[k][e];
     } else {
       const uint32_t r = sl / kCols, c = sl % kCols;
       const uint32_t row = (blockIdx.x - J.wg_begin) * kRowsWG + r;
@@ -229,8 +238,29 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
 #pragma unroll
       for (uint32_t e = 0; e < 4u; e++) {
         const size_t tok = tok0 + 4u * c + e;
-        const size_t o = J.tmajor ? tok * J.rows + row : static_cast<size_t>(row) * T + tok;
+        const size_t o = static_cast<size_t>(row) * T + tok;
         if (o < J.out_len) J.out[o] = y[k][e];
+      }
+    }
+  }
+  if (!sp.tmajor && J.tmajor) {  // the tile back by token: (token sl / 32, rows 4 (sl % 32) ..)
+    __syncthreads();
+#pragma unroll
+    for (uint32_t k = 0; k < kSlots; k++) {
+      const uint32_t sl = threadIdx.x + 256u * k, t = sl / 32u, rq = sl % 32u;
+      const uint32_t row = (blockIdx.x - J.wg_begin) * kRowsWG + 4u * rq;
+      const size_t tok = tok0 + t;
+      if (t >= tw || row >= J.rows) continue;
+      const f32x4 v = *reinterpret_cast<const f32x4*>(tile + t * kTileStride + 4u * rq);
+      if (runs) {
+        const size_t o = tok * J.rows + row;
+        if (o + 4u <= J.out_len) *reinterpret_cast<f32x4*>(J.out + o) = v;
+        continue;
+      }
+#pragma unroll
+      for (uint32_t e = 0; e < 4u; e++) {
+        const size_t o = tok * J.rows + row + e;
+        if (row + e < J.rows && o < J.out_len) J.out[o] = v[e];
       }
     }
   }
@@ -578,7 +608,8 @@ __global__ __launch_bounds__(256) void gemm_kq_rows_kernel(GemvJobs jobs, Q8Dev 
   }
   if constexpr (SPLIT) {
     __shared__ uint32_t fix_last;
-    if (split.counters) split_fixup<NT>(jobs, split, T, tok0, &fix_last);
+    static_assert(32u * NT * kTileStride * 4u <= rows_kernel_lds<NT>(), "the fixup's tile fits the LDS");
+    if (split.counters) split_fixup<NT>(jobs, split, T, tok0, &fix_last, reinterpret_cast<float*>(lds));
   }
 }
 
@@ -734,10 +765,11 @@ hipError_t launch_rows(GemvJobs jobs, const Q8Dev& q, size_t tokens, const Split
                      static_cast<size_t>(wgs) * tiles <= kFixupTiles && tuning().gemm_fixup &&
                      plan.planes <= kFixupMaxPlanes &&
                      static_cast<size_t>(plan.planes) * plan.rows_pad * tokens * sizeof(float) <= 0x7fffffffu;
-  // token-major planes for the caller, and for the combine or fixup of
-  // token-major outputs (its reads and stores then both run along rows;
-  // every job of a launch has the same tmajor)
-  const uint32_t tplanes = defer || jobs.j[0].tmajor ? 1u : 0u;
+  // token-major planes for the caller, and for the combine of token-major
+  // outputs (its reads and stores then both run along rows; every job of a
+  // launch has the same tmajor); the fixup's device-coherent plane stores
+  // run along tokens ([rows_pad][tokens]) and it transposes through LDS
+  const uint32_t tplanes = defer || (!fixup && jobs.j[0].tmajor) ? 1u : 0u;
   hipLaunchKernelGGL((gemm_kq_rows_kernel<FMT, NT, true>), dim3(wgs, tiles, plan.segs), dim3(256), lds, s,
                      jobs, q, tokens,
                      SplitTerms{terms, plan.seg_len, plan.rows_pad, tplanes, plan.planes, fixup ? counters : nullptr});
