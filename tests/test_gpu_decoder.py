@@ -214,6 +214,22 @@ def test_grouped_attention_matches_the_cpu_path(ctx, norm_path, heads, kv_heads,
     cpu.close()
 
 
+def test_token_major_split_gemms_over_partial_token_tiles(ctx):
+    # batches of 36, 12 and 52 tokens (multiples of 4, not of 32): the split
+    # QKV GEMM's tile fixup transposes the last, partial token tile of its
+    # token-major outputs through LDS, the O planes and the down combine are
+    # token-major; 66 tokens (not a multiple of 4) take the combine launch
+    cfg = dict(SMALL, embedding_length=1024, head_count=16, head_count_kv=2, head_dim=64, context_length=256)
+    model = synth.decoder_model(cfg, seed=37)
+    gpu, cpu = R.Decoder(ctx, model), O.Decoder(model, threads=16)
+    tokens = np.random.default_rng(37).integers(0, cfg["vocab_size"], 166).astype(np.uint32)
+    for start, end in ((0, 36), (36, 48), (48, 100), (100, 166)):
+        g, c = gpu.forward_batch(tokens[start:end], start), cpu.forward_batch(tokens[start:end], start)
+        assert same_bits(g, c), f"start {start}: max |diff| {diff(g, c)}"
+    gpu.close()
+    cpu.close()
+
+
 @pytest.mark.parametrize("tokens", [200, 320])
 def test_long_batches_store_the_residual_token_major_without_a_split(ctx, tokens):
     # batches long enough that the O and down GEMMs run unsplit store the
