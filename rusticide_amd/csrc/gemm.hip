@@ -89,11 +89,10 @@ constexpr uint32_t kRowsWG = 128;  // rows a GEMM workgroup owns
 // last of the tile's gridDim.z segments to arrive sums the tile's planes,
 // plane 0 then planes 1.. one addition at a time as gemm_combine_kernel
 // does (the same bits), stores the outputs and sets the counter back to 0
-// for the next launch. No workgroup waits on another. Tokens come in
-// multiples of 4 (the host checks): a thread's slot is four consecutive
-// tokens of a row in [rows_pad][tokens] planes, or four consecutive rows of
-// a token in token-major planes (token-major outputs), one 16-byte load
-// either way.
+// for the next launch. No workgroup waits on another. The planes are
+// [rows_pad][tokens] and tokens come in multiples of 4 (the host checks): a
+// thread's slot is four consecutive tokens of a row, one 16-byte load a
+// plane.
 //
 // Coherence without cache maintenance: the workgroups of a tile may sit on
 // different XCDs, whose L2 caches are not coherent with one another. The
@@ -124,27 +123,16 @@ __device__ __forceinline__ void store_plane(float* p, float v, bool coherent) {
 // A lane's 16 values of one token into a plane: register 4q + u holds row
 // 8q + 4g + u of the wave's 32 (the MFMA's D layout), so a token-major
 // plane takes them as four 16-byte stores of four consecutive rows (a store
-// instruction then writes 32 bytes a token instead of 4); device-coherent
-// ones (a fixup reads them) as sc1 buffer stores.
+// instruction then writes 32 bytes a token instead of 4). A fixup's planes
+// (device-coherent stores) are never token-major.
 __device__ __forceinline__ void store_lane_plane(const SplitTerms& sp, float* plane, uint32_t r0, uint32_t g,
                                                  size_t tok, size_t T, const float (&v)[16]) {
   const bool coherent = sp.counters != nullptr;
-  if (sp.tmajor) {
-    const size_t at = static_cast<size_t>(plane - sp.terms) + tok * sp.rows_pad + r0 + 4u * g;
-    if (coherent) {
-      const uint32_t bytes = 4u * sp.rows_pad * static_cast<uint32_t>(T) * sp.planes;  // below 2^31
-      const __amdgpu_buffer_rsrc_t rs =
-          __builtin_amdgcn_make_buffer_rsrc(sp.terms, 0, static_cast<int>(bytes), kBufferRsrcWord3);
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        __builtin_amdgcn_raw_buffer_store_b128(
-            __builtin_bit_cast(u32x4, f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]}), rs,
-            static_cast<int>(4u * (static_cast<uint32_t>(at) + 8u * q)), 0, kCoherentSc1);
-      return;
-    }
+  if (sp.tmajor && !coherent) {
+    float* p = plane + tok * sp.rows_pad + r0 + 4u * g;
 #pragma unroll
     for (int q = 0; q < 4; q++)
-      *reinterpret_cast<f32x4*>(sp.terms + at + 8u * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
+      *reinterpret_cast<f32x4*>(p + 8u * q) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
     return;
   }
 #pragma unroll
@@ -171,10 +159,9 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
     *last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u == gridDim.z;
   __syncthreads();
   if (!*last) return;
-  // kSlots slots a thread: [rows_pad][tokens] planes, slot (row sl / kCols,
-  // tokens 4 (sl % kCols) ..); token-major planes, slot (token sl / 32, rows
-  // 4 (sl % 32) ..). Byte offsets within the planes (below 2^31, the host
-  // checks); slots past the tile's tokens read its first and store nothing
+  // kSlots slots a thread, slot (row sl / kCols, tokens 4 (sl % kCols) ..);
+  // byte offsets within the planes (below 2^31, the host checks); slots
+  // past the tile's tokens read its first and store nothing
   constexpr uint32_t kCols = 8u * NT, kSlots = kRowsWG * kCols / 256u, kAhead = kFixupPlanes / NT;
   const uint32_t tw = static_cast<uint32_t>(min(static_cast<size_t>(32u * NT), T - tok0));
   const uint32_t n4 = 4u * sp.rows_pad * static_cast<uint32_t>(T), R0 = blockIdx.x * kRowsWG;
@@ -184,14 +171,8 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
   f32x4 y[kSlots];
 #pragma unroll
   for (uint32_t k = 0; k < kSlots; k++) {
-    const uint32_t sl = threadIdx.x + 256u * k;
-    if (sp.tmajor) {
-      const uint32_t t = sl / 32u, rq = sl % 32u;
-      base[k] = 4u * ((tok0 + (t < tw ? t : 0u)) * sp.rows_pad + R0 + 4u * rq);
-    } else {
-      const uint32_t r = sl / kCols, c = sl % kCols;
-      base[k] = 4u * ((R0 + r) * static_cast<uint32_t>(T) + tok0 + 4u * (4u * c < tw ? c : 0u));
-    }
+    const uint32_t sl = threadIdx.x + 256u * k, r = sl / kCols, c = sl % kCols;
+    base[k] = 4u * ((R0 + r) * static_cast<uint32_t>(T) + tok0 + 4u * (4u * c < tw ? c : 0u));
     y[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, base[k], 0, kCoherentSc1));
   }
   for (uint32_t p0 = 1; p0 < sp.planes; p0 += kAhead) {
@@ -212,27 +193,11 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
   const bool runs = J.tmajor && J.rows % 4u == 0 && (reinterpret_cast<uintptr_t>(J.out) & 15u) == 0;
 #pragma unroll
   for (uint32_t k = 0; k < kSlots; k++) {
-    const uint32_t sl = threadIdx.x + 256u * k;
-    if (sp.tmajor) {
-      const uint32_t t = sl / 32u, row = (blockIdx.x - J.wg_begin) * kRowsWG + 4u * (sl % 32u);
-      const size_t tok = tok0 + t;
-      if (t >= tw || row >= J.rows) continue;
-      if (runs) {  // four rows of the token, one 16-byte store
-        const size_t o = tok * J.rows + row;
-        if (o + 4u <= J.out_len) *reinterpret_cast<f32x4*>(J.out + o) = y[k];
-        continue;
-      }
-#pragma unroll
-      for (uint32_t e = 0; e < 4u; e++) {
-        const size_t o = J.tmajor ? tok * J.rows + row + e : static_cast<size_t>(row + e) * T + tok;
-        if (row + e < J.rows && o < J.out_len) J.out[o] = y[k][e];
-      }
-    } else if (J.tmajor) {  // into the tile, by row
-      const uint32_t r = sl / kCols, c = sl % kCols;
+    const uint32_t sl = threadIdx.x + 256u * k, r = sl / kCols, c = sl % kCols;
+    if (J.tmajor) {  // into the tile, by row
 #pragma unroll
       for (uint32_t e = 0; e < 4u; e++) tile[(4u * c + e) * kTileStride + r] = y[k][e];
     } else {
-      const uint32_t r = sl / kCols, c = sl % kCols;
       const uint32_t row = (blockIdx.x - J.wg_begin) * kRowsWG + r;
       if (4u * c >= tw || row >= J.rows) continue;
 #pragma unroll
@@ -243,7 +208,7 @@ __device__ __forceinline__ void split_fixup(const GemvJobs& jobs, const SplitTer
       }
     }
   }
-  if (!sp.tmajor && J.tmajor) {  // the tile back by token: (token sl / 32, rows 4 (sl % 32) ..)
+  if (J.tmajor) {  // the tile back by token: (token sl / 32, rows 4 (sl % 32) ..)
     __syncthreads();
 #pragma unroll
     for (uint32_t k = 0; k < kSlots; k++) {
