@@ -13,8 +13,9 @@ rows. Weights rotate over more than 1 GiB of distinct HBM copies, so the
 rows*row_bytes (+32 I2_S trailer) + 4*cols (f32 x) + 4*rows (f32 y).
 `roofline.achieved` is the same bytes over the average duration of the step's
 GEMV kernel, measured with HIP events on the stream it is launched on, around
-`steps` launches that the host queues behind a bounded hold kernel
-(rh_hold_device) so that they run back to back. Every warm-up makes whole
+max(`steps`, 200) launches that the host queues behind a bounded hold kernel
+(rh_hold_device) so that they run back to back (at least 200, so that the
+first launch after the hold does not weigh on a short run's average). Every warm-up makes whole
 passes over the rotation of copies and lasts at least 50 ms, so the timed
 launches read copies whose pages are mapped and which the Infinity Cache no
 longer holds.
@@ -116,6 +117,7 @@ def load_rotation(ctx, name: str):
 
 
 WARM_MIN_S = 0.05  # every warm-up runs at least this long, whatever --warmup says
+HELD_MIN = 200  # launches a held measurement averages over, whatever --steps says
 
 
 def hold_us_for(launches: int, per_launch_host_us: float = 20.0) -> int:
@@ -193,15 +195,16 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
     ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
     unheld_us = 1e3 * start.elapsed_ms(end) / steps
     gpu_out = out.numpy()
-    # the same number of launches, continuing the rotation, queued behind a
-    # hold: the kernel's back-to-back time per launch, without the host's
-    # latency to the first launch
-    kernel_us, held, host_us = held_events(ctx, lambda: run(handles[1], steps), steps)
+    # launches continuing the rotation, queued behind a hold: the kernel's
+    # back-to-back time per launch, without the host's latency to the first
+    # launch, over at least HELD_MIN of them
+    nheld = max(steps, HELD_MIN)
+    kernel_us, held, host_us = held_events(ctx, lambda: run(handles[1], nheld), nheld)
 
     # the same kernel on one cache-resident copy (Infinity Cache), labelled warm
     one = R.matrix_handles(mats[:1])
     run(one, max(warmup, 50))
-    warm_us = held_events(ctx, lambda: run(one, steps), steps)[0]
+    warm_us = held_events(ctx, lambda: run(one, nheld), nheld)[0]
 
     # the unfused form for comparison: the GEMV alone on a pre-quantized activation
     kind = R.ROW if type_id == 36 else R.SUPER_BLOCK
@@ -210,10 +213,10 @@ def measure_gpu(ctx, name: str, steps: int, warmup: int):
         R.dot_matrix_device(mats[i], q8, out)
 
     def prequant():
-        for i in range(steps):
+        for i in range(nheld):
             R.dot_matrix_device(mats[i % ncopies], q8, out)
 
-    prequant_us = held_events(ctx, prequant, steps, per_launch_host_us=60.0)[0]
+    prequant_us = held_events(ctx, prequant, nheld, per_launch_host_us=60.0)[0]
     q8.free()
     for m in mats:
         m.free()
@@ -260,7 +263,8 @@ def measure_stream_read(ctx, nbytes: int, copies: int, steps: int, warmup: int) 
     more = math.ceil(max(0.0, WARM_MIN_S - el) / (el / passes))
     if more:
         run(more * copies)
-    us = held_events(ctx, lambda: run(steps), steps)[0]
+    nheld = max(steps, HELD_MIN)
+    us = held_events(ctx, lambda: run(nheld), nheld)[0]
     for b in bufs:
         b.free()
     sink.free()
@@ -741,9 +745,9 @@ def main() -> int:
                      "unheld_kernel_avg_us": round(h["unheld_kernel_us"], 3),
                      "queued_inside_hold": h["held"],
                      "host_us_per_launch": round(h["host_us_per_launch"], 2),
-                     "timing": "HIP events on the kernel's stream around `steps` launches queued behind a "
-                               "bounded hold (back to back); unheld_kernel_avg_us: events around the "
-                               "wall-clock timed region itself"},
+                     "timing": "HIP events on the kernel's stream around max(steps, 200) launches queued "
+                               "behind a bounded hold (back to back); unheld_kernel_avg_us: events around "
+                               "the wall-clock timed region itself"},
         "cpu_baseline": cpu,
         "also": also,
     }
