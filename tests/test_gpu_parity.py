@@ -310,15 +310,19 @@ def test_split_k_gives_the_unsplit_bits(ctx, tuning, type_id, rows, cols, tokens
     assert_same_bits(split, oracle_matmul(type_id, data, rows, cols, x, tokens, threads=16))
 
 
+@pytest.mark.parametrize("bn", ["", "64"])
 @pytest.mark.parametrize("tokens", [64, 36, 12])
-def test_split_k_tile_fixup_matches_the_combine_launch(ctx, tuning, tokens):
+def test_split_k_tile_fixup_matches_the_combine_launch(ctx, tuning, tokens, bn):
     # a split launch of up to 9 planes whose token count is a multiple of 4
     # sums each tile's planes in the tile's last-arriving workgroup
     # (device-scope arrival counters, reset by that workgroup);
     # RUSTICIDE_HIP_GEMM_FIXUP=0 sums them in gemm_combine_kernel. Jobs whose
     # rows end mid-tile (two in one Q4_K launch), a 21-plane Q6_K launch
     # (always combined) between them, the calls repeated so that a counter
-    # left non-zero shows
+    # left non-zero shows; RUSTICIDE_HIP_GEMM_BN=64 takes the fixup's
+    # 64-token tiles
+    if bn:
+        tuning.set("RUSTICIDE_HIP_GEMM_BN", bn)
     cols = 2048
     specs = [(12, 300, synth.matrix(12, 300, cols, seed=11)), (12, 45, synth.matrix(12, 45, cols, seed=12)),
              (14, 100, synth.matrix(14, 100, cols, seed=14))]
