@@ -272,8 +272,8 @@ def measure_stream_read(ctx, nbytes: int, copies: int, steps: int, warmup: int) 
 
 
 # The reference's own published single-thread kernel rates for these formats
-# (weights per second, 1 token), with the GB/s they imply at
-# the format's bytes per weight.
+# (weights per second, 1 token, from its bench baselines cited in `source`),
+# with the GB/s they imply at the format's bytes per weight.
 REFERENCE_CPU_PUBLISHED = {
     14: {"format": "Q6_K", "bytes_per_weight": 210 / 256,
          "avx2_xeon_w2150b_gw_s": 16.39, "neon_m1_pro_gw_s": 28.82,
