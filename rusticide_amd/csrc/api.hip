@@ -801,8 +801,8 @@ rh_status rh_init(int device, rh_ctx** out) {
   // the split GEMMs' arrival counters, zeroed once; without them split
   // GEMMs combine in a launch of their own
   if (hipMalloc(&ctx->tile_counters, kFixupTiles * sizeof(uint32_t)) != hipSuccess ||
-      hipMemset(ctx->tile_counters, 0, kFixupTiles * sizeof(uint32_t)) != hipSuccess ||
-      hipDeviceSynchronize() != hipSuccess) {
+      hipMemsetAsync(ctx->tile_counters, 0, kFixupTiles * sizeof(uint32_t), ctx->stream) != hipSuccess ||
+      hipStreamSynchronize(ctx->stream) != hipSuccess) {
     (void)hipGetLastError();
     if (ctx->tile_counters) (void)hipFree(ctx->tile_counters);
     ctx->tile_counters = nullptr;
