@@ -628,6 +628,27 @@ def pmc_probe(steps: int) -> int:
     return 0
 
 
+def pmc_prefill(reps: int) -> int:
+    """A short sequence for `rocprofv3 --pmc` runs over the batched forward:
+    `reps` 64-token prefills (Decoder.forward_batch from position 0) of the
+    e2e section's TinyLlama-shaped model, after one untimed one."""
+    import rusticide_amd as R
+    from rusticide_amd import hip as H
+    from rusticide_amd import synth
+
+    ctx = R.Context(0)
+    dec = R.Decoder(ctx, synth.decoder_model(synth.TINYLLAMA, seed=7))
+    prompt = np.random.default_rng(1).integers(0, synth.TINYLLAMA["vocab_size"], 64).astype(np.uint32)
+    for _ in range(reps + 1):
+        dec.reset()
+        dec.forward_batch(prompt, 0)
+    H.synchronize()
+    log(f"[pmc] prefill: {reps + 1} x 64-token forward_batch")
+    dec.close()
+    ctx.close()
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -637,6 +658,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--pmc", action="store_true", help="run the short sequence rocprofv3 --pmc profiles")
+    ap.add_argument("--pmc-prefill", action="store_true", help="run 64-token prefills for rocprofv3 --pmc")
     ap.add_argument("--decode-reps", type=int, default=5, help="timed 64+128-token generations (0 skips)")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM measurement")
     args = ap.parse_args()
@@ -648,6 +670,8 @@ def main() -> int:
         return 2
     if args.pmc:
         return pmc_probe(20)
+    if args.pmc_prefill:
+        return pmc_prefill(5)
 
     import rusticide_amd as R
     default = [n for n in WORKLOADS if n != "q4k_32000"]
